@@ -1,0 +1,344 @@
+"""CPU oracle for the quantized-GEMM hot path. TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this module, and only as the checker (or the timed CPU
+baseline). The product path (``amd-kernels_amd``) never imports it.
+
+The element-level arithmetic lives in ``hkq_oracle.c`` (plain scalar C, built
+by ``oracle/Makefile`` into ``oracle/_build/liboracle.so``); this file wraps it
+with numpy and adds the fp32/fp64 dequant-matmul references of the GEMMs.
+
+How each function is pinned (tests/test_oracle_*.py):
+
+=====================  ==========================================================
+e4m3_encode/decode     torch.float8_e4m3fn (the reference test's own encoder,
+                       tests/test_moe.py:997-999): every bf16 value, every fp32
+                       within +-2 ulp of every e4m3 rounding boundary, 4M random
+                       fp32; all 256 codes decoded.
+e2m1_encode/decode     value table (moe-gemm/moe_op_mxfp4/kernel.cpp:32-35) and
+                       brute-force nearest-even search over the grid.
+mx_scale_exp           the reference's float formula (fused_mxfp4_quant/
+                       kernel.cpp:99-105) evaluated with numpy log2/floor over
+                       every positive bf16 value.
+quant_rowwise          an independent vectorised numpy/torch restatement of
+                       quant/kernel.cpp:46-107 (and of the reference test
+                       formula tests/test_misc.py:532-536, within 1 code);
+                       hand-computed known answers.
+mx_quant_fp4/fp8       vectorised numpy restatement + round-trip property
+                       (decode(encode(x)) is the nearest grid point).
+static_fp8             torch reference formula (tests/test_moe.py:997-999).
+gemm refs              reference formulas (tests/test_gemm.py:116,148-153,
+                       gemm_a8w8_blockscale/test_parity.py:57-76), torch fp32,
+                       plus closed forms (rank-1 / identity operands).
+moe_ref / ogs_routing  tests/test_moe.py:97-128,733-753 restated; invariants
+                       (histogram sum, exclusive scan, gather permutation) and
+                       agreement with per-expert dense GEMMs.
+=====================  ==========================================================
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+_lib = None
+
+
+def build():
+    """Compile hkq_oracle.c with gcc (oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        L.orc_e4m3fn_encode.restype = ctypes.c_uint8
+        L.orc_e4m3fn_encode.argtypes = [ctypes.c_float]
+        L.orc_e4m3fn_decode.restype = ctypes.c_float
+        L.orc_e4m3fn_decode.argtypes = [ctypes.c_uint8]
+        L.orc_e2m1_encode.restype = ctypes.c_uint8
+        L.orc_e2m1_encode.argtypes = [ctypes.c_float]
+        L.orc_e2m1_decode.restype = ctypes.c_float
+        L.orc_e2m1_decode.argtypes = [ctypes.c_uint8]
+        L.orc_mx_scale_exp.restype = ctypes.c_int
+        L.orc_mx_scale_exp.argtypes = [ctypes.c_float]
+        L.orc_f32_to_bf16.restype = ctypes.c_uint16
+        L.orc_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.orc_quant_rowwise.restype = None
+        L.orc_quant_rowwise.argtypes = [P, I64, I64, I64, I64, ctypes.c_int, P, I64, P, I64]
+        L.orc_static_fp8.restype = None
+        L.orc_static_fp8.argtypes = [P, I64, ctypes.c_float, P]
+        L.orc_mx_quant_fp4.restype = None
+        L.orc_mx_quant_fp4.argtypes = [P, I64, I64, P, P]
+        L.orc_mx_quant_fp8.restype = None
+        L.orc_mx_quant_fp8.argtypes = [P, I64, I64, P, P]
+        L.orc_mx_dequant.restype = None
+        L.orc_mx_dequant.argtypes = [P, P, I64, I64, ctypes.c_int, P]
+        L.orc_e4m3fn_decode_array.restype = None
+        L.orc_e4m3fn_decode_array.argtypes = [P, I64, P]
+        L.orc_mx_fp4_dequant_f32.restype = None
+        L.orc_mx_fp4_dequant_f32.argtypes = [P, P, I64, I64, P]
+        for name in ("orc_e4m3fn_encode_array", "orc_e2m1_encode_array", "orc_mx_scale_exp_array"):
+            getattr(L, name).restype = None
+            getattr(L, name).argtypes = [P, I64, P]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ----------------------------------------------------------------------------
+# bf16 helpers (numpy has no bf16: bf16 tensors travel as uint16 bit patterns)
+# ----------------------------------------------------------------------------
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round fp32 to bf16 (nearest even), returned as uint16 bits."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Values of x (any float dtype) after rounding to fp32 then bf16."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(x, dtype=np.float32)))
+
+
+# ----------------------------------------------------------------------------
+# Codecs
+# ----------------------------------------------------------------------------
+
+def e4m3_encode(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint8)
+    lib().orc_e4m3fn_encode_array(_p(x), x.size, _p(out))
+    return out
+
+
+_E4M3_TABLE = None
+
+
+def e4m3_decode(c: np.ndarray) -> np.ndarray:
+    global _E4M3_TABLE
+    if _E4M3_TABLE is None:
+        codes = np.arange(256, dtype=np.uint8)
+        out = np.empty(256, dtype=np.float32)
+        lib().orc_e4m3fn_decode_array(_p(codes), 256, _p(out))
+        _E4M3_TABLE = out
+    return _E4M3_TABLE[np.asarray(c, dtype=np.uint8)]
+
+
+def e2m1_encode(q: np.ndarray) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.empty(q.shape, dtype=np.uint8)
+    lib().orc_e2m1_encode_array(_p(q), q.size, _p(out))
+    return out
+
+
+def e2m1_decode(n: np.ndarray) -> np.ndarray:
+    f = lib().orc_e2m1_decode
+    table = np.array([f(i) for i in range(16)], dtype=np.float32)
+    return table[np.asarray(n, dtype=np.uint8) & 0xF]
+
+
+def mx_scale_exp(amax) -> np.ndarray:
+    """Unbiased e8m0 exponent(s) of the MXFP4 scale rule for amax value(s)."""
+    a = np.ascontiguousarray(amax, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.int32)
+    lib().orc_mx_scale_exp_array(_p(a), a.size, _p(out))
+    return out
+
+
+def e8m0_decode(s: np.ndarray) -> np.ndarray:
+    s = np.asarray(s, dtype=np.int32)
+    v = np.ldexp(np.float32(1.0), np.minimum(s, 254) - 127).astype(np.float32)
+    return np.where(s == 255, np.float32(np.nan), v)
+
+
+# ----------------------------------------------------------------------------
+# Quantizers (inputs: bf16 bit patterns, uint16 [M, K] C-contiguous)
+# ----------------------------------------------------------------------------
+
+def quant_rowwise(xb: np.ndarray, group: int | None = None, kind: str = "fp8"):
+    """Per-token (group=None) or 1 x group quantization. Returns (q uint8
+    [M,K], s float32 [M, K//group])."""
+    xb = np.ascontiguousarray(xb, dtype=np.uint16)
+    M, K = xb.shape
+    g = K if group is None else group
+    assert K % g == 0
+    q = np.empty((M, K), dtype=np.uint8)
+    s = np.empty((M, K // g), dtype=np.float32)
+    lib().orc_quant_rowwise(_p(xb), M, K, K, g, 0 if kind == "fp8" else 1, _p(q), K, _p(s), K // g)
+    return q, s
+
+
+def quant_static_fp8(xb: np.ndarray, scale: float) -> np.ndarray:
+    xb = np.ascontiguousarray(xb, dtype=np.uint16)
+    y = np.empty(xb.shape, dtype=np.uint8)
+    lib().orc_static_fp8(_p(xb), xb.size, float(scale), _p(y))
+    return y
+
+
+def mx_quant_fp4(xb: np.ndarray):
+    """Returns (q uint8 [M, K/2], s uint8 e8m0 [M, K/32])."""
+    xb = np.ascontiguousarray(xb, dtype=np.uint16)
+    M, K = xb.shape
+    assert K % 32 == 0
+    q = np.empty((M, K // 2), dtype=np.uint8)
+    s = np.empty((M, K // 32), dtype=np.uint8)
+    lib().orc_mx_quant_fp4(_p(xb), M, K, _p(q), _p(s))
+    return q, s
+
+
+def mx_quant_fp8(xb: np.ndarray):
+    xb = np.ascontiguousarray(xb, dtype=np.uint16)
+    M, K = xb.shape
+    q = np.empty((M, K), dtype=np.uint8)
+    s = np.empty((M, K // 32), dtype=np.uint8)
+    lib().orc_mx_quant_fp8(_p(xb), M, K, _p(q), _p(s))
+    return q, s
+
+
+def mx_dequant(q: np.ndarray, s: np.ndarray, M: int, K: int, is_fp4: bool) -> np.ndarray:
+    """bf16 bits [M, K]."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    s = np.ascontiguousarray(s, dtype=np.uint8)
+    out = np.empty((M, K), dtype=np.uint16)
+    lib().orc_mx_dequant(_p(q), _p(s), M, K, int(is_fp4), _p(out))
+    return out
+
+
+def mx_fp4_dequant_f32(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    s = np.ascontiguousarray(s, dtype=np.uint8)
+    R, Kh = q.shape
+    K = Kh * 2
+    out = np.empty((R, K), dtype=np.float32)
+    lib().orc_mx_fp4_dequant_f32(_p(q), _p(s), R, K, _p(out))
+    return out
+
+
+# ----------------------------------------------------------------------------
+# GEMM references (fp64 accumulation of exactly decoded operands)
+# ----------------------------------------------------------------------------
+
+def gemm_a8w8_ref(A: np.ndarray, B: np.ndarray, sa: np.ndarray, sb: np.ndarray) -> np.ndarray:
+    """C = (A . B^T) * sa[:,None] * sb[None,:] (tests/test_gemm.py:116) on
+    e4m3fn codes A [M,K], B [N,K]; fp64 result [M, N]."""
+    a = e4m3_decode(A).astype(np.float64)
+    b = e4m3_decode(B).astype(np.float64)
+    return (a @ b.T) * np.asarray(sa, np.float64).reshape(-1, 1) * np.asarray(sb, np.float64).reshape(1, -1)
+
+
+def gemm_blockscale_ref(A, B, sa, sb, group_k: int = 128, group_n: int = 128) -> np.ndarray:
+    """C = sum_kg (A_kg . B_kg^T) * sa[:, kg] * sb[kg, n // group_n]
+    (gemm_a8w8_blockscale/test_parity.py:57-76; tests/test_gemm.py:148-153)."""
+    a = e4m3_decode(A).astype(np.float64)
+    b = e4m3_decode(B).astype(np.float64)
+    M, K = a.shape
+    N = b.shape[0]
+    sa = np.asarray(sa, np.float64).reshape(M, -1)
+    sb = np.asarray(sb, np.float64)
+    sb = sb.reshape(sa.shape[1], -1)
+    C = np.zeros((M, N), dtype=np.float64)
+    for kg in range(sa.shape[1]):
+        ks, ke = kg * group_k, min((kg + 1) * group_k, K)
+        part = a[:, ks:ke] @ b[:, ks:ke].T
+        bs = np.repeat(sb[kg], group_n)[:N]
+        C += part * sa[:, kg:kg + 1] * bs[None, :]
+    return C
+
+
+def gemm_mxfp4_ref(Aq, As, Bq, Bs) -> np.ndarray:
+    """C = sum_k e2m1(a) 2^(sa-127) e2m1(b) 2^(sb-127) (moe-gemm/moe_op_mxfp4/
+    kernel.cpp:191-207 with dense indexing); fp64 [M, N]."""
+    a = mx_fp4_dequant_f32(Aq, As).astype(np.float64)
+    b = mx_fp4_dequant_f32(Bq, Bs).astype(np.float64)
+    return a @ b.T
+
+
+# ----------------------------------------------------------------------------
+# MoE: OGS routing metadata and the grouped GEMM reference
+# ----------------------------------------------------------------------------
+
+def ogs_routing(assigns: np.ndarray, num_experts: int, block_m: int = 128):
+    """OGS metadata from top-k expert assignments [T, topk]
+    (tests/test_moe.py:97-128): hist[e], offs[e] (exclusive scan), gather
+    (sorted slot -> t*topk+k, token-major within an expert), expt_data
+    (e | block << 16 per block_m rows)."""
+    assigns = np.asarray(assigns, dtype=np.int64)
+    T, topk = assigns.shape
+    hist = np.bincount(assigns.ravel(), minlength=num_experts).astype(np.int32)
+    offs = np.zeros(num_experts, dtype=np.int32)
+    offs[1:] = np.cumsum(hist)[:-1]
+    flat = assigns.ravel()  # index t*topk + k
+    order = np.argsort(flat, kind="stable")  # stable: token-major within expert
+    gather = order.astype(np.int32)
+    tiles = []
+    for e in range(num_experts):
+        for b in range((int(hist[e]) + block_m - 1) // block_m):
+            tiles.append(e | (b << 16))
+    return hist, offs, gather, np.array(tiles, dtype=np.int32)
+
+
+def moe_ref(X, W, x_scale, w_scale, bias, gather, hist, offs, expt_data, topk,
+            block_m: int = 128, w_layout: str = "ekn"):
+    """Y[start+gm] = (X[gather[start+gm] // topk] . W[e]) * xs * ws + bias[e]
+    (tests/test_moe.py:733-753; rows gm >= hist[e] skipped, no % M wrap).
+
+    X: e4m3 codes [T, K]; W: e4m3 codes [E, K, N] ("ekn") or [E, N, K] ("enk").
+    x_scale: fp32 broadcastable to [T] (per-token) or scalar;
+    w_scale: fp32 [E] (per-expert) or [E, N] (per-channel).
+    Returns fp64 [T*topk, N] with untouched rows left as NaN."""
+    x = e4m3_decode(X).astype(np.float64)
+    w = e4m3_decode(W).astype(np.float64)
+    if w_layout == "enk":
+        w = np.transpose(w, (0, 2, 1))
+    E, K, N = w.shape
+    T = x.shape[0]
+    xs = np.broadcast_to(np.asarray(x_scale, np.float64).reshape(-1), (T,)) if np.size(x_scale) in (1, T) else None
+    ws = np.asarray(w_scale, np.float64)
+    Y = np.full((T * topk, N), np.nan, dtype=np.float64)
+    for ed in np.asarray(expt_data).tolist():
+        e, b = ed & 0xFFFF, ed >> 16
+        rows = [b * block_m + lm for lm in range(block_m) if b * block_m + lm < hist[e]]
+        if not rows:
+            continue
+        sidx = offs[e] + np.array(rows)
+        tok = np.asarray(gather)[sidx] // topk
+        r = x[tok] @ w[e]
+        r = r * xs[tok][:, None]
+        r = r * (ws[e] if ws.ndim == 1 else ws[e][None, :])
+        if bias is not None:
+            r = r + np.asarray(bias, np.float64)[e][None, :]
+        Y[sidx] = r
+    return Y
+
+
+# ----------------------------------------------------------------------------
+# Input generation (seeded CPU generator, so CPU and GPU see identical bytes)
+# ----------------------------------------------------------------------------
+
+def randn_bf16(shape, std: float = 1.0, seed: int = 0) -> np.ndarray:
+    """bf16 bits of N(0, std) drawn with torch's CPU generator."""
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    t = (torch.randn(*shape, generator=g, dtype=torch.float32) * std).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16).copy()
