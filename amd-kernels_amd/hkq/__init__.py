@@ -1,0 +1,157 @@
+"""ctypes binding of libhkq.so (the C ABI declared in include/hkq.h).
+
+This is the layer the parity tests and bench.py call: plain device pointers,
+explicit sizes and an explicit stream. Torch is used only to allocate device
+memory and to name the stream. If the library is missing, loading raises -- there
+is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG, "lib", "libhkq.so")
+
+KIND_FP8 = 0
+KIND_INT8 = 1
+
+# Every entry point declared in include/hkq.h, with its ctypes signature.
+_P, _I64, _I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+SIGNATURES = {
+    "hkq_last_error": (ctypes.c_char_p, []),
+    "hkq_version": (_I, []),
+    "hkq_per_token_quant": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P]),
+    "hkq_group_quant": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P]),
+    "hkq_static_quant_fp8": (_I, [_P, _P, _P, _I64, _P]),
+    "hkq_mx_quant": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _P]),
+    "hkq_mx_dequant": (_I, [_P, _P, _P, _I64, _I64, _I, _P]),
+    "hkq_gemm_a8w8": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "hkq_gemm_mxfp4": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+}
+
+
+class HkqError(RuntimeError):
+    """A C-ABI call returned a non-zero hipError_t."""
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libhkq.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HkqError(f"{LIB_PATH} is missing: build it with `python amd-kernels_amd/build.py`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().hkq_last_error().decode(errors="replace")
+        raise HkqError(f"{name} failed with code {rc}: {msg}")
+
+
+# ----------------------------------------------------------------------------
+# torch-tensor conveniences over the C ABI (device pointers + current stream)
+# ----------------------------------------------------------------------------
+
+def _ptr(t) -> int:
+    return t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    import torch
+
+    s = torch.cuda.current_stream() if stream is None else stream
+    return s.cuda_stream
+
+
+def per_token_quant(x, kind: int = KIND_FP8, q=None, s=None, stream=None):
+    """x bf16 [M, K] -> (q [M, K] float8_e4m3fn / int8, s fp32 [M])."""
+    import torch
+
+    M, K = x.shape
+    if q is None:
+        q = torch.empty((M, K), dtype=torch.float8_e4m3fn if kind == KIND_FP8 else torch.int8, device=x.device)
+    if s is None:
+        s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    call("hkq_per_token_quant", _ptr(x), _ptr(q), _ptr(s), M, K, x.stride(0), q.stride(0), kind, _stream(stream))
+    return q, s
+
+
+def group_quant(x, group: int = 128, kind: int = KIND_FP8, q=None, s=None, stream=None):
+    """x bf16 [M, K] -> (q [M, K], s fp32 [M, K/group])."""
+    import torch
+
+    M, K = x.shape
+    if q is None:
+        q = torch.empty((M, K), dtype=torch.float8_e4m3fn if kind == KIND_FP8 else torch.int8, device=x.device)
+    if s is None:
+        s = torch.empty((M, K // group), dtype=torch.float32, device=x.device)
+    call("hkq_group_quant", _ptr(x), _ptr(q), _ptr(s), M, K, x.stride(0), q.stride(0), s.stride(0), group, kind,
+         _stream(stream))
+    return q, s
+
+
+def static_quant_fp8(x, scale, y=None, stream=None):
+    import torch
+
+    if y is None:
+        y = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    call("hkq_static_quant_fp8", _ptr(x), _ptr(y), _ptr(scale), x.numel(), _stream(stream))
+    return y
+
+
+def mx_quant(x, is_fp4: bool = True, stream=None):
+    """x bf16 [M, K] -> (q uint8 [M, K/2 or K], s uint8 [M, K/32])."""
+    import torch
+
+    M, K = x.shape
+    q = torch.empty((M, K // 2 if is_fp4 else K), dtype=torch.uint8, device=x.device)
+    s = torch.empty((M, K // 32), dtype=torch.uint8, device=x.device)
+    call("hkq_mx_quant", _ptr(x), _ptr(q), _ptr(s), M, K, x.stride(0), int(is_fp4), _stream(stream))
+    return q, s
+
+
+def mx_dequant(q, s, K: int, is_fp4: bool = True, stream=None):
+    import torch
+
+    M = q.shape[0]
+    out = torch.empty((M, K), dtype=torch.bfloat16, device=q.device)
+    call("hkq_mx_dequant", _ptr(q), _ptr(s), _ptr(out), M, K, int(is_fp4), _stream(stream))
+    return out
+
+
+def gemm_a8w8(A, B, sa, sb, C=None, stream=None):
+    """A [M, K], B [N, K] E4M3FN codes; sa [M], sb [N] fp32 -> C bf16 [M, N]."""
+    import torch
+
+    M, K = A.shape
+    N = B.shape[0]
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
+    call("hkq_gemm_a8w8", _ptr(A), _ptr(B), _ptr(sa), _ptr(sb), _ptr(C), M, N, K, A.stride(0), B.stride(0),
+         C.stride(0), _stream(stream))
+    return C
+
+
+def gemm_mxfp4(A, As, B, Bs, C=None, stream=None):
+    """A u8 [M, K/2], As u8 [M, K/32], B u8 [N, K/2], Bs u8 [N, K/32] -> C bf16 [M, N]."""
+    import torch
+
+    M, K = A.shape[0], A.shape[1] * 2
+    N = B.shape[0]
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
+    call("hkq_gemm_mxfp4", _ptr(A), _ptr(As), _ptr(B), _ptr(Bs), _ptr(C), M, N, K, A.stride(0), B.stride(0),
+         As.stride(0), Bs.stride(0), C.stride(0), _stream(stream))
+    return C

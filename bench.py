@@ -1,0 +1,186 @@
+#!/usr/bin/env python3
+"""Headline benchmark: FP8 A8W8 GEMM (per-token x per-channel scales) at
+M=4096, N=14336, K=4096 on one MI355X, plus the MXFP4 A4W4 GEMM at
+M=4096, N=K=8192 and the per-token FP8 quantizer at [4096, 4096].
+
+A step is one launch of the A8W8 GEMM over resident HBM inputs (synthetic,
+seeded on the CPU: acts ~N(0,1), weights ~N(0,0.02), quantized by this
+library's own quantizers). Kernel time comes from HIP events recorded on the
+stream the kernels are launched on (torch's current stream), bracketing
+exactly --steps launches after --warmup untimed ones.
+
+Prints ONE JSON line. `roofline` describes the dominant kernel (the A8W8
+GEMM): algorithmic flops per launch / average launch duration against the
+MI355X dense FP8 peak; `traffic` is the HBM bytes per launch measured with
+rocprofv3 PMC counters (FETCH_SIZE + WRITE_SIZE) and read from the committed
+profile summary. `cpu_baseline` times the CPU port of the reference formula
+(oracle/cpu_baseline.py) on BASELINE config 0.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "amd-kernels_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_FP8_TFLOPS = 5000.0   # MI355X dense FP8 (e4m3) MFMA
+PEAK_FP4_TFLOPS = 10100.0  # MI355X dense MXFP4 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+HEADLINE = dict(M=4096, N=14336, K=4096)
+MXFP4 = dict(M=4096, N=8192, K=8192)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_a8w8_4096x14336x4096_pmc.txt")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def seeded_bf16(shape, std, seed):
+    import torch
+
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(torch.bfloat16).cuda()
+
+
+def time_launches(fn, steps, warmup):
+    """Average ms per launch over `steps` back-to-back launches on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed PMC summary (null if absent)."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch\s*=\s*([0-9.eE+]+)", open(TRAFFIC_FILE).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant"], default=None,
+                    help="run one kernel only (for profiling); prints no JSON line")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import hkq
+
+    torch.cuda.set_device(0)
+    steps, warmup = args.steps, args.warmup
+
+    # ---- A8W8 headline ----
+    M, N, K = HEADLINE["M"], HEADLINE["N"], HEADLINE["K"]
+    x = seeded_bf16((M, K), 1.0, 1)
+    w = seeded_bf16((N, K), 0.02, 2)
+    qa, sa = hkq.per_token_quant(x)
+    qb, sb = hkq.per_token_quant(w)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()
+    res = {}
+    if args.only in (None, "a8w8"):
+        log(f"a8w8 {M}x{N}x{K}: warmup {warmup}, steps {steps}")
+        ms = time_launches(lambda: hkq.gemm_a8w8(qa, qb, sa, sb, C), steps, warmup)
+        res["a8w8"] = ms
+    del x, w
+
+    # ---- MXFP4 ----
+    if args.only in (None, "mxfp4"):
+        m4, n4, k4 = MXFP4["M"], MXFP4["N"], MXFP4["K"]
+        xa = seeded_bf16((m4, k4), 1.0, 3)
+        xw = seeded_bf16((n4, k4), 0.02, 4)
+        Aq, As = hkq.mx_quant(xa, True)
+        Bq, Bs = hkq.mx_quant(xw, True)
+        C4 = torch.empty((m4, n4), dtype=torch.bfloat16, device="cuda")
+        torch.cuda.synchronize()
+        log(f"mxfp4 {m4}x{n4}x{k4}")
+        res["mxfp4"] = time_launches(lambda: hkq.gemm_mxfp4(Aq, As, Bq, Bs, C4), steps, warmup)
+        del xa, xw
+
+    # ---- per-token FP8 quantizer, bf16 [4096, 4096] ----
+    if args.only in (None, "quant"):
+        xq = seeded_bf16((4096, 4096), 1.0, 5)
+        q = torch.empty((4096, 4096), dtype=torch.float8_e4m3fn, device="cuda")
+        s = torch.empty((4096,), dtype=torch.float32, device="cuda")
+        log("per-token quant 4096x4096")
+        res["quant"] = time_launches(lambda: hkq.per_token_quant(xq, hkq.KIND_FP8, q, s), steps, warmup)
+
+    if args.only is not None:
+        log(json.dumps({k: round(v * 1e3, 2) for k, v in res.items()}) + "  (us per launch)")
+        return
+
+    ms = res["a8w8"]
+    flops = 2.0 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+    m4, n4, k4 = MXFP4["M"], MXFP4["N"], MXFP4["K"]
+    tflops4 = 2.0 * m4 * n4 * k4 / (res["mxfp4"] * 1e-3) / 1e12
+    qbytes = 4096 * 4096 * 3 + 4096 * 4
+    quant_gbs = qbytes / (res["quant"] * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle/cpu_baseline.py, BASELINE config 0)")
+        from oracle import cpu_baseline
+
+        r = cpu_baseline.run()
+        cpu = {"value": round(r["tflops"], 6), "unit": "TFLOP/s", "cores": r["threads"], "kind": "port",
+               "sample": r["sample"], "quant_ms": round(r["quant_ms"], 3), "matmul_ms": round(r["matmul_ms"], 3),
+               "total_ms": round(r["total_ms"], 3)}
+
+    out = {
+        "metric": "FP8 A8W8 GEMM TFLOPS & % MFMA peak (4096x14336x4096); MXFP4 TFLOPS",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3fn",
+        "data": "synthetic (seeded CPU generator: acts ~N(0,1), weights ~N(0,0.02); per-token / per-channel "
+                "E4M3FN quantization by this library)",
+        "config": {"workload": "A8W8 GEMM, per-token x per-channel fp32 scales, bf16 out", "M": M, "N": N, "K": K,
+                   "parallelism": "single GPU"},
+        "pct_fp8_peak": round(100 * tflops / PEAK_FP8_TFLOPS, 2),
+        "mxfp4": {"M": m4, "N": n4, "K": k4, "tflops": round(tflops4, 2), "ms": round(res["mxfp4"], 5),
+                  "pct_fp4_peak": round(100 * tflops4 / PEAK_FP4_TFLOPS, 2)},
+        "quant_per_token_fp8": {"M": 4096, "K": 4096, "GB/s": round(quant_gbs, 1), "ms": round(res["quant"], 5),
+                                "pct_hbm_peak": round(100 * quant_gbs / PEAK_HBM_GBS, 2)},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_FP8_TFLOPS, 4), "traffic": read_traffic()},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,100 @@
+/*
+ * hkq.h -- C ABI of the MI355X (gfx950) quantized-GEMM library (libhkq.so).
+ *
+ * Plain pointers and sizes only: every tensor is a caller-owned device buffer,
+ * every call is asynchronous on `stream` (0 = the null stream, which is where
+ * the reference launches everything), and every call returns 0 on success or a
+ * hipError_t code. Argument errors return hipErrorInvalidValue (1) before any
+ * launch; the message is available from hkq_last_error().
+ *
+ * Data formats
+ *   bf16     : raw 16-bit patterns;
+ *   FP8      : OCP E4M3FN codes (torch.float8_e4m3fn), one byte each;
+ *   FP4      : OCP E2M1 codes, two per byte, even K index in the low nibble;
+ *   e8m0     : one byte, value 2^(code - 127);
+ *   strides  : in elements of the tensor they describe (bytes for u8 tensors).
+ *
+ * Each entry point names the reference interface it replaces (paths relative
+ * to the m8than/amd-kernels repository).
+ */
+#ifndef HKQ_H
+#define HKQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hkq_stream_t; /* the same type as hipStream_t */
+
+#define HKQ_KIND_FP8 0  /* E4M3FN codes, QMAX 448 */
+#define HKQ_KIND_INT8 1 /* int8, QMAX 127, round-half-even (the reference quant_tk rule) */
+
+/* Message of the last argument or launch error raised on this thread. */
+const char* hkq_last_error(void);
+
+/* Library version, (major << 16) | minor. */
+int hkq_version(void);
+
+/* ---- quantizers ------------------------------------------------------------ */
+
+/* Per-token dynamic quantization: s[m] = max(amax(x[m,:]) / QMAX, 1e-10),
+ * q[m,k] = encode(clamp(x[m,k] * (1/s[m]), +-QMAX)).
+ * x bf16 [M, ldx]; q u8/i8 [M, ldq]; s fp32 [M]. K % 8 == 0, K <= 32768.
+ * Replaces quant_tk.per_token_quant_fwd (kernels/quantization/quant/kernel.cpp:140-166),
+ * which is the HKQ_KIND_INT8 rule; HKQ_KIND_FP8 is the same rule with QMAX 448
+ * and an E4M3FN encoder. */
+int hkq_per_token_quant(const void* x, void* q, float* s, int64_t M, int64_t K, int64_t ldx, int64_t ldq, int kind,
+                        hkq_stream_t stream);
+
+/* 1 x group dynamic quantization (group in {32,64,128,256,512}):
+ * s[m, g] over columns [g*group, (g+1)*group), same rule as above.
+ * s fp32 [M, lds]. Replaces the quantization step of
+ * fused_fp8_quant_tk.fused_rmsnorm_fp8_quant_fwd
+ * (kernels/quantization/fused_fp8_quant/kernel.cpp:190-206, 240-268) without the
+ * RMSNorm and with a real E4M3FN encoder in place of the affine byte at :206. */
+int hkq_group_quant(const void* x, void* q, float* s, int64_t M, int64_t K, int64_t ldx, int64_t ldq, int64_t lds,
+                    int64_t group, int kind, hkq_stream_t stream);
+
+/* y = E4M3FN(clamp(x / scale[0], +-448)), n elements (n % 8 == 0).
+ * Replaces quant_moe_tk.downcast_to_static_fp8 (kernels/moe-misc/quant_moe/kernel.cpp:392-410),
+ * with round-to-nearest-even in place of its truncating encoder (:50-73). */
+int hkq_static_quant_fp8(const void* x, void* y, const float* scale, int64_t n, hkq_stream_t stream);
+
+/* MX quantization along the contiguous dim in blocks of 32, x bf16 [M, ldx].
+ * is_fp4: q [M, K/2] E2M1 pairs, s [M, K/32] e8m0 by the MXFP4 rule of
+ *   fused_mxfp4_quant (kernels/quantization/fused_mxfp4_quant/kernel.cpp:97-162);
+ * else  : q [M, K] E4M3FN, s [M, K/32] by the MX-FP8 rule of
+ *   quant_moe (kernels/moe-misc/quant_moe/kernel.cpp:143-217).
+ * Replaces quant_moe_tk.downcast_to_mxfp (quant_moe/kernel.cpp:412-431), whose
+ * FP4 branch writes zeros (:211-214). */
+int hkq_mx_quant(const void* x, void* q, void* s, int64_t M, int64_t K, int64_t ldx, int is_fp4, hkq_stream_t stream);
+
+/* out bf16 [M, K] = decode(q) * 2^(s - 127), s = 0xFF -> NaN.
+ * Replaces quant_moe_tk.upcast_from_mxfp (kernels/moe-misc/quant_moe/kernel.cpp:433-450). */
+int hkq_mx_dequant(const void* q, const void* s, void* out, int64_t M, int64_t K, int is_fp4, hkq_stream_t stream);
+
+/* ---- dense GEMMs (A [M, K], B [N, K], both K-contiguous; C bf16 [M, ldc]) ---- */
+
+/* C = bf16((A . B^T) * sa[m] * sb[n]); A, B E4M3FN; sa fp32 [M], sb fp32 [N].
+ * K % 16 == 0, N % 4 == 0. Replaces gemm_a8w8_tk.dispatch(A, B, a_scale, b_scale, C)
+ * (kernels/gemm-basic/gemm_a8w8/kernel.cpp:162-175) and
+ * gemm_a8w8_per_token_scale_tk.dispatch(A, B, C, a_scale, b_scale)
+ * (kernels/gemm-basic/gemm_a8w8_per_token_scale/kernel.cpp:158-171). */
+int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M, int64_t N,
+                  int64_t K, int64_t lda, int64_t ldb, int64_t ldc, hkq_stream_t stream);
+
+/* MXFP4 A4W4: C = bf16(sum_k e2m1(A) 2^(As-127) e2m1(B) 2^(Bs-127)).
+ * A u8 [M, lda >= K/2], As u8 [M, ldsa >= K/32], B u8 [N, ldb], Bs u8 [N, ldsb].
+ * K % 256 == 0. Replaces gemm_afp4wfp4_tk.dispatch (kernels/gemm-basic/gemm_afp4wfp4/kernel.cpp:147-159),
+ * taking the packed format its header documents (:3-6) instead of
+ * pre-dequantized bf16. */
+int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
+                   int64_t K, int64_t lda, int64_t ldb, int64_t ldsa, int64_t ldsb, int64_t ldc, hkq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HKQ_H */

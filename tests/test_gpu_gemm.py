@@ -1,0 +1,140 @@
+"""GPU parity of the dense GEMMs against the CPU oracle, through the C ABI.
+
+Bar (north star): bf16 C within |C - ref| <= 2e-2 + 1e-2 |ref| of the fp64
+dequant matmul of the same codes and scales, and Frobenius relative error
+< 1e-2. Inputs follow BASELINE's distributions (acts ~N(0,1), weights
+~N(0,0.02)) through the oracle quantizers, so the GEMM test does not depend on
+the GPU quantizer. Small shapes are compared in full (including M = 1, ragged
+M/N and a K tail); BASELINE sizes are checked on a sampled 96 x 96 block of C
+plus closed forms.
+"""
+import numpy as np
+import pytest
+import torch
+
+import hkq
+from gpu_util import assert_gemm_close, dev_f32, dev_u8, host_bf16_f32, require_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def a8w8_inputs(orc, M, N, K, seed):
+    xa = orc.randn_bf16((M, K), seed=seed)
+    xw = orc.randn_bf16((N, K), seed=seed + 1, std=0.02)
+    A, sa = orc.quant_rowwise(xa, None, "fp8")
+    B, sb = orc.quant_rowwise(xw, None, "fp8")
+    return A, B, sa.reshape(-1), sb.reshape(-1)
+
+
+def run_a8w8(A, B, sa, sb):
+    C = hkq.gemm_a8w8(dev_u8(A), dev_u8(B), dev_f32(sa), dev_f32(sb))
+    torch.cuda.synchronize()
+    return host_bf16_f32(C)
+
+
+A8W8_SHAPES = [(256, 256, 128), (1, 256, 256), (16, 512, 512), (100, 260, 4112), (333, 1000, 512),
+               (513, 772, 1040), (128, 4096, 4096), (1024, 1024, 2048)]
+
+
+@pytest.mark.parametrize("M,N,K", A8W8_SHAPES)
+def test_gemm_a8w8(orc, M, N, K):
+    require_gpu()
+    A, B, sa, sb = a8w8_inputs(orc, M, N, K, seed=M + N + K)
+    C = run_a8w8(A, B, sa, sb)
+    assert_gemm_close(C, orc.gemm_a8w8_ref(A, B, sa, sb), f"a8w8 {M}x{N}x{K}")
+
+
+def test_gemm_a8w8_closed_form(orc):
+    """All codes 1.0 (0x38): C = K * sa[m] * sb[n] exactly representable pattern."""
+    require_gpu()
+    M, N, K = 300, 516, 1024
+    rng = np.random.default_rng(1)
+    sa = (rng.integers(1, 8, M) / 64).astype(np.float32)
+    sb = (rng.integers(1, 8, N) / 64).astype(np.float32)
+    C = run_a8w8(np.full((M, K), 0x38, np.uint8), np.full((N, K), 0x38, np.uint8), sa, sb)
+    assert np.array_equal(C, (K * sa[:, None].astype(np.float64) * sb[None, :]).astype(np.float32))
+
+
+def test_gemm_a8w8_strided_and_out_of_place_rows(orc):
+    """lda/ldb/ldc larger than K/N; bytes outside the logical matrices untouched."""
+    require_gpu()
+    M, N, K = 200, 132, 384
+    A, B, sa, sb = a8w8_inputs(orc, M, N, K, seed=77)
+    Ad = torch.zeros((M, K + 128), dtype=torch.uint8, device="cuda")
+    Bd = torch.zeros((N, K + 64), dtype=torch.uint8, device="cuda")
+    Ad[:, :K] = dev_u8(A)
+    Bd[:, :K] = dev_u8(B)
+    Cd = torch.full((M, N + 12), 7.0, dtype=torch.bfloat16, device="cuda")
+    sad, sbd = dev_f32(sa), dev_f32(sb)  # keep the tensors alive while the kernel reads them
+    hkq.call("hkq_gemm_a8w8", Ad.data_ptr(), Bd.data_ptr(), sad.data_ptr(), sbd.data_ptr(),
+             Cd.data_ptr(), M, N, K, K + 128, K + 64, N + 12, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    C = host_bf16_f32(Cd)
+    assert_gemm_close(C[:, :N], orc.gemm_a8w8_ref(A, B, sa, sb), "strided")
+    assert np.all(C[:, N:] == 7.0)
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 14336, 4096), (16, 28672, 4096), (1024, 4096, 14336)])
+def test_gemm_a8w8_baseline_sizes_sampled(orc, M, N, K):
+    require_gpu()
+    A, B, sa, sb = a8w8_inputs(orc, M, N, K, seed=K)
+    C = run_a8w8(A, B, sa, sb)
+    rng = np.random.default_rng(M)
+    rows = np.sort(rng.choice(M, min(M, 96), replace=False))
+    cols = np.sort(rng.choice(N, 96, replace=False))
+    rows[-1], cols[-1] = M - 1, N - 1
+    ref = orc.gemm_a8w8_ref(A[rows], B[cols], sa[rows], sb[cols])
+    assert_gemm_close(C[np.ix_(rows, cols)], ref, f"a8w8 {M}x{N}x{K} sampled")
+    assert np.isfinite(C).all()
+
+
+def mx_inputs(orc, M, N, K, seed):
+    xa = orc.randn_bf16((M, K), seed=seed)
+    xw = orc.randn_bf16((N, K), seed=seed + 1, std=0.02)
+    Aq, As = orc.mx_quant_fp4(xa)
+    Bq, Bs = orc.mx_quant_fp4(xw)
+    return Aq, As, Bq, Bs
+
+
+def run_mxfp4(Aq, As, Bq, Bs):
+    C = hkq.gemm_mxfp4(dev_u8(Aq), dev_u8(As), dev_u8(Bq), dev_u8(Bs))
+    torch.cuda.synchronize()
+    return host_bf16_f32(C)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (1, 256, 512), (128, 512, 8192), (77, 300, 768),
+                                   (600, 1028, 1536)])
+def test_gemm_mxfp4(orc, M, N, K):
+    require_gpu()
+    Aq, As, Bq, Bs = mx_inputs(orc, M, N, K, seed=M * 7 + K)
+    C = run_mxfp4(Aq, As, Bq, Bs)
+    assert_gemm_close(C, orc.gemm_mxfp4_ref(Aq, As, Bq, Bs), f"mxfp4 {M}x{N}x{K}")
+
+
+def test_gemm_mxfp4_closed_form_scales(orc):
+    """Elements 1.0, per-block scales 2^(r%5 - 2) on A and 2^(c%3 - 1) on B:
+    C[m, n] = sum_blocks 32 * sA * sB is exact in fp32, so the bf16 output is
+    exactly that sum rounded to nearest even."""
+    require_gpu()
+    M, N, K = 256, 256, 1024
+    Aq = np.full((M, K // 2), 0x22, np.uint8)
+    Bq = np.full((N, K // 2), 0x22, np.uint8)
+    As = (127 + (np.arange(M)[:, None] + np.arange(K // 32)[None, :]) % 5 - 2).astype(np.uint8)
+    Bs = (127 + (np.arange(N)[:, None] * 3 + np.arange(K // 32)[None, :]) % 3 - 1).astype(np.uint8)
+    C = run_mxfp4(Aq, As, Bq, Bs)
+    ref = orc.bf16_round(orc.gemm_mxfp4_ref(Aq, As, Bq, Bs))
+    assert np.array_equal(C, ref)
+
+
+@pytest.mark.parametrize("M", [128, 4096])
+def test_gemm_mxfp4_baseline_sizes_sampled(orc, M):
+    require_gpu()
+    N = K = 8192
+    Aq, As, Bq, Bs = mx_inputs(orc, M, N, K, seed=M)
+    C = run_mxfp4(Aq, As, Bq, Bs)
+    rng = np.random.default_rng(M)
+    rows = np.sort(rng.choice(M, 96, replace=False))
+    cols = np.sort(rng.choice(N, 96, replace=False))
+    ref = orc.gemm_mxfp4_ref(Aq[rows], As[rows], Bq[cols], Bs[cols])
+    assert_gemm_close(C[np.ix_(rows, cols)], ref, f"mxfp4 {M}x{N}x{K} sampled")
+    assert np.isfinite(C).all()
