@@ -90,6 +90,13 @@ def link_lib(objs):
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+    # A kernel template whose host-side instantiation failed leaves its launch
+    # stub undefined without any compiler diagnostic: refuse such a library.
+    und = subprocess.run(["nm", "-C", "--undefined-only", tmp], capture_output=True, text=True).stdout
+    missing = [l.strip() for l in und.splitlines() if "hkq::" in l]
+    if missing:
+        os.remove(tmp)
+        raise RuntimeError("libhkq.so has undefined library symbols:\n  " + "\n  ".join(missing))
     os.replace(tmp, LIB)
 
 

@@ -31,14 +31,35 @@ struct DenseParams {
     int tiles_m, tiles_n, group_m;
 };
 
+// Pipeline (per wave; one barrier per K-tile):
+//   tile kt is consumed in SUB MFMA K-steps of 64 values (FP8: 2, FP4: 4);
+//   fragments are double-buffered, so the LDS reads of step s+1 are issued
+//   between the MFMAs of step s; half of the last step's MFMAs are issued before
+//   the barrier (keeping the matrix pipe busy while waves meet), which (a) makes
+//   tile kt+1's LDS-direct loads visible and (b) retires every wave's reads of
+//   tile kt's stage; the other half is interleaved with the loads that refill
+//   that stage with tile kt+2 and the reads of step 0 of tile kt+1. Chunks are
+//   separated by sched_barrier so the compiler keeps this order.
 template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(const DenseParams p) {
     constexpr int NW = WAVES_M * WAVES_N;
     constexpr int BM = WAVES_M * TM * 32, BN = WAVES_N * TN * 32;
     constexpr int LA = BM / 8 / NW, LB = BN / 8 / NW;
     constexpr bool FP4 = MODE == MODE_MXFP4;
-    constexpr int STAGE = (BM + BN) * KT_BYTES;
+    constexpr int SUB = FP4 ? 4 : 2;
+    // FP4: the tile's e8m0 scales (8 bytes per row per K-tile) ride in LDS after the data
+    constexpr int SCA = FP4 ? BM * 8 : 0, SCB = FP4 ? BN * 8 : 0;
+    constexpr int LSA = FP4 ? BM / 32 / NW : 0, LSB = FP4 ? BN / 32 / NW : 0;
+    constexpr int STAGE = (BM + BN) * KT_BYTES + SCA + SCB;
+    constexpr int NLD = LA + LB + LSA + LSB;           // LDS-direct loads per K-tile
+    constexpr int PARTS = FP4 ? 1 : 2;                 // ds_read_b128 per fragment
+    constexpr int NRD = (TM + TN) * PARTS;             // fragment reads per K-step
+    constexpr int NSC = FP4 ? TM + TN : 0;             // scale reads per K-tile
+    constexpr int NMF = TM * TN;                       // MFMAs per K-step
+    constexpr int HALF = NMF / 2;
     static_assert(LA >= 1 && LB >= 1, "tile too small for the wave count");
+    static_assert(!FP4 || (LSA >= 1 && LSB >= 1), "scale tile too small for the wave count");
+    static_assert(NRD <= NMF, "phase A pairs at most one fragment read with each MFMA");
 
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
@@ -52,7 +73,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
     const int m0 = tm * BM, n0 = tn * BN;
     const int rows_a = min(p.M - m0, BM), rows_b = min(p.N - n0, BN);
 
-    // load pattern: same logical chunk for every instruction of this lane
+    // global -> LDS load pattern (identical logical chunk for every instruction of a lane)
     const uint32_t chunk_off = (uint32_t)(((lane & 7) ^ (lane >> 3)) << 4);
     uint32_t a_off[LA], b_off[LB];
 #pragma unroll
@@ -63,42 +84,95 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
     const uint8_t* b_base = p.B + (int64_t)n0 * p.ldb;
     const int64_t a_bytes = min((int64_t)rows_a * p.lda, (int64_t)0x7FFFFFFF);
     const int64_t b_bytes = min((int64_t)rows_b * p.ldb, (int64_t)0x7FFFFFFF);
+    const uint8_t* as_base = FP4 ? static_cast<const uint8_t*>(p.sa) + (int64_t)m0 * p.lsa : nullptr;
+    const uint8_t* bs_base = FP4 ? static_cast<const uint8_t*>(p.sb) + (int64_t)n0 * p.lsb : nullptr;
+    const int64_t as_bytes = FP4 ? min((int64_t)rows_a * p.lsa, (int64_t)0x7FFFFFFF) : 0;
+    const int64_t bs_bytes = FP4 ? min((int64_t)rows_b * p.lsb, (int64_t)0x7FFFFFFF) : 0;
     const int KT = (p.kbytes + KT_BYTES - 1) / KT_BYTES;
 
-    auto issue = [&](int kt, int stage) {
+    // Where tile kt's loads come from; for kt >= KT all sizes are zero, so every
+    // load reads zero (keeps the main loop free of branches). Plain fields only:
+    // the buffer resources are built per load (a few scalar instructions).
+    struct TileLoad {
+        const uint8_t *a, *b, *sa, *sb;
+        uint32_t na, nb, nsa, nsb, left;
+        int stage;
+        bool tail;
+    };
+    auto tile_load = [&](int kt, int stage) {
+        TileLoad T;
         const int kb = kt * KT_BYTES;
-        const bool tail = kb + KT_BYTES > p.kbytes;
-        const uint32_t left = (uint32_t)(p.kbytes - kb);
-        auto ra = make_rsrc(a_base + kb, (uint32_t)max(a_bytes - kb, (int64_t)0));
-        auto rb = make_rsrc(b_base + kb, (uint32_t)max(b_bytes - kb, (int64_t)0));
-        HKQ_LDS uint8_t* st = smem + stage * STAGE;
-        load_tile_lds<BM, NW>(ra, st, wave, a_off, chunk_off, tail, left);
-        load_tile_lds<BN, NW>(rb, st + BM * KT_BYTES, wave, b_off, chunk_off, tail, left);
+        const bool live = kt < KT;
+        T.tail = kb + KT_BYTES > p.kbytes;
+        T.left = (uint32_t)(p.kbytes - kb);
+        T.a = a_base + kb;
+        T.b = b_base + kb;
+        T.na = live ? (uint32_t)max(a_bytes - kb, (int64_t)0) : 0u;
+        T.nb = live ? (uint32_t)max(b_bytes - kb, (int64_t)0) : 0u;
+        T.sa = as_base + kt * 8;
+        T.sb = bs_base + kt * 8;
+        T.nsa = (FP4 && live) ? (uint32_t)max(as_bytes - kt * 8, (int64_t)0) : 0u;
+        T.nsb = (FP4 && live) ? (uint32_t)max(bs_bytes - kt * 8, (int64_t)0) : 0u;
+        T.stage = stage;
+        return T;
+    };
+    // Load instruction idx of a tile: A rows, B rows, then (FP4) 4-byte scale
+    // words, row = (i*NW + wave)*32 + lane/2, half = lane & 1.
+    auto load_piece = [&](const TileLoad& T, int idx) {
+        HKQ_LDS uint8_t* st = smem + T.stage * STAGE;
+        if (idx < LA) {
+            uint32_t off = a_off[idx] + chunk_off;
+            if (T.tail) off = chunk_off < T.left ? off : OOB;
+            lds_load16(T.a, T.na, st + (idx * NW + wave) * 1024, off);
+        } else if (idx < LA + LB) {
+            const int i = idx - LA;
+            uint32_t off = b_off[i] + chunk_off;
+            if (T.tail) off = chunk_off < T.left ? off : OOB;
+            lds_load16(T.b, T.nb, st + BM * KT_BYTES + (i * NW + wave) * 1024, off);
+        } else if (idx < LA + LB + LSA) {
+            const int i = idx - LA - LB;
+            const uint32_t off = (uint32_t)(((i * NW + wave) * 32 + (lane >> 1)) * p.lsa + (lane & 1) * 4);
+            lds_load4(T.sa, T.nsa, st + (BM + BN) * KT_BYTES + (i * NW + wave) * 256, off);
+        } else {
+            const int i = idx - LA - LB - LSA;
+            const uint32_t off = (uint32_t)(((i * NW + wave) * 32 + (lane >> 1)) * p.lsb + (lane & 1) * 4);
+            lds_load4(T.sb, T.nsb, st + (BM + BN) * KT_BYTES + SCA + (i * NW + wave) * 256, off);
+        }
     };
 
-    // MXFP4 scales: per m-tile / n-tile, the 8 e8m0 bytes of this K-tile for
-    // the lane's row, pre-shifted so that bytes 0 and 2 of each word are the
-    // lane's K-block for substeps (0,1) and (2,3).
-    int sa_cur[TM][2], sb_cur[TN][2];
-    const int srow_a = m0 + wm * TM * 32 + (lane & 31);
-    const int srow_b = n0 + wn * TN * 32 + (lane & 31);
-    auto load_scales = [&](int kt, int (&sa)[TM][2], int (&sb)[TN][2]) {
-        const uint8_t* As = static_cast<const uint8_t*>(p.sa);
-        const uint8_t* Bs = static_cast<const uint8_t*>(p.sb);
-        const int sh = (lane >> 5) * 8;
-#pragma unroll
-        for (int t = 0; t < TM; ++t) {
-            const int m = srow_a + t * 32;
-            uint2 v = m < p.M ? *reinterpret_cast<const uint2*>(As + (int64_t)m * p.lsa + kt * 8) : make_uint2(0, 0);
-            sa[t][0] = (int)(v.x >> sh);
-            sa[t][1] = (int)(v.y >> sh);
-        }
-#pragma unroll
-        for (int t = 0; t < TN; ++t) {
-            const int n = srow_b + t * 32;
-            uint2 v = n < p.N ? *reinterpret_cast<const uint2*>(Bs + (int64_t)n * p.lsb + kt * 8) : make_uint2(0, 0);
-            sb[t][0] = (int)(v.x >> sh);
-            sb[t][1] = (int)(v.y >> sh);
+    const int arow = wm * TM * 32 + (lane & 31);
+    const int brow = wn * TN * 32 + (lane & 31);
+    const int khalf = lane >> 5;
+
+    struct Frags {
+        v4i a[TM][PARTS], b[TN][PARTS];
+    };
+    // Fragment read idx of K-step ks: A tiles then B tiles, PARTS 16-byte chunks each
+    // (FP8: logical chunks ks*4 + 2*khalf + part; FP4: chunk ks*2 + khalf).
+    auto read_piece = [&](int stage, int ks, Frags& f, int idx) {
+        const HKQ_LDS uint8_t* At = smem + stage * STAGE;
+        const bool isa = idx < TM * PARTS;
+        const int t = (isa ? idx : idx - TM * PARTS) / PARTS, part = idx % PARTS;
+        const int row = (isa ? arow : brow) + t * 32;
+        const int chunk = FP4 ? ks * 2 + khalf : ks * 4 + khalf * 2 + part;
+        const v4i v = *reinterpret_cast<const HKQ_LDS v4i*>(At + (isa ? 0 : BM * KT_BYTES) + lds_swz(row, chunk));
+        if (isa) f.a[t][part] = v;
+        else f.b[t][part] = v;
+    };
+    // MXFP4: per m/n-tile the 8 scale bytes of the tile for the lane's row,
+    // shifted so bytes 0 and 2 of word w are the lane's K-block of steps 2w, 2w+1.
+    struct Scales {
+        int a[TM][2], b[TN][2];
+    };
+    auto read_scale = [&](int stage, Scales& s, int idx) {
+        if constexpr (FP4) {
+            const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KT_BYTES;
+            const bool isa = idx < TM;
+            const int t = isa ? idx : idx - TM;
+            const v2i v = *reinterpret_cast<const HKQ_LDS v2i*>(sca + (isa ? (arow + t * 32) * 8 : SCA + (brow + t * 32) * 8));
+            const int sh = khalf * 8;
+            if (isa) { s.a[t][0] = (int)((uint32_t)v[0] >> sh); s.a[t][1] = (int)((uint32_t)v[1] >> sh); }
+            else { s.b[t][0] = (int)((uint32_t)v[0] >> sh); s.b[t][1] = (int)((uint32_t)v[1] >> sh); }
         }
     };
 
@@ -108,64 +182,70 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = v16f{};
 
-    issue(0, 0);
-    if constexpr (FP4) load_scales(0, sa_cur, sb_cur);
-    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) lgkmcnt(0)
-    __syncthreads();
+    auto frag8 = [](const v4i (&h)[PARTS]) -> v8i {
+        if constexpr (PARTS == 2) return v8i{h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
+        else return v8i{h[0][0], h[0][1], h[0][2], h[0][3], 0, 0, 0, 0};
+    };
+    // MFMA idx (accumulator i*TM + j) of K-step ks
+    auto mfma_one = [&](const Frags& f, int ks, const Scales& s, int idx) {
+        const int i = idx / TM, j = idx % TM;
+        if constexpr (FP4) {
+            if (ks & 1)
+                acc[i][j] = mfma_sel<true, 2, 2>(frag8(f.b[i]), frag8(f.a[j]), acc[i][j], s.b[i][ks >> 1], s.a[j][ks >> 1]);
+            else
+                acc[i][j] = mfma_sel<true, 0, 0>(frag8(f.b[i]), frag8(f.a[j]), acc[i][j], s.b[i][ks >> 1], s.a[j][ks >> 1]);
+        } else {
+            acc[i][j] = mfma<false>(frag8(f.b[i]), frag8(f.a[j]), acc[i][j], 127, 127);
+        }
+    };
 
-    const int arow = wm * TM * 32 + (lane & 31);
-    const int brow = wn * TN * 32 + (lane & 31);
-    const int khalf = lane >> 5;
+    Frags F[2];
+    Scales S[2];
+    {
+        const TileLoad T0 = tile_load(0, 0), T1 = tile_load(1, 1);
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) load_piece(T0, i);
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) load_piece(T1, i);
+    }
+    tile_barrier();  // start-up only: both prologue tiles resident
+#pragma unroll
+    for (int i = 0; i < NRD; ++i) read_piece(0, 0, F[0], i);
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) read_scale(0, S[0], i);
 
     for (int kt = 0; kt < KT; ++kt) {
         const int stage = kt & 1;
-        int sa_nxt[TM][2], sb_nxt[TN][2];
-        if (kt + 1 < KT) {
-            issue(kt + 1, stage ^ 1);
-            if constexpr (FP4) load_scales(kt + 1, sa_nxt, sb_nxt);
-        }
-        const HKQ_LDS uint8_t* At = smem + stage * STAGE;
-        const HKQ_LDS uint8_t* Bt = At + BM * KT_BYTES;
-        if constexpr (!FP4) {
+        // phase A: steps 0 .. SUB-2, one fragment read of the next step per MFMA
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                v8i af[TM], bf[TN];
+        for (int ks = 0; ks + 1 < SUB; ++ks) {
 #pragma unroll
-                for (int t = 0; t < TM; ++t) af[t] = read_frag_fp8(At, arow + t * 32, ks * 4 + khalf * 2);
-#pragma unroll
-                for (int t = 0; t < TN; ++t) bf[t] = read_frag_fp8(Bt, brow + t * 32, ks * 4 + khalf * 2);
-#pragma unroll
-                for (int i = 0; i < TN; ++i)
-#pragma unroll
-                    for (int j = 0; j < TM; ++j) acc[i][j] = mfma<false>(bf[i], af[j], acc[i][j], 127, 127);
-            }
-        } else {
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                v8i af[TM], bf[TN];
-#pragma unroll
-                for (int t = 0; t < TM; ++t) af[t] = read_frag_fp4(At, arow + t * 32, ks * 2 + khalf);
-#pragma unroll
-                for (int t = 0; t < TN; ++t) bf[t] = read_frag_fp4(Bt, brow + t * 32, ks * 2 + khalf);
-#pragma unroll
-                for (int i = 0; i < TN; ++i)
-#pragma unroll
-                    for (int j = 0; j < TM; ++j) {
-                        if (ks & 1)
-                            acc[i][j] = mfma_sel<true, 2, 2>(bf[i], af[j], acc[i][j], sb_cur[i][ks >> 1], sa_cur[j][ks >> 1]);
-                        else
-                            acc[i][j] = mfma_sel<true, 0, 0>(bf[i], af[j], acc[i][j], sb_cur[i][ks >> 1], sa_cur[j][ks >> 1]);
-                    }
-            }
-            if (kt + 1 < KT) {
-#pragma unroll
-                for (int t = 0; t < TM; ++t) { sa_cur[t][0] = sa_nxt[t][0]; sa_cur[t][1] = sa_nxt[t][1]; }
-#pragma unroll
-                for (int t = 0; t < TN; ++t) { sb_cur[t][0] = sb_nxt[t][0]; sb_cur[t][1] = sb_nxt[t][1]; }
+            for (int c = 0; c < NMF; ++c) {
+                mfma_one(F[ks & 1], ks, S[0], c);
+                if (c < NRD) read_piece(stage, ks + 1, F[(ks + 1) & 1], c);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        // phase B: last step
+        constexpr int LAST = SUB - 1;
+#pragma unroll
+        for (int c = 0; c < HALF; ++c) mfma_one(F[LAST & 1], LAST, S[0], c);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_barrier();  // retires this stage's reads everywhere; tile kt+1 is resident
+        __builtin_amdgcn_sched_barrier(0);
+        const TileLoad T = tile_load(kt + 2, stage);
+#pragma unroll
+        for (int c = 0; c < HALF; ++c) {
+            mfma_one(F[LAST & 1], LAST, S[0], HALF + c);
+#pragma unroll
+            for (int i = c * NLD / HALF; i < (c + 1) * NLD / HALF; ++i) load_piece(T, i);
+#pragma unroll
+            for (int i = c * NRD / HALF; i < (c + 1) * NRD / HALF; ++i) read_piece(stage ^ 1, 0, F[0], i);
+#pragma unroll
+            for (int i = c * NSC / HALF; i < (c + 1) * NSC / HALF; ++i) read_scale(stage ^ 1, S[1], i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (FP4) S[0] = S[1];
     }
     mfma_drain();
 
@@ -203,7 +283,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
 template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN>
 static int launch_dense(DenseParams& p, hipStream_t stream) {
     constexpr int BM = WAVES_M * TM * 32, BN = WAVES_N * TN * 32;
-    constexpr int LDS = 2 * (BM + BN) * KT_BYTES;
+    constexpr int SC = MODE == MODE_MXFP4 ? (BM + BN) * 8 : 0;
+    constexpr int LDS = 2 * ((BM + BN) * KT_BYTES + SC);
     auto kern = dense_gemm_kernel<MODE, WAVES_M, WAVES_N, TM, TN>;
     static bool attr_set = false;  // per instantiation; the attribute is per-process
     if (!attr_set) {

@@ -55,6 +55,17 @@ __device__ __forceinline__ void load_tile_lds(__amdgpu_buffer_rsrc_t rsrc, HKQ_L
     }
 }
 
+// One LDS-direct load of `size` (4 or 16) bytes per lane from [base, base + bytes)
+// at byte offset `off` to `dst` + lane * size. Kept out of lambdas: a target
+// builtin called directly in a lambda inside a kernel template makes the host
+// pass drop that kernel's launch stub without a diagnostic.
+__device__ __forceinline__ void lds_load16(const void* base, uint32_t bytes, HKQ_LDS void* dst, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(base, bytes), dst, 16, off, 0, 0, 0);
+}
+__device__ __forceinline__ void lds_load4(const void* base, uint32_t bytes, HKQ_LDS void* dst, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(base, bytes), dst, 4, off, 0, 0, 0);
+}
+
 // Per-lane constants of the load pattern: the lane's row within its 8-row
 // group and logical chunk (so that physical chunk = lane % 8).
 __device__ __forceinline__ void load_lane_coords(int lane, int wave, int NW, int i, int& row, int& chunk) {
@@ -85,6 +96,15 @@ template <bool FP4, int OPA, int OPB>
 __device__ __forceinline__ v16f mfma_sel(const v8i& a, const v8i& b, const v16f& c, int sa, int sb) {
     if (FP4) return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 4, 4, OPA, sa, OPB, sb);
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, OPA, sa, OPB, sb);
+}
+
+// Workgroup barrier that also waits for this wave's LDS-direct loads
+// (vmcnt): __syncthreads' workgroup-scope fence does not cover the
+// buffer_load ... lds writes, so without the explicit wait a wave could read a
+// K-tile that another wave's loads have not finished writing.
+__device__ __forceinline__ void tile_barrier() {
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+    __syncthreads();
 }
 
 // Wait states after the last MFMA before its accumulators are read by VALU or
