@@ -8,12 +8,11 @@
 //                        e8m0 scales per 32 K-values fed to the MFMA scale
 //                        operands (gemm-basic/gemm_afp4wfp4/kernel.cpp:1-12 for
 //                        the data format; the reference kernel itself consumes
-//                        pre-dequantized bf16);
-//   hkq_gemm_blockscale  C = bf16(sum_kt (A_kt . B_kt^T) * sa[m,kt] * sb[kt,n/128])
-//                        with 128-wide K groups (gemm_a8w8_blockscale/kernel.cpp:
-//                        129-153; formula gemm_a8w8_blockscale/test_parity.py:57-76).
+//                        pre-dequantized bf16).
 #include "gemm_core.h"
 #include "hkq_host.h"
+
+#include <type_traits>
 
 namespace hkq {
 
@@ -24,42 +23,61 @@ struct DenseParams {
     const void* sa;
     const void* sb;
     int M, N, K;          // K in elements
-    int kbytes;           // K in bytes per row of A/B
+    int kbytes;           // K in bytes per row of A/B (a multiple of KT_BYTES)
     int64_t lda, ldb;     // bytes
     int64_t ldc;          // elements
-    int64_t lsa, lsb;     // scale row strides (MXFP4: bytes; block-scale: floats)
+    int64_t lsa, lsb;     // MXFP4 scale row strides (bytes)
     int tiles_m, tiles_n, group_m;
+    int c16;              // rows of C are 16-byte aligned (ldc % 8 == 0, C 16-byte aligned)
 };
 
-// Pipeline (per wave; one barrier per K-tile):
-//   tile kt is consumed in SUB MFMA K-steps of 64 values (FP8: 2, FP4: 4);
-//   fragments are double-buffered, so the LDS reads of step s+1 are issued
-//   between the MFMAs of step s; half of the last step's MFMAs are issued before
-//   the barrier (keeping the matrix pipe busy while waves meet), which (a) makes
-//   tile kt+1's LDS-direct loads visible and (b) retires every wave's reads of
-//   tile kt's stage; the other half is interleaved with the loads that refill
-//   that stage with tile kt+2 and the reads of step 0 of tile kt+1. Chunks are
-//   separated by sched_barrier so the compiler keeps this order.
 template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(const DenseParams p) {
-    constexpr int NW = WAVES_M * WAVES_N;
-    constexpr int BM = WAVES_M * TM * 32, BN = WAVES_N * TN * 32;
-    constexpr int LA = BM / 8 / NW, LB = BN / 8 / NW;
-    constexpr bool FP4 = MODE == MODE_MXFP4;
-    constexpr int SUB = FP4 ? 4 : 2;
-    // FP4: the tile's e8m0 scales (8 bytes per row per K-tile) ride in LDS after the data
-    constexpr int SCA = FP4 ? BM * 8 : 0, SCB = FP4 ? BN * 8 : 0;
-    constexpr int LSA = FP4 ? BM / 32 / NW : 0, LSB = FP4 ? BN / 32 / NW : 0;
-    constexpr int STAGE = (BM + BN) * KT_BYTES + SCA + SCB;
-    constexpr int NLD = LA + LB + LSA + LSB;           // LDS-direct loads per K-tile
-    constexpr int PARTS = FP4 ? 1 : 2;                 // ds_read_b128 per fragment
-    constexpr int NRD = (TM + TN) * PARTS;             // fragment reads per K-step
-    constexpr int NSC = FP4 ? TM + TN : 0;             // scale reads per K-tile
-    constexpr int NMF = TM * TN;                       // MFMAs per K-step
-    constexpr int HALF = NMF / 2;
+struct DenseCfg {
+    static constexpr int NW = WAVES_M * WAVES_N;
+    static constexpr int BM = WAVES_M * TM * 32, BN = WAVES_N * TN * 32;
+    static constexpr bool FP4 = MODE == MODE_MXFP4;
+    static constexpr int SUB = FP4 ? 2 : 1;                    // 64-deep MFMA K-steps per K-tile
+    static constexpr int LA = BM / ROWS_PER_LOAD / NW, LB = BN / ROWS_PER_LOAD / NW;
+    // FP4: the K-tile's e8m0 scales (4 bytes per row: 128 values) ride in LDS
+    // after the data; one 4-byte LDS-direct load per lane covers 64 rows.
+    static constexpr int SCA = FP4 ? BM * 4 : 0, SCB = FP4 ? BN * 4 : 0;
+    static constexpr int LSA = FP4 ? BM / 64 / NW : 0, LSB = FP4 ? BN / 64 / NW : 0;
+    static constexpr int STAGE = (BM + BN) * KT_BYTES + SCA + SCB;
+    static constexpr int NLD = LA + LB + LSA + LSB;           // LDS-direct loads per K-tile
+    static constexpr int PARTS = FP4 ? 1 : 2;                 // ds_read_b128 per fragment
+    static constexpr int NRD = 2 * PARTS * (TM > TN ? TM : TN);  // fragment read slots per K-step
+    static constexpr int NSC = FP4 ? TM + TN : 0;             // scale reads per K-tile
+    static constexpr int NMF = TM * TN, HALF = NMF / 2;       // MFMAs per K-step
+    // epilogue: each wave stages its (TM*32) x (TN*32) bf16 sub-tile in LDS with a
+    // padded row pitch, then writes whole 256-byte row segments of C
+    static constexpr int EP_PITCH = TN * 32 * 2 + 16;
+    static constexpr int EP_BYTES = NW * TM * 32 * EP_PITCH;
+    static constexpr int lds_bytes(int ns) { return ns * STAGE > EP_BYTES ? ns * STAGE : EP_BYTES; }
     static_assert(LA >= 1 && LB >= 1, "tile too small for the wave count");
     static_assert(!FP4 || (LSA >= 1 && LSB >= 1), "scale tile too small for the wave count");
     static_assert(NRD <= NMF, "phase A pairs at most one fragment read with each MFMA");
+    static_assert((TN * 32 * 2) % 256 == 0, "epilogue rows are whole 256-byte segments");
+};
+
+// Pipeline (per wave; one barrier per K-tile, NS ring stages):
+//   K-tile kt lives in stage kt % NS. Its SUB K-steps run their MFMAs with
+//   double-buffered fragments: the LDS reads of the next step are issued between
+//   the MFMAs of the current one. In the last step, half of the MFMAs are issued
+//   before the barrier (the matrix pipe stays busy while the waves meet); the
+//   barrier (a) waits until K-tile kt+1 is resident (at most NS-2 K-tiles of
+//   loads still in flight) and (b) retires every wave's reads of stage kt % NS,
+//   which is then refilled with K-tile kt+NS while the other half of the MFMAs
+//   issue together with the reads of K-tile kt+1's first step. sched_barrier
+//   between chunks keeps this order through the compiler's scheduler.
+template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int NS>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(const DenseParams p) {
+    using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN>;
+    constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN, SUB = Cfg::SUB;
+    constexpr int LA = Cfg::LA, LB = Cfg::LB, LSA = Cfg::LSA, SCA = Cfg::SCA, STAGE = Cfg::STAGE;
+    constexpr int NLD = Cfg::NLD, PARTS = Cfg::PARTS, NRD = Cfg::NRD, NSC = Cfg::NSC;
+    constexpr int NMF = Cfg::NMF, HALF = Cfg::HALF;
+    constexpr bool FP4 = Cfg::FP4;
+    static_assert(NS >= 2 && (NS - 1) * NLD <= 63, "vmcnt budget");
 
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
@@ -73,13 +91,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
     const int m0 = tm * BM, n0 = tn * BN;
     const int rows_a = min(p.M - m0, BM), rows_b = min(p.N - n0, BN);
 
-    // global -> LDS load pattern (identical logical chunk for every instruction of a lane)
-    const uint32_t chunk_off = (uint32_t)(((lane & 7) ^ (lane >> 3)) << 4);
+    // global -> LDS: instruction i of this wave fills rows (i*NW + wave)*16 + lane/4
+    const uint32_t chunk_off = (uint32_t)(load_chunk(lane) << 4);
     uint32_t a_off[LA], b_off[LB];
 #pragma unroll
-    for (int i = 0; i < LA; ++i) a_off[i] = (uint32_t)(((i * NW + wave) * 8 + (lane >> 3)) * p.lda);
+    for (int i = 0; i < LA; ++i) a_off[i] = (uint32_t)(((i * NW + wave) * ROWS_PER_LOAD + (lane >> 2)) * p.lda) + chunk_off;
 #pragma unroll
-    for (int i = 0; i < LB; ++i) b_off[i] = (uint32_t)(((i * NW + wave) * 8 + (lane >> 3)) * p.ldb);
+    for (int i = 0; i < LB; ++i) b_off[i] = (uint32_t)(((i * NW + wave) * ROWS_PER_LOAD + (lane >> 2)) * p.ldb) + chunk_off;
     const uint8_t* a_base = p.A + (int64_t)m0 * p.lda;
     const uint8_t* b_base = p.B + (int64_t)n0 * p.ldb;
     const int64_t a_bytes = min((int64_t)rows_a * p.lda, (int64_t)0x7FFFFFFF);
@@ -88,55 +106,31 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
     const uint8_t* bs_base = FP4 ? static_cast<const uint8_t*>(p.sb) + (int64_t)n0 * p.lsb : nullptr;
     const int64_t as_bytes = FP4 ? min((int64_t)rows_a * p.lsa, (int64_t)0x7FFFFFFF) : 0;
     const int64_t bs_bytes = FP4 ? min((int64_t)rows_b * p.lsb, (int64_t)0x7FFFFFFF) : 0;
-    const int KT = (p.kbytes + KT_BYTES - 1) / KT_BYTES;
+    const int KT = p.kbytes / KT_BYTES;
 
-    // Where tile kt's loads come from; for kt >= KT all sizes are zero, so every
-    // load reads zero (keeps the main loop free of branches). Plain fields only:
-    // the buffer resources are built per load (a few scalar instructions).
-    struct TileLoad {
-        const uint8_t *a, *b, *sa, *sb;
-        uint32_t na, nb, nsa, nsb, left;
-        int stage;
-        bool tail;
-    };
-    auto tile_load = [&](int kt, int stage) {
-        TileLoad T;
+    // Load instruction idx of K-tile kt into `stage`: A rows, B rows, then (FP4)
+    // the 4-byte scale word of row (i*NW + wave)*64 + lane. For kt >= KT the
+    // buffers are empty, so the loads read zero (the loop needs no branches).
+    auto load_piece = [&](int kt, int stage, int idx) {
         const int kb = kt * KT_BYTES;
         const bool live = kt < KT;
-        T.tail = kb + KT_BYTES > p.kbytes;
-        T.left = (uint32_t)(p.kbytes - kb);
-        T.a = a_base + kb;
-        T.b = b_base + kb;
-        T.na = live ? (uint32_t)max(a_bytes - kb, (int64_t)0) : 0u;
-        T.nb = live ? (uint32_t)max(b_bytes - kb, (int64_t)0) : 0u;
-        T.sa = as_base + kt * 8;
-        T.sb = bs_base + kt * 8;
-        T.nsa = (FP4 && live) ? (uint32_t)max(as_bytes - kt * 8, (int64_t)0) : 0u;
-        T.nsb = (FP4 && live) ? (uint32_t)max(bs_bytes - kt * 8, (int64_t)0) : 0u;
-        T.stage = stage;
-        return T;
-    };
-    // Load instruction idx of a tile: A rows, B rows, then (FP4) 4-byte scale
-    // words, row = (i*NW + wave)*32 + lane/2, half = lane & 1.
-    auto load_piece = [&](const TileLoad& T, int idx) {
-        HKQ_LDS uint8_t* st = smem + T.stage * STAGE;
+        HKQ_LDS uint8_t* st = smem + stage * STAGE;
         if (idx < LA) {
-            uint32_t off = a_off[idx] + chunk_off;
-            if (T.tail) off = chunk_off < T.left ? off : OOB;
-            lds_load16(T.a, T.na, st + (idx * NW + wave) * 1024, off);
+            lds_load16(a_base + kb, live ? (uint32_t)(a_bytes - kb) : 0u, st + (idx * NW + wave) * 1024, a_off[idx]);
         } else if (idx < LA + LB) {
             const int i = idx - LA;
-            uint32_t off = b_off[i] + chunk_off;
-            if (T.tail) off = chunk_off < T.left ? off : OOB;
-            lds_load16(T.b, T.nb, st + BM * KT_BYTES + (i * NW + wave) * 1024, off);
+            lds_load16(b_base + kb, live ? (uint32_t)(b_bytes - kb) : 0u, st + BM * KT_BYTES + (i * NW + wave) * 1024,
+                       b_off[i]);
         } else if (idx < LA + LB + LSA) {
             const int i = idx - LA - LB;
-            const uint32_t off = (uint32_t)(((i * NW + wave) * 32 + (lane >> 1)) * p.lsa + (lane & 1) * 4);
-            lds_load4(T.sa, T.nsa, st + (BM + BN) * KT_BYTES + (i * NW + wave) * 256, off);
+            const uint32_t off = (uint32_t)(((i * NW + wave) * 64 + lane) * p.lsa);
+            lds_load4(as_base + kt * 4, live ? (uint32_t)(as_bytes - kt * 4) : 0u,
+                      st + (BM + BN) * KT_BYTES + (i * NW + wave) * 256, off);
         } else {
             const int i = idx - LA - LB - LSA;
-            const uint32_t off = (uint32_t)(((i * NW + wave) * 32 + (lane >> 1)) * p.lsb + (lane & 1) * 4);
-            lds_load4(T.sb, T.nsb, st + (BM + BN) * KT_BYTES + SCA + (i * NW + wave) * 256, off);
+            const uint32_t off = (uint32_t)(((i * NW + wave) * 64 + lane) * p.lsb);
+            lds_load4(bs_base + kt * 4, live ? (uint32_t)(bs_bytes - kt * 4) : 0u,
+                      st + (BM + BN) * KT_BYTES + SCA + (i * NW + wave) * 256, off);
         }
     };
 
@@ -147,32 +141,34 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
     struct Frags {
         v4i a[TM][PARTS], b[TN][PARTS];
     };
-    // Fragment read idx of K-step ks: A tiles then B tiles, PARTS 16-byte chunks each
-    // (FP8: logical chunks ks*4 + 2*khalf + part; FP4: chunk ks*2 + khalf).
+    // Fragment read slot idx of K-step ks, A and B tiles interleaved
+    // (a0 b0 a1 b1 ...) so the first MFMAs' operands arrive first; slots past
+    // TM (A) or TN (B) tiles are empty. FP8: logical chunks 2*khalf + part;
+    // FP4: chunk 2*ks + khalf.
     auto read_piece = [&](int stage, int ks, Frags& f, int idx) {
         const HKQ_LDS uint8_t* At = smem + stage * STAGE;
-        const bool isa = idx < TM * PARTS;
-        const int t = (isa ? idx : idx - TM * PARTS) / PARTS, part = idx % PARTS;
-        const int row = (isa ? arow : brow) + t * 32;
-        const int chunk = FP4 ? ks * 2 + khalf : ks * 4 + khalf * 2 + part;
-        const v4i v = *reinterpret_cast<const HKQ_LDS v4i*>(At + (isa ? 0 : BM * KT_BYTES) + lds_swz(row, chunk));
-        if (isa) f.a[t][part] = v;
-        else f.b[t][part] = v;
+        const int t = idx / (2 * PARTS), isb = (idx / PARTS) & 1, part = idx % PARTS;
+        if ((isb ? TN : TM) <= t) return;
+        const int row = (isb ? brow : arow) + t * 32;
+        const int chunk = FP4 ? ks * 2 + khalf : khalf * 2 + part;
+        const v4i v = lds_read16(At + (isb ? BM * KT_BYTES : 0) + lds_swz(row, chunk));
+        if (isb) f.b[t][part] = v;
+        else f.a[t][part] = v;
     };
-    // MXFP4: per m/n-tile the 8 scale bytes of the tile for the lane's row,
-    // shifted so bytes 0 and 2 of word w are the lane's K-block of steps 2w, 2w+1.
+    // MXFP4: per m/n-tile the 4 scale bytes of the K-tile for the lane's row,
+    // shifted so bytes 0 and 2 are the lane's K-block of steps 0 and 1.
     struct Scales {
-        int a[TM][2], b[TN][2];
+        int a[TM], b[TN];
     };
     auto read_scale = [&](int stage, Scales& s, int idx) {
         if constexpr (FP4) {
             const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KT_BYTES;
             const bool isa = idx < TM;
             const int t = isa ? idx : idx - TM;
-            const v2i v = *reinterpret_cast<const HKQ_LDS v2i*>(sca + (isa ? (arow + t * 32) * 8 : SCA + (brow + t * 32) * 8));
-            const int sh = khalf * 8;
-            if (isa) { s.a[t][0] = (int)((uint32_t)v[0] >> sh); s.a[t][1] = (int)((uint32_t)v[1] >> sh); }
-            else { s.b[t][0] = (int)((uint32_t)v[0] >> sh); s.b[t][1] = (int)((uint32_t)v[1] >> sh); }
+            const uint32_t w = *reinterpret_cast<const HKQ_LDS uint32_t*>(
+                sca + (isa ? (arow + t * 32) * 4 : SCA + (brow + t * 32) * 4));
+            if (isa) s.a[t] = (int)(w >> (khalf * 8));
+            else s.b[t] = (int)(w >> (khalf * 8));
         }
     };
 
@@ -182,75 +178,91 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = v16f{};
 
-    auto frag8 = [](const v4i (&h)[PARTS]) -> v8i {
-        if constexpr (PARTS == 2) return v8i{h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
-        else return v8i{h[0][0], h[0][1], h[0][2], h[0][3], 0, 0, 0, 0};
-    };
     // MFMA idx (accumulator i*TM + j) of K-step ks
     auto mfma_one = [&](const Frags& f, int ks, const Scales& s, int idx) {
         const int i = idx / TM, j = idx % TM;
-        if constexpr (FP4) {
-            if (ks & 1)
-                acc[i][j] = mfma_sel<true, 2, 2>(frag8(f.b[i]), frag8(f.a[j]), acc[i][j], s.b[i][ks >> 1], s.a[j][ks >> 1]);
-            else
-                acc[i][j] = mfma_sel<true, 0, 0>(frag8(f.b[i]), frag8(f.a[j]), acc[i][j], s.b[i][ks >> 1], s.a[j][ks >> 1]);
+        v8i a, b;
+        if constexpr (PARTS == 2) {
+            b = v8i{f.b[i][0][0], f.b[i][0][1], f.b[i][0][2], f.b[i][0][3], f.b[i][1][0], f.b[i][1][1], f.b[i][1][2], f.b[i][1][3]};
+            a = v8i{f.a[j][0][0], f.a[j][0][1], f.a[j][0][2], f.a[j][0][3], f.a[j][1][0], f.a[j][1][1], f.a[j][1][2], f.a[j][1][3]};
         } else {
-            acc[i][j] = mfma<false>(frag8(f.b[i]), frag8(f.a[j]), acc[i][j], 127, 127);
+            b = v8i{f.b[i][0][0], f.b[i][0][1], f.b[i][0][2], f.b[i][0][3], 0, 0, 0, 0};
+            a = v8i{f.a[j][0][0], f.a[j][0][1], f.a[j][0][2], f.a[j][0][3], 0, 0, 0, 0};
+        }
+        if constexpr (FP4) {
+            if (ks & 1) acc[i][j] = mfma_sel<true, 2, 2>(b, a, acc[i][j], s.b[i], s.a[j]);
+            else acc[i][j] = mfma_sel<true, 0, 0>(b, a, acc[i][j], s.b[i], s.a[j]);
+        } else {
+            acc[i][j] = mfma_sel<false, 0, 0>(b, a, acc[i][j], 127, 127);
         }
     };
 
     Frags F[2];
     Scales S[2];
-    {
-        const TileLoad T0 = tile_load(0, 0), T1 = tile_load(1, 1);
 #pragma unroll
-        for (int i = 0; i < NLD; ++i) load_piece(T0, i);
+    for (int t = 0; t < NS; ++t)
 #pragma unroll
-        for (int i = 0; i < NLD; ++i) load_piece(T1, i);
-    }
-    tile_barrier();  // start-up only: both prologue tiles resident
+        for (int i = 0; i < NLD; ++i) load_piece(t, t, i);
+    tile_barrier<(NS - 1) * NLD>();  // K-tile 0 resident
 #pragma unroll
     for (int i = 0; i < NRD; ++i) read_piece(0, 0, F[0], i);
 #pragma unroll
     for (int i = 0; i < NSC; ++i) read_scale(0, S[0], i);
 
-    for (int kt = 0; kt < KT; ++kt) {
-        const int stage = kt & 1;
+    // One K-tile; P is the tile's parity (fragment and scale buffers alternate).
+    auto ktile = [&](int kt, int stage, auto parity) {
+        constexpr int P = decltype(parity)::value;
+        const int next_stage = stage + 1 == NS ? 0 : stage + 1;
         // phase A: steps 0 .. SUB-2, one fragment read of the next step per MFMA
 #pragma unroll
         for (int ks = 0; ks + 1 < SUB; ++ks) {
 #pragma unroll
             for (int c = 0; c < NMF; ++c) {
-                mfma_one(F[ks & 1], ks, S[0], c);
-                if (c < NRD) read_piece(stage, ks + 1, F[(ks + 1) & 1], c);
+                mfma_one(F[(P * SUB + ks) & 1], ks, S[P], c);
+                if (c < NRD) read_piece(stage, ks + 1, F[(P * SUB + ks + 1) & 1], c);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
         // phase B: last step
         constexpr int LAST = SUB - 1;
+        const Frags& cur = F[(P * SUB + LAST) & 1];
+        Frags& nxt = F[(P * SUB + LAST + 1) & 1];
 #pragma unroll
-        for (int c = 0; c < HALF; ++c) mfma_one(F[LAST & 1], LAST, S[0], c);
+        for (int c = 0; c < HALF; ++c) mfma_one(cur, LAST, S[P], c);
         __builtin_amdgcn_sched_barrier(0);
-        tile_barrier();  // retires this stage's reads everywhere; tile kt+1 is resident
+        tile_barrier<(NS - 2) * NLD>();  // K-tile kt+1 resident; stage kt % NS retired
         __builtin_amdgcn_sched_barrier(0);
-        const TileLoad T = tile_load(kt + 2, stage);
 #pragma unroll
         for (int c = 0; c < HALF; ++c) {
-            mfma_one(F[LAST & 1], LAST, S[0], HALF + c);
+            mfma_one(cur, LAST, S[P], HALF + c);
 #pragma unroll
-            for (int i = c * NLD / HALF; i < (c + 1) * NLD / HALF; ++i) load_piece(T, i);
+            for (int i = c * NLD / HALF; i < (c + 1) * NLD / HALF; ++i) load_piece(kt + NS, stage, i);
 #pragma unroll
-            for (int i = c * NRD / HALF; i < (c + 1) * NRD / HALF; ++i) read_piece(stage ^ 1, 0, F[0], i);
+            for (int i = c * NRD / HALF; i < (c + 1) * NRD / HALF; ++i) read_piece(next_stage, 0, nxt, i);
 #pragma unroll
-            for (int i = c * NSC / HALF; i < (c + 1) * NSC / HALF; ++i) read_scale(stage ^ 1, S[1], i);
+            for (int i = c * NSC / HALF; i < (c + 1) * NSC / HALF; ++i) read_scale(next_stage, S[P ^ 1], i);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (FP4) S[0] = S[1];
-    }
-    mfma_drain();
+    };
 
-    // Epilogue: lane holds, for m-tile j and n-tile i, D[n][m] with
-    // m = (lane & 31), n = 8*(r/4) + 4*(lane/32) + r%4.
+    int stage = 0;
+    int kt = 0;
+    for (; kt + 1 < KT; kt += 2) {
+        ktile(kt, stage, std::integral_constant<int, 0>{});
+        stage = stage + 1 == NS ? 0 : stage + 1;
+        ktile(kt + 1, stage, std::integral_constant<int, 1>{});
+        stage = stage + 1 == NS ? 0 : stage + 1;
+    }
+    if (kt < KT) ktile(kt, stage, std::integral_constant<int, 0>{});
+    mfma_drain();
+    tile_barrier<0>();  // every wave is done with the stages and no load is in flight
+
+    // Epilogue: scale in registers, stage the wave's bf16 sub-tile in LDS (row
+    // m, col n, padded pitch), then store whole row segments of C.
+    // Lane holds, for m-tile j and n-tile i, D[n][m] with m = (lane & 31),
+    // n = 8*(r/4) + 4*(lane/32) + r%4.
+    constexpr int PITCH = Cfg::EP_PITCH;
+    HKQ_LDS uint8_t* ep = smem + wave * (TM * 32) * PITCH;
     const float* sa = static_cast<const float*>(p.sa);
     const float* sb = static_cast<const float*>(p.sb);
     float ascale[TM];
@@ -263,29 +275,53 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
     for (int i = 0; i < TN; ++i) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int n = n0 + wn * TN * 32 + i * 32 + 8 * g + 4 * khalf;
-            if (n >= p.N) continue;
+            const int nl = i * 32 + 8 * g + 4 * khalf;
+            const int n = n0 + wn * TN * 32 + nl;
             float4 bs = make_float4(1.f, 1.f, 1.f, 1.f);
-            if constexpr (MODE == MODE_A8W8) bs = *reinterpret_cast<const float4*>(sb + n);
+            if constexpr (MODE == MODE_A8W8) {
+                if (n < p.N) bs = *reinterpret_cast<const float4*>(sb + n);
+            }
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
-                const int m = m0 + arow + j * 32;
-                if (m >= p.M) continue;
                 const float a = ascale[j];
-                uint32_t lo = f32_to_bf16(acc[i][j][4 * g + 0] * a * bs.x) | (f32_to_bf16(acc[i][j][4 * g + 1] * a * bs.y) << 16);
-                uint32_t hi = f32_to_bf16(acc[i][j][4 * g + 2] * a * bs.z) | (f32_to_bf16(acc[i][j][4 * g + 3] * a * bs.w) << 16);
-                *reinterpret_cast<uint2*>(p.C + (int64_t)m * p.ldc + n) = make_uint2(lo, hi);
+                const uint32_t lo = f32_to_bf16(acc[i][j][4 * g + 0] * a * bs.x) | (f32_to_bf16(acc[i][j][4 * g + 1] * a * bs.y) << 16);
+                const uint32_t hi = f32_to_bf16(acc[i][j][4 * g + 2] * a * bs.z) | (f32_to_bf16(acc[i][j][4 * g + 3] * a * bs.w) << 16);
+                *reinterpret_cast<HKQ_LDS v2i*>(ep + (j * 32 + (lane & 31)) * PITCH + nl * 2) = v2i{(int)lo, (int)hi};
+            }
+        }
+    }
+    // LDS operations of a wave complete in order: the reads below see the writes above.
+    constexpr int SEGS = TN * 32 * 2 / 16;  // 16-byte pieces per row
+    constexpr int ROWS_PER_PASS = 64 / SEGS;
+#pragma unroll 4
+    for (int r0 = 0; r0 < TM * 32; r0 += ROWS_PER_PASS) {
+        const int r = r0 + lane / SEGS, seg = lane % SEGS;
+        const v4i v = lds_read16(ep + r * PITCH + seg * 16);
+        const int m = m0 + wm * TM * 32 + r;
+        const int n = n0 + wn * TN * 32 + seg * 8;
+        if (m < p.M) {
+            // N % 4 == 0: a piece is whole, half (4 values) or out of range
+            uint16_t* dst = p.C + (int64_t)m * p.ldc + n;
+            if (n + 8 <= p.N) {
+                if (p.c16) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(dst));
+                } else {
+                    __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
+                    __builtin_nontemporal_store(v2i{v[2], v[3]}, reinterpret_cast<v2i*>(dst + 4));
+                }
+            } else if (n < p.N) {
+                __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
             }
         }
     }
 }
 
-template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN>
+template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int NS>
 static int launch_dense(DenseParams& p, hipStream_t stream) {
-    constexpr int BM = WAVES_M * TM * 32, BN = WAVES_N * TN * 32;
-    constexpr int SC = MODE == MODE_MXFP4 ? (BM + BN) * 8 : 0;
-    constexpr int LDS = 2 * ((BM + BN) * KT_BYTES + SC);
-    auto kern = dense_gemm_kernel<MODE, WAVES_M, WAVES_N, TM, TN>;
+    using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN>;
+    constexpr int LDS = Cfg::lds_bytes(NS);
+    static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
+    auto kern = dense_gemm_kernel<MODE, WAVES_M, WAVES_N, TM, TN, NS>;
     static bool attr_set = false;  // per instantiation; the attribute is per-process
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
@@ -295,9 +331,10 @@ static int launch_dense(DenseParams& p, hipStream_t stream) {
         }
         attr_set = true;
     }
-    p.tiles_m = (p.M + BM - 1) / BM;
-    p.tiles_n = (p.N + BN - 1) / BN;
+    p.tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
+    p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
     if (p.group_m <= 0) p.group_m = 8;
+    p.c16 = (p.ldc % 8 == 0) && (reinterpret_cast<uintptr_t>(p.C) % 16 == 0);
     const int64_t nblk = (int64_t)p.tiles_m * p.tiles_n;
     if (nblk == 0) return 0;
     kern<<<dim3((unsigned)nblk), 64 * WAVES_M * WAVES_N, LDS, stream>>>(p);
@@ -322,7 +359,7 @@ extern "C" {
 int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M, int64_t N,
                   int64_t K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t stream) {
     if (int e = check_common(M, N, K, ldc, C)) return e;
-    HKQ_CHECK_ARG(K % 16 == 0, "K must be a multiple of 16");
+    HKQ_CHECK_ARG(K % 64 == 0, "K must be a multiple of 64");
     HKQ_CHECK_ARG(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0,
                   "lda/ldb must be >= K and multiples of 16");
     HKQ_CHECK_ALIGN(A, 16);
@@ -336,21 +373,21 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
     p.sb = sb;
     p.M = (int)M; p.N = (int)N; p.K = (int)K; p.kbytes = (int)K;
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
-    return launch_dense<MODE_A8W8, 2, 2, 4, 4>(p, stream);
+    return launch_dense<MODE_A8W8, 2, 2, 4, 4, 4>(p, stream);
 }
 
 int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
                    int64_t K, int64_t lda, int64_t ldb, int64_t ldsa, int64_t ldsb, int64_t ldc, hipStream_t stream) {
     if (int e = check_common(M, N, K, ldc, C)) return e;
-    HKQ_CHECK_ARG(K % 256 == 0, "K must be a multiple of 256");
+    HKQ_CHECK_ARG(K % 128 == 0, "K must be a multiple of 128");
     HKQ_CHECK_ARG(lda >= K / 2 && ldb >= K / 2 && lda % 16 == 0 && ldb % 16 == 0,
                   "lda/ldb (bytes) must be >= K/2 and multiples of 16");
-    HKQ_CHECK_ARG(ldsa >= K / 32 && ldsb >= K / 32 && ldsa % 8 == 0 && ldsb % 8 == 0,
-                  "scale row strides must be >= K/32 and multiples of 8");
+    HKQ_CHECK_ARG(ldsa >= K / 32 && ldsb >= K / 32 && ldsa % 4 == 0 && ldsb % 4 == 0,
+                  "scale row strides must be >= K/32 and multiples of 4");
     HKQ_CHECK_ALIGN(A, 16);
     HKQ_CHECK_ALIGN(B, 16);
-    HKQ_CHECK_ALIGN(As, 8);
-    HKQ_CHECK_ALIGN(Bs, 8);
+    HKQ_CHECK_ALIGN(As, 4);
+    HKQ_CHECK_ALIGN(Bs, 4);
     DenseParams p{};
     p.A = static_cast<const uint8_t*>(A);
     p.B = static_cast<const uint8_t*>(B);
@@ -360,7 +397,7 @@ int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs,
     p.M = (int)M; p.N = (int)N; p.K = (int)K; p.kbytes = (int)(K / 2);
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
     p.lsa = ldsa; p.lsb = ldsb;
-    return launch_dense<MODE_MXFP4, 2, 2, 4, 4>(p, stream);
+    return launch_dense<MODE_MXFP4, 2, 2, 4, 4, 4>(p, stream);
 }
 
 }  // extern "C"

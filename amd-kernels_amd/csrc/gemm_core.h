@@ -1,23 +1,25 @@
-// gemm_core.h -- the CDNA4 scaled-MFMA GEMM main loop shared by the dense
-// A8W8, block-scale, MXFP4 and MoE entry points.
+// gemm_core.h -- building blocks of the CDNA4 scaled-MFMA GEMMs (dense A8W8,
+// block-scale, MXFP4 and the MoE grouped GEMM).
 //
 // C[m, n] = sum_k A[m, k] * B[n, k]   (both operands K-contiguous, "NT")
 //
-// Work decomposition
-//   * one workgroup per BM x BN tile of C (BM = WAVES_M*TM*32, BN = WAVES_N*TN*32);
-//   * K is consumed in tiles of 128 bytes per row (128 FP8 or 256 FP4 values),
-//     staged HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging),
-//     two LDS stages so the next tile streams in while the current one feeds
-//     the matrix cores;
-//   * each wave owns a (TM*32) x (TN*32) sub-tile held in TM*TN 32x32 fp32
-//     accumulators of v_mfma_scale_f32_32x32x64_f8f6f4;
+// Shared design
+//   * one workgroup per BM x BN tile of C; waves own (TM*32) x (TN*32) sub-tiles
+//     held in TM*TN 32x32 fp32 accumulators of v_mfma_scale_f32_32x32x64_f8f6f4;
+//   * K is consumed in K-tiles of 64 bytes per row (64 FP8 or 128 FP4 values),
+//     staged HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging) into
+//     NS ring stages, so a tile is requested NS-1 K-tiles before it is needed;
 //   * the MFMA "A" operand is the B tile (rows n) and the MFMA "B" operand is
-//     the A tile (rows m), so that a lane's accumulator registers hold four
-//     consecutive n of one m -- the epilogue stores 8 bytes of bf16 per lane.
+//     the A tile (rows m): a lane's accumulator registers then hold four
+//     consecutive n of one m.
 //
-// LDS tile layout: row r (0..BM-1) of 128 bytes = 8 chunks of 16 bytes; logical
-// chunk c lives at physical chunk c ^ (r & 7), so the 32 lanes of a fragment
-// read (32 rows, same logical chunk) spread over all banks.
+// LDS K-tile layout: row r of 64 bytes = 4 chunks of 16 bytes; logical chunk c
+// lives at physical chunk c ^ ((r >> 2) & 3). A fragment read has 16 lanes on
+// 16 consecutive rows with one logical chunk; their 16-byte slots
+// (r & 3) * 4 + (c ^ ((r >> 2) & 3)) modulo 256 bytes are all distinct, so the
+// read is free of bank conflicts on the 64 x 4-byte LDS banks. A wave-wide
+// LDS-direct load writes 1 KB = 16 rows contiguously; lane l carries row l/4,
+// physical chunk l%4, hence logical chunk (l & 3) ^ ((l >> 4) & 3).
 //
 // Operand fragment layout of the 32x32x64 MFMA (verified on gfx950): lane l
 // supplies row (l % 32) and the 32 K-values [32*(l/32), 32*(l/32)+32) of the
@@ -30,67 +32,48 @@
 
 namespace hkq {
 
-constexpr int KT_BYTES = 128;  // K-tile width in bytes per row
+constexpr int KT_BYTES = 64;           // K-tile width in bytes per row
+constexpr int ROWS_PER_LOAD = 16;      // rows written by one wave-wide 16-byte LDS-direct load
 constexpr uint32_t OOB = 0x80000000u;  // buffer offset that always reads zero (num_records <= 2^31 - 1)
 
 enum GemmMode { MODE_A8W8 = 0, MODE_BLOCKSCALE = 1, MODE_MXFP4 = 2 };
 
-__device__ __forceinline__ int lds_swz(int r, int c) { return r * KT_BYTES + ((c ^ (r & 7)) << 4); }
+__device__ __forceinline__ int lds_swz(int r, int c) { return r * KT_BYTES + ((c ^ ((r >> 2) & 3)) << 4); }
 
-// Issue the LDS-direct loads of one K-tile of one operand: ROWS rows of 128
-// bytes. Wave w, instruction i fills LDS bytes [(i*NW + w)*1024, +1024): rows
-// (i*NW + w)*8 + lane/8, physical chunk lane%8. row_off[i] is the byte offset
-// of that row inside the buffer (OOB for rows past the edge); chunk_off is the
-// lane's logical chunk * 16.
-template <int ROWS, int NW>
-__device__ __forceinline__ void load_tile_lds(__amdgpu_buffer_rsrc_t rsrc, HKQ_LDS uint8_t* lds, int wave,
-                                              const uint32_t (&row_off)[ROWS / 8 / NW], uint32_t chunk_off,
-                                              bool k_tail, uint32_t k_left) {
-#pragma unroll
-    for (int i = 0; i < ROWS / 8 / NW; ++i) {
-        uint32_t off = row_off[i] + chunk_off;
-        if (k_tail) off = chunk_off < k_left ? off : OOB;
-        HKQ_LDS void* dst = lds + (i * NW + wave) * 1024;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, off, 0, 0, 0);
-    }
-}
+// Logical chunk carried by `lane` in a wave-wide LDS-direct load.
+__device__ __forceinline__ int load_chunk(int lane) { return (lane & 3) ^ ((lane >> 4) & 3); }
 
 // One LDS-direct load of `size` (4 or 16) bytes per lane from [base, base + bytes)
-// at byte offset `off` to `dst` + lane * size. Kept out of lambdas: a target
-// builtin called directly in a lambda inside a kernel template makes the host
-// pass drop that kernel's launch stub without a diagnostic.
+// at byte offset `off` to `dst` + lane * size (buffer_load ... lds: M0 holds
+// the wave-uniform LDS destination).
+//
+// Issued as inline assembly on purpose: the compiler's wait-count pass treats a
+// builtin LDS-direct load as a pending LDS write that any later ds_read might
+// alias and strengthens the pipeline's vmcnt(N) waits to vmcnt(0), which would
+// serialize the K-tile ring. The kernels order these loads themselves: every
+// read of a stage is preceded by tile_barrier<N>, whose vmcnt(N) covers the
+// loads that filled it, and a vmcnt(0) barrier precedes any other use of the
+// LDS or of the vector-memory counter after the main loop.
+__device__ __forceinline__ v4i buffer_desc(const void* base, uint32_t bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    return v4i{(int)(uint32_t)b, (int)((uint32_t)(b >> 32) & 0xFFFFu), (int)bytes, 0x00020000};
+}
 __device__ __forceinline__ void lds_load16(const void* base, uint32_t bytes, HKQ_LDS void* dst, uint32_t off) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(base, bytes), dst, 16, off, 0, 0, 0);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(off), "s"(buffer_desc(base, bytes))
+                 : "memory", "m0");
 }
 __device__ __forceinline__ void lds_load4(const void* base, uint32_t bytes, HKQ_LDS void* dst, uint32_t off) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(base, bytes), dst, 4, off, 0, 0, 0);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(off), "s"(buffer_desc(base, bytes))
+                 : "memory", "m0");
 }
 
-// Per-lane constants of the load pattern: the lane's row within its 8-row
-// group and logical chunk (so that physical chunk = lane % 8).
-__device__ __forceinline__ void load_lane_coords(int lane, int wave, int NW, int i, int& row, int& chunk) {
-    row = (i * NW + wave) * 8 + (lane >> 3);
-    chunk = (lane & 7) ^ (row & 7);
-}
-
-// Read the FP8 fragment (32 bytes: logical chunks c0, c0+1) of row r.
-__device__ __forceinline__ v8i read_frag_fp8(const HKQ_LDS uint8_t* tile, int r, int c0) {
-    const v4i lo = *reinterpret_cast<const HKQ_LDS v4i*>(tile + lds_swz(r, c0));
-    const v4i hi = *reinterpret_cast<const HKQ_LDS v4i*>(tile + lds_swz(r, c0 + 1));
-    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-// Read the FP4 fragment (16 bytes: logical chunk c) of row r.
-__device__ __forceinline__ v8i read_frag_fp4(const HKQ_LDS uint8_t* tile, int r, int c) {
-    const v4i v = *reinterpret_cast<const HKQ_LDS v4i*>(tile + lds_swz(r, c));
-    return v8i{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
-}
-
-template <bool FP4>
-__device__ __forceinline__ v16f mfma(const v8i& a, const v8i& b, const v16f& c, int sa, int sb) {
-    if (FP4) return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 4, 4, 0, sa, 0, sb);
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
-}
+__device__ __forceinline__ v4i lds_read16(const HKQ_LDS uint8_t* p) { return *reinterpret_cast<const HKQ_LDS v4i*>(p); }
 
 template <bool FP4, int OPA, int OPB>
 __device__ __forceinline__ v16f mfma_sel(const v8i& a, const v8i& b, const v16f& c, int sa, int sb) {
@@ -98,12 +81,18 @@ __device__ __forceinline__ v16f mfma_sel(const v8i& a, const v8i& b, const v16f&
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, OPA, sa, OPB, sb);
 }
 
-// Workgroup barrier that also waits for this wave's LDS-direct loads
-// (vmcnt): __syncthreads' workgroup-scope fence does not cover the
-// buffer_load ... lds writes, so without the explicit wait a wave could read a
-// K-tile that another wave's loads have not finished writing.
+// s_waitcnt immediate (gfx9 encoding): vmcnt in [3:0] and [15:14], expcnt in
+// [6:4], lgkmcnt in [11:8].
+constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8); }
+
+// Workgroup barrier that first waits until at most VM of this wave's vector
+// memory operations are outstanding and all its LDS operations are done.
+// __syncthreads' workgroup-scope fence does not cover buffer_load ... lds, so
+// the explicit vmcnt wait is what makes another wave's K-tile visible.
+template <int VM>
 __device__ __forceinline__ void tile_barrier() {
-    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+    static_assert(VM >= 0 && VM <= 63, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(VM, 0));
     __syncthreads();
 }
 
@@ -112,8 +101,8 @@ __device__ __forceinline__ void tile_barrier() {
 // under-counts the 16-pass FP8 form across block boundaries).
 __device__ __forceinline__ void mfma_drain() {
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_sched_barrier(0); asm volatile("s_nop 15");
-    __builtin_amdgcn_sched_barrier(0); asm volatile("s_nop 15");
+    asm volatile("s_nop 15");
+    asm volatile("s_nop 15");
     __builtin_amdgcn_sched_barrier(0);
 }
 

@@ -50,10 +50,24 @@ def seeded_bf16(shape, std, seed):
     return (torch.randn(*shape, generator=g) * std).to(torch.bfloat16).cuda()
 
 
+PREHEAT_S = 0.3  # untimed device load before the warmup steps
+
+
 def time_launches(fn, steps, warmup):
-    """Average ms per launch over `steps` back-to-back launches on the current stream."""
+    """Average ms per launch over `steps` back-to-back launches on the current stream.
+
+    Before the `warmup` launches, the kernel runs untimed for PREHEAT_S seconds:
+    MI355X engine clocks take tens of milliseconds of sustained load to settle,
+    and a handful of warmup launches would otherwise time a ramping clock."""
+    import time
+
     import torch
 
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < PREHEAT_S:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -81,8 +95,9 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant"], default=None,
-                    help="run one kernel only (for profiling); prints no JSON line")
+    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant", "copy"], default=None,
+                    help="run one kernel only (for profiling); prints no JSON line. 'copy' is a plain "
+                         "1 GiB device copy used to calibrate the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
@@ -95,6 +110,13 @@ def main():
 
     torch.cuda.set_device(0)
     steps, warmup = args.steps, args.warmup
+
+    if args.only == "copy":
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        ms = time_launches(lambda: dst.copy_(src), steps, warmup)
+        log(json.dumps({"copy_bytes": 1 << 30, "us": round(ms * 1e3, 2), "GB/s": round(2 * (1 << 30) / ms / 1e6, 1)}))
+        return
 
     # ---- A8W8 headline ----
     M, N, K = HEADLINE["M"], HEADLINE["N"], HEADLINE["K"]

@@ -78,7 +78,8 @@ int hkq_mx_dequant(const void* q, const void* s, void* out, int64_t M, int64_t K
 /* ---- dense GEMMs (A [M, K], B [N, K], both K-contiguous; C bf16 [M, ldc]) ---- */
 
 /* C = bf16((A . B^T) * sa[m] * sb[n]); A, B E4M3FN; sa fp32 [M], sb fp32 [N].
- * K % 16 == 0, N % 4 == 0. Replaces gemm_a8w8_tk.dispatch(A, B, a_scale, b_scale, C)
+ * K % 64 == 0 (as the reference requires), N % 4 == 0, ldc % 4 == 0.
+ * Replaces gemm_a8w8_tk.dispatch(A, B, a_scale, b_scale, C)
  * (kernels/gemm-basic/gemm_a8w8/kernel.cpp:162-175) and
  * gemm_a8w8_per_token_scale_tk.dispatch(A, B, C, a_scale, b_scale)
  * (kernels/gemm-basic/gemm_a8w8_per_token_scale/kernel.cpp:158-171). */
@@ -87,7 +88,7 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
 
 /* MXFP4 A4W4: C = bf16(sum_k e2m1(A) 2^(As-127) e2m1(B) 2^(Bs-127)).
  * A u8 [M, lda >= K/2], As u8 [M, ldsa >= K/32], B u8 [N, ldb], Bs u8 [N, ldsb].
- * K % 256 == 0. Replaces gemm_afp4wfp4_tk.dispatch (kernels/gemm-basic/gemm_afp4wfp4/kernel.cpp:147-159),
+ * K % 128 == 0, N % 4 == 0, ldc % 4 == 0. Replaces gemm_afp4wfp4_tk.dispatch (kernels/gemm-basic/gemm_afp4wfp4/kernel.cpp:147-159),
  * taking the packed format its header documents (:3-6) instead of
  * pre-dequantized bf16. */
 int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,

@@ -54,11 +54,13 @@ def test_argument_errors_are_reported_before_launch():
     _expect_invalid("hkq_group_quant", p, p, p, 4, 256, 256, 256, 2, 96, 0, None, match="group")
     _expect_invalid("hkq_group_quant", p, p, p, 4, 200, 200, 200, 2, 128, 0, None, match="multiple of group")
     _expect_invalid("hkq_mx_quant", p, p, p, 4, 48, 48, 1, None, match="multiple of 32")
-    _expect_invalid("hkq_gemm_a8w8", p, p, p, p, p, 16, 16, 40, 40, 40, 16, None, match="multiple of 16")
-    _expect_invalid("hkq_gemm_a8w8", p, p, p, p, p, 16, 18, 64, 64, 64, 18, None, match="N must be a multiple of 4")
+    _expect_invalid("hkq_gemm_a8w8", p, p, p, p, p, 16, 16, 96, 96, 96, 16, None, match="multiple of 64")
+    _expect_invalid("hkq_gemm_a8w8", p, p, p, p, p, 16, 18, 64, 64, 64, 24, None, match="N must be a multiple of 4")
+    _expect_invalid("hkq_gemm_a8w8", p, p, p, p, p, 16, 20, 64, 64, 64, 18, None, match="ldc")
     _expect_invalid("hkq_gemm_a8w8", p + 4, p, p, p, p, 16, 16, 64, 64, 64, 16, None, match="aligned")
-    _expect_invalid("hkq_gemm_mxfp4", p, p, p, p, p, 16, 16, 128, 64, 64, 8, 8, 16, None, match="multiple of 256")
-    assert "multiple of 256" in hkq.lib().hkq_last_error().decode()
+    _expect_invalid("hkq_gemm_a8w8", p, p, p, p, p + 4, 16, 16, 64, 64, 64, 16, None, match="aligned")
+    _expect_invalid("hkq_gemm_mxfp4", p, p, p, p, p, 16, 16, 192, 96, 96, 8, 8, 16, None, match="multiple of 128")
+    assert "multiple of 128" in hkq.lib().hkq_last_error().decode()
 
 
 def test_hipkittens_discovery_and_errors():

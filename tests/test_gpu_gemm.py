@@ -5,7 +5,7 @@ dequant matmul of the same codes and scales, and Frobenius relative error
 < 1e-2. Inputs follow BASELINE's distributions (acts ~N(0,1), weights
 ~N(0,0.02)) through the oracle quantizers, so the GEMM test does not depend on
 the GPU quantizer. Small shapes are compared in full (including M = 1, ragged
-M/N and a K tail); BASELINE sizes are checked on a sampled 96 x 96 block of C
+M/N, a single K-tile and odd K-tile counts); BASELINE sizes are checked on a sampled 96 x 96 block of C
 plus closed forms.
 """
 import numpy as np
@@ -32,8 +32,8 @@ def run_a8w8(A, B, sa, sb):
     return host_bf16_f32(C)
 
 
-A8W8_SHAPES = [(256, 256, 128), (1, 256, 256), (16, 512, 512), (100, 260, 4112), (333, 1000, 512),
-               (513, 772, 1040), (128, 4096, 4096), (1024, 1024, 2048)]
+A8W8_SHAPES = [(256, 256, 64), (256, 256, 128), (1, 256, 256), (16, 512, 512), (100, 260, 4160), (333, 1000, 576),
+               (513, 772, 1088), (128, 4096, 4096), (1024, 1024, 2048), (300, 300, 320)]
 
 
 @pytest.mark.parametrize("M,N,K", A8W8_SHAPES)
@@ -102,8 +102,8 @@ def run_mxfp4(Aq, As, Bq, Bs):
     return host_bf16_f32(C)
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (1, 256, 512), (128, 512, 8192), (77, 300, 768),
-                                   (600, 1028, 1536)])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (256, 256, 256), (1, 256, 512), (128, 512, 8192), (77, 300, 768),
+                                   (600, 1028, 1536), (260, 264, 384)])
 def test_gemm_mxfp4(orc, M, N, K):
     require_gpu()
     Aq, As, Bq, Bs = mx_inputs(orc, M, N, K, seed=M * 7 + K)
