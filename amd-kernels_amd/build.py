@@ -40,7 +40,7 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-HIP_SOURCES = ["quant.hip", "gemm.hip"]
+HIP_SOURCES = ["quant.hip", "gemm.hip", "gemm_blockscale.hip"]
 CPP_SOURCES = ["hkq_error.cpp"]
 
 # pybind11 module name -> binding source (module names are the reference's)
@@ -50,6 +50,7 @@ MODULES = {
     "gemm_a8w8_tk": "bind_gemm_a8w8.cpp",
     "gemm_a8w8_per_token_scale_tk": "bind_gemm_a8w8_per_token_scale.cpp",
     "gemm_afp4wfp4_tk": "bind_gemm_afp4wfp4.cpp",
+    "gemm_a8w8_blockscale_tk": "bind_gemm_a8w8_blockscale.cpp",
 }
 
 

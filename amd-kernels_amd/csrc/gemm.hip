@@ -257,63 +257,20 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
     mfma_drain();
     tile_barrier<0>();  // every wave is done with the stages and no load is in flight
 
-    // Epilogue: scale in registers, stage the wave's bf16 sub-tile in LDS (row
-    // m, col n, padded pitch), then store whole row segments of C.
-    // Lane holds, for m-tile j and n-tile i, D[n][m] with m = (lane & 31),
-    // n = 8*(r/4) + 4*(lane/32) + r%4.
-    constexpr int PITCH = Cfg::EP_PITCH;
-    HKQ_LDS uint8_t* ep = smem + wave * (TM * 32) * PITCH;
+    // Epilogue (scales of A8W8 applied in registers; MXFP4 has none left)
     const float* sa = static_cast<const float*>(p.sa);
     const float* sb = static_cast<const float*>(p.sb);
-    float ascale[TM];
-#pragma unroll
-    for (int j = 0; j < TM; ++j) {
-        const int m = m0 + arow + j * 32;
-        ascale[j] = (MODE == MODE_A8W8 && m < p.M) ? sa[m] : 1.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < TN; ++i) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int nl = i * 32 + 8 * g + 4 * khalf;
-            const int n = n0 + wn * TN * 32 + nl;
-            float4 bs = make_float4(1.f, 1.f, 1.f, 1.f);
-            if constexpr (MODE == MODE_A8W8) {
-                if (n < p.N) bs = *reinterpret_cast<const float4*>(sb + n);
-            }
-#pragma unroll
-            for (int j = 0; j < TM; ++j) {
-                const float a = ascale[j];
-                const uint32_t lo = f32_to_bf16(acc[i][j][4 * g + 0] * a * bs.x) | (f32_to_bf16(acc[i][j][4 * g + 1] * a * bs.y) << 16);
-                const uint32_t hi = f32_to_bf16(acc[i][j][4 * g + 2] * a * bs.z) | (f32_to_bf16(acc[i][j][4 * g + 3] * a * bs.w) << 16);
-                *reinterpret_cast<HKQ_LDS v2i*>(ep + (j * 32 + (lane & 31)) * PITCH + nl * 2) = v2i{(int)lo, (int)hi};
-            }
-        }
-    }
-    // LDS operations of a wave complete in order: the reads below see the writes above.
-    constexpr int SEGS = TN * 32 * 2 / 16;  // 16-byte pieces per row
-    constexpr int ROWS_PER_PASS = 64 / SEGS;
-#pragma unroll 4
-    for (int r0 = 0; r0 < TM * 32; r0 += ROWS_PER_PASS) {
-        const int r = r0 + lane / SEGS, seg = lane % SEGS;
-        const v4i v = lds_read16(ep + r * PITCH + seg * 16);
-        const int m = m0 + wm * TM * 32 + r;
-        const int n = n0 + wn * TN * 32 + seg * 8;
-        if (m < p.M) {
-            // N % 4 == 0: a piece is whole, half (4 values) or out of range
-            uint16_t* dst = p.C + (int64_t)m * p.ldc + n;
-            if (n + 8 <= p.N) {
-                if (p.c16) {
-                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(dst));
-                } else {
-                    __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
-                    __builtin_nontemporal_store(v2i{v[2], v[3]}, reinterpret_cast<v2i*>(dst + 4));
-                }
-            } else if (n < p.N) {
-                __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
-            }
-        }
-    }
+    const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
+    store_tile_bf16<TM, TN>(
+        acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0,
+        [&](int j) {
+            const int m = mw + j * 32 + (lane & 31);
+            return (MODE == MODE_A8W8 && m < p.M) ? sa[m] : 1.0f;
+        },
+        [&](int i, int g) {
+            const int n = nw + i * 32 + 8 * g + 4 * khalf;
+            return (MODE == MODE_A8W8 && n < p.N) ? *reinterpret_cast<const float4*>(sb + n) : make_float4(1.f, 1.f, 1.f, 1.f);
+        });
 }
 
 template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int NS>

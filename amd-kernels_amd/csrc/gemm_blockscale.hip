@@ -1,0 +1,250 @@
+// gemm_blockscale.hip -- FP8 GEMM with per-K-group fp32 scales (DeepSeek-V3
+// style), restating gemm-basic/gemm_a8w8_blockscale/kernel.cpp:129-153 (and
+// the formula of gemm_a8w8_blockscale/test_parity.py:57-76):
+//
+//   C[m, n] = bf16( sum_g (A_g . B_g^T)[m, n] * sa[m, g] * sb[g, n / GN] ),
+//   g = 128-wide K group, GN = 128 (128x128 weight blocks) or 1 (per column,
+//   the layout of the reference test: b_scale [K/128, N]).
+//
+// fp32 scales cannot ride in the MFMA's e8m0 scale operands, so every K group
+// is "promoted" on the VALU: per 32x32 sub-tile two chained MFMAs (the group's
+// two 64-deep K-steps) produce a fresh partial P, then acc += P * sa * sb.
+// K-tiles are 128 bytes wide (one scale group), held in a 2-stage LDS ring;
+// the group scales live in their own 3-slot LDS rings (a tile's scales are read
+// while its stage is being refilled). Fragments of the next K-tile are read
+// into the registers of the current one as soon as those are consumed.
+#include "gemm_core.h"
+#include "hkq_host.h"
+
+namespace hkq {
+
+struct BlockScaleParams {
+    const uint8_t* A;
+    const uint8_t* B;
+    uint16_t* C;
+    const float* sa;  // [M, lsa]: column g = K group
+    const float* sb;  // [K/128, lsb]: column n/128 (GN 128) or n (GN 1)
+    int M, N, K;
+    int64_t lda, ldb, ldc, lsa, lsb;
+    int tiles_m, tiles_n, group_m, c16;
+};
+
+constexpr int BS_KT = 128;  // K-tile bytes per row = one 128-wide scale group
+
+__device__ __forceinline__ int lds_swz128(int r, int c) { return r * BS_KT + ((c ^ ((r >> 1) & 7)) << 4); }
+
+template <bool GN1>
+__global__ __launch_bounds__(256, 1) void blockscale_gemm_kernel(const BlockScaleParams p) {
+    constexpr int WAVES_M = 2, WAVES_N = 2, NW = 4, TM = 4, TN = 4;
+    constexpr int BM = WAVES_M * TM * 32, BN = WAVES_N * TN * 32;
+    constexpr int LA = BM * BS_KT / 1024 / NW, LB = BN * BS_KT / 1024 / NW;  // 16-byte loads per wave
+    constexpr int STAGE = (BM + BN) * BS_KT;
+    constexpr int SA_RING = 2 * STAGE, SB_RING = SA_RING + 3 * 1024;  // 3 slots of 256 floats each
+
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
+    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int khalf = lane >> 5;
+
+    int tm, tn;
+    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int rows_a = min(p.M - m0, BM), rows_b = min(p.N - n0, BN);
+    const int KT = p.K / BS_KT;
+
+    // A/B loads: instruction i fills rows (i*NW + wave)*8 + lane/8 at physical
+    // chunk lane%8; with this swizzle the logical chunk depends on the lane and
+    // the wave's parity only.
+    const uint32_t chunk_off = (uint32_t)(((lane & 7) ^ (((wave & 1) * 4 + (lane >> 4)) & 7)) << 4);
+    uint32_t a_off[LA], b_off[LB];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) a_off[i] = (uint32_t)(((i * NW + wave) * 8 + (lane >> 3)) * p.lda) + chunk_off;
+#pragma unroll
+    for (int i = 0; i < LB; ++i) b_off[i] = (uint32_t)(((i * NW + wave) * 8 + (lane >> 3)) * p.ldb) + chunk_off;
+    const uint8_t* a_base = p.A + (int64_t)m0 * p.lda;
+    const uint8_t* b_base = p.B + (int64_t)n0 * p.ldb;
+    const int64_t a_bytes = min((int64_t)rows_a * p.lda, (int64_t)0x7FFFFFFF);
+    const int64_t b_bytes = min((int64_t)rows_b * p.ldb, (int64_t)0x7FFFFFFF);
+    // scale loads: sa rows m0 + wave*64 + lane (one float per row per group);
+    // sb GN1: columns n0 + wave*64 + lane of row g; GN128: columns n0/128 + {0,1}
+    const float* sa_base = p.sa + (int64_t)m0 * p.lsa;
+    const int64_t sa_bytes = min((int64_t)rows_a * p.lsa * 4, (int64_t)0x7FFFFFFF);
+    const uint32_t sa_off = (uint32_t)((wave * 64 + lane) * p.lsa * 4);
+    const int sb_col0 = GN1 ? n0 : n0 / 128;
+    const int sb_cols = GN1 ? rows_b : min((p.N + 127) / 128 - n0 / 128, 2);
+    const uint32_t sb_off = GN1 ? (uint32_t)((wave * 64 + lane) * 4) : (wave == 0 && lane < 2 ? (uint32_t)(lane * 4) : OOB);
+
+    auto issue = [&](int kt) {
+        const bool live = kt < KT;
+        const int kb = kt * BS_KT;
+        HKQ_LDS uint8_t* st = smem + (kt & 1) * STAGE;
+#pragma unroll
+        for (int i = 0; i < LA; ++i)
+            lds_load16(a_base + kb, live ? (uint32_t)(a_bytes - kb) : 0u, st + (i * NW + wave) * 1024, a_off[i]);
+#pragma unroll
+        for (int i = 0; i < LB; ++i)
+            lds_load16(b_base + kb, live ? (uint32_t)(b_bytes - kb) : 0u, st + BM * BS_KT + (i * NW + wave) * 1024, b_off[i]);
+        const int slot = kt % 3;
+        lds_load4(sa_base + kt, live ? (uint32_t)(sa_bytes - kt * 4) : 0u, smem + SA_RING + slot * 1024 + wave * 256, sa_off);
+        lds_load4(p.sb + (int64_t)kt * p.lsb + sb_col0, live ? (uint32_t)(sb_cols * 4) : 0u,
+                  smem + SB_RING + slot * 1024 + wave * 256, sb_off);
+    };
+
+    const int arow = wm * TM * 32 + (lane & 31);
+    const int brow = wn * TN * 32 + (lane & 31);
+    // fragment of row r, K-step ks (0/1): logical chunks ks*4 + 2*khalf + {0,1}
+    auto frag = [&](const HKQ_LDS uint8_t* tile, int r, int ks) {
+        const v4i lo = lds_read16(tile + lds_swz128(r, ks * 4 + khalf * 2));
+        const v4i hi = lds_read16(tile + lds_swz128(r, ks * 4 + khalf * 2 + 1));
+        return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    v16f acc[TN][TM];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j) acc[i][j] = v16f{};
+
+    v8i fa[TM][2], fb[TN][2];
+    issue(0);
+    issue(1);
+    tile_barrier<0>();
+    {
+        const HKQ_LDS uint8_t* At = smem;
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) fa[j][ks] = frag(At, arow + j * 32, ks);
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) fb[i][ks] = frag(At + BM * BS_KT, brow + i * 32, ks);
+    }
+
+    for (int kt = 0; kt < KT; ++kt) {
+        // everything issued so far has landed (K-tile kt+1 resident) and every wave
+        // has read K-tile kt's fragments: its stage takes K-tile kt+2
+        tile_barrier<0>();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(kt + 2);
+        const HKQ_LDS uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE;
+        const int slot = kt % 3;
+        const HKQ_LDS float* sas = reinterpret_cast<const HKQ_LDS float*>(smem + SA_RING + slot * 1024);
+        const HKQ_LDS float* sbs = reinterpret_cast<const HKQ_LDS float*>(smem + SB_RING + slot * 1024);
+        float sa_j[TM];
+#pragma unroll
+        for (int j = 0; j < TM; ++j) sa_j[j] = sas[arow + j * 32];
+        float sbw = 0.f;
+        v4f sbn[4];
+        if constexpr (!GN1) sbw = sbs[wn];
+        auto load_sbn = [&](int i) {
+            if constexpr (GN1) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    sbn[g] = *reinterpret_cast<const HKQ_LDS v4f*>(sbs + wn * TN * 32 + i * 32 + 8 * g + 4 * khalf);
+            }
+        };
+        load_sbn(0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < TN; ++i) {
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                v16f P = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i][0], fa[j][0], v16f{}, 0, 0, 0, 127, 0, 127);
+                P = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i][1], fa[j][1], P, 0, 0, 0, 127, 0, 127);
+                if constexpr (GN1) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        acc[i][j][r] += P[r] * sa_j[j] * sbn[r / 4][r & 3];
+                    }
+                } else {
+                    const float s = sa_j[j] * sbw;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] += P[r] * s;
+                }
+                // registers freed by this sub-tile take the next K-tile's fragments
+                if (j == TM - 1) {
+                    fb[i][0] = frag(nxt + BM * BS_KT, brow + i * 32, 0);
+                    fb[i][1] = frag(nxt + BM * BS_KT, brow + i * 32, 1);
+                    if (i + 1 < TN) load_sbn(i + 1);
+                }
+                if (i == TN - 1) {
+                    fa[j][0] = frag(nxt, arow + j * 32, 0);
+                    fa[j][1] = frag(nxt, arow + j * 32, 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+    mfma_drain();
+    tile_barrier<0>();
+
+    const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
+    store_tile_bf16<TM, TN>(
+        acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, [](int) { return 1.0f; },
+        [](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); });
+}
+
+template <bool GN1>
+static int launch_blockscale(BlockScaleParams& p, hipStream_t stream) {
+    constexpr int BM = 256, BN = 256;
+    constexpr int LDS_RING = 2 * (BM + BN) * BS_KT + 6 * 1024;
+    constexpr int LDS_EPI = 4 * 128 * (128 * 2 + 16);
+    constexpr int LDS = LDS_RING > LDS_EPI ? LDS_RING : LDS_EPI;
+    static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
+    auto kern = blockscale_gemm_kernel<GN1>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
+        if (e != hipSuccess) {
+            set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", LDS, hipGetErrorString(e));
+            return (int)e;
+        }
+        attr_set = true;
+    }
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + BN - 1) / BN;
+    if (p.group_m <= 0) p.group_m = 8;
+    p.c16 = (p.ldc % 8 == 0) && (reinterpret_cast<uintptr_t>(p.C) % 16 == 0);
+    const int64_t nblk = (int64_t)p.tiles_m * p.tiles_n;
+    if (nblk == 0) return 0;
+    kern<<<dim3((unsigned)nblk), 256, LDS, stream>>>(p);
+    return hkq_launch_status();
+}
+
+}  // namespace hkq
+
+using namespace hkq;
+
+extern "C" int hkq_gemm_blockscale(const void* A, const void* B, const float* sa, const float* sb, void* C,
+                                   int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t lsa,
+                                   int64_t lsb, int64_t ldc, int64_t group_n, hipStream_t stream) {
+    HKQ_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "M, N must be >= 0 and K > 0");
+    HKQ_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), "dimensions must be < 2^30");
+    HKQ_CHECK_ARG(K % 128 == 0, "K must be a multiple of the 128-wide scale group");
+    HKQ_CHECK_ARG(N % 4 == 0, "N must be a multiple of 4");
+    HKQ_CHECK_ARG(group_n == 1 || group_n == 128, "group_n must be 1 or 128");
+    HKQ_CHECK_ARG(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0, "lda/ldb must be >= K and multiples of 16");
+    HKQ_CHECK_ARG(ldc >= N && ldc % 4 == 0, "ldc must be >= N and a multiple of 4");
+    // a stride only matters when there is more than one row to step over
+    HKQ_CHECK_ARG(M <= 1 || lsa >= K / 128, "a_scale row stride must be >= K/128");
+    HKQ_CHECK_ARG(K / 128 <= 1 || lsb >= (group_n == 1 ? N : (N + 127) / 128),
+                  "b_scale row stride must cover N / group_n columns");
+    HKQ_CHECK_ALIGN(A, 16);
+    HKQ_CHECK_ALIGN(B, 16);
+    HKQ_CHECK_ALIGN(C, 8);
+    HKQ_CHECK_ALIGN(sa, 4);
+    HKQ_CHECK_ALIGN(sb, 4);
+    BlockScaleParams p{};
+    p.A = static_cast<const uint8_t*>(A);
+    p.B = static_cast<const uint8_t*>(B);
+    p.C = static_cast<uint16_t*>(C);
+    p.sa = sa;
+    p.sb = sb;
+    p.M = (int)M; p.N = (int)N; p.K = (int)K;
+    p.lda = lda; p.ldb = ldb; p.ldc = ldc; p.lsa = lsa; p.lsb = lsb;
+    return group_n == 1 ? launch_blockscale<true>(p, stream) : launch_blockscale<false>(p, stream);
+}

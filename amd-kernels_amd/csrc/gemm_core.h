@@ -124,4 +124,65 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
     tn = in_g / gsize;
 }
 
+// Epilogue shared by the GEMMs: scale in registers, stage each wave's bf16
+// (TM*32) x (TN*32) sub-tile in LDS (row m, col n, row pitch TN*64 + 16 bytes),
+// then store whole 256-byte row segments of C (16-byte stores when C's rows are
+// 16-byte aligned, else two 8-byte stores; N % 4 == 0). The caller has retired
+// every LDS use of the main loop (a vmcnt(0) barrier) before calling.
+//   acc[i][j]: accumulator of n-tile i, m-tile j, D[n][m] layout
+//   (lane: m = lane & 31; register r: n = 8*(r/4) + 4*(lane/32) + r%4);
+//   row_scale(j) -> scale of the lane's m in m-tile j; col_scale4(i, g) -> the
+//   4 scales of n = i*32 + 8g + 4*(lane/32) + 0..3 (both relative to the wave).
+template <int TM, int TN, typename RowScale, typename ColScale4>
+__device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uint8_t* smem, int wave, int lane,
+                                                uint16_t* C, int64_t ldc, int M, int N, int mw, int nw, bool c16,
+                                                RowScale row_scale, ColScale4 col_scale4) {
+    constexpr int PITCH = TN * 32 * 2 + 16;
+    static_assert((TN * 32 * 2) % 256 == 0, "rows are whole 256-byte segments");
+    HKQ_LDS uint8_t* ep = smem + wave * (TM * 32) * PITCH;
+    const int khalf = lane >> 5;
+    float rs[TM];
+#pragma unroll
+    for (int j = 0; j < TM; ++j) rs[j] = row_scale(j);
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int nl = i * 32 + 8 * g + 4 * khalf;
+            const float4 cs = col_scale4(i, g);
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const float a = rs[j];
+                const uint32_t lo = f32_to_bf16(acc[i][j][4 * g + 0] * a * cs.x) | (f32_to_bf16(acc[i][j][4 * g + 1] * a * cs.y) << 16);
+                const uint32_t hi = f32_to_bf16(acc[i][j][4 * g + 2] * a * cs.z) | (f32_to_bf16(acc[i][j][4 * g + 3] * a * cs.w) << 16);
+                *reinterpret_cast<HKQ_LDS v2i*>(ep + (j * 32 + (lane & 31)) * PITCH + nl * 2) = v2i{(int)lo, (int)hi};
+            }
+        }
+    }
+    // LDS operations of a wave complete in order: the reads below see the writes above.
+    constexpr int SEGS = TN * 32 * 2 / 16;  // 16-byte pieces per row
+    constexpr int ROWS_PER_PASS = 64 / SEGS;
+#pragma unroll 4
+    for (int r0 = 0; r0 < TM * 32; r0 += ROWS_PER_PASS) {
+        const int r = r0 + lane / SEGS, seg = lane % SEGS;
+        const v4i v = lds_read16(ep + r * PITCH + seg * 16);
+        const int m = mw + r;
+        const int n = nw + seg * 8;
+        if (m < M) {
+            // N % 4 == 0: a piece is whole, half (4 values) or out of range
+            uint16_t* dst = C + (int64_t)m * ldc + n;
+            if (n + 8 <= N) {
+                if (c16) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(dst));
+                } else {
+                    __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
+                    __builtin_nontemporal_store(v2i{v[2], v[3]}, reinterpret_cast<v2i*>(dst + 4));
+                }
+            } else if (n < N) {
+                __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
+            }
+        }
+    }
+}
+
 }  // namespace hkq

@@ -28,6 +28,7 @@ SIGNATURES = {
     "hkq_mx_dequant": (_I, [_P, _P, _P, _I64, _I64, _I, _P]),
     "hkq_gemm_a8w8": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "hkq_gemm_mxfp4": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "hkq_gemm_blockscale": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
 }
 
 
@@ -154,4 +155,18 @@ def gemm_mxfp4(A, As, B, Bs, C=None, stream=None):
         C = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
     call("hkq_gemm_mxfp4", _ptr(A), _ptr(As), _ptr(B), _ptr(Bs), _ptr(C), M, N, K, A.stride(0), B.stride(0),
          As.stride(0), Bs.stride(0), C.stride(0), _stream(stream))
+    return C
+
+
+def gemm_blockscale(A, B, sa, sb, C=None, group_n: int = 128, stream=None):
+    """A [M, K], B [N, K] E4M3FN codes; sa fp32 [M, K/128]; sb fp32 [K/128, N/group_n]
+    -> C bf16 [M, N]."""
+    import torch
+
+    M, K = A.shape
+    N = B.shape[0]
+    if C is None:
+        C = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
+    call("hkq_gemm_blockscale", _ptr(A), _ptr(B), _ptr(sa), _ptr(sb), _ptr(C), M, N, K, A.stride(0), B.stride(0),
+         sa.stride(0), sb.stride(0), C.stride(0), group_n, _stream(stream))
     return C

@@ -94,6 +94,18 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
 int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
                    int64_t K, int64_t lda, int64_t ldb, int64_t ldsa, int64_t ldsb, int64_t ldc, hkq_stream_t stream);
 
+/* Block-scale FP8 GEMM (DeepSeek-V3 style):
+ * C = bf16(sum_g (A_g . B_g^T) * sa[m, g] * sb[g, n / group_n]), g = 128-wide K group.
+ * A, B E4M3FN [M, K] / [N, K]; sa fp32 [M, lsa >= K/128]; sb fp32 [K/128, lsb] with
+ * lsb >= N (group_n 1, per column) or >= ceil(N/128) (group_n 128, 128x128 blocks).
+ * K % 128 == 0, N % 4 == 0, ldc % 4 == 0. Replaces
+ * gemm_a8w8_blockscale_tk.dispatch(A, B, C, a_scale, b_scale)
+ * (kernels/gemm-basic/gemm_a8w8_blockscale/kernel.cpp:167-180; formula
+ * kernels/gemm-basic/gemm_a8w8_blockscale/test_parity.py:57-76). */
+int hkq_gemm_blockscale(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M, int64_t N,
+                        int64_t K, int64_t lda, int64_t ldb, int64_t lsa, int64_t lsb, int64_t ldc, int64_t group_n,
+                        hkq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,8 @@ e2m1_encode/decode     value table (moe-gemm/moe_op_mxfp4/kernel.cpp:32-35) and
 mx_scale_exp           the reference's float formula (fused_mxfp4_quant/
                        kernel.cpp:99-105) evaluated with numpy log2/floor over
                        every positive bf16 value.
+quant_block_2d         per-block loop in numpy against the per-token rule on
+                       each flattened block (tests/test_oracle_quant.py).
 quant_rowwise          an independent vectorised numpy/torch restatement of
                        quant/kernel.cpp:46-107 (and of the reference test
                        formula tests/test_misc.py:532-536, within 1 code);
@@ -187,6 +189,22 @@ def quant_rowwise(xb: np.ndarray, group: int | None = None, kind: str = "fp8"):
     s = np.empty((M, K // g), dtype=np.float32)
     lib().orc_quant_rowwise(_p(xb), M, K, K, g, 0 if kind == "fp8" else 1, _p(q), K, _p(s), K // g)
     return q, s
+
+
+def quant_block_2d(xb: np.ndarray, block: int = 128):
+    """128 x 128 block quantization of a weight matrix (DeepSeek-V3 weights):
+    s[nb, kb] = max(amax(block) / 448, 1e-10), q = E4M3FN(clamp(w * (1/s)))
+    -- the rule of quant/kernel.cpp:46-107 with the group taken over a 2-D
+    block instead of a row. xb bf16 bits [N, K] (N, K multiples of `block`).
+    Returns (q uint8 [N, K], s float32 [N/block, K/block])."""
+    xb = np.ascontiguousarray(xb, dtype=np.uint16)
+    N, K = xb.shape
+    assert N % block == 0 and K % block == 0
+    nb, kb = N // block, K // block
+    blocks = xb.reshape(nb, block, kb, block).transpose(0, 2, 1, 3).reshape(nb * kb, block * block)
+    q, s = quant_rowwise(np.ascontiguousarray(blocks), None, "fp8")
+    q = q.reshape(nb, kb, block, block).transpose(0, 2, 1, 3).reshape(N, K)
+    return np.ascontiguousarray(q), s.reshape(nb, kb)
 
 
 def quant_static_fp8(xb: np.ndarray, scale: float) -> np.ndarray:

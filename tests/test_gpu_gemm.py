@@ -138,3 +138,64 @@ def test_gemm_mxfp4_baseline_sizes_sampled(orc, M):
     ref = orc.gemm_mxfp4_ref(Aq[rows], As[rows], Bq[cols], Bs[cols])
     assert_gemm_close(C[np.ix_(rows, cols)], ref, f"mxfp4 {M}x{N}x{K} sampled")
     assert np.isfinite(C).all()
+
+
+# ---------------------------------------------------------------------------
+# Block-scale FP8 GEMM (1x128 activation scales, 128x128 or 128x1 weight scales)
+# ---------------------------------------------------------------------------
+
+def blockscale_inputs(orc, M, N, K, seed, group_n):
+    xa = orc.randn_bf16((M, K), seed=seed)
+    A, sa = orc.quant_rowwise(xa, 128, "fp8")              # [M, K/128]
+    Np = (N + 127) // 128 * 128
+    xw = orc.randn_bf16((Np, K), seed=seed + 1, std=0.02)
+    if group_n == 128:
+        B, sbt = orc.quant_block_2d(xw)                    # sbt [N/128, K/128]
+        sb = np.ascontiguousarray(sbt.T)                   # [K/128, N/128]
+    else:
+        B, sbr = orc.quant_rowwise(xw, 128, "fp8")         # per (n, k-group)
+        sb = np.ascontiguousarray(sbr.T)                   # [K/128, N]
+    return A, np.ascontiguousarray(B[:N]), sa, (sb if group_n == 128 else np.ascontiguousarray(sb[:, :N]))
+
+
+def run_blockscale(A, B, sa, sb, group_n):
+    C = hkq.gemm_blockscale(dev_u8(A), dev_u8(B), dev_f32(sa), dev_f32(sb), group_n=group_n)
+    torch.cuda.synchronize()
+    return host_bf16_f32(C)
+
+
+@pytest.mark.parametrize("group_n", [128, 1])
+@pytest.mark.parametrize("M,N,K", [(128, 128, 256), (256, 256, 128), (333, 516, 384), (1, 256, 1024),
+                                   (600, 772, 2048)])
+def test_gemm_blockscale(orc, M, N, K, group_n):
+    require_gpu()
+    A, B, sa, sb = blockscale_inputs(orc, M, N, K, M + N + K, group_n)
+    C = run_blockscale(A, B, sa, sb, group_n)
+    assert_gemm_close(C, orc.gemm_blockscale_ref(A, B, sa, sb, 128, group_n), f"blockscale {M}x{N}x{K} gn{group_n}")
+
+
+def test_gemm_blockscale_uniform_scales_reduce_to_a8w8(orc):
+    """Scales constant over K groups: the block-scale GEMM equals the A8W8 GEMM
+    with the same per-row / per-column factors."""
+    require_gpu()
+    M, N, K = 256, 512, 1024
+    A, B, sa1, sb1 = a8w8_inputs(orc, M, N, K, seed=5)
+    sa = np.repeat(sa1[:, None], K // 128, axis=1).astype(np.float32)
+    sb = np.repeat(sb1[None, :], K // 128, axis=0).astype(np.float32)
+    C = run_blockscale(A, B, sa, sb, 1)
+    assert_gemm_close(C, orc.gemm_a8w8_ref(A, B, sa1, sb1), "blockscale uniform")
+
+
+@pytest.mark.parametrize("N,K", [(24576, 1536), (7168, 18432), (7168, 2048)])
+def test_gemm_blockscale_baseline_sizes_sampled(orc, N, K):
+    require_gpu()
+    M = 2048
+    A, B, sa, sb = blockscale_inputs(orc, M, N, K, K, 128)
+    C = run_blockscale(A, B, sa, sb, 128)
+    rng = np.random.default_rng(N)
+    rows = np.sort(rng.choice(M, 96, replace=False))
+    cols = np.sort(rng.choice(N, 96, replace=False))
+    sb_cols = sb[:, cols // 128]                           # per-column view of the sampled columns
+    ref = orc.gemm_blockscale_ref(A[rows], B[cols], sa[rows], sb_cols, 128, 1)
+    assert_gemm_close(C[np.ix_(rows, cols)], ref, f"blockscale {M}x{N}x{K} sampled")
+    assert np.isfinite(C).all()

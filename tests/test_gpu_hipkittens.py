@@ -97,3 +97,20 @@ def test_quant_moe_module(orc):
     qm.downcast_to_static_fp8(x, y, dev_f32(np.array([0.25], np.float32)), M, K)
     torch.cuda.synchronize()
     assert np.array_equal(host_u8(y), orc.quant_static_fp8(xb, 0.25))
+
+
+def test_blockscale_dispatch(orc):
+    require_gpu()
+    import hipkittens as hk
+
+    M, N, K = 128, 256, 512
+    A, sa = orc.quant_rowwise(orc.randn_bf16((M, K), seed=9), 128, "fp8")
+    B, sbr = orc.quant_rowwise(orc.randn_bf16((N, K), seed=10, std=0.02), 128, "fp8")
+    sb = np.ascontiguousarray(sbr.T)  # [K/128, N]: the reference test's per-column layout
+    Ad, Bd = dev_u8(A).view(torch.float8_e4m3fn), dev_u8(B).view(torch.float8_e4m3fn)
+    sad, sbd = dev_f32(sa), dev_f32(sb)
+    ref = hkq.gemm_blockscale(Ad, Bd, sad, sbd, group_n=1)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    hk.gemm.a8w8_blockscale.dispatch(Ad, Bd, C, sad, sbd)     # C third, as in the reference
+    torch.cuda.synchronize()
+    assert torch.equal(C, ref)

@@ -261,3 +261,22 @@ def test_moe_ref_matches_dense(orc, layout):
         e = assigns[t, k]
         ref = (x[t] @ w[e]) * xs[t] * ws[e] + bias[e]
         np.testing.assert_allclose(Y[slot], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_quant_block_2d(orc):
+    """Each 128x128 block quantized like one 16384-wide row (loop over blocks),
+    with known answers for a block of constant magnitude."""
+    xb = orc.randn_bf16((256, 384), seed=21, std=0.02)
+    xb[:128, 128:256] = orc.f32_to_bf16_bits(np.full((128, 128), -0.5, np.float32))
+    q, s = orc.quant_block_2d(xb)
+    assert q.shape == (256, 384) and s.shape == (2, 3)
+    x = orc.bf16_bits_to_f32(xb)
+    for nb in range(2):
+        for kb in range(3):
+            blk = x[nb * 128:(nb + 1) * 128, kb * 128:(kb + 1) * 128]
+            qn, sn = numpy_rowwise(blk.reshape(1, -1), 128 * 128, 448.0)
+            assert s[nb, kb] == sn[0, 0]
+            assert np.array_equal(q[nb * 128:(nb + 1) * 128, kb * 128:(kb + 1) * 128], qn.reshape(128, 128))
+    # constant block: amax 0.5 -> s = 0.5/448, every code is -448 (0xFE)
+    assert s[0, 1] == np.float32(np.float32(0.5) / np.float32(448.0))
+    assert np.all(q[:128, 128:256] == 0xFE)
