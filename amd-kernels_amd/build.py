@@ -40,7 +40,7 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-HIP_SOURCES = ["quant.hip", "gemm.hip", "gemm_blockscale.hip"]
+HIP_SOURCES = ["quant.hip", "gemm.hip", "gemm_blockscale.hip", "moe.hip"]
 CPP_SOURCES = ["hkq_error.cpp"]
 
 # pybind11 module name -> binding source (module names are the reference's)
@@ -51,6 +51,8 @@ MODULES = {
     "gemm_a8w8_per_token_scale_tk": "bind_gemm_a8w8_per_token_scale.cpp",
     "gemm_afp4wfp4_tk": "bind_gemm_afp4wfp4.cpp",
     "gemm_a8w8_blockscale_tk": "bind_gemm_a8w8_blockscale.cpp",
+    "moe_op_gemm_a8w8_tk": "bind_moe_op_gemm_a8w8.cpp",
+    "moe_op_gemm_a8w8_blockscale_tk": "bind_moe_op_gemm_a8w8_blockscale.cpp",
 }
 
 

@@ -185,7 +185,8 @@ __global__ __launch_bounds__(256, 1) void blockscale_gemm_kernel(const BlockScal
     const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
     store_tile_bf16<TM, TN>(
         acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, [](int) { return 1.0f; },
-        [](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); });
+        [](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); },
+        [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); });
 }
 
 template <bool GN1>

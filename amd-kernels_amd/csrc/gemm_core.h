@@ -132,11 +132,12 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 //   acc[i][j]: accumulator of n-tile i, m-tile j, D[n][m] layout
 //   (lane: m = lane & 31; register r: n = 8*(r/4) + 4*(lane/32) + r%4);
 //   row_scale(j) -> scale of the lane's m in m-tile j; col_scale4(i, g) -> the
-//   4 scales of n = i*32 + 8g + 4*(lane/32) + 0..3 (both relative to the wave).
-template <int TM, int TN, typename RowScale, typename ColScale4>
+//   4 scales of n = i*32 + 8g + 4*(lane/32) + 0..3 (both relative to the wave);
+//   col_bias4(i, g) -> the 4 values added after scaling (zero when unused).
+template <int TM, int TN, typename RowScale, typename ColScale4, typename ColBias4>
 __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uint8_t* smem, int wave, int lane,
                                                 uint16_t* C, int64_t ldc, int M, int N, int mw, int nw, bool c16,
-                                                RowScale row_scale, ColScale4 col_scale4) {
+                                                RowScale row_scale, ColScale4 col_scale4, ColBias4 col_bias4) {
     constexpr int PITCH = TN * 32 * 2 + 16;
     static_assert((TN * 32 * 2) % 256 == 0, "rows are whole 256-byte segments");
     HKQ_LDS uint8_t* ep = smem + wave * (TM * 32) * PITCH;
@@ -150,11 +151,14 @@ __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uin
         for (int g = 0; g < 4; ++g) {
             const int nl = i * 32 + 8 * g + 4 * khalf;
             const float4 cs = col_scale4(i, g);
+            const float4 cb = col_bias4(i, g);
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const float a = rs[j];
-                const uint32_t lo = f32_to_bf16(acc[i][j][4 * g + 0] * a * cs.x) | (f32_to_bf16(acc[i][j][4 * g + 1] * a * cs.y) << 16);
-                const uint32_t hi = f32_to_bf16(acc[i][j][4 * g + 2] * a * cs.z) | (f32_to_bf16(acc[i][j][4 * g + 3] * a * cs.w) << 16);
+                const uint32_t lo = f32_to_bf16(acc[i][j][4 * g + 0] * a * cs.x + cb.x) |
+                                    (f32_to_bf16(acc[i][j][4 * g + 1] * a * cs.y + cb.y) << 16);
+                const uint32_t hi = f32_to_bf16(acc[i][j][4 * g + 2] * a * cs.z + cb.z) |
+                                    (f32_to_bf16(acc[i][j][4 * g + 3] * a * cs.w + cb.w) << 16);
                 *reinterpret_cast<HKQ_LDS v2i*>(ep + (j * 32 + (lane & 31)) * PITCH + nl * 2) = v2i{(int)lo, (int)hi};
             }
         }

@@ -1,0 +1,199 @@
+// moe.hip -- A8W8 MoE grouped GEMM over OGS routing metadata
+// (moe-gemm/moe_op_gemm_a8w8/kernel.cpp:61-169 and the per-token x
+// per-channel case of moe_op_gemm_a8w8_blockscale/kernel.cpp:54-167, i.e.
+// group_k = K):
+//
+//   for each tile entry ExptData[pm] = e | (b << 16) (-1: skip), rows
+//   gm = b*128 + r < ExptHist[e], sorted index s = ExptOffs[e] + gm,
+//   token = GatherIndx[s] / topk (or s without a gather):
+//     Y[s, n] = bf16( (sum_k X[token, k] W[e, n, k]) * xs(token) * ws(e, n) + bias[e, n] )
+//
+// with xs per tensor (xs[0]) or per token (xs[token * xs_tok]) and ws per
+// expert (ws[e]) or per output channel group (ws[e * ws_e + (n / ws_gn) * ws_n]).
+// Output rows stay in expert-sorted order, as in the reference (no combine).
+//
+// Tiles are 128 rows (one OGS block) x 512 columns; the K loop is the shared
+// pipelined main loop with the A rows gathered per lane through the routing
+// index (rows of other tokens never enter LDS). Metadata is bounds-checked:
+// entries naming an expert >= E, rows past the gather index or tokens past T
+// read zero or are skipped instead of faulting.
+#include "gemm_mainloop.h"
+#include "hkq_host.h"
+
+namespace hkq {
+
+struct MoeParams {
+    const uint8_t* X;        // [T, sxm] E4M3FN, K contiguous
+    const uint8_t* W;        // expert e at W + e*swe, row n at + n*swn, K contiguous
+    uint16_t* Y;             // sorted row s at Y + s*sym
+    const float* xs;         // nullptr: 1
+    const float* ws;         // nullptr: 1
+    const float* bias;       // nullptr: 0; else bias[e * bias_e + n]
+    const int32_t* gather;   // nullptr: token = s
+    const int32_t* hist;
+    const int32_t* offs;
+    const int32_t* expt_data;
+    int T, E, N, K, topk, grid_m, y_rows, g_len;
+    int64_t sxm, swe, swn, sym;
+    int64_t xs_tok, ws_e, ws_n, ws_gn, bias_e;
+    int tiles_n, group_m, c16;
+};
+
+constexpr int MOE_BM = 128;  // rows per OGS routing block
+
+template <int WAVES_N, int TN, int NS>
+__global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoeParams p) {
+    constexpr int WAVES_M = 1, TM = 4;
+    using Cfg = DenseCfg<MODE_A8W8, WAVES_M, WAVES_N, TM, TN>;
+    constexpr int NW = Cfg::NW, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
+    static_assert(Cfg::BM == MOE_BM, "one tile row block per routing entry");
+
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
+    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wn = wave % WAVES_N;
+    const int khalf = lane >> 5;
+
+    int pm, tn;
+    tile_coords(blockIdx.x, p.grid_m, p.tiles_n, p.group_m, pm, tn);
+    const int ed = p.expt_data[pm];
+    if (ed == -1) return;
+    const int e = ed & 0xFFFF, blk = ed >> 16;
+    if (e >= p.E) return;
+    const int m_e = p.hist[e], start = p.offs[e];
+    const int row0 = blk * MOE_BM;
+    const int rows = min(m_e - row0, MOE_BM);
+    if (rows <= 0 || start < 0) return;
+    const int n0 = tn * BN;
+    const int rows_b = min(p.N - n0, BN);
+
+    // token of tile row r (-1 when the row is past the expert's rows or the metadata)
+    auto token_of = [&](int r) {
+        const int s = start + row0 + r;
+        if (r >= rows || s >= p.g_len) return -1;
+        const int t = p.gather ? p.gather[s] / p.topk : s;
+        return (t >= 0 && t < p.T) ? t : -1;
+    };
+
+    LoopSrc src;
+    src.a = p.X;
+    src.a_bytes = min((int64_t)p.T * p.sxm, (int64_t)0x7FFFFFFF);
+    src.b = p.W + (int64_t)e * p.swe + (int64_t)n0 * p.swn;
+    src.b_bytes = min((int64_t)rows_b * p.swn, (int64_t)0x7FFFFFFF);
+    src.as = src.bs = nullptr;
+    src.as_bytes = src.bs_bytes = src.lsa = src.lsb = 0;
+    src.KT = p.K / KT_BYTES;
+    uint32_t a_off[LA], b_off[LB];
+    const uint32_t chunk_off = (uint32_t)(load_chunk(lane) << 4);
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+        const int t = token_of((i * NW + wave) * ROWS_PER_LOAD + (lane >> 2));
+        a_off[i] = t < 0 ? OOB : (uint32_t)(t * p.sxm) + chunk_off;
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW>(i, wave, lane, p.swn);
+
+    v16f acc[TN][TM];
+    gemm_mainloop<MODE_A8W8, WAVES_M, WAVES_N, TM, TN, NS>(src, a_off, b_off, smem, lane, wave, acc);
+
+    const int s0 = start + row0;
+    const int nw = n0 + wn * TN * 32;
+    const int out_rows = min(rows, p.y_rows - s0);
+    store_tile_bf16<TM, TN>(
+        acc, smem, wave, lane, p.Y + (int64_t)s0 * p.sym, p.sym, out_rows, p.N, 0, nw, p.c16 != 0,
+        [&](int j) {
+            if (!p.xs) return 1.0f;
+            const int t = token_of(j * 32 + (lane & 31));
+            return t < 0 ? 0.0f : p.xs[(int64_t)t * p.xs_tok];
+        },
+        [&](int i, int g) {
+            const int n = nw + i * 32 + 8 * g + 4 * khalf;
+            float v[4] = {1.f, 1.f, 1.f, 1.f};
+            if (p.ws) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    v[c] = n + c < p.N ? p.ws[(int64_t)e * p.ws_e + (int64_t)((n + c) / p.ws_gn) * p.ws_n] : 0.f;
+            }
+            return make_float4(v[0], v[1], v[2], v[3]);
+        },
+        [&](int i, int g) {
+            const int n = nw + i * 32 + 8 * g + 4 * khalf;
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            if (p.bias) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = n + c < p.N ? p.bias[(int64_t)e * p.bias_e + n + c] : 0.f;
+            }
+            return make_float4(v[0], v[1], v[2], v[3]);
+        });
+}
+
+template <int WAVES_N, int TN, int NS>
+static int launch_moe(MoeParams& p, hipStream_t stream) {
+    using Cfg = DenseCfg<MODE_A8W8, 1, WAVES_N, 4, TN>;
+    constexpr int LDS = Cfg::lds_bytes(NS);
+    static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
+    auto kern = moe_gemm_kernel<WAVES_N, TN, NS>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
+        if (e != hipSuccess) {
+            set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", LDS, hipGetErrorString(e));
+            return (int)e;
+        }
+        attr_set = true;
+    }
+    p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
+    if (p.group_m <= 0) p.group_m = 8;
+    const int64_t nblk = (int64_t)p.grid_m * p.tiles_n;
+    if (nblk == 0) return 0;
+    kern<<<dim3((unsigned)nblk), 64 * WAVES_N, LDS, stream>>>(p);
+    return hkq_launch_status();
+}
+
+}  // namespace hkq
+
+using namespace hkq;
+
+extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* x_scale, int64_t xs_stride_tok,
+                            const float* w_scale, int64_t ws_stride_e, int64_t ws_stride_n, int64_t ws_group_n,
+                            const float* bias, int64_t bias_stride_e, const int32_t* gather, const int32_t* hist,
+                            const int32_t* offs, const int32_t* expt_data, int64_t T, int64_t E, int64_t N,
+                            int64_t K, int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we,
+                            int64_t stride_wn, int64_t stride_ym, int64_t y_rows, int64_t gather_len,
+                            hipStream_t stream) {
+    HKQ_CHECK_ARG(T >= 0 && E > 0 && E <= 0xFFFF && N >= 0 && K > 0 && grid_m >= 0 && topk > 0,
+                  "T, grid_m >= 0; 0 < E <= 65535; K, topk > 0");
+    HKQ_CHECK_ARG(T < (1 << 30) && N < (1 << 30) && K < (1 << 30) && grid_m < (1 << 30), "dimensions must be < 2^30");
+    HKQ_CHECK_ARG(K % 64 == 0, "K must be a multiple of 64");
+    HKQ_CHECK_ARG(N % 4 == 0, "N must be a multiple of 4");
+    HKQ_CHECK_ARG(stride_xm >= K && stride_xm % 16 == 0, "stride_xm must be >= K and a multiple of 16");
+    HKQ_CHECK_ARG(stride_wn >= K && stride_wn % 16 == 0, "stride_wn must be >= K and a multiple of 16 (W[e] is [N, K])");
+    HKQ_CHECK_ARG(stride_we >= 0 && stride_we % 16 == 0, "stride_we must be a non-negative multiple of 16");
+    HKQ_CHECK_ARG(stride_ym >= N && stride_ym % 4 == 0, "stride_ym must be >= N and a multiple of 4");
+    HKQ_CHECK_ARG(ws_group_n >= 1, "ws_group_n must be >= 1");
+    HKQ_CHECK_ARG(y_rows >= 0 && gather_len >= 0, "y_rows and gather_len must be >= 0");
+    HKQ_CHECK_ARG(hist && offs && expt_data, "routing metadata pointers must not be null");
+    HKQ_CHECK_ALIGN(X, 16);
+    HKQ_CHECK_ALIGN(W, 16);
+    HKQ_CHECK_ALIGN(Y, 8);
+    MoeParams p{};
+    p.X = static_cast<const uint8_t*>(X);
+    p.W = static_cast<const uint8_t*>(W);
+    p.Y = static_cast<uint16_t*>(Y);
+    p.xs = x_scale;
+    p.ws = w_scale;
+    p.bias = bias;
+    p.gather = gather;
+    p.hist = hist;
+    p.offs = offs;
+    p.expt_data = expt_data;
+    p.T = (int)T; p.E = (int)E; p.N = (int)N; p.K = (int)K; p.topk = (int)topk; p.grid_m = (int)grid_m;
+    p.y_rows = (int)y_rows;
+    p.g_len = gather ? (int)gather_len : (int)y_rows;
+    p.sxm = stride_xm; p.swe = stride_we; p.swn = stride_wn; p.sym = stride_ym;
+    p.xs_tok = xs_stride_tok; p.ws_e = ws_stride_e; p.ws_n = ws_stride_n; p.ws_gn = ws_group_n; p.bias_e = bias_stride_e;
+    p.c16 = (stride_ym % 8 == 0) && (reinterpret_cast<uintptr_t>(Y) % 16 == 0);
+    return launch_moe<4, 4, 3>(p, stream);
+}

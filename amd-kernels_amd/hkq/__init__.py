@@ -29,6 +29,8 @@ SIGNATURES = {
     "hkq_gemm_a8w8": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "hkq_gemm_mxfp4": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "hkq_gemm_blockscale": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "hkq_moe_a8w8": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]
+                     + [_I64] * 12 + [_P]),
 }
 
 
@@ -170,3 +172,31 @@ def gemm_blockscale(A, B, sa, sb, C=None, group_n: int = 128, stream=None):
     call("hkq_gemm_blockscale", _ptr(A), _ptr(B), _ptr(sa), _ptr(sb), _ptr(C), M, N, K, A.stride(0), B.stride(0),
          sa.stride(0), sb.stride(0), C.stride(0), group_n, _stream(stream))
     return C
+
+
+def moe_a8w8(X, W, hist, offs, expt_data, topk, gather=None, x_scale=None, w_scale=None, bias=None, Y=None,
+             y_rows=None, stream=None):
+    """OGS-routed A8W8 MoE GEMM. X [T, K] E4M3FN; W [E, N, K] E4M3FN (K contiguous);
+    x_scale: None, [1] (per tensor) or [T] (per token); w_scale: None, [E] (per
+    expert) or [E, N] (per channel); bias: None or fp32 [E, N]; int32 routing
+    tensors as in the reference (gather [T*topk], hist [E], offs [E],
+    expt_data [grid_m]). Returns Y bf16 [y_rows (default T*topk), N]."""
+    import torch
+
+    T, K = X.shape
+    E, N = W.shape[0], W.shape[1]
+    rows = T * topk if y_rows is None else y_rows
+    if Y is None:
+        Y = torch.zeros((rows, N), dtype=torch.bfloat16, device=X.device)
+    xs_tok = 0 if (x_scale is None or x_scale.numel() == 1) else 1
+    if w_scale is None or w_scale.numel() == E:
+        ws_e, ws_n = 1, 0
+    else:
+        ws_e, ws_n = N, 1
+    null = 0
+    call("hkq_moe_a8w8", _ptr(X), _ptr(W), _ptr(Y), _ptr(x_scale) if x_scale is not None else null, xs_tok,
+         _ptr(w_scale) if w_scale is not None else null, ws_e, ws_n, 1,
+         _ptr(bias) if bias is not None else null, N, _ptr(gather) if gather is not None else null,
+         _ptr(hist), _ptr(offs), _ptr(expt_data), T, E, N, K, expt_data.numel(), topk, X.stride(0), W.stride(0),
+         W.stride(1), Y.stride(0), rows, gather.numel() if gather is not None else 0, _stream(stream))
+    return Y

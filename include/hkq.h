@@ -106,6 +106,31 @@ int hkq_gemm_blockscale(const void* A, const void* B, const float* sa, const flo
                         int64_t K, int64_t lda, int64_t ldb, int64_t lsa, int64_t lsb, int64_t ldc, int64_t group_n,
                         hkq_stream_t stream);
 
+/* ---- MoE grouped GEMM over OGS routing metadata -------------------------- */
+
+/* For every routing tile ExptData[pm] = e | (b << 16) (-1: skipped), pm < grid_m,
+ * rows gm = b*128 + r < hist[e], sorted index s = offs[e] + gm,
+ * token = gather[s] / topk (gather == NULL: token = s):
+ *   Y[s, n] = bf16((sum_k X[token, k] * W[e, n, k]) * xs(token) * ws(e, n) + bias[e, n]).
+ * X E4M3FN [T, stride_xm], K contiguous; W E4M3FN with expert stride stride_we and
+ * row (n) stride stride_wn, K contiguous (the reference's [E, K, N] layout has to
+ * be passed transposed to [E, N, K]); Y bf16 rows of stride_ym, y_rows of them.
+ * xs: NULL (1), x_scale[0] (xs_stride_tok 0) or x_scale[token * xs_stride_tok].
+ * ws: NULL (1) or w_scale[e * ws_stride_e + (n / ws_group_n) * ws_stride_n]
+ *   (per expert: ws_stride_n 0; per channel: ws_stride_e N, ws_stride_n 1, ws_group_n 1).
+ * bias: NULL or fp32 bias[e * bias_stride_e + n]. K % 64 == 0, N % 4 == 0.
+ * Routing entries that name an expert >= E, rows past gather_len and tokens past
+ * T read zero or are skipped. Replaces moe_op_gemm_a8w8_tk.moe_a8w8
+ * (kernels/moe-gemm/moe_op_gemm_a8w8/kernel.cpp:194-271) and, for group_k == K,
+ * moe_op_gemm_a8w8_blockscale_tk.moe_a8w8_blockscale
+ * (kernels/moe-gemm/moe_op_gemm_a8w8_blockscale/kernel.cpp:192-280). */
+int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* x_scale, int64_t xs_stride_tok,
+                 const float* w_scale, int64_t ws_stride_e, int64_t ws_stride_n, int64_t ws_group_n, const float* bias,
+                 int64_t bias_stride_e, const int32_t* gather, const int32_t* hist, const int32_t* offs,
+                 const int32_t* expt_data, int64_t T, int64_t E, int64_t N, int64_t K, int64_t grid_m, int64_t topk,
+                 int64_t stride_xm, int64_t stride_we, int64_t stride_wn, int64_t stride_ym, int64_t y_rows,
+                 int64_t gather_len, hkq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,199 @@
+"""GPU parity of the A8W8 MoE grouped GEMM against the CPU oracle
+(oracle.moe_ref: tests/test_moe.py:733-753 restated, no % M wrap), through the
+C ABI and through the reference-named modules.
+
+Routing metadata follows the OGS contract (tests/test_moe.py:97-128) built by
+oracle.ogs_routing. Bar: the north-star GEMM tolerance on every routed row;
+rows that no tile covers stay untouched.
+"""
+import numpy as np
+import pytest
+import torch
+
+import hkq
+from gpu_util import assert_gemm_close, dev_f32, dev_u8, host_bf16_f32, require_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_i32(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).cuda()
+
+
+def make_problem(orc, T, E, topk, K, N, seed, skew=None):
+    rng = np.random.default_rng(seed)
+    if skew is None:
+        assigns = np.stack([rng.permutation(E)[:topk] for _ in range(T)])
+    else:
+        assigns = skew(rng, T, E, topk)
+    hist, offs, gather, ed = orc.ogs_routing(assigns, E, 128)
+    X, xs = orc.quant_rowwise(orc.randn_bf16((T, K), seed=seed + 1), None, "fp8")
+    Wf = orc.randn_bf16((E * N, K), seed=seed + 2, std=0.02)
+    Wq, ws = orc.quant_rowwise(Wf, None, "fp8")
+    return assigns, hist, offs, gather, ed, X, xs.reshape(-1), Wq.reshape(E, N, K), ws.reshape(E, N)
+
+
+def run_moe(X, W, hist, offs, gather, ed, topk, xs=None, ws=None, bias=None, y_rows=None):
+    Xd, Wd = dev_u8(X), dev_u8(W)
+    args = dict(gather=dev_i32(gather) if gather is not None else None,
+                x_scale=dev_f32(xs) if xs is not None else None,
+                w_scale=dev_f32(ws) if ws is not None else None,
+                bias=dev_f32(bias) if bias is not None else None)
+    Y = hkq.moe_a8w8(Xd, Wd, dev_i32(hist), dev_i32(offs), dev_i32(ed), topk, y_rows=y_rows, **args)
+    torch.cuda.synchronize()
+    return host_bf16_f32(Y)
+
+
+def check_rows(orc, Y, ref):
+    routed = ~np.isnan(ref).any(axis=1)
+    assert_gemm_close(Y[routed], ref[routed], "moe routed rows")
+    assert np.all(Y[~routed] == 0)  # output preallocated with zeros: untouched rows stay zero
+
+
+def test_moe_reference_setup(orc):
+    """The reference test's setup (tests/test_moe.py:689-764): T=64, E=8, top-2,
+    K=N=256, per-tensor activation scale, per-expert weight scale, bias."""
+    require_gpu()
+    T, E, topk, K, N = 64, 8, 2, 256, 256
+    _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, T, E, topk, K, N, 1)
+    rng = np.random.default_rng(2)
+    xs = np.array([0.01], np.float32)
+    ws = (rng.random(E) * 0.01).astype(np.float32)
+    bias = (rng.standard_normal((E, N)) * 0.1).astype(np.float32)
+    Y = run_moe(X, W, hist, offs, gather, ed, topk, xs, ws, bias)
+    ref = orc.moe_ref(X, W, xs, ws, bias, gather, hist, offs, ed, topk, 128, "enk")
+    check_rows(orc, Y, ref)
+
+
+@pytest.mark.parametrize("T,E,topk,K,N", [(300, 4, 2, 512, 520), (1, 8, 2, 256, 512), (1000, 8, 2, 1024, 1024),
+                                          (257, 3, 1, 384, 260)])
+def test_moe_per_token_per_channel(orc, T, E, topk, K, N):
+    require_gpu()
+    _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, T + N)
+    Y = run_moe(X, W, hist, offs, gather, ed, topk, xs, ws)
+    ref = orc.moe_ref(X, W, xs, ws, None, gather, hist, offs, ed, topk, 128, "enk")
+    check_rows(orc, Y, ref)
+
+
+def test_moe_skewed_routing_and_padding(orc):
+    """Most tokens on one expert (several 128-row blocks), two experts empty,
+    and -1 padding entries appended to ExptData."""
+    require_gpu()
+    T, E, topk, K, N = 600, 6, 2, 256, 512
+
+    def skew(rng, T, E, topk):
+        a = np.zeros((T, topk), np.int64)
+        a[:, 0] = 0
+        a[:, 1] = np.where(rng.random(T) < 0.8, 1, 3)
+        return a
+
+    _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 7, skew)
+    assert hist[2] == 0 and hist[4] == 0 and hist[0] == T
+    ed_pad = np.concatenate([ed, np.full(5, -1, np.int32)])
+    Y = run_moe(X, W, hist, offs, gather, ed_pad, topk, xs, ws)
+    ref = orc.moe_ref(X, W, xs, ws, None, gather, hist, offs, ed, topk, 128, "enk")
+    check_rows(orc, Y, ref)
+
+
+def test_moe_without_gather(orc):
+    """GatherIndx None: tile rows read X[start + gm] directly (pre-sorted X)."""
+    require_gpu()
+    E, K, N = 4, 256, 256
+    hist = np.array([130, 0, 70, 256], np.int32)
+    offs = np.concatenate([[0], np.cumsum(hist)[:-1]]).astype(np.int32)
+    ed = np.array([e | (b << 16) for e in range(E) for b in range((hist[e] + 127) // 128)], np.int32)
+    rows = int(hist.sum())
+    X, xs = orc.quant_rowwise(orc.randn_bf16((rows, K), seed=3), None, "fp8")
+    Wq, ws = orc.quant_rowwise(orc.randn_bf16((E * N, K), seed=4, std=0.02), None, "fp8")
+    W, ws = Wq.reshape(E, N, K), ws.reshape(E, N)
+    Y = run_moe(X, W, hist, offs, None, ed, 1, xs.reshape(-1), ws)
+    ident = np.arange(rows, dtype=np.int32)  # gather = s with topk 1 is the same thing
+    ref = orc.moe_ref(X, W, xs.reshape(-1), ws, None, ident, hist, offs, ed, 1, 128, "enk")
+    check_rows(orc, Y, ref)
+
+
+def test_moe_malformed_metadata_does_not_fault(orc):
+    """Entries naming an expert >= E, gather values past T and an offset past
+    the gather index are skipped or read zero; the valid tiles are exact."""
+    require_gpu()
+    T, E, topk, K, N = 128, 2, 1, 128, 256
+    _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 11)
+    bad = np.concatenate([ed, np.array([7 | (0 << 16), 1 | (9 << 16)], np.int32)])  # expert 7, block 9
+    g2 = gather.copy()
+    g2[5] = T * topk + 40  # token past T: the row reads zero
+    Y = run_moe(X, W, hist, offs, g2, bad, topk, xs, ws)
+    ref = orc.moe_ref(X, W, xs, ws, None, gather, hist, offs, ed, topk, 128, "enk")
+    ref[5] = 0.0
+    check_rows(orc, Y, ref)
+
+
+@pytest.mark.parametrize("K,N", [(4096, 28672), (14336, 4096)])
+def test_moe_mixtral_sampled(orc, K, N):
+    """BASELINE MoE shapes (Mixtral-8x7B: T=4096, E=8, top-2; gate/up K=4096,
+    N=28672 and down K=14336, N=4096), softmax top-2 routing from seeded logits;
+    weights quantized per channel on the GPU; sampled rows/columns vs the oracle."""
+    require_gpu()
+    T, E, topk = 4096, 8, 2
+    g = torch.Generator(device="cpu").manual_seed(K)
+    logits = torch.randn(T, E, generator=g)
+    assigns = torch.topk(torch.softmax(logits, -1), topk, dim=-1).indices.numpy()
+    hist, offs, gather, ed = orc.ogs_routing(assigns, E, 128)
+    xb = orc.randn_bf16((T, K), seed=K + 1)
+    X, xs = orc.quant_rowwise(xb, None, "fp8")
+    w = (torch.randn(E * N, K, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    Wq_d, ws_d = hkq.per_token_quant(w)
+    torch.cuda.synchronize()
+    del w
+    W = Wq_d.view(torch.uint8).cpu().numpy().reshape(E, N, K)
+    ws = ws_d.cpu().numpy().reshape(E, N)
+    Y = run_moe(X, W, hist, offs, gather, ed, topk, xs.reshape(-1), ws)
+    rng = np.random.default_rng(N)
+    srows = np.sort(rng.choice(T * topk, 64, replace=False))
+    cols = np.sort(rng.choice(N, 64, replace=False))
+    # sampled reference: expert of each sorted row from the offsets, token from the gather
+    e_of = np.searchsorted(offs, srows, side="right") - 1
+    tok = gather[srows] // topk
+    x = orc.e4m3_decode(X[tok]).astype(np.float64)
+    ref = np.empty((len(srows), len(cols)))
+    for i, (e, t) in enumerate(zip(e_of, tok)):
+        wcols = orc.e4m3_decode(W[e][cols]).astype(np.float64)
+        ref[i] = (wcols @ x[i]) * xs.reshape(-1)[t] * ws[e, cols]
+    assert_gemm_close(Y[np.ix_(srows, cols)], ref, f"moe K={K} N={N} sampled")
+    assert np.isfinite(Y).all()
+
+
+def test_moe_hipkittens_modules(orc):
+    """moe_op_gemm_a8w8_tk.moe_a8w8 and moe_op_gemm_a8w8_blockscale_tk with the
+    reference argument orders give the C-ABI bytes; [E, K, N] weights (the
+    reference test's layout, stride_wk != 1) are rejected with a clear error."""
+    require_gpu()
+    import hipkittens as hk
+
+    T, E, topk, K, N = 96, 4, 2, 256, 256
+    _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 21)
+    Xd, Wd = dev_u8(X).view(torch.float8_e4m3fn), dev_u8(W).view(torch.float8_e4m3fn)
+    hd, od, gd, edd = dev_i32(hist), dev_i32(offs), dev_i32(gather), dev_i32(ed)
+    xsd, wsd = dev_f32(np.array([0.02], np.float32)), dev_f32(ws[:, 0].copy())
+    bias = dev_f32(np.random.default_rng(1).standard_normal((E, N)).astype(np.float32))
+    ref = hkq.moe_a8w8(Xd, Wd, hd, od, edd, topk, gather=gd, x_scale=xsd, w_scale=wsd, bias=bias)
+    Y = torch.zeros((T * topk, N), dtype=torch.bfloat16, device="cuda")
+    grid_m, grid_n = len(ed), (N + 127) // 128
+    hk.moe.a8w8.moe_a8w8(Xd, Wd, Y, xsd, wsd, bias, gd, hd, od, edd, N, K, grid_m, grid_n, topk,
+                         N, 1, K, 1, N * K, 1, K, False, 0.0)
+    torch.cuda.synchronize()
+    assert torch.equal(Y, ref)
+    with pytest.raises(ValueError, match="K-contiguous"):
+        hk.moe.a8w8.moe_a8w8(Xd, Wd, Y, xsd, wsd, bias, gd, hd, od, edd, N, K, grid_m, grid_n, topk,
+                             N, 1, K, 1, N * K, N, 1, False, 0.0)
+    # blockscale module, group_k == K: per-token x per-channel scales (strided [T,1] / [E,1,N])
+    xs_t = dev_f32(xs.reshape(T, 1))
+    ws_c = dev_f32(ws.reshape(E, 1, N))
+    ref2 = hkq.moe_a8w8(Xd, Wd, hd, od, edd, topk, gather=gd, x_scale=dev_f32(xs.reshape(-1)), w_scale=dev_f32(ws))
+    Y2 = torch.zeros((T * topk, N), dtype=torch.bfloat16, device="cuda")
+    hk.moe.a8w8_blockscale.moe_a8w8_blockscale(Xd, Wd, Y2, xs_t, ws_c, None, gd, hd, od, edd, N, K, K, 1,
+                                                grid_m, grid_n, topk, N, 1, K, 1, N * K, 1, K, 1, 1, N, N, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(Y2, ref2)
+    with pytest.raises(ValueError, match="group_k"):
+        hk.moe.a8w8_blockscale.moe_a8w8_blockscale(Xd, Wd, Y2, xs_t, ws_c, None, gd, hd, od, edd, N, K, 128, 1,
+                                                    grid_m, grid_n, topk, N, 1, K, 1, N * K, 1, K, 1, 1, N, N, 1)
