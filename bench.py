@@ -36,6 +36,8 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 HEADLINE = dict(M=4096, N=14336, K=4096)
 MXFP4 = dict(M=4096, N=8192, K=8192)
+BLOCKSCALE = [(2048, 24576, 1536), (2048, 7168, 18432), (2048, 7168, 2048)]
+MOE = dict(T=4096, E=8, topk=2, hidden=4096, ffn=14336)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_a8w8_4096x14336x4096_pmc.txt")
 
 
@@ -51,6 +53,14 @@ def seeded_bf16(shape, std, seed):
 
 
 PREHEAT_S = 0.3  # untimed device load before the warmup steps
+
+
+def seeded_bf16_dev(shape, std, seed):
+    """Like seeded_bf16 but drawn with a seeded device generator (large weights)."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return (torch.randn(*shape, generator=g, device="cuda") * std).to(torch.bfloat16)
 
 
 def time_launches(fn, steps, warmup):
@@ -81,6 +91,24 @@ def time_launches(fn, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+def ogs_routing(assigns, num_experts, block_m=128):
+    """OGS routing metadata (int32 device tensors) from top-k assignments [T, topk]:
+    per-expert counts and exclusive offsets, the sorted-slot -> t*topk+k gather
+    index (token-major within an expert) and one e | (block << 16) entry per
+    block_m rows of each expert -- the contract of the reference's
+    tests/test_moe.py:97-128."""
+    import torch
+
+    flat = assigns.reshape(-1).to(torch.int64)
+    hist = torch.bincount(flat, minlength=num_experts).to(torch.int32)
+    offs = torch.zeros(num_experts, dtype=torch.int32)
+    offs[1:] = torch.cumsum(hist, 0)[:-1].to(torch.int32)
+    gather = torch.argsort(flat, stable=True).to(torch.int32)
+    tiles = [e | (b << 16) for e in range(num_experts) for b in range((int(hist[e]) + block_m - 1) // block_m)]
+    dev = lambda t: t.cuda()
+    return dev(hist), dev(offs), dev(gather), dev(torch.tensor(tiles, dtype=torch.int32))
+
+
 def read_traffic():
     """HBM bytes per launch from the committed PMC summary (null if absent)."""
     if not os.path.exists(TRAFFIC_FILE):
@@ -95,7 +123,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant", "copy"], default=None,
+    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant", "blockscale", "moe", "copy"], default=None,
                     help="run one kernel only (for profiling); prints no JSON line. 'copy' is a plain "
                          "1 GiB device copy used to calibrate the HBM byte counters")
     args = ap.parse_args()
@@ -154,6 +182,50 @@ def main():
         log("per-token quant 4096x4096")
         res["quant"] = time_launches(lambda: hkq.per_token_quant(xq, hkq.KIND_FP8, q, s), steps, warmup)
 
+    # ---- block-scale FP8 GEMM at the DeepSeek-V3 shapes (1x128 act / 128x128 weight scales) ----
+    bs_res = []
+    if args.only in (None, "blockscale"):
+        for (bm, bn, bk) in BLOCKSCALE:
+            xa = seeded_bf16((bm, bk), 1.0, 6)
+            xw = seeded_bf16((bn, bk), 0.02, 7)
+            qa_b, sa_b = hkq.group_quant(xa, 128)
+            qw_b, sw_rows = hkq.group_quant(xw, 128)  # per (n, k-group)
+            # 128x128 weight blocks: one scale per (k-group, n-block)
+            sb_b = sw_rows.view(bn // 128, 128, bk // 128).amax(dim=1).t().contiguous()
+            Cb = torch.empty((bm, bn), dtype=torch.bfloat16, device="cuda")
+            torch.cuda.synchronize()
+            log(f"blockscale {bm}x{bn}x{bk}")
+            ms_b = time_launches(lambda: hkq.gemm_blockscale(qa_b, qw_b, sa_b, sb_b, Cb, 128), steps, warmup)
+            bs_res.append({"M": bm, "N": bn, "K": bk, "ms": round(ms_b, 5),
+                           "tflops": round(2.0 * bm * bn * bk / (ms_b * 1e-3) / 1e12, 2)})
+            del xa, xw, qa_b, qw_b
+        res["blockscale"] = sum(r["ms"] for r in bs_res)
+
+    # ---- A8W8 MoE grouped GEMM, Mixtral-8x7B (E=8, top-2, 4096 tokens, 4096 -> 14336 gate/up, down) ----
+    moe_res = []
+    if args.only in (None, "moe"):
+        T, E, topk, hidden, ffn = MOE["T"], MOE["E"], MOE["topk"], MOE["hidden"], MOE["ffn"]
+        g = torch.Generator(device="cpu").manual_seed(8)
+        assigns = torch.topk(torch.softmax(torch.randn(T, E, generator=g), -1), topk, dim=-1).indices
+        hist, offs, gather, expt_data = ogs_routing(assigns, E, 128)
+        xm = seeded_bf16((T, hidden), 1.0, 9)
+        qx, sx = hkq.per_token_quant(xm)
+        for name, (nn, kk) in (("gate_up", (2 * ffn, hidden)), ("down", (hidden, ffn))):
+            wq = torch.empty((E, nn, kk), dtype=torch.float8_e4m3fn, device="cuda")
+            ws_m = torch.empty((E, nn), dtype=torch.float32, device="cuda")
+            for e in range(E):  # per-channel quantization of each expert's [N, K] weights
+                hkq.per_token_quant(seeded_bf16_dev((nn, kk), 0.02, 10 + e), hkq.KIND_FP8, wq[e], ws_m[e])
+            xin, sin = (qx, sx) if kk == hidden else hkq.per_token_quant(seeded_bf16_dev((T, kk), 1.0, 20))
+            Ym = torch.empty((T * topk, nn), dtype=torch.bfloat16, device="cuda")
+            torch.cuda.synchronize()
+            log(f"moe {name} N={nn} K={kk}")
+            ms_m = time_launches(lambda: hkq.moe_a8w8(xin, wq, hist, offs, expt_data, topk, gather=gather,
+                                                      x_scale=sin, w_scale=ws_m, Y=Ym), steps, warmup)
+            moe_res.append({"proj": name, "N": nn, "K": kk, "ms": round(ms_m, 5),
+                            "tflops": round(2.0 * T * topk * nn * kk / (ms_m * 1e-3) / 1e12, 2)})
+            del wq
+        res["moe"] = sum(r["ms"] for r in moe_res)
+
     if args.only is not None:
         log(json.dumps({k: round(v * 1e3, 2) for k, v in res.items()}) + "  (us per launch)")
         return
@@ -197,6 +269,8 @@ def main():
                   "pct_fp4_peak": round(100 * tflops4 / PEAK_FP4_TFLOPS, 2)},
         "quant_per_token_fp8": {"M": 4096, "K": 4096, "GB/s": round(quant_gbs, 1), "ms": round(res["quant"], 5),
                                 "pct_hbm_peak": round(100 * quant_gbs / PEAK_HBM_GBS, 2)},
+        "blockscale": bs_res,
+        "moe_mixtral": moe_res,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_FP8_TFLOPS, 4), "traffic": read_traffic()},
         "cpu_baseline": cpu,
