@@ -26,27 +26,33 @@ struct DenseParams {
     int64_t ldc;          // elements
     int64_t lsa, lsb;     // MXFP4 scale row strides (bytes)
     int tiles_m, tiles_n, group_m;
+    int n_whole;          // workgroups [0, n_whole) compute whole tiles 0 .. n_whole-1
+    int n_split;          // tiles n_whole .. n_whole+n_split-1 are computed as two M halves
     int c16;              // rows of C are 16-byte aligned (ldc % 8 == 0, C 16-byte aligned)
 };
 
-template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int NS>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(const DenseParams p) {
+// Tile geometry of the dense GEMMs: 256 x 256 tiles computed by 4 waves of
+// 128 x 128 (whole tiles) or 64 x 128 (M halves of a tile, 128 x 256).
+constexpr int DENSE_WAVES_M = 2, DENSE_WAVES_N = 2, DENSE_TM = 4, DENSE_TN = 4, DENSE_NS = 4;
+constexpr int DENSE_BM = DENSE_WAVES_M * DENSE_TM * 32, DENSE_BN = DENSE_WAVES_N * DENSE_TN * 32;
+
+// One (TM*64) x 256 block of C: rows [m0, m0 + TM*64) of tile (tm, tn) of the
+// 256 x 256 tile grid, starting `half` * 128 rows into the tile.
+template <int MODE, int TM>
+__device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn, int half, HKQ_LDS uint8_t* smem) {
+    constexpr int WAVES_M = DENSE_WAVES_M, WAVES_N = DENSE_WAVES_N, TN = DENSE_TN, NS = DENSE_NS;
     using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN>;
     constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
     constexpr bool FP4 = Cfg::FP4;
-
-    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
-    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int khalf = lane >> 5;
 
-    int tm, tn;
-    tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tm * DENSE_BM + half * BM, n0 = tn * BN;
     const int rows_a = min(p.M - m0, BM), rows_b = min(p.N - n0, BN);
+    if (rows_a <= 0) return;  // the M half below the last row (uniform per workgroup)
 
     LoopSrc src;
     src.a = p.A + (int64_t)m0 * p.lda;
@@ -86,12 +92,38 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void dense_gemm_kernel(c
         [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); });
 }
 
-template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int NS>
+// Workgroup u < n_whole computes tile u. When the last round of tiles would
+// leave at least half of the CUs idle, its tiles are instead computed as M
+// halves by twice as many workgroups: unit v = u - n_whole (XCD v & 7, as the
+// dispatcher assigns workgroups round-robin) computes half (v >> 3) & 1 of tile
+// n_whole + 8 * (v >> 4) + (v & 7), so both halves of a tile run on one XCD.
+// Tile ids then go through tile_coords' XCD-aware order.
+template <int MODE>
+__global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_gemm_kernel(const DenseParams p) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
+    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+    const int u = blockIdx.x;
+    int tm, tn;
+    if (u < p.n_whole) {
+        tile_coords(u, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+        dense_block<MODE, DENSE_TM>(p, tm, tn, 0, smem);
+        return;
+    }
+    const int v = u - p.n_whole;
+    const int t = 8 * (v >> 4) + (v & 7);
+    if (t >= p.n_split) return;
+    tile_coords(p.n_whole + t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    dense_block<MODE, DENSE_TM / 2>(p, tm, tn, (v >> 3) & 1, smem);
+}
+
+template <int MODE>
 static int launch_dense(DenseParams& p, hipStream_t stream) {
-    using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN>;
-    constexpr int LDS = Cfg::lds_bytes(NS);
+    using Whole = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM, DENSE_TN>;
+    using Half = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM / 2, DENSE_TN>;
+    constexpr int LDS = Whole::lds_bytes(DENSE_NS) > Half::lds_bytes(DENSE_NS) ? Whole::lds_bytes(DENSE_NS)
+                                                                                : Half::lds_bytes(DENSE_NS);
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
-    auto kern = dense_gemm_kernel<MODE, WAVES_M, WAVES_N, TM, TN, NS>;
+    auto kern = dense_gemm_kernel<MODE>;
     static bool attr_set = false;  // per instantiation; the attribute is per-process
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
@@ -101,13 +133,21 @@ static int launch_dense(DenseParams& p, hipStream_t stream) {
         }
         attr_set = true;
     }
-    p.tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
-    p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
+    p.tiles_m = (p.M + DENSE_BM - 1) / DENSE_BM;
+    p.tiles_n = (p.N + DENSE_BN - 1) / DENSE_BN;
     if (p.group_m <= 0) p.group_m = 8;
     p.c16 = (p.ldc % 8 == 0) && (reinterpret_cast<uintptr_t>(p.C) % 16 == 0);
-    const int64_t nblk = (int64_t)p.tiles_m * p.tiles_n;
-    if (nblk == 0) return 0;
-    kern<<<dim3((unsigned)nblk), 64 * WAVES_M * WAVES_N, LDS, stream>>>(p);
+    const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+    if (tiles == 0) return 0;
+    // Split the last round into M halves when it would fill at most half of the
+    // CUs and the tiles have rows in both halves.
+    const int ncu = cu_count();
+    const int64_t last = ncu > 0 ? tiles % ncu : 0;
+    int64_t split = (last > 0 && 2 * last <= ncu && p.M > DENSE_BM / 2) ? last : 0;
+    p.n_whole = (int)(tiles - split);
+    p.n_split = (int)split;
+    const int64_t nblk = p.n_whole + 2 * ((split + 7) / 8 * 8);
+    kern<<<dim3((unsigned)nblk), 64 * DENSE_WAVES_M * DENSE_WAVES_N, LDS, stream>>>(p);
     return hkq_launch_status();
 }
 
@@ -143,7 +183,7 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
     p.sb = sb;
     p.M = (int)M; p.N = (int)N; p.K = (int)K; p.kbytes = (int)K;
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
-    return launch_dense<MODE_A8W8, 2, 2, 4, 4, 4>(p, stream);
+    return launch_dense<MODE_A8W8>(p, stream);
 }
 
 int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
@@ -167,7 +207,7 @@ int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs,
     p.M = (int)M; p.N = (int)N; p.K = (int)K; p.kbytes = (int)(K / 2);
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
     p.lsa = ldsa; p.lsb = ldsb;
-    return launch_dense<MODE_MXFP4, 2, 2, 4, 4, 4>(p, stream);
+    return launch_dense<MODE_MXFP4>(p, stream);
 }
 
 }  // extern "C"

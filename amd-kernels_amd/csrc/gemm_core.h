@@ -155,10 +155,8 @@ __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uin
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const float a = rs[j];
-                const uint32_t lo = f32_to_bf16(acc[i][j][4 * g + 0] * a * cs.x + cb.x) |
-                                    (f32_to_bf16(acc[i][j][4 * g + 1] * a * cs.y + cb.y) << 16);
-                const uint32_t hi = f32_to_bf16(acc[i][j][4 * g + 2] * a * cs.z + cb.z) |
-                                    (f32_to_bf16(acc[i][j][4 * g + 3] * a * cs.w + cb.w) << 16);
+                const uint32_t lo = pk_bf16(acc[i][j][4 * g + 0] * a * cs.x + cb.x, acc[i][j][4 * g + 1] * a * cs.y + cb.y);
+                const uint32_t hi = pk_bf16(acc[i][j][4 * g + 2] * a * cs.z + cb.z, acc[i][j][4 * g + 3] * a * cs.w + cb.w);
                 *reinterpret_cast<HKQ_LDS v2i*>(ep + (j * 32 + (lane & 31)) * PITCH + nl * 2) = v2i{(int)lo, (int)hi};
             }
         }

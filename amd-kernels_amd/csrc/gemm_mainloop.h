@@ -16,9 +16,12 @@ struct DenseCfg {
     static constexpr int SUB = FP4 ? 2 : 1;                    // 64-deep MFMA K-steps per K-tile
     static constexpr int LA = BM / ROWS_PER_LOAD / NW, LB = BN / ROWS_PER_LOAD / NW;
     // FP4: the K-tile's e8m0 scales (4 bytes per row: 128 values) ride in LDS
-    // after the data; one 4-byte LDS-direct load per lane covers 64 rows.
+    // after the data; one 4-byte LDS-direct load per lane covers 64 rows. When
+    // a tile has fewer 64-row groups than waves, waves load the same group
+    // (identical bytes to the same place) so that every wave issues the same
+    // number of loads per K-tile, which the vmcnt accounting relies on.
     static constexpr int SCA = FP4 ? BM * 4 : 0, SCB = FP4 ? BN * 4 : 0;
-    static constexpr int LSA = FP4 ? BM / 64 / NW : 0, LSB = FP4 ? BN / 64 / NW : 0;
+    static constexpr int LSA = FP4 ? (BM / 64 + NW - 1) / NW : 0, LSB = FP4 ? (BN / 64 + NW - 1) / NW : 0;
     static constexpr int STAGE = (BM + BN) * KT_BYTES + SCA + SCB;
     static constexpr int NLD = LA + LB + LSA + LSB;           // LDS-direct loads per K-tile
     static constexpr int PARTS = FP4 ? 1 : 2;                 // ds_read_b128 per fragment
@@ -31,8 +34,9 @@ struct DenseCfg {
     static constexpr int EP_BYTES = NW * TM * 32 * EP_PITCH;
     static constexpr int lds_bytes(int ns) { return ns * STAGE > EP_BYTES ? ns * STAGE : EP_BYTES; }
     static_assert(LA >= 1 && LB >= 1, "tile too small for the wave count");
-    static_assert(!FP4 || (LSA >= 1 && LSB >= 1), "scale tile too small for the wave count");
-    static_assert(NRD <= NMF, "phase A pairs at most one fragment read with each MFMA");
+    static_assert(!FP4 || ((BM / 64) % NW == 0 || NW % (BM / 64) == 0), "A scale groups vs waves");
+    static_assert(!FP4 || ((BN / 64) % NW == 0 || NW % (BN / 64) == 0), "B scale groups vs waves");
+    static_assert(SUB == 1 || NRD <= NMF, "phase A pairs at most one fragment read with each MFMA");
     static_assert((TN * 32 * 2) % 256 == 0, "epilogue rows are whole 256-byte segments");
 };
 
@@ -97,15 +101,15 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const uint32_t
             lds_load16(src.b + kb, live ? (uint32_t)(src.b_bytes - kb) : 0u, st + BM * KT_BYTES + (i * NW + wave) * 1024,
                        b_off[i]);
         } else if (idx < LA + LB + LSA) {
-            const int i = idx - LA - LB;
-            const uint32_t off = (uint32_t)(((i * NW + wave) * 64 + lane) * src.lsa);
+            const int g = ((idx - LA - LB) * NW + wave) % (BM / 64);
+            const uint32_t off = (uint32_t)((g * 64 + lane) * src.lsa);
             lds_load4(src.as + kt * 4, live ? (uint32_t)(src.as_bytes - kt * 4) : 0u,
-                      st + (BM + BN) * KT_BYTES + (i * NW + wave) * 256, off);
+                      st + (BM + BN) * KT_BYTES + g * 256, off);
         } else {
-            const int i = idx - LA - LB - LSA;
-            const uint32_t off = (uint32_t)(((i * NW + wave) * 64 + lane) * src.lsb);
+            const int g = ((idx - LA - LB - LSA) * NW + wave) % (BN / 64);
+            const uint32_t off = (uint32_t)((g * 64 + lane) * src.lsb);
             lds_load4(src.bs + kt * 4, live ? (uint32_t)(src.bs_bytes - kt * 4) : 0u,
-                      st + (BM + BN) * KT_BYTES + SCA + (i * NW + wave) * 256, off);
+                      st + (BM + BN) * KT_BYTES + SCA + g * 256, off);
         }
     };
 
@@ -118,32 +122,36 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const uint32_t
     };
     // Fragment read slot idx of K-step ks, A and B tiles interleaved
     // (a0 b0 a1 b1 ...) so the first MFMAs' operands arrive first; slots past
-    // TM (A) or TN (B) tiles are empty. FP8: logical chunks 2*khalf + part;
-    // FP4: chunk 2*ks + khalf.
+    // TM (A) or TN (B) tiles are empty. Lane half h reads logical chunks 2h and
+    // 2h + 1: FP8 both in one step (parts 0, 1), FP4 one per step (ks 0, 1).
+    // The order in which K enters the sum is the same for A and B, so the
+    // product is unchanged; for FP4 it puts the lane's two scale bytes side by
+    // side (bytes 2h, 2h + 1 of the row's scale word).
     auto read_piece = [&](int stage, int ks, Frags& f, int idx) {
         const HKQ_LDS uint8_t* At = smem + stage * STAGE;
         const int t = idx / (2 * PARTS), isb = (idx / PARTS) & 1, part = idx % PARTS;
         if ((isb ? TN : TM) <= t) return;
         const int row = (isb ? brow : arow) + t * 32;
-        const int chunk = FP4 ? ks * 2 + khalf : khalf * 2 + part;
+        const int chunk = khalf * 2 + (FP4 ? ks : part);
         const v4i v = lds_read16(At + (isb ? BM * KT_BYTES : 0) + lds_swz(row, chunk));
         if (isb) f.b[t][part] = v;
         else f.a[t][part] = v;
     };
-    // MXFP4: per m/n-tile the 4 scale bytes of the K-tile for the lane's row,
-    // shifted so bytes 0 and 2 are the lane's K-block of steps 0 and 1.
+    // MXFP4: per m/n-tile the two e8m0 bytes of the lane's row and K blocks
+    // (2h, 2h + 1) as one 16-bit LDS read: byte 0 scales step 0, byte 1 step 1.
+    // The value goes to the MFMA unchanged (no VALU work waits on the read).
     struct Scales {
         int a[TM], b[TN];
     };
     auto read_scale = [&](int stage, Scales& s, int idx) {
         if constexpr (FP4) {
-            const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KT_BYTES;
+            const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KT_BYTES + khalf * 2;
             const bool isa = idx < TM;
             const int t = isa ? idx : idx - TM;
-            const uint32_t w = *reinterpret_cast<const HKQ_LDS uint32_t*>(
+            const int w = *reinterpret_cast<const HKQ_LDS uint16_t*>(
                 sca + (isa ? (arow + t * 32) * 4 : SCA + (brow + t * 32) * 4));
-            if (isa) s.a[t] = (int)(w >> (khalf * 8));
-            else s.b[t] = (int)(w >> (khalf * 8));
+            if (isa) s.a[t] = w;
+            else s.b[t] = w;
         }
     };
 
@@ -164,7 +172,7 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const uint32_t
             a = v8i{f.a[j][0][0], f.a[j][0][1], f.a[j][0][2], f.a[j][0][3], 0, 0, 0, 0};
         }
         if constexpr (FP4) {
-            if (ks & 1) acc[i][j] = mfma_sel<true, 2, 2>(b, a, acc[i][j], s.b[i], s.a[j]);
+            if (ks & 1) acc[i][j] = mfma_sel<true, 1, 1>(b, a, acc[i][j], s.b[i], s.a[j]);
             else acc[i][j] = mfma_sel<true, 0, 0>(b, a, acc[i][j], s.b[i], s.a[j]);
         } else {
             acc[i][j] = mfma_sel<false, 0, 0>(b, a, acc[i][j], 127, 127);

@@ -31,6 +31,15 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
     return u >> 16;
 }
 
+// Two fp32 -> two bf16 (round to nearest even) packed as lo | hi << 16: one
+// v_cvt_pk_bf16_f32. Finite values round exactly as f32_to_bf16; NaN comes out
+// as a quiet NaN (payload bits not guaranteed).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+
 // IEEE maxNum / minNum (a NaN operand is ignored): v_max_f32 / v_min_f32 under
 // the default IEEE mode, the semantics of fmaxf/fminf.
 __device__ __forceinline__ float max_num(float a, float b) { return __builtin_fmaxf(a, b); }

@@ -10,6 +10,7 @@
 namespace hkq {
 void set_error(const char* fmt, ...);
 int fail_arg(const char* file, int line, const char* msg);
+int cu_count();
 }  // namespace hkq
 
 #define HKQ_CHECK_ARG(cond, msg)                                     \
