@@ -21,7 +21,7 @@ struct DenseParams {
     const void* sa;
     const void* sb;
     int M, N, K;          // K in elements
-    int kbytes;           // K in bytes per row of A/B (a multiple of KT_BYTES)
+    int kbytes;           // K in bytes per row of A/B (a multiple of the K-tile)
     int64_t lda, ldb;     // bytes
     int64_t ldc;          // elements
     int64_t lsa, lsb;     // MXFP4 scale row strides (bytes)
@@ -32,16 +32,21 @@ struct DenseParams {
 };
 
 // Tile geometry of the dense GEMMs: 256 x 256 tiles computed by 4 waves of
-// 128 x 128 (whole tiles) or 64 x 128 (M halves of a tile, 128 x 256).
-constexpr int DENSE_WAVES_M = 2, DENSE_WAVES_N = 2, DENSE_TM = 4, DENSE_TN = 4, DENSE_NS = 4;
+// 128 x 128 (whole tiles) or 64 x 128 (M halves of a tile, 128 x 256). K-tiles
+// are 128 bytes per row (whole 128-byte lines per row and load: half the
+// cache-line requests of 64-byte K-tiles) in a 2-stage ring when K allows,
+// else 64 bytes in a 4-stage ring.
+constexpr int DENSE_WAVES_M = 2, DENSE_WAVES_N = 2, DENSE_TM = 4, DENSE_TN = 4;
 constexpr int DENSE_BM = DENSE_WAVES_M * DENSE_TM * 32, DENSE_BN = DENSE_WAVES_N * DENSE_TN * 32;
+template <int KTB>
+constexpr int dense_ns() { return KTB == 128 ? 2 : 4; }
 
 // One (TM*64) x 256 block of C: rows [m0, m0 + TM*64) of tile (tm, tn) of the
 // 256 x 256 tile grid, starting `half` * 128 rows into the tile.
-template <int MODE, int TM>
+template <int MODE, int TM, int KTB>
 __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn, int half, HKQ_LDS uint8_t* smem) {
-    constexpr int WAVES_M = DENSE_WAVES_M, WAVES_N = DENSE_WAVES_N, TN = DENSE_TN, NS = DENSE_NS;
-    using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN>;
+    constexpr int WAVES_M = DENSE_WAVES_M, WAVES_N = DENSE_WAVES_N, TN = DENSE_TN, NS = dense_ns<KTB>();
+    using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>;
     constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
     constexpr bool FP4 = Cfg::FP4;
 
@@ -65,15 +70,15 @@ __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn
     src.bs_bytes = FP4 ? min((int64_t)rows_b * p.lsb, (int64_t)0x7FFFFFFF) : 0;
     src.lsa = p.lsa;
     src.lsb = p.lsb;
-    src.KT = p.kbytes / KT_BYTES;
+    src.KT = p.kbytes / KTB;
     uint32_t a_off[LA], b_off[LB];
 #pragma unroll
-    for (int i = 0; i < LA; ++i) a_off[i] = dense_row_off<NW>(i, wave, lane, p.lda);
+    for (int i = 0; i < LA; ++i) a_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.lda);
 #pragma unroll
-    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW>(i, wave, lane, p.ldb);
+    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.ldb);
 
     v16f acc[TN][TM];
-    gemm_mainloop<MODE, WAVES_M, WAVES_N, TM, TN, NS>(src, a_off, b_off, smem, lane, wave, acc);
+    gemm_mainloop<MODE, WAVES_M, WAVES_N, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
 
     // Epilogue (scales of A8W8 applied in registers; MXFP4 has none left)
     const float* sa = static_cast<const float*>(p.sa);
@@ -98,7 +103,7 @@ __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn
 // dispatcher assigns workgroups round-robin) computes half (v >> 3) & 1 of tile
 // n_whole + 8 * (v >> 4) + (v & 7), so both halves of a tile run on one XCD.
 // Tile ids then go through tile_coords' XCD-aware order.
-template <int MODE>
+template <int MODE, int KTB>
 __global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_gemm_kernel(const DenseParams p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
@@ -106,24 +111,24 @@ __global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_g
     int tm, tn;
     if (u < p.n_whole) {
         tile_coords(u, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-        dense_block<MODE, DENSE_TM>(p, tm, tn, 0, smem);
+        dense_block<MODE, DENSE_TM, KTB>(p, tm, tn, 0, smem);
         return;
     }
     const int v = u - p.n_whole;
     const int t = 8 * (v >> 4) + (v & 7);
     if (t >= p.n_split) return;
     tile_coords(p.n_whole + t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-    dense_block<MODE, DENSE_TM / 2>(p, tm, tn, (v >> 3) & 1, smem);
+    dense_block<MODE, DENSE_TM / 2, KTB>(p, tm, tn, (v >> 3) & 1, smem);
 }
 
-template <int MODE>
-static int launch_dense(DenseParams& p, hipStream_t stream) {
-    using Whole = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM, DENSE_TN>;
-    using Half = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM / 2, DENSE_TN>;
-    constexpr int LDS = Whole::lds_bytes(DENSE_NS) > Half::lds_bytes(DENSE_NS) ? Whole::lds_bytes(DENSE_NS)
-                                                                                : Half::lds_bytes(DENSE_NS);
+template <int MODE, int KTB>
+static int launch_dense_ktb(DenseParams& p, hipStream_t stream) {
+    constexpr int NS = dense_ns<KTB>();
+    using Whole = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM, DENSE_TN, KTB>;
+    using Half = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM / 2, DENSE_TN, KTB>;
+    constexpr int LDS = Whole::lds_bytes(NS) > Half::lds_bytes(NS) ? Whole::lds_bytes(NS) : Half::lds_bytes(NS);
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
-    auto kern = dense_gemm_kernel<MODE>;
+    auto kern = dense_gemm_kernel<MODE, KTB>;
     static bool attr_set = false;  // per instantiation; the attribute is per-process
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
@@ -149,6 +154,13 @@ static int launch_dense(DenseParams& p, hipStream_t stream) {
     const int64_t nblk = p.n_whole + 2 * ((split + 7) / 8 * 8);
     kern<<<dim3((unsigned)nblk), 64 * DENSE_WAVES_M * DENSE_WAVES_N, LDS, stream>>>(p);
     return hkq_launch_status();
+}
+
+// 128-byte K-tiles need whole 128-byte K-tiles in every row: a partial last
+// K-tile would read the next row's bytes instead of zeros.
+template <int MODE>
+static int launch_dense(DenseParams& p, hipStream_t stream) {
+    return p.kbytes % 128 == 0 ? launch_dense_ktb<MODE, 128>(p, stream) : launch_dense_ktb<MODE, 64>(p, stream);
 }
 
 }  // namespace hkq

@@ -6,20 +6,22 @@
 // Shared design
 //   * one workgroup per BM x BN tile of C; waves own (TM*32) x (TN*32) sub-tiles
 //     held in TM*TN 32x32 fp32 accumulators of v_mfma_scale_f32_32x32x64_f8f6f4;
-//   * K is consumed in K-tiles of 64 bytes per row (64 FP8 or 128 FP4 values),
-//     staged HBM -> LDS with buffer_load_dwordx4 ... lds (no VGPR staging) into
-//     NS ring stages, so a tile is requested NS-1 K-tiles before it is needed;
+//   * K is consumed in K-tiles of KTB = 64 or 128 bytes per row (FP8: 64 or
+//     128 values, FP4: twice that), staged HBM -> LDS with buffer_load_dwordx4
+//     ... lds (no VGPR staging) into NS ring stages, so a tile is requested
+//     NS-1 K-tiles before it is needed;
 //   * the MFMA "A" operand is the B tile (rows n) and the MFMA "B" operand is
 //     the A tile (rows m): a lane's accumulator registers then hold four
 //     consecutive n of one m.
 //
-// LDS K-tile layout: row r of 64 bytes = 4 chunks of 16 bytes; logical chunk c
-// lives at physical chunk c ^ ((r >> 2) & 3). A fragment read has 16 lanes on
-// 16 consecutive rows with one logical chunk; their 16-byte slots
-// (r & 3) * 4 + (c ^ ((r >> 2) & 3)) modulo 256 bytes are all distinct, so the
-// read is free of bank conflicts on the 64 x 4-byte LDS banks. A wave-wide
-// LDS-direct load writes 1 KB = 16 rows contiguously; lane l carries row l/4,
-// physical chunk l%4, hence logical chunk (l & 3) ^ ((l >> 4) & 3).
+// LDS K-tile layout (KTB = 64 or 128 bytes of K per row, KTB/16 chunks of 16
+// bytes): logical chunk c of row r lives at physical chunk c ^ f(r) with
+// f(r) = (r >> 2) & 3 (KTB 64) or (r >> 1) & 7 (KTB 128). A fragment read has
+// 16 lanes on 16 consecutive rows with one logical chunk; their 16-byte slots
+// modulo 256 bytes are then all distinct, so the read is free of bank
+// conflicts on the 64 x 4-byte LDS banks. A wave-wide LDS-direct load writes
+// 1 KB = 1024/KTB rows contiguously: lane l carries row l / (KTB/16) of the
+// load and physical chunk l % (KTB/16).
 //
 // Operand fragment layout of the 32x32x64 MFMA (verified on gfx950): lane l
 // supplies row (l % 32) and the 32 K-values [32*(l/32), 32*(l/32)+32) of the
@@ -32,16 +34,23 @@
 
 namespace hkq {
 
-constexpr int KT_BYTES = 64;           // K-tile width in bytes per row
-constexpr int ROWS_PER_LOAD = 16;      // rows written by one wave-wide 16-byte LDS-direct load
 constexpr uint32_t OOB = 0x80000000u;  // buffer offset that always reads zero (num_records <= 2^31 - 1)
 
 enum GemmMode { MODE_A8W8 = 0, MODE_BLOCKSCALE = 1, MODE_MXFP4 = 2 };
 
-__device__ __forceinline__ int lds_swz(int r, int c) { return r * KT_BYTES + ((c ^ ((r >> 2) & 3)) << 4); }
-
-// Logical chunk carried by `lane` in a wave-wide LDS-direct load.
-__device__ __forceinline__ int load_chunk(int lane) { return (lane & 3) ^ ((lane >> 4) & 3); }
+template <int KTB>
+struct KTile {
+    static_assert(KTB == 64 || KTB == 128, "K-tile rows of 64 or 128 bytes");
+    static constexpr int CHUNKS = KTB / 16;
+    static constexpr int ROWS_PER_LOAD = 1024 / KTB;  // rows written by one wave-wide 16-byte LDS-direct load
+    __device__ static __forceinline__ int phys(int r, int c) {
+        return KTB == 64 ? (c ^ ((r >> 2) & 3)) : (c ^ ((r >> 1) & 7));
+    }
+    // LDS byte offset of logical chunk c of row r
+    __device__ static __forceinline__ int swz(int r, int c) { return r * KTB + (phys(r, c) << 4); }
+    // Logical chunk carried by `lane` of a load whose lane writes row r of the tile.
+    __device__ static __forceinline__ int load_chunk(int lane, int r) { return phys(r, lane % CHUNKS); }
+};
 
 // One LDS-direct load of `size` (4 or 16) bytes per lane from [base, base + bytes)
 // at byte offset `off` to `dst` + lane * size (buffer_load ... lds: M0 holds

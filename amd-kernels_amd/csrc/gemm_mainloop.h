@@ -8,23 +8,28 @@
 
 namespace hkq {
 
-template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN>
+template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int KTB>
 struct DenseCfg {
+    using KT = KTile<KTB>;
     static constexpr int NW = WAVES_M * WAVES_N;
     static constexpr int BM = WAVES_M * TM * 32, BN = WAVES_N * TN * 32;
     static constexpr bool FP4 = MODE == MODE_MXFP4;
-    static constexpr int SUB = FP4 ? 2 : 1;                    // 64-deep MFMA K-steps per K-tile
-    static constexpr int LA = BM / ROWS_PER_LOAD / NW, LB = BN / ROWS_PER_LOAD / NW;
-    // FP4: the K-tile's e8m0 scales (4 bytes per row: 128 values) ride in LDS
-    // after the data; one 4-byte LDS-direct load per lane covers 64 rows. When
-    // a tile has fewer 64-row groups than waves, waves load the same group
-    // (identical bytes to the same place) so that every wave issues the same
-    // number of loads per K-tile, which the vmcnt accounting relies on.
-    static constexpr int SCA = FP4 ? BM * 4 : 0, SCB = FP4 ? BN * 4 : 0;
-    static constexpr int LSA = FP4 ? (BM / 64 + NW - 1) / NW : 0, LSB = FP4 ? (BN / 64 + NW - 1) / NW : 0;
-    static constexpr int STAGE = (BM + BN) * KT_BYTES + SCA + SCB;
-    static constexpr int NLD = LA + LB + LSA + LSB;           // LDS-direct loads per K-tile
-    static constexpr int PARTS = FP4 ? 1 : 2;                 // ds_read_b128 per fragment
+    static constexpr int SUB = (KTB / 64) * (FP4 ? 2 : 1);   // 64-deep MFMA K-steps per K-tile
+    static constexpr int RPL = KT::ROWS_PER_LOAD;
+    static constexpr int LA = BM / RPL / NW, LB = BN / RPL / NW;
+    // FP4: the K-tile's e8m0 scales (KTB/16 bytes per row: one per 32 values)
+    // ride in LDS after the data, as KTB/64 planes of one 4-byte word per row;
+    // one 4-byte LDS-direct load per lane covers 64 rows of one plane. When a
+    // tile has fewer (plane, 64-row group) pairs than waves, waves load the same
+    // pair (identical bytes to the same place) so that every wave issues the
+    // same number of loads per K-tile, which the vmcnt accounting relies on.
+    static constexpr int PLANES = KTB / 64;
+    static constexpr int SCA = FP4 ? BM * 4 * PLANES : 0, SCB = FP4 ? BN * 4 * PLANES : 0;
+    static constexpr int GA = FP4 ? BM / 64 * PLANES : 1, GB = FP4 ? BN / 64 * PLANES : 1;
+    static constexpr int LSA = FP4 ? (GA + NW - 1) / NW : 0, LSB = FP4 ? (GB + NW - 1) / NW : 0;
+    static constexpr int STAGE = (BM + BN) * KTB + SCA + SCB;
+    static constexpr int NLD = LA + LB + LSA + LSB;           // LDS-direct loads per wave per K-tile
+    static constexpr int PARTS = FP4 ? 1 : 2;                 // ds_read_b128 per fragment per K-step
     static constexpr int NRD = 2 * PARTS * (TM > TN ? TM : TN);  // fragment read slots per K-step
     static constexpr int NSC = FP4 ? TM + TN : 0;             // scale reads per K-tile
     static constexpr int NMF = TM * TN, HALF = NMF / 2;       // MFMAs per K-step
@@ -34,9 +39,8 @@ struct DenseCfg {
     static constexpr int EP_BYTES = NW * TM * 32 * EP_PITCH;
     static constexpr int lds_bytes(int ns) { return ns * STAGE > EP_BYTES ? ns * STAGE : EP_BYTES; }
     static_assert(LA >= 1 && LB >= 1, "tile too small for the wave count");
-    static_assert(!FP4 || ((BM / 64) % NW == 0 || NW % (BM / 64) == 0), "A scale groups vs waves");
-    static_assert(!FP4 || ((BN / 64) % NW == 0 || NW % (BN / 64) == 0), "B scale groups vs waves");
-    static_assert(SUB == 1 || NRD <= NMF, "phase A pairs at most one fragment read with each MFMA");
+    static_assert(!FP4 || (GA % NW == 0 || NW % GA == 0), "A scale groups vs waves");
+    static_assert(!FP4 || (GB % NW == 0 || NW % GB == 0), "B scale groups vs waves");
     static_assert((TN * 32 * 2) % 256 == 0, "epilogue rows are whole 256-byte segments");
 };
 
@@ -48,14 +52,16 @@ struct LoopSrc {
     int64_t a_bytes, b_bytes;
     const uint8_t *as, *bs;
     int64_t as_bytes, bs_bytes, lsa, lsb;
-    int KT;  // K-tiles of KT_BYTES
+    int KT;  // K-tiles
 };
 
-// Row offset (bytes, excluding the K position) of LDS-direct load instruction i
-// of `wave` for a plain row-major operand: rows (i*NW + wave)*16 + lane/4.
-template <int NW>
+// Byte offset (row and logical chunk, excluding the K position) of LDS-direct
+// load instruction i of `wave` for a plain row-major operand.
+template <int NW, int KTB>
 __device__ __forceinline__ uint32_t dense_row_off(int i, int wave, int lane, int64_t ld) {
-    return (uint32_t)(((i * NW + wave) * ROWS_PER_LOAD + (lane >> 2)) * ld) + (uint32_t)(load_chunk(lane) << 4);
+    using KT = KTile<KTB>;
+    const int r = (i * NW + wave) * KT::ROWS_PER_LOAD + lane / KT::CHUNKS;
+    return (uint32_t)(r * ld) + (uint32_t)(KT::load_chunk(lane, r) << 4);
 }
 
 // Pipeline (per wave; one barrier per K-tile, NS ring stages):
@@ -69,47 +75,65 @@ __device__ __forceinline__ uint32_t dense_row_off(int i, int wave, int lane, int
 //   issue together with the reads of K-tile kt+1's first step. sched_barrier
 //   between chunks keeps this order through the compiler's scheduler.
 //
+// Fragments: lane half h (lane / 32) owns logical chunks [h * KTB/32, (h+1) *
+// KTB/32) of every row; K-step ks uses chunks h*KTB/32 + 2ks + {0, 1} (FP8) or
+// h*KTB/32 + ks (FP4). The order in which K enters the sums is the same for A
+// and B, so the products are unchanged; for FP4 it makes the lane's e8m0 bytes
+// of one K-tile contiguous (2 bytes for KTB 64, one 4-byte plane for KTB 128),
+// and the MFMA's opsel picks byte ks.
+//
 // a_off/b_off: per load instruction, the byte offset of the lane's row and
 // logical chunk inside src.a / src.b (OOB for rows that must read zero).
 // On return acc holds the tile's fp32 sums and every wave is past a vmcnt(0)
 // barrier, so the caller may reuse the LDS.
-template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int NS>
-__device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const uint32_t (&a_off)[DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN>::LA],
-                                              const uint32_t (&b_off)[DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN>::LB],
+template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int KTB, int NS>
+__device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
+                                              const uint32_t (&a_off)[DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>::LA],
+                                              const uint32_t (&b_off)[DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>::LB],
                                               HKQ_LDS uint8_t* smem, int lane, int wave, v16f (&acc)[TN][TM]) {
-    using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN>;
+    using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>;
+    using KT = KTile<KTB>;
     constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN, SUB = Cfg::SUB;
     constexpr int LA = Cfg::LA, LB = Cfg::LB, LSA = Cfg::LSA, SCA = Cfg::SCA, STAGE = Cfg::STAGE;
+    constexpr int GA = Cfg::GA, GB = Cfg::GB;
     constexpr int NLD = Cfg::NLD, PARTS = Cfg::PARTS, NRD = Cfg::NRD, NSC = Cfg::NSC;
     constexpr int NMF = Cfg::NMF, HALF = Cfg::HALF;
     constexpr bool FP4 = Cfg::FP4;
-    static_assert(NS >= 2 && (NS - 1) * NLD <= 63, "vmcnt budget");
+    constexpr int HCH = KTB / 32;  // logical chunks per lane half
+    static_assert(NS >= 2 && (NS - 1) * NLD <= 63, "ring depth and vmcnt budget");
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-    const int KT = src.KT;
+    const int KTN = src.KT;
 
     // Load instruction idx of K-tile kt into `stage`: A rows, B rows, then (FP4)
-    // the 4-byte scale word of row (i*NW + wave)*64 + lane. For kt >= KT the
-    // buffers are empty, so the loads read zero (the loop needs no branches).
+    // scale words: group g covers plane g % PLANES of rows (g / PLANES)*64 + lane.
+    // For kt >= KTN the buffers are empty, so the loads read zero (the loop needs
+    // no branches).
     auto load_piece = [&](int kt, int stage, int idx) {
-        const int kb = kt * KT_BYTES;
-        const bool live = kt < KT;
+        const int kb = kt * KTB;
+        const bool live = kt < KTN;
         HKQ_LDS uint8_t* st = smem + stage * STAGE;
         if (idx < LA) {
             lds_load16(src.a + kb, live ? (uint32_t)(src.a_bytes - kb) : 0u, st + (idx * NW + wave) * 1024, a_off[idx]);
         } else if (idx < LA + LB) {
             const int i = idx - LA;
-            lds_load16(src.b + kb, live ? (uint32_t)(src.b_bytes - kb) : 0u, st + BM * KT_BYTES + (i * NW + wave) * 1024,
+            lds_load16(src.b + kb, live ? (uint32_t)(src.b_bytes - kb) : 0u, st + BM * KTB + (i * NW + wave) * 1024,
                        b_off[i]);
         } else if (idx < LA + LB + LSA) {
-            const int g = ((idx - LA - LB) * NW + wave) % (BM / 64);
-            const uint32_t off = (uint32_t)((g * 64 + lane) * src.lsa);
-            lds_load4(src.as + kt * 4, live ? (uint32_t)(src.as_bytes - kt * 4) : 0u,
-                      st + (BM + BN) * KT_BYTES + g * 256, off);
+            constexpr int PL = Cfg::PLANES;
+            const int g = ((idx - LA - LB) * NW + wave) % GA;
+            const int plane = g % PL, rows = g / PL;
+            const int kb4 = kt * 4 * PL + plane * 4;
+            const uint32_t off = (uint32_t)((rows * 64 + lane) * src.lsa);
+            lds_load4(src.as + kb4, live ? (uint32_t)(src.as_bytes - kb4) : 0u,
+                      st + (BM + BN) * KTB + plane * BM * 4 + rows * 256, off);
         } else {
-            const int g = ((idx - LA - LB - LSA) * NW + wave) % (BN / 64);
-            const uint32_t off = (uint32_t)((g * 64 + lane) * src.lsb);
-            lds_load4(src.bs + kt * 4, live ? (uint32_t)(src.bs_bytes - kt * 4) : 0u,
-                      st + (BM + BN) * KT_BYTES + SCA + g * 256, off);
+            constexpr int PL = Cfg::PLANES;
+            const int g = ((idx - LA - LB - LSA) * NW + wave) % GB;
+            const int plane = g % PL, rows = g / PL;
+            const int kb4 = kt * 4 * PL + plane * 4;
+            const uint32_t off = (uint32_t)((rows * 64 + lane) * src.lsb);
+            lds_load4(src.bs + kb4, live ? (uint32_t)(src.bs_bytes - kb4) : 0u,
+                      st + (BM + BN) * KTB + SCA + plane * BN * 4 + rows * 256, off);
         }
     };
 
@@ -122,34 +146,33 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const uint32_t
     };
     // Fragment read slot idx of K-step ks, A and B tiles interleaved
     // (a0 b0 a1 b1 ...) so the first MFMAs' operands arrive first; slots past
-    // TM (A) or TN (B) tiles are empty. Lane half h reads logical chunks 2h and
-    // 2h + 1: FP8 both in one step (parts 0, 1), FP4 one per step (ks 0, 1).
-    // The order in which K enters the sum is the same for A and B, so the
-    // product is unchanged; for FP4 it puts the lane's two scale bytes side by
-    // side (bytes 2h, 2h + 1 of the row's scale word).
+    // TM (A) or TN (B) tiles are empty.
     auto read_piece = [&](int stage, int ks, Frags& f, int idx) {
         const HKQ_LDS uint8_t* At = smem + stage * STAGE;
         const int t = idx / (2 * PARTS), isb = (idx / PARTS) & 1, part = idx % PARTS;
         if ((isb ? TN : TM) <= t) return;
         const int row = (isb ? brow : arow) + t * 32;
-        const int chunk = khalf * 2 + (FP4 ? ks : part);
-        const v4i v = lds_read16(At + (isb ? BM * KT_BYTES : 0) + lds_swz(row, chunk));
+        const int chunk = khalf * HCH + (FP4 ? ks : 2 * ks + part);
+        const v4i v = lds_read16(At + (isb ? BM * KTB : 0) + KT::swz(row, chunk));
         if (isb) f.b[t][part] = v;
         else f.a[t][part] = v;
     };
-    // MXFP4: per m/n-tile the two e8m0 bytes of the lane's row and K blocks
-    // (2h, 2h + 1) as one 16-bit LDS read: byte 0 scales step 0, byte 1 step 1.
-    // The value goes to the MFMA unchanged (no VALU work waits on the read).
+    // MXFP4: per m/n-tile the lane's e8m0 bytes of the K-tile, byte ks for
+    // K-step ks: 16 bits at byte 2h of the row's word (KTB 64) or the row's word
+    // of plane h (KTB 128). The value goes to the MFMA unchanged.
     struct Scales {
         int a[TM], b[TN];
     };
     auto read_scale = [&](int stage, Scales& s, int idx) {
         if constexpr (FP4) {
-            const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KT_BYTES + khalf * 2;
+            const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KTB;
             const bool isa = idx < TM;
             const int t = isa ? idx : idx - TM;
-            const int w = *reinterpret_cast<const HKQ_LDS uint16_t*>(
-                sca + (isa ? (arow + t * 32) * 4 : SCA + (brow + t * 32) * 4));
+            const int row = (isa ? arow : brow) + t * 32;
+            const HKQ_LDS uint8_t* base = isa ? sca : sca + SCA;
+            int w;
+            if constexpr (KTB == 64) w = *reinterpret_cast<const HKQ_LDS uint16_t*>(base + row * 4 + khalf * 2);
+            else w = *reinterpret_cast<const HKQ_LDS int*>(base + khalf * (isa ? BM : BN) * 4 + row * 4);
             if (isa) s.a[t] = w;
             else s.b[t] = w;
         }
@@ -172,8 +195,12 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const uint32_t
             a = v8i{f.a[j][0][0], f.a[j][0][1], f.a[j][0][2], f.a[j][0][3], 0, 0, 0, 0};
         }
         if constexpr (FP4) {
-            if (ks & 1) acc[i][j] = mfma_sel<true, 1, 1>(b, a, acc[i][j], s.b[i], s.a[j]);
-            else acc[i][j] = mfma_sel<true, 0, 0>(b, a, acc[i][j], s.b[i], s.a[j]);
+            switch (ks & 3) {
+                case 0: acc[i][j] = mfma_sel<true, 0, 0>(b, a, acc[i][j], s.b[i], s.a[j]); break;
+                case 1: acc[i][j] = mfma_sel<true, 1, 1>(b, a, acc[i][j], s.b[i], s.a[j]); break;
+                case 2: acc[i][j] = mfma_sel<true, 2, 2>(b, a, acc[i][j], s.b[i], s.a[j]); break;
+                default: acc[i][j] = mfma_sel<true, 3, 3>(b, a, acc[i][j], s.b[i], s.a[j]); break;
+            }
         } else {
             acc[i][j] = mfma_sel<false, 0, 0>(b, a, acc[i][j], 127, 127);
         }
@@ -195,13 +222,16 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const uint32_t
     auto ktile = [&](int kt, int stage, auto parity) {
         constexpr int P = decltype(parity)::value;
         const int next_stage = stage + 1 == NS ? 0 : stage + 1;
-        // phase A: steps 0 .. SUB-2, one fragment read of the next step per MFMA
+        // phase A: steps 0 .. SUB-2, the fragment reads of the next step spread
+        // over the MFMAs
 #pragma unroll
         for (int ks = 0; ks + 1 < SUB; ++ks) {
 #pragma unroll
             for (int c = 0; c < NMF; ++c) {
                 mfma_one(F[(P * SUB + ks) & 1], ks, S[P], c);
-                if (c < NRD) read_piece(stage, ks + 1, F[(P * SUB + ks + 1) & 1], c);
+#pragma unroll
+                for (int i = c * NRD / NMF; i < (c + 1) * NRD / NMF; ++i)
+                    read_piece(stage, ks + 1, F[(P * SUB + ks + 1) & 1], i);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -229,13 +259,13 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const uint32_t
 
     int stage = 0;
     int kt = 0;
-    for (; kt + 1 < KT; kt += 2) {
+    for (; kt + 1 < KTN; kt += 2) {
         ktile(kt, stage, std::integral_constant<int, 0>{});
         stage = stage + 1 == NS ? 0 : stage + 1;
         ktile(kt + 1, stage, std::integral_constant<int, 1>{});
         stage = stage + 1 == NS ? 0 : stage + 1;
     }
-    if (kt < KT) ktile(kt, stage, std::integral_constant<int, 0>{});
+    if (kt < KTN) ktile(kt, stage, std::integral_constant<int, 0>{});
     mfma_drain();
     tile_barrier<0>();  // every wave is done with the stages and no load is in flight
 }

@@ -5,7 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/hkq.h"
+#include "hkq.h"
 
 namespace hkq {
 void set_error(const char* fmt, ...);

@@ -44,7 +44,8 @@ constexpr int MOE_BM = 128;  // rows per OGS routing block
 template <int WAVES_N, int TN, int NS>
 __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoeParams p) {
     constexpr int WAVES_M = 1, TM = 4;
-    using Cfg = DenseCfg<MODE_A8W8, WAVES_M, WAVES_N, TM, TN>;
+    constexpr int KTB = 64;
+    using Cfg = DenseCfg<MODE_A8W8, WAVES_M, WAVES_N, TM, TN, KTB>;
     constexpr int NW = Cfg::NW, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
     static_assert(Cfg::BM == MOE_BM, "one tile row block per routing entry");
 
@@ -84,19 +85,19 @@ __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoePara
     src.b_bytes = min((int64_t)rows_b * p.swn, (int64_t)0x7FFFFFFF);
     src.as = src.bs = nullptr;
     src.as_bytes = src.bs_bytes = src.lsa = src.lsb = 0;
-    src.KT = p.K / KT_BYTES;
+    src.KT = p.K / KTB;
     uint32_t a_off[LA], b_off[LB];
-    const uint32_t chunk_off = (uint32_t)(load_chunk(lane) << 4);
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
-        const int t = token_of((i * NW + wave) * ROWS_PER_LOAD + (lane >> 2));
-        a_off[i] = t < 0 ? OOB : (uint32_t)(t * p.sxm) + chunk_off;
+        const int r = (i * NW + wave) * Cfg::RPL + lane / Cfg::KT::CHUNKS;
+        const int t = token_of(r);
+        a_off[i] = t < 0 ? OOB : (uint32_t)(t * p.sxm) + (uint32_t)(Cfg::KT::load_chunk(lane, r) << 4);
     }
 #pragma unroll
-    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW>(i, wave, lane, p.swn);
+    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.swn);
 
     v16f acc[TN][TM];
-    gemm_mainloop<MODE_A8W8, WAVES_M, WAVES_N, TM, TN, NS>(src, a_off, b_off, smem, lane, wave, acc);
+    gemm_mainloop<MODE_A8W8, WAVES_M, WAVES_N, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
 
     const int s0 = start + row0;
     const int nw = n0 + wn * TN * 32;
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoePara
 
 template <int WAVES_N, int TN, int NS>
 static int launch_moe(MoeParams& p, hipStream_t stream) {
-    using Cfg = DenseCfg<MODE_A8W8, 1, WAVES_N, 4, TN>;
+    using Cfg = DenseCfg<MODE_A8W8, 1, WAVES_N, 4, TN, 64>;
     constexpr int LDS = Cfg::lds_bytes(NS);
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
     auto kern = moe_gemm_kernel<WAVES_N, TN, NS>;
