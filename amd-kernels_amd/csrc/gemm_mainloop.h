@@ -67,13 +67,13 @@ __device__ __forceinline__ uint32_t dense_row_off(int i, int wave, int lane, int
 // Pipeline (per wave; one barrier per K-tile, NS ring stages):
 //   K-tile kt lives in stage kt % NS. Its SUB K-steps run their MFMAs with
 //   double-buffered fragments: the LDS reads of the next step are issued between
-//   the MFMAs of the current one. In the last step, half of the MFMAs are issued
-//   before the barrier (the matrix pipe stays busy while the waves meet); the
-//   barrier (a) waits until K-tile kt+1 is resident (at most NS-2 K-tiles of
-//   loads still in flight) and (b) retires every wave's reads of stage kt % NS,
-//   which is then refilled with K-tile kt+NS while the other half of the MFMAs
-//   issue together with the reads of K-tile kt+1's first step. sched_barrier
-//   between chunks keeps this order through the compiler's scheduler.
+//   the MFMAs of the current one. Before the last step's MFMAs (SUB > 1) or
+//   half-way through them (SUB == 1) a barrier (a) waits until K-tile kt+1 is
+//   resident (at most NS-2 K-tiles of loads still in flight) and (b) retires
+//   every wave's reads of stage kt % NS, which is then refilled with K-tile
+//   kt+NS while the remaining MFMAs issue together with the reads of K-tile
+//   kt+1's first step. sched_barrier between chunks keeps this order through
+//   the compiler's scheduler.
 //
 // Fragments: lane half h (lane / 32) owns logical chunks [h * KTB/32, (h+1) *
 // KTB/32) of every row; K-step ks uses chunks h*KTB/32 + 2ks + {0, 1} (FP8) or
@@ -235,24 +235,29 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        // phase B: last step
+        // phase B: last step. Its fragments were read during the previous step,
+        // so with SUB > 1 the stage is retired as soon as phase A's reads are
+        // done and the barrier comes first (the refill of the stage then spreads
+        // over all of the step's MFMAs); with SUB == 1 half of the MFMAs are
+        // issued before the barrier, keeping the matrix pipe busy meanwhile.
         constexpr int LAST = SUB - 1;
+        constexpr int PRE = SUB > 1 ? 0 : HALF, POST = NMF - PRE;
         const Frags& cur = F[(P * SUB + LAST) & 1];
         Frags& nxt = F[(P * SUB + LAST + 1) & 1];
 #pragma unroll
-        for (int c = 0; c < HALF; ++c) mfma_one(cur, LAST, S[P], c);
+        for (int c = 0; c < PRE; ++c) mfma_one(cur, LAST, S[P], c);
         __builtin_amdgcn_sched_barrier(0);
         tile_barrier<(NS - 2) * NLD>();  // K-tile kt+1 resident; stage kt % NS retired
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int c = 0; c < HALF; ++c) {
-            mfma_one(cur, LAST, S[P], HALF + c);
+        for (int c = 0; c < POST; ++c) {
+            mfma_one(cur, LAST, S[P], PRE + c);
 #pragma unroll
-            for (int i = c * NLD / HALF; i < (c + 1) * NLD / HALF; ++i) load_piece(kt + NS, stage, i);
+            for (int i = c * NLD / POST; i < (c + 1) * NLD / POST; ++i) load_piece(kt + NS, stage, i);
 #pragma unroll
-            for (int i = c * NRD / HALF; i < (c + 1) * NRD / HALF; ++i) read_piece(next_stage, 0, nxt, i);
+            for (int i = c * NRD / POST; i < (c + 1) * NRD / POST; ++i) read_piece(next_stage, 0, nxt, i);
 #pragma unroll
-            for (int i = c * NSC / HALF; i < (c + 1) * NSC / HALF; ++i) read_scale(next_stage, S[P ^ 1], i);
+            for (int i = c * NSC / POST; i < (c + 1) * NSC / POST; ++i) read_scale(next_stage, S[P ^ 1], i);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
