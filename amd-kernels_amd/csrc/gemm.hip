@@ -41,6 +41,19 @@ constexpr int DENSE_BM = DENSE_WAVES_M * DENSE_TM * 32, DENSE_BN = DENSE_WAVES_N
 template <int KTB>
 constexpr int dense_ns() { return KTB == 128 ? 2 : 4; }
 
+// LDS of a dense workgroup: the K-tile ring / epilogue staging (the larger of
+// the whole- and half-tile configurations), then (A8W8) the tile's row and
+// column scales, 256 floats each, fetched at the start of the tile.
+template <int MODE, int KTB>
+constexpr int dense_ring_lds() {
+    using Whole = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM, DENSE_TN, KTB>;
+    using Half = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM / 2, DENSE_TN, KTB>;
+    constexpr int NS = dense_ns<KTB>();
+    return Whole::lds_bytes(NS) > Half::lds_bytes(NS) ? Whole::lds_bytes(NS) : Half::lds_bytes(NS);
+}
+template <int MODE, int KTB>
+constexpr int dense_lds() { return dense_ring_lds<MODE, KTB>() + (MODE == MODE_A8W8 ? 2 * DENSE_BM * 4 : 0); }
+
 // One (TM*64) x 256 block of C: rows [m0, m0 + TM*64) of tile (tm, tn) of the
 // 256 x 256 tile grid, starting `half` * 128 rows into the tile.
 template <int MODE, int TM, int KTB>
@@ -77,22 +90,36 @@ __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn
 #pragma unroll
     for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.ldb);
 
+    // A8W8: the tile's row and column scales go to LDS while the K loop runs
+    // (rows past M / columns past N read zero); each wave loads 64 of each.
+    // These loads are older than the K-tile loads, so the loop's vmcnt waits
+    // cover them, and its final vmcnt(0) barrier makes them visible.
+    HKQ_LDS uint8_t* scl = smem + dense_ring_lds<MODE, KTB>();
+    if constexpr (MODE == MODE_A8W8) {
+        const float* sa = static_cast<const float*>(p.sa) + m0;
+        const float* sb = static_cast<const float*>(p.sb) + n0;
+        lds_load4(sa, (uint32_t)rows_a * 4u, scl + wave * 256, (uint32_t)(wave * 64 + lane) * 4u);
+        lds_load4(sb, (uint32_t)rows_b * 4u, scl + DENSE_BM * 4 + wave * 256, (uint32_t)(wave * 64 + lane) * 4u);
+    }
+
     v16f acc[TN][TM];
     gemm_mainloop<MODE, WAVES_M, WAVES_N, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
 
     // Epilogue (scales of A8W8 applied in registers; MXFP4 has none left)
-    const float* sa = static_cast<const float*>(p.sa);
-    const float* sb = static_cast<const float*>(p.sb);
     const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
     store_tile_bf16<TM, TN>(
         acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0,
         [&](int j) {
-            const int m = mw + j * 32 + (lane & 31);
-            return (MODE == MODE_A8W8 && m < p.M) ? sa[m] : 1.0f;
+            const int r = wm * TM * 32 + j * 32 + (lane & 31);
+            return MODE == MODE_A8W8 ? *reinterpret_cast<const HKQ_LDS float*>(scl + r * 4) : 1.0f;
         },
         [&](int i, int g) {
-            const int n = nw + i * 32 + 8 * g + 4 * khalf;
-            return (MODE == MODE_A8W8 && n < p.N) ? *reinterpret_cast<const float4*>(sb + n) : make_float4(1.f, 1.f, 1.f, 1.f);
+            const int n = wn * TN * 32 + i * 32 + 8 * g + 4 * khalf;
+            if constexpr (MODE == MODE_A8W8) {
+                const v4f c = *reinterpret_cast<const HKQ_LDS v4f*>(scl + DENSE_BM * 4 + n * 4);
+                return make_float4(c[0], c[1], c[2], c[3]);
+            }
+            return make_float4(1.f, 1.f, 1.f, 1.f);
         },
         [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); });
 }
@@ -108,25 +135,28 @@ __global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_g
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
     const int u = blockIdx.x;
-    int tm, tn;
+    int whole = -1, t = -1, half = 0;
     if (u < p.n_whole) {
-        tile_coords(u, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-        dense_block<MODE, DENSE_TM, KTB>(p, tm, tn, 0, smem);
-        return;
+        whole = u;
+    } else {
+        const int v = u - p.n_whole;
+        t = 8 * (v >> 4) + (v & 7);
+        half = (v >> 3) & 1;
+        if (t >= p.n_split) return;
     }
-    const int v = u - p.n_whole;
-    const int t = 8 * (v >> 4) + (v & 7);
-    if (t >= p.n_split) return;
-    tile_coords(p.n_whole + t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-    dense_block<MODE, DENSE_TM / 2, KTB>(p, tm, tn, (v >> 3) & 1, smem);
+    int tm, tn;
+    if (whole >= 0) {
+        tile_coords(whole, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+        dense_block<MODE, DENSE_TM, KTB>(p, tm, tn, 0, smem);
+    } else {
+        tile_coords(p.n_whole + t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+        dense_block<MODE, DENSE_TM / 2, KTB>(p, tm, tn, half, smem);
+    }
 }
 
 template <int MODE, int KTB>
 static int launch_dense_ktb(DenseParams& p, hipStream_t stream) {
-    constexpr int NS = dense_ns<KTB>();
-    using Whole = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM, DENSE_TN, KTB>;
-    using Half = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM / 2, DENSE_TN, KTB>;
-    constexpr int LDS = Whole::lds_bytes(NS) > Half::lds_bytes(NS) ? Whole::lds_bytes(NS) : Half::lds_bytes(NS);
+    constexpr int LDS = dense_lds<MODE, KTB>();
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
     auto kern = dense_gemm_kernel<MODE, KTB>;
     static bool attr_set = false;  // per instantiation; the attribute is per-process
@@ -148,7 +178,7 @@ static int launch_dense_ktb(DenseParams& p, hipStream_t stream) {
     // CUs and the tiles have rows in both halves.
     const int ncu = cu_count();
     const int64_t last = ncu > 0 ? tiles % ncu : 0;
-    int64_t split = (last > 0 && 2 * last <= ncu && p.M > DENSE_BM / 2) ? last : 0;
+    const int64_t split = (last > 0 && 2 * last <= ncu && p.M > DENSE_BM / 2) ? last : 0;
     p.n_whole = (int)(tiles - split);
     p.n_split = (int)split;
     const int64_t nblk = p.n_whole + 2 * ((split + 7) / 8 * 8);

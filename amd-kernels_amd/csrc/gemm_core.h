@@ -173,9 +173,28 @@ __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uin
     // LDS operations of a wave complete in order: the reads below see the writes above.
     constexpr int SEGS = TN * 32 * 2 / 16;  // 16-byte pieces per row
     constexpr int ROWS_PER_PASS = 64 / SEGS;
+    constexpr int PASSES = TM * 32 / ROWS_PER_PASS;
+    constexpr int BATCH = 8;  // LDS reads in flight before their stores
+    static_assert(PASSES % BATCH == 0, "whole batches");
+    const int rl = lane / SEGS, seg = lane % SEGS;
+    if (c16 && mw + TM * 32 <= M && nw + TN * 32 <= N) {
+        // the wave's sub-tile lies inside C: no per-piece checks
+        uint16_t* dst = C + (int64_t)(mw + rl) * ldc + nw + seg * 8;
+        const int64_t step = (int64_t)ROWS_PER_PASS * ldc;
+#pragma unroll
+        for (int b = 0; b < PASSES; b += BATCH) {
+            v4i v[BATCH];
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k) v[k] = lds_read16(ep + ((b + k) * ROWS_PER_PASS + rl) * PITCH + seg * 16);
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k)
+                __builtin_nontemporal_store(v[k], reinterpret_cast<v4i*>(dst + (b + k) * step));
+        }
+        return;
+    }
 #pragma unroll 4
     for (int r0 = 0; r0 < TM * 32; r0 += ROWS_PER_PASS) {
-        const int r = r0 + lane / SEGS, seg = lane % SEGS;
+        const int r = r0 + rl;
         const v4i v = lds_read16(ep + r * PITCH + seg * 16);
         const int m = mw + r;
         const int n = nw + seg * 8;
