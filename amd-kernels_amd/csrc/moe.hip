@@ -41,10 +41,9 @@ struct MoeParams {
 
 constexpr int MOE_BM = 128;  // rows per OGS routing block
 
-template <int WAVES_N, int TN, int NS>
+template <int WAVES_N, int TN, int KTB, int NS>
 __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoeParams p) {
     constexpr int WAVES_M = 1, TM = 4;
-    constexpr int KTB = 64;
     using Cfg = DenseCfg<MODE_A8W8, WAVES_M, WAVES_N, TM, TN, KTB>;
     constexpr int NW = Cfg::NW, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
     static_assert(Cfg::BM == MOE_BM, "one tile row block per routing entry");
@@ -130,12 +129,12 @@ __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoePara
         });
 }
 
-template <int WAVES_N, int TN, int NS>
+template <int WAVES_N, int TN, int KTB, int NS>
 static int launch_moe(MoeParams& p, hipStream_t stream) {
-    using Cfg = DenseCfg<MODE_A8W8, 1, WAVES_N, 4, TN, 64>;
+    using Cfg = DenseCfg<MODE_A8W8, 1, WAVES_N, 4, TN, KTB>;
     constexpr int LDS = Cfg::lds_bytes(NS);
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
-    auto kern = moe_gemm_kernel<WAVES_N, TN, NS>;
+    auto kern = moe_gemm_kernel<WAVES_N, TN, KTB, NS>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
@@ -196,5 +195,7 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     p.sxm = stride_xm; p.swe = stride_we; p.swn = stride_wn; p.sym = stride_ym;
     p.xs_tok = xs_stride_tok; p.ws_e = ws_stride_e; p.ws_n = ws_stride_n; p.ws_gn = ws_group_n; p.bias_e = bias_stride_e;
     p.c16 = (stride_ym % 8 == 0) && (reinterpret_cast<uintptr_t>(Y) % 16 == 0);
-    return launch_moe<4, 4, 3>(p, stream);
+    // 128-byte K-tiles (2-stage ring) when every row has whole ones: a partial
+    // last K-tile would read the next row's bytes instead of zeros
+    return K % 128 == 0 ? launch_moe<4, 4, 128, 2>(p, stream) : launch_moe<4, 4, 64, 3>(p, stream);
 }

@@ -66,7 +66,7 @@ def test_moe_reference_setup(orc):
 
 
 @pytest.mark.parametrize("T,E,topk,K,N", [(300, 4, 2, 512, 520), (1, 8, 2, 256, 512), (1000, 8, 2, 1024, 1024),
-                                          (257, 3, 1, 384, 260)])
+                                          (257, 3, 1, 384, 260), (77, 4, 2, 320, 256)])
 def test_moe_per_token_per_channel(orc, T, E, topk, K, N):
     require_gpu()
     _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, T + N)
