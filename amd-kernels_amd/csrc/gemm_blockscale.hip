@@ -149,35 +149,43 @@ __global__ __launch_bounds__(256, 1) void blockscale_gemm_kernel(const BlockScal
         };
         load_sbn(0);
         __builtin_amdgcn_sched_barrier(0);
+        // Sub-tile s = i*TM + j: its two chained MFMAs make the group partial P,
+        // which is promoted (acc += P * scales) only after the MFMAs of sub-tile
+        // s+1 are issued, so the VALU promotion of one sub-tile runs while the
+        // matrix pipe works on the next.
+        v16f P[2];
+        auto promote = [&](int s2, const v16f& Ps) {
+            const int i = s2 / TM, j = s2 % TM;
+            if constexpr (GN1) {
 #pragma unroll
-        for (int i = 0; i < TN; ++i) {
+                for (int r = 0; r < 16; ++r) acc[i][j][r] += Ps[r] * sa_j[j] * sbn[r / 4][r & 3];
+            } else {
+                const float sc = sa_j[j] * sbw;
 #pragma unroll
-            for (int j = 0; j < TM; ++j) {
-                v16f P = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i][0], fa[j][0], v16f{}, 0, 0, 0, 127, 0, 127);
-                P = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i][1], fa[j][1], P, 0, 0, 0, 127, 0, 127);
-                if constexpr (GN1) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        acc[i][j][r] += P[r] * sa_j[j] * sbn[r / 4][r & 3];
-                    }
-                } else {
-                    const float s = sa_j[j] * sbw;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] += P[r] * s;
-                }
-                // registers freed by this sub-tile take the next K-tile's fragments
-                if (j == TM - 1) {
-                    fb[i][0] = frag(nxt + BM * BS_KT, brow + i * 32, 0);
-                    fb[i][1] = frag(nxt + BM * BS_KT, brow + i * 32, 1);
-                    if (i + 1 < TN) load_sbn(i + 1);
-                }
-                if (i == TN - 1) {
-                    fa[j][0] = frag(nxt, arow + j * 32, 0);
-                    fa[j][1] = frag(nxt, arow + j * 32, 1);
-                }
-                __builtin_amdgcn_sched_barrier(0);
+                for (int r = 0; r < 16; ++r) acc[i][j][r] += Ps[r] * sc;
             }
+        };
+#pragma unroll
+        for (int s2 = 0; s2 < TN * TM; ++s2) {
+            const int i = s2 / TM, j = s2 % TM;
+            v16f Pn = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i][0], fa[j][0], v16f{}, 0, 0, 0, 127, 0, 127);
+            P[s2 & 1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i][1], fa[j][1], Pn, 0, 0, 0, 127, 0, 127);
+            // registers freed by this sub-tile's MFMAs take the next K-tile's fragments
+            if (j == TM - 1) {
+                fb[i][0] = frag(nxt + BM * BS_KT, brow + i * 32, 0);
+                fb[i][1] = frag(nxt + BM * BS_KT, brow + i * 32, 1);
+            }
+            if (i == TN - 1) {
+                fa[j][0] = frag(nxt, arow + j * 32, 0);
+                fa[j][1] = frag(nxt, arow + j * 32, 1);
+            }
+            if (s2 > 0) promote(s2 - 1, P[(s2 - 1) & 1]);
+            // the column scales of n-tile i+1 replace those of n-tile i once
+            // sub-tile (i, TM-1) is promoted
+            if (j == 0 && i > 0) load_sbn(i);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        promote(TN * TM - 1, P[(TN * TM - 1) & 1]);
     }
     mfma_drain();
     tile_barrier<0>();
