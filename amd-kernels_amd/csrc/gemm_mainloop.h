@@ -14,22 +14,32 @@ struct DenseCfg {
     static constexpr int NW = WAVES_M * WAVES_N;
     static constexpr int BM = WAVES_M * TM * 32, BN = WAVES_N * TN * 32;
     static constexpr bool FP4 = MODE == MODE_MXFP4;
-    static constexpr int SUB = (KTB / 64) * (FP4 ? 2 : 1);   // 64-deep MFMA K-steps per K-tile
+    // K-steps per K-tile: 64 bytes of K per row each (FP8: one 64-deep MFMA per
+    // output sub-tile; FP4: two, one per 32-byte half of the lane's fragment)
+    static constexpr int SUB = KTB / 64;
     static constexpr int RPL = KT::ROWS_PER_LOAD;
     static constexpr int LA = BM / RPL / NW, LB = BN / RPL / NW;
-    // FP4: the K-tile's e8m0 scales (KTB/16 bytes per row: one per 32 values)
-    // ride in LDS after the data, as KTB/64 planes of one 4-byte word per row;
-    // one 4-byte LDS-direct load per lane covers 64 rows of one plane. When a
-    // tile has fewer (plane, 64-row group) pairs than waves, waves load the same
-    // pair (identical bytes to the same place) so that every wave issues the
+    // FP4 e8m0 scales, KTB/16 bytes per row per K-tile (one per 32 values).
+    // KTB 128 (SBLK): the scales of SB_KT = 4 K-tiles (32 bytes per row) form a
+    // block, held in a 2-slot ring after the K-tile ring; a block is fetched in
+    // 32-row groups (two lanes per row, 16 bytes each: 32 lines of 32 bytes per
+    // load instead of 64 lines of 4 bytes), one group per wave per K-tile over
+    // the 4 K-tiles before it is first read.
+    // KTB 64: the K-tile's 4 scale bytes per row ride in its stage after the
+    // data; one 4-byte LDS-direct load per lane covers 64 rows.
+    // When there are fewer groups than load slots, slots load the same group
+    // again (identical bytes to the same place) so that every wave issues the
     // same number of loads per K-tile, which the vmcnt accounting relies on.
-    static constexpr int PLANES = KTB / 64;
-    static constexpr int SCA = FP4 ? BM * 4 * PLANES : 0, SCB = FP4 ? BN * 4 * PLANES : 0;
-    static constexpr int GA = FP4 ? BM / 64 * PLANES : 1, GB = FP4 ? BN / 64 * PLANES : 1;
-    static constexpr int LSA = FP4 ? (GA + NW - 1) / NW : 0, LSB = FP4 ? (GB + NW - 1) / NW : 0;
+    static constexpr bool SBLK = FP4 && KTB == 128;
+    static constexpr int SB_KT = 4, SB_GROUPS = (BM + BN) / 32, SB_SLOT = (BM + BN) * 32;
+    static constexpr int SB_BYTES = SBLK ? 2 * SB_SLOT : 0;
+    static constexpr bool SK = FP4 && !SBLK;
+    static constexpr int SCA = SK ? BM * 4 : 0, SCB = SK ? BN * 4 : 0;
+    static constexpr int GA = SK ? BM / 64 : 1, GB = SK ? BN / 64 : 1;
+    static constexpr int LSA = SK ? (GA + NW - 1) / NW : 0, LSB = SK ? (GB + NW - 1) / NW : 0;
     static constexpr int STAGE = (BM + BN) * KTB + SCA + SCB;
-    static constexpr int NLD = LA + LB + LSA + LSB;           // LDS-direct loads per wave per K-tile
-    static constexpr int PARTS = FP4 ? 1 : 2;                 // ds_read_b128 per fragment per K-step
+    static constexpr int NLD = LA + LB + LSA + LSB + (SBLK ? 1 : 0);  // LDS-direct loads per wave per K-tile
+    static constexpr int PARTS = 2;                           // ds_read_b128 per fragment per K-step
     static constexpr int NRD = 2 * PARTS * (TM > TN ? TM : TN);  // fragment read slots per K-step
     static constexpr int NSC = FP4 ? TM + TN : 0;             // scale reads per K-tile
     static constexpr int NMF = TM * TN, HALF = NMF / 2;       // MFMAs per K-step
@@ -37,10 +47,11 @@ struct DenseCfg {
     // padded row pitch, then writes whole 256-byte row segments of C
     static constexpr int EP_PITCH = TN * 32 * 2 + 16;
     static constexpr int EP_BYTES = NW * TM * 32 * EP_PITCH;
-    static constexpr int lds_bytes(int ns) { return ns * STAGE > EP_BYTES ? ns * STAGE : EP_BYTES; }
+    static constexpr int lds_bytes(int ns) { return ns * STAGE + SB_BYTES > EP_BYTES ? ns * STAGE + SB_BYTES : EP_BYTES; }
     static_assert(LA >= 1 && LB >= 1, "tile too small for the wave count");
-    static_assert(!FP4 || (GA % NW == 0 || NW % GA == 0), "A scale groups vs waves");
-    static_assert(!FP4 || (GB % NW == 0 || NW % GB == 0), "B scale groups vs waves");
+    static_assert(!SK || (GA % NW == 0 || NW % GA == 0), "A scale groups vs waves");
+    static_assert(!SK || (GB % NW == 0 || NW % GB == 0), "B scale groups vs waves");
+    static_assert(!SBLK || (SB_GROUPS <= SB_KT * NW && BM % 32 == 0), "scale block groups vs load slots");
     static_assert((TN * 32 * 2) % 256 == 0, "epilogue rows are whole 256-byte segments");
 };
 
@@ -76,11 +87,12 @@ __device__ __forceinline__ uint32_t dense_row_off(int i, int wave, int lane, int
 //   the compiler's scheduler.
 //
 // Fragments: lane half h (lane / 32) owns logical chunks [h * KTB/32, (h+1) *
-// KTB/32) of every row; K-step ks uses chunks h*KTB/32 + 2ks + {0, 1} (FP8) or
-// h*KTB/32 + ks (FP4). The order in which K enters the sums is the same for A
-// and B, so the products are unchanged; for FP4 it makes the lane's e8m0 bytes
-// of one K-tile contiguous (2 bytes for KTB 64, one 4-byte plane for KTB 128),
-// and the MFMA's opsel picks byte ks.
+// KTB/32) of every row; K-step ks uses chunks h*KTB/32 + 2ks + {0, 1}, read as
+// two 16-byte parts (FP8: the two halves of one MFMA operand; FP4: one MFMA
+// each). The order in which K enters the sums is the same for A and B, so the
+// products are unchanged; for FP4 it makes the lane's e8m0 bytes of one K-tile
+// contiguous (2 bytes for KTB 64, one 4-byte plane for KTB 128), and the MFMA's
+// opsel picks byte 2ks + part.
 //
 // a_off/b_off: per load instruction, the byte offset of the lane's row and
 // logical chunk inside src.a / src.b (OOB for rows that must read zero).
@@ -100,18 +112,44 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
     constexpr int NMF = Cfg::NMF, HALF = Cfg::HALF;
     constexpr bool FP4 = Cfg::FP4;
     constexpr int HCH = KTB / 32;  // logical chunks per lane half
-    static_assert(NS >= 2 && (NS - 1) * NLD <= 63, "ring depth and vmcnt budget");
+    static_assert(NS >= 2 && (NS - 1) * NLD + 3 <= 63, "ring depth and vmcnt budget");
+    static_assert(!Cfg::SBLK || NS == 2, "the scale-block schedule assumes a 2-stage ring");
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int KTN = src.KT;
 
+    // Scale unit u (SBLK): group slot u % SB_KT of block u / SB_KT; this wave
+    // loads group (slot * NW + wave) % SB_GROUPS of the block's [A; B] rows.
+    HKQ_LDS uint8_t* sblk = smem + NS * STAGE;
+    auto load_scale_unit = [&](int u) {
+        const int blk = u / Cfg::SB_KT;
+        const int g = ((u % Cfg::SB_KT) * NW + wave) % Cfg::SB_GROUPS;
+        const bool live = blk * Cfg::SB_KT < KTN;
+        const int r = g * 32 + (lane >> 1);
+        const bool isa = g * 32 < BM;
+        const uint8_t* base = (isa ? src.as : src.bs) + blk * 32;
+        const int64_t bytes = (isa ? src.as_bytes : src.bs_bytes) - blk * 32;
+        const uint32_t off = (uint32_t)((isa ? r : r - BM) * (isa ? src.lsa : src.lsb)) + (uint32_t)((lane & 1) * 16);
+        lds_load16(base, live && bytes > 0 ? (uint32_t)bytes : 0u, sblk + (blk & 1) * Cfg::SB_SLOT + g * 1024, off);
+    };
+
     // Load instruction idx of K-tile kt into `stage`: A rows, B rows, then (FP4)
-    // scale words: group g covers plane g % PLANES of rows (g / PLANES)*64 + lane.
+    // scales: KTB 64: group g covers rows g*64 + lane; KTB 128: one scale unit,
+    // kt + SB_KT - 1 (with the 2-stage ring the loads issued in K-tile j are
+    // those of K-tile j + 2, so K-tile j fetches unit j + SB_KT + 1: block b + 1
+    // arrives during K-tiles 4b-1 .. 4b+2, after block b-1, which used the same
+    // slot, was last read in K-tile 4b-2, and before K-tile 4b+3 reads it).
     // For kt >= KTN the buffers are empty, so the loads read zero (the loop needs
     // no branches).
     auto load_piece = [&](int kt, int stage, int idx) {
         const int kb = kt * KTB;
         const bool live = kt < KTN;
         HKQ_LDS uint8_t* st = smem + stage * STAGE;
+        if constexpr (Cfg::SBLK) {
+            if (idx == LA + LB) {
+                load_scale_unit(kt + Cfg::SB_KT - 1);
+                return;
+            }
+        }
         if (idx < LA) {
             lds_load16(src.a + kb, live ? (uint32_t)(src.a_bytes - kb) : 0u, st + (idx * NW + wave) * 1024, a_off[idx]);
         } else if (idx < LA + LB) {
@@ -119,21 +157,15 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
             lds_load16(src.b + kb, live ? (uint32_t)(src.b_bytes - kb) : 0u, st + BM * KTB + (i * NW + wave) * 1024,
                        b_off[i]);
         } else if (idx < LA + LB + LSA) {
-            constexpr int PL = Cfg::PLANES;
             const int g = ((idx - LA - LB) * NW + wave) % GA;
-            const int plane = g % PL, rows = g / PL;
-            const int kb4 = kt * 4 * PL + plane * 4;
-            const uint32_t off = (uint32_t)((rows * 64 + lane) * src.lsa);
-            lds_load4(src.as + kb4, live ? (uint32_t)(src.as_bytes - kb4) : 0u,
-                      st + (BM + BN) * KTB + plane * BM * 4 + rows * 256, off);
+            const int kb4 = kt * 4;
+            const uint32_t off = (uint32_t)((g * 64 + lane) * src.lsa);
+            lds_load4(src.as + kb4, live ? (uint32_t)(src.as_bytes - kb4) : 0u, st + (BM + BN) * KTB + g * 256, off);
         } else {
-            constexpr int PL = Cfg::PLANES;
             const int g = ((idx - LA - LB - LSA) * NW + wave) % GB;
-            const int plane = g % PL, rows = g / PL;
-            const int kb4 = kt * 4 * PL + plane * 4;
-            const uint32_t off = (uint32_t)((rows * 64 + lane) * src.lsb);
-            lds_load4(src.bs + kb4, live ? (uint32_t)(src.bs_bytes - kb4) : 0u,
-                      st + (BM + BN) * KTB + SCA + plane * BN * 4 + rows * 256, off);
+            const int kb4 = kt * 4;
+            const uint32_t off = (uint32_t)((g * 64 + lane) * src.lsb);
+            lds_load4(src.bs + kb4, live ? (uint32_t)(src.bs_bytes - kb4) : 0u, st + (BM + BN) * KTB + SCA + g * 256, off);
         }
     };
 
@@ -152,27 +184,32 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
         const int t = idx / (2 * PARTS), isb = (idx / PARTS) & 1, part = idx % PARTS;
         if ((isb ? TN : TM) <= t) return;
         const int row = (isb ? brow : arow) + t * 32;
-        const int chunk = khalf * HCH + (FP4 ? ks : 2 * ks + part);
+        const int chunk = khalf * HCH + 2 * ks + part;
         const v4i v = lds_read16(At + (isb ? BM * KTB : 0) + KT::swz(row, chunk));
         if (isb) f.b[t][part] = v;
         else f.a[t][part] = v;
     };
-    // MXFP4: per m/n-tile the lane's e8m0 bytes of the K-tile, byte ks for
-    // K-step ks: 16 bits at byte 2h of the row's word (KTB 64) or the row's word
-    // of plane h (KTB 128). The value goes to the MFMA unchanged.
+    // MXFP4: per m/n-tile the lane's e8m0 bytes of K-tile kt, byte 2ks + part
+    // for part `part` of K-step ks: KTB 64: 16 bits at byte 2h of the row's word
+    // in the stage; KTB 128: the 4 bytes at 8 * (kt % SB_KT) + 4h of the row's
+    // 32 bytes in the block slot. The value goes to the MFMA unchanged.
     struct Scales {
         int a[TM], b[TN];
     };
-    auto read_scale = [&](int stage, Scales& s, int idx) {
+    auto read_scale = [&](int stage, int kt, Scales& s, int idx) {
         if constexpr (FP4) {
-            const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KTB;
             const bool isa = idx < TM;
             const int t = isa ? idx : idx - TM;
             const int row = (isa ? arow : brow) + t * 32;
-            const HKQ_LDS uint8_t* base = isa ? sca : sca + SCA;
             int w;
-            if constexpr (KTB == 64) w = *reinterpret_cast<const HKQ_LDS uint16_t*>(base + row * 4 + khalf * 2);
-            else w = *reinterpret_cast<const HKQ_LDS int*>(base + khalf * (isa ? BM : BN) * 4 + row * 4);
+            if constexpr (Cfg::SBLK) {
+                const HKQ_LDS uint8_t* slot = sblk + ((kt / Cfg::SB_KT) & 1) * Cfg::SB_SLOT;
+                w = *reinterpret_cast<const HKQ_LDS int*>(slot + (isa ? row : BM + row) * 32 + (kt % Cfg::SB_KT) * 8 +
+                                                         khalf * 4);
+            } else {
+                const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KTB + (isa ? 0 : SCA);
+                w = *reinterpret_cast<const HKQ_LDS uint16_t*>(sca + row * 4 + khalf * 2);
+            }
             if (isa) s.a[t] = w;
             else s.b[t] = w;
         }
@@ -183,40 +220,47 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = v16f{};
 
-    // MFMA idx (accumulator i*TM + j) of K-step ks
+    // MFMA slot idx (accumulator i*TM + j) of K-step ks: one FP8 MFMA on the
+    // 32-byte fragments, or two FP4 MFMAs (one per 16-byte half, scale bytes
+    // 2ks and 2ks + 1 of the lane's scale word)
     auto mfma_one = [&](const Frags& f, int ks, const Scales& s, int idx) {
         const int i = idx / TM, j = idx % TM;
-        v8i a, b;
-        if constexpr (PARTS == 2) {
-            b = v8i{f.b[i][0][0], f.b[i][0][1], f.b[i][0][2], f.b[i][0][3], f.b[i][1][0], f.b[i][1][1], f.b[i][1][2], f.b[i][1][3]};
-            a = v8i{f.a[j][0][0], f.a[j][0][1], f.a[j][0][2], f.a[j][0][3], f.a[j][1][0], f.a[j][1][1], f.a[j][1][2], f.a[j][1][3]};
-        } else {
-            b = v8i{f.b[i][0][0], f.b[i][0][1], f.b[i][0][2], f.b[i][0][3], 0, 0, 0, 0};
-            a = v8i{f.a[j][0][0], f.a[j][0][1], f.a[j][0][2], f.a[j][0][3], 0, 0, 0, 0};
-        }
         if constexpr (FP4) {
-            switch (ks & 3) {
-                case 0: acc[i][j] = mfma_sel<true, 0, 0>(b, a, acc[i][j], s.b[i], s.a[j]); break;
-                case 1: acc[i][j] = mfma_sel<true, 1, 1>(b, a, acc[i][j], s.b[i], s.a[j]); break;
-                case 2: acc[i][j] = mfma_sel<true, 2, 2>(b, a, acc[i][j], s.b[i], s.a[j]); break;
-                default: acc[i][j] = mfma_sel<true, 3, 3>(b, a, acc[i][j], s.b[i], s.a[j]); break;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const v8i b = v8i{f.b[i][q][0], f.b[i][q][1], f.b[i][q][2], f.b[i][q][3], 0, 0, 0, 0};
+                const v8i a = v8i{f.a[j][q][0], f.a[j][q][1], f.a[j][q][2], f.a[j][q][3], 0, 0, 0, 0};
+                switch ((2 * ks + q) & 3) {
+                    case 0: acc[i][j] = mfma_sel<true, 0, 0>(b, a, acc[i][j], s.b[i], s.a[j]); break;
+                    case 1: acc[i][j] = mfma_sel<true, 1, 1>(b, a, acc[i][j], s.b[i], s.a[j]); break;
+                    case 2: acc[i][j] = mfma_sel<true, 2, 2>(b, a, acc[i][j], s.b[i], s.a[j]); break;
+                    default: acc[i][j] = mfma_sel<true, 3, 3>(b, a, acc[i][j], s.b[i], s.a[j]); break;
+                }
             }
         } else {
+            const v8i b = v8i{f.b[i][0][0], f.b[i][0][1], f.b[i][0][2], f.b[i][0][3], f.b[i][1][0], f.b[i][1][1], f.b[i][1][2], f.b[i][1][3]};
+            const v8i a = v8i{f.a[j][0][0], f.a[j][0][1], f.a[j][0][2], f.a[j][0][3], f.a[j][1][0], f.a[j][1][1], f.a[j][1][2], f.a[j][1][3]};
             acc[i][j] = mfma_sel<false, 0, 0>(b, a, acc[i][j], 127, 127);
         }
     };
 
     Frags F[2];
     Scales S[2];
+    // prologue: (SBLK) units 0 .. SB_KT-2 of scale block 0, then K-tiles 0 .. NS-1
+    // (whose loads carry units SB_KT-1, SB_KT: the rest of block 0, the start of 1)
+    if constexpr (Cfg::SBLK) {
+#pragma unroll
+        for (int u = 0; u + 1 < Cfg::SB_KT; ++u) load_scale_unit(u);
+    }
 #pragma unroll
     for (int t = 0; t < NS; ++t)
 #pragma unroll
         for (int i = 0; i < NLD; ++i) load_piece(t, t, i);
-    tile_barrier<(NS - 1) * NLD>();  // K-tile 0 resident
+    tile_barrier<(NS - 1) * NLD>();  // K-tile 0 (and everything issued before it) resident
 #pragma unroll
     for (int i = 0; i < NRD; ++i) read_piece(0, 0, F[0], i);
 #pragma unroll
-    for (int i = 0; i < NSC; ++i) read_scale(0, S[0], i);
+    for (int i = 0; i < NSC; ++i) read_scale(0, 0, S[0], i);
 
     // One K-tile; P is the tile's parity (fragment and scale buffers alternate).
     auto ktile = [&](int kt, int stage, auto parity) {
@@ -257,7 +301,7 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
 #pragma unroll
             for (int i = c * NRD / POST; i < (c + 1) * NRD / POST; ++i) read_piece(next_stage, 0, nxt, i);
 #pragma unroll
-            for (int i = c * NSC / POST; i < (c + 1) * NSC / POST; ++i) read_scale(next_stage, S[P ^ 1], i);
+            for (int i = c * NSC / POST; i < (c + 1) * NSC / POST; ++i) read_scale(next_stage, kt + 1, S[P ^ 1], i);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
