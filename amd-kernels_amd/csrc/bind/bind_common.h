@@ -80,6 +80,29 @@ inline hkq_stream_t current_stream() {
     return reinterpret_cast<hkq_stream_t>(s);
 }
 
+// Device workspace of `bytes` bytes from torch's caching allocator on the
+// device of `like`, alive while the returned object is (the allocator hands the
+// memory out again only in the order of the work queued on the current stream,
+// which is where the launch goes). Without torch loaded there is no workspace
+// and the library runs the plan that needs none.
+struct Workspace {
+    py::object keep;
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+inline Workspace workspace(size_t bytes, py::object like) {
+    Workspace w;
+    if (bytes == 0) return w;
+    py::dict mods = py::module_::import("sys").attr("modules");
+    if (!mods.contains("torch")) return w;
+    py::object torch = py::module_::import("torch");
+    w.keep = torch.attr("empty")(py::make_tuple(bytes), py::arg("dtype") = torch.attr("uint8"),
+                                 py::arg("device") = like.attr("device"));
+    w.ptr = reinterpret_cast<void*>(w.keep.attr("data_ptr")().cast<uint64_t>());
+    w.bytes = bytes;
+    return w;
+}
+
 inline void check(int rc, const char* what) {
     if (rc != 0) throw std::runtime_error(std::string(what) + ": " + hkq_last_error() + " (code " + std::to_string(rc) + ")");
 }

@@ -26,8 +26,9 @@ void dispatch(py::object A, py::object B, py::object C, py::object A_scale, py::
     expect(sa.shape.size() == 2 && sa.dim(0) == M && sa.dim(1) == K / 32, "A_scale must be [M, K/32]");
     expect(sb.shape.size() == 2 && sb.dim(0) == N && sb.dim(1) == K / 32, "B_scale must be [N, K/32]");
     const int64_t lsa = row_stride(sa, "A_scale"), lsb = row_stride(sb, "B_scale");
-    check(hkq_gemm_mxfp4((const void*)a.ptr, (const void*)sa.ptr, (const void*)b.ptr, (const void*)sb.ptr,
-                         (void*)c.ptr, M, N, K, lda, ldb, lsa, lsb, ldc, current_stream()),
+    Workspace ws = workspace(hkq_gemm_mxfp4_workspace(M, N, K), A);
+    check(hkq_gemm_mxfp4_ws((const void*)a.ptr, (const void*)sa.ptr, (const void*)b.ptr, (const void*)sb.ptr,
+                            (void*)c.ptr, M, N, K, lda, ldb, lsa, lsb, ldc, ws.ptr, ws.bytes, current_stream()),
           "gemm_afp4wfp4");
 }
 

@@ -24,8 +24,9 @@ inline void gemm_a8w8(py::object A, py::object B, py::object a_scale, py::object
     expect(c.dim(0) == M && c.dim(1) == N, "C must be [M, N]");
     expect(sa.numel() == M && sa.contiguous(), "a_scale must be contiguous with M elements");
     expect(sb.numel() == N && sb.contiguous(), "b_scale must be contiguous with N elements");
-    check(hkq_gemm_a8w8((const void*)a.ptr, (const void*)b.ptr, (const float*)sa.ptr, (const float*)sb.ptr,
-                        (void*)c.ptr, M, N, K, lda, ldb, ldc, current_stream()),
+    Workspace ws = workspace(hkq_gemm_a8w8_workspace(M, N, K), A);
+    check(hkq_gemm_a8w8_ws((const void*)a.ptr, (const void*)b.ptr, (const float*)sa.ptr, (const float*)sb.ptr,
+                           (void*)c.ptr, M, N, K, lda, ldb, ldc, ws.ptr, ws.bytes, current_stream()),
           "gemm_a8w8");
 }
 

@@ -9,6 +9,8 @@
 //                        operands (gemm-basic/gemm_afp4wfp4/kernel.cpp:1-12 for
 //                        the data format; the reference kernel itself consumes
 //                        pre-dequantized bf16).
+#include <algorithm>
+
 #include "gemm_mainloop.h"
 #include "hkq_host.h"
 
@@ -29,6 +31,9 @@ struct DenseParams {
     int n_whole;          // workgroups [0, n_whole) compute whole tiles 0 .. n_whole-1
     int n_split;          // tiles n_whole .. n_whole+n_split-1 are computed as two M halves
     int c16;              // rows of C are 16-byte aligned (ldc % 8 == 0, C 16-byte aligned)
+    int splits;           // K splits of the split/skinny path (1: none)
+    int kt_split;         // K-tiles per split
+    float* ws;            // split partials (splits > 1)
 };
 
 // Tile geometry of the dense GEMMs: 256 x 256 tiles computed by 4 waves of
@@ -38,6 +43,9 @@ struct DenseParams {
 // else 64 bytes in a 4-stage ring.
 constexpr int DENSE_WAVES_M = 2, DENSE_WAVES_N = 2, DENSE_TM = 4, DENSE_TN = 4;
 constexpr int DENSE_BM = DENSE_WAVES_M * DENSE_TM * 32, DENSE_BN = DENSE_WAVES_N * DENSE_TN * 32;
+// Skinny geometry (M <= 64): one row of (TM*32) x 256 tiles, 4 waves of
+// (TM*32) x 64 side by side.
+constexpr int SKINNY_WAVES_N = 4, SKINNY_TN = 2, SKINNY_BN = SKINNY_WAVES_N * SKINNY_TN * 32;
 template <int KTB>
 constexpr int dense_ns() { return KTB == 128 ? 2 : 4; }
 
@@ -54,14 +62,48 @@ constexpr int dense_ring_lds() {
 template <int MODE, int KTB>
 constexpr int dense_lds() { return dense_ring_lds<MODE, KTB>() + (MODE == MODE_A8W8 ? 2 * DENSE_BM * 4 : 0); }
 
+// K loop of one (WM*TM*32) x (WN*TN*32) block of C at (m0, n0) over K-tiles
+// [kt0, kt1): the operand sources start kt0 K-tiles into the rows, so the
+// loop (and its scale-block schedule) counts K-tiles from 0.
+template <int MODE, int WM, int WN, int TM, int TN, int KTB>
+__device__ __forceinline__ void dense_kloop(const DenseParams& p, int m0, int n0, int kt0, int kt1, HKQ_LDS uint8_t* smem,
+                                            v16f (&acc)[TN][TM]) {
+    using Cfg = DenseCfg<MODE, WM, WN, TM, TN, KTB>;
+    constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
+    constexpr bool FP4 = Cfg::FP4;
+    constexpr int SCB_PER_KT = KTB / 16;  // FP4 scale bytes per row per K-tile
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rows_a = min(p.M - m0, BM), rows_b = min(p.N - n0, BN);
+    const int64_t kb0 = (int64_t)kt0 * KTB, ks0 = (int64_t)kt0 * SCB_PER_KT;
+
+    LoopSrc src;
+    src.a = p.A + (int64_t)m0 * p.lda + kb0;
+    src.b = p.B + (int64_t)n0 * p.ldb + kb0;
+    src.a_bytes = min((int64_t)rows_a * p.lda - kb0, (int64_t)0x7FFFFFFF);
+    src.b_bytes = min((int64_t)rows_b * p.ldb - kb0, (int64_t)0x7FFFFFFF);
+    src.as = FP4 ? static_cast<const uint8_t*>(p.sa) + (int64_t)m0 * p.lsa + ks0 : nullptr;
+    src.bs = FP4 ? static_cast<const uint8_t*>(p.sb) + (int64_t)n0 * p.lsb + ks0 : nullptr;
+    src.as_bytes = FP4 ? min((int64_t)rows_a * p.lsa - ks0, (int64_t)0x7FFFFFFF) : 0;
+    src.bs_bytes = FP4 ? min((int64_t)rows_b * p.lsb - ks0, (int64_t)0x7FFFFFFF) : 0;
+    src.lsa = p.lsa;
+    src.lsb = p.lsb;
+    src.KT = kt1 - kt0;
+    uint32_t a_off[LA], b_off[LB];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) a_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.lda);
+#pragma unroll
+    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.ldb);
+    gemm_mainloop<MODE, WM, WN, TM, TN, KTB, dense_ns<KTB>()>(src, a_off, b_off, smem, lane, wave, acc);
+}
+
 // One (TM*64) x 256 block of C: rows [m0, m0 + TM*64) of tile (tm, tn) of the
 // 256 x 256 tile grid, starting `half` * 128 rows into the tile.
 template <int MODE, int TM, int KTB>
 __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn, int half, HKQ_LDS uint8_t* smem) {
-    constexpr int WAVES_M = DENSE_WAVES_M, WAVES_N = DENSE_WAVES_N, TN = DENSE_TN, NS = dense_ns<KTB>();
+    constexpr int WAVES_M = DENSE_WAVES_M, WAVES_N = DENSE_WAVES_N, TN = DENSE_TN;
     using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>;
-    constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
-    constexpr bool FP4 = Cfg::FP4;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -71,24 +113,6 @@ __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn
     const int m0 = tm * DENSE_BM + half * BM, n0 = tn * BN;
     const int rows_a = min(p.M - m0, BM), rows_b = min(p.N - n0, BN);
     if (rows_a <= 0) return;  // the M half below the last row (uniform per workgroup)
-
-    LoopSrc src;
-    src.a = p.A + (int64_t)m0 * p.lda;
-    src.b = p.B + (int64_t)n0 * p.ldb;
-    src.a_bytes = min((int64_t)rows_a * p.lda, (int64_t)0x7FFFFFFF);
-    src.b_bytes = min((int64_t)rows_b * p.ldb, (int64_t)0x7FFFFFFF);
-    src.as = FP4 ? static_cast<const uint8_t*>(p.sa) + (int64_t)m0 * p.lsa : nullptr;
-    src.bs = FP4 ? static_cast<const uint8_t*>(p.sb) + (int64_t)n0 * p.lsb : nullptr;
-    src.as_bytes = FP4 ? min((int64_t)rows_a * p.lsa, (int64_t)0x7FFFFFFF) : 0;
-    src.bs_bytes = FP4 ? min((int64_t)rows_b * p.lsb, (int64_t)0x7FFFFFFF) : 0;
-    src.lsa = p.lsa;
-    src.lsb = p.lsb;
-    src.KT = p.kbytes / KTB;
-    uint32_t a_off[LA], b_off[LB];
-#pragma unroll
-    for (int i = 0; i < LA; ++i) a_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.lda);
-#pragma unroll
-    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.ldb);
 
     // A8W8: the tile's row and column scales go to LDS while the K loop runs
     // (rows past M / columns past N read zero); each wave loads 64 of each.
@@ -103,7 +127,7 @@ __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn
     }
 
     v16f acc[TN][TM];
-    gemm_mainloop<MODE, WAVES_M, WAVES_N, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
+    dense_kloop<MODE, WAVES_M, WAVES_N, TM, TN, KTB>(p, m0, n0, 0, p.kbytes / KTB, smem, acc);
 
     // Epilogue (scales of A8W8 applied in registers; MXFP4 has none left)
     const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
@@ -154,24 +178,198 @@ __global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_g
     }
 }
 
+// ---------------------------------------------------------------------------
+// Smaller tiles and split K. A grid of 256 x 256 tiles that would fill at most
+// half of the CUs runs on 128 x 128 tiles (4 waves of 64 x 64), and M <= 64
+// on one row of (32 or 64) x 256 tiles (4 waves side by side); if that still
+// fills at most half of the CUs, K is split as well: workgroup u computes tile
+// u % tiles over K-tiles [s * kt_split, (s+1) * kt_split), s = u / tiles, and
+// writes its fp32 sums to the workspace in register order (per wave, float4 q
+// of lane l at (q * 64 + l) * 16 bytes: every store is a contiguous 1 KB);
+// dense_reduce_kernel adds the splits element-wise and writes C. Without a
+// split the workgroup runs the epilogue itself, reading the scales from memory.
+template <int MODE, int WM, int WN, int TM, int TN>
+__device__ __forceinline__ void dense_epilogue_global(const DenseParams& p, v16f (&acc)[TN][TM], HKQ_LDS uint8_t* smem,
+                                                      int wave, int lane, int mw, int nw) {
+    const float* sa = static_cast<const float*>(p.sa);
+    const float* sb = static_cast<const float*>(p.sb);
+    const int khalf = lane >> 5;
+    store_tile_bf16<TM, TN>(
+        acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0,
+        [&](int j) {
+            const int m = mw + j * 32 + (lane & 31);
+            return (MODE == MODE_A8W8 && m < p.M) ? sa[m] : 1.0f;
+        },
+        [&](int i, int g) {
+            const int n = nw + i * 32 + 8 * g + 4 * khalf;
+            return (MODE == MODE_A8W8 && n < p.N) ? *reinterpret_cast<const float4*>(sb + n) : make_float4(1.f, 1.f, 1.f, 1.f);
+        },
+        [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); });
+}
+
+template <int MODE, int WM, int WN, int TM, int TN, int KTB, int MINB>
+__global__ __launch_bounds__(64 * WM * WN, MINB) void dense_tile_kernel(const DenseParams p) {
+    using Cfg = DenseCfg<MODE, WM, WN, TM, TN, KTB>;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::NW;
+    constexpr int NQ = TN * TM * 4;  // float4 of accumulators per lane
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
+    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tiles = p.tiles_m * p.tiles_n;
+    const int tile = blockIdx.x % tiles, split = blockIdx.x / tiles;
+    int tm, tn;
+    tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int KT = p.kbytes / KTB;
+    const int kt0 = split * p.kt_split, kt1 = min(KT, kt0 + p.kt_split);
+
+    v16f acc[TN][TM];
+    dense_kloop<MODE, WM, WN, TM, TN, KTB>(p, m0, n0, kt0, kt1, smem, acc);
+
+    if (p.splits > 1) {
+        v4f* slot = reinterpret_cast<v4f*>(p.ws) + ((int64_t)(split * tiles + tile) * NW + wave) * NQ * 64;
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    __builtin_nontemporal_store(v4f{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                                    acc[i][j][4 * g + 3]},
+                                                slot + ((i * TM + j) * 4 + g) * 64 + lane);
+        return;
+    }
+    const int wm = wave / WN, wn = wave % WN;
+    dense_epilogue_global<MODE, WM, WN, TM, TN>(p, acc, smem, wave, lane, m0 + wm * TM * 32, n0 + wn * TN * 32);
+}
+
+// One thread per float4 of the partial sums: adds the splits, scales and
+// writes the four bf16 values of C it covers (D[n][m] layout of the MFMA: the
+// float4 g of m-tile j, n-tile i holds n = i*32 + 8g + 4*(lane/32) + 0..3 of
+// m = j*32 + lane % 32, relative to the wave's sub-tile).
+template <int MODE, int WM, int WN, int TM, int TN>
+__global__ __launch_bounds__(256) void dense_reduce_kernel(const DenseParams p, int64_t total) {
+    constexpr int NW = WM * WN, NQ = TN * TM * 4, BM = WM * TM * 32, BN = WN * TN * 32;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= total) return;
+    const int lane = (int)(gid & 63);
+    const int q = (int)((gid >> 6) % NQ);
+    const int64_t wt = (gid >> 6) / NQ;
+    const int wave = (int)(wt % NW), tile = (int)(wt / NW);
+    int tm, tn;
+    tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    const int i = q / (4 * TM), j = (q / 4) % TM, g = q % 4;
+    const int m = tm * BM + (wave / WN) * TM * 32 + j * 32 + (lane & 31);
+    const int n = tn * BN + (wave % WN) * TN * 32 + i * 32 + 8 * g + 4 * (lane >> 5);
+    if (m >= p.M || n >= p.N) return;
+    const v4f* src = reinterpret_cast<const v4f*>(p.ws) + gid;
+    v4f v = __builtin_nontemporal_load(src);
+    for (int s = 1; s < p.splits; ++s) v += __builtin_nontemporal_load(src + (int64_t)s * total);
+    float a = 1.f;
+    v4f b = v4f{1.f, 1.f, 1.f, 1.f};
+    if constexpr (MODE == MODE_A8W8) {
+        a = static_cast<const float*>(p.sa)[m];
+        b = *reinterpret_cast<const v4f*>(static_cast<const float*>(p.sb) + n);  // N % 4 == 0: n..n+3 < N
+    }
+    const uint32_t lo = pk_bf16(v[0] * a * b[0], v[1] * a * b[1]);
+    const uint32_t hi = pk_bf16(v[2] * a * b[2], v[3] * a * b[3]);
+    *reinterpret_cast<v2i*>(p.C + (int64_t)m * p.ldc + n) = v2i{(int)lo, (int)hi};
+}
+
+template <typename K>
+static int set_lds(K kern, int lds, bool& done) {
+    if (done) return 0;
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) {
+        set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", lds, hipGetErrorString(e));
+        return (int)e;
+    }
+    done = true;
+    return 0;
+}
+
+// Plan of a dense GEMM: the tile geometry, how many K splits, and the
+// workspace the splits need (bytes). The same function answers the workspace
+// query, so a caller's workspace always matches the launch.
+enum DenseGeo { GEO_256 = 0, GEO_128 = 1, GEO_SKINNY = 2 };
+struct DensePlan {
+    int geo;
+    int skinny_tm;  // GEO_SKINNY: TM = 1 or 2
+    int64_t tiles;
+    int splits, kt_split;
+    size_t ws_bytes;
+};
+
+static DensePlan dense_plan(int64_t M, int64_t N, int64_t kbytes, bool allow_split) {
+    DensePlan pl{};
+    const int ktb = kbytes % 128 == 0 ? 128 : 64;
+    const int64_t KT = kbytes / ktb;
+    const int ncu = cu_count() > 0 ? cu_count() : 256;
+    auto ntiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    int64_t bm = DENSE_BM, bn = DENSE_BN;
+    pl.geo = GEO_256;
+    if (ktb == 128 && M <= 64) {
+        pl.geo = GEO_SKINNY;
+        pl.skinny_tm = M <= 32 ? 1 : 2;
+        bm = 32 * pl.skinny_tm;
+        bn = SKINNY_BN;
+    } else if (ktb == 128 && 2 * ntiles(DENSE_BM, DENSE_BN) <= ncu) {
+        pl.geo = GEO_128;
+        bm = bn = 128;
+    }
+    pl.tiles = ntiles(bm, bn);
+    pl.splits = 1;
+    pl.kt_split = (int)KT;
+    // split K when the tiles fill at most half of the CUs, keeping at least 4
+    // K-tiles per split
+    if (allow_split && pl.geo != GEO_256 && pl.tiles > 0 && 2 * pl.tiles <= ncu && KT >= 8) {
+        int64_t s = (ncu + pl.tiles - 1) / pl.tiles;
+        s = std::min<int64_t>(s, KT / 4);
+        if (s > 1) {
+            const int64_t per = (KT + s - 1) / s;
+            pl.splits = (int)((KT + per - 1) / per);
+            pl.kt_split = (int)per;
+        }
+    }
+    if (pl.splits > 1) pl.ws_bytes = (size_t)pl.splits * (size_t)pl.tiles * (size_t)(bm * bn) * 4;
+    return pl;
+}
+
+template <int MODE, int WM, int WN, int TM, int TN, int KTB, int MINB>
+static int launch_dense_tiles(DenseParams& p, const DensePlan& pl, hipStream_t stream) {
+    using Cfg = DenseCfg<MODE, WM, WN, TM, TN, KTB>;
+    constexpr int LDS = Cfg::lds_bytes(dense_ns<KTB>());
+    static_assert(LDS * MINB <= 160 * 1024, "LDS budget of a CDNA4 CU");
+    auto kern = dense_tile_kernel<MODE, WM, WN, TM, TN, KTB, MINB>;
+    static bool attr_set = false;
+    if (int e = set_lds(kern, LDS, attr_set)) return e;
+    p.tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
+    p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
+    if (p.group_m <= 0) p.group_m = 8;
+    p.splits = pl.splits;
+    p.kt_split = pl.kt_split;
+    const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+    if (tiles == 0) return 0;
+    kern<<<dim3((unsigned)(tiles * p.splits)), 64 * WM * WN, LDS, stream>>>(p);
+    if (int e = hkq_launch_status()) return e;
+    if (p.splits == 1) return 0;
+    const int64_t total = tiles * Cfg::NW * (TN * TM * 4) * 64;  // float4 per split
+    auto red = dense_reduce_kernel<MODE, WM, WN, TM, TN>;
+    red<<<dim3((unsigned)((total + 255) / 256)), 256, 0, stream>>>(p, total);
+    return hkq_launch_status();
+}
+
 template <int MODE, int KTB>
-static int launch_dense_ktb(DenseParams& p, hipStream_t stream) {
+static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
     constexpr int LDS = dense_lds<MODE, KTB>();
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
     auto kern = dense_gemm_kernel<MODE, KTB>;
     static bool attr_set = false;  // per instantiation; the attribute is per-process
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
-        if (e != hipSuccess) {
-            set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", LDS, hipGetErrorString(e));
-            return (int)e;
-        }
-        attr_set = true;
-    }
+    if (int e = set_lds(kern, LDS, attr_set)) return e;
     p.tiles_m = (p.M + DENSE_BM - 1) / DENSE_BM;
     p.tiles_n = (p.N + DENSE_BN - 1) / DENSE_BN;
     if (p.group_m <= 0) p.group_m = 8;
-    p.c16 = (p.ldc % 8 == 0) && (reinterpret_cast<uintptr_t>(p.C) % 16 == 0);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     if (tiles == 0) return 0;
     // Split the last round into M halves when it would fill at most half of the
@@ -188,9 +386,26 @@ static int launch_dense_ktb(DenseParams& p, hipStream_t stream) {
 
 // 128-byte K-tiles need whole 128-byte K-tiles in every row: a partial last
 // K-tile would read the next row's bytes instead of zeros.
+template <int MODE, int KTB>
+static int launch_dense_ktb(DenseParams& p, void* ws, size_t ws_bytes, hipStream_t stream) {
+    p.c16 = (p.ldc % 8 == 0) && (reinterpret_cast<uintptr_t>(p.C) % 16 == 0);
+    DensePlan pl = dense_plan(p.M, p.N, p.kbytes, true);
+    if (pl.splits > 1 && (ws == nullptr || ws_bytes < pl.ws_bytes)) pl = dense_plan(p.M, p.N, p.kbytes, false);
+    p.ws = static_cast<float*>(ws);
+    if constexpr (KTB == 128) {  // smaller tiles need a full 16-byte load per lane for their A rows
+        if (pl.geo == GEO_SKINNY) {
+            if (pl.skinny_tm == 1) return launch_dense_tiles<MODE, 1, SKINNY_WAVES_N, 1, SKINNY_TN, KTB, 1>(p, pl, stream);
+            return launch_dense_tiles<MODE, 1, SKINNY_WAVES_N, 2, SKINNY_TN, KTB, 1>(p, pl, stream);
+        }
+        if (pl.geo == GEO_128) return launch_dense_tiles<MODE, 2, 2, 2, 2, KTB, 2>(p, pl, stream);
+    }
+    return launch_dense_whole<MODE, KTB>(p, stream);
+}
+
 template <int MODE>
-static int launch_dense(DenseParams& p, hipStream_t stream) {
-    return p.kbytes % 128 == 0 ? launch_dense_ktb<MODE, 128>(p, stream) : launch_dense_ktb<MODE, 64>(p, stream);
+static int launch_dense(DenseParams& p, void* ws, size_t ws_bytes, hipStream_t stream) {
+    return p.kbytes % 128 == 0 ? launch_dense_ktb<MODE, 128>(p, ws, ws_bytes, stream)
+                               : launch_dense_ktb<MODE, 64>(p, ws, ws_bytes, stream);
 }
 
 }  // namespace hkq
@@ -208,8 +423,14 @@ static int check_common(int64_t M, int64_t N, int64_t K, int64_t ldc, const void
 
 extern "C" {
 
-int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M, int64_t N,
-                  int64_t K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t stream) {
+size_t hkq_gemm_a8w8_workspace(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0) return 0;
+    return dense_plan(M, N, K, true).ws_bytes;
+}
+
+int hkq_gemm_a8w8_ws(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M, int64_t N,
+                     int64_t K, int64_t lda, int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
     if (int e = check_common(M, N, K, ldc, C)) return e;
     HKQ_CHECK_ARG(K % 64 == 0, "K must be a multiple of 64");
     HKQ_CHECK_ARG(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0,
@@ -217,6 +438,7 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
     HKQ_CHECK_ALIGN(A, 16);
     HKQ_CHECK_ALIGN(B, 16);
     HKQ_CHECK_ALIGN(sb, 16);
+    HKQ_CHECK_ALIGN(workspace, 16);
     DenseParams p{};
     p.A = static_cast<const uint8_t*>(A);
     p.B = static_cast<const uint8_t*>(B);
@@ -225,11 +447,22 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
     p.sb = sb;
     p.M = (int)M; p.N = (int)N; p.K = (int)K; p.kbytes = (int)K;
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
-    return launch_dense<MODE_A8W8>(p, stream);
+    return launch_dense<MODE_A8W8>(p, workspace, workspace_bytes, stream);
 }
 
-int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
-                   int64_t K, int64_t lda, int64_t ldb, int64_t ldsa, int64_t ldsb, int64_t ldc, hipStream_t stream) {
+int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M, int64_t N,
+                  int64_t K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t stream) {
+    return hkq_gemm_a8w8_ws(A, B, sa, sb, C, M, N, K, lda, ldb, ldc, nullptr, 0, stream);
+}
+
+size_t hkq_gemm_mxfp4_workspace(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return 0;
+    return dense_plan(M, N, K / 2, true).ws_bytes;
+}
+
+int hkq_gemm_mxfp4_ws(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
+                      int64_t K, int64_t lda, int64_t ldb, int64_t ldsa, int64_t ldsb, int64_t ldc, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream) {
     if (int e = check_common(M, N, K, ldc, C)) return e;
     HKQ_CHECK_ARG(K % 128 == 0, "K must be a multiple of 128");
     HKQ_CHECK_ARG(lda >= K / 2 && ldb >= K / 2 && lda % 16 == 0 && ldb % 16 == 0,
@@ -240,6 +473,7 @@ int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs,
     HKQ_CHECK_ALIGN(B, 16);
     HKQ_CHECK_ALIGN(As, 4);
     HKQ_CHECK_ALIGN(Bs, 4);
+    HKQ_CHECK_ALIGN(workspace, 16);
     DenseParams p{};
     p.A = static_cast<const uint8_t*>(A);
     p.B = static_cast<const uint8_t*>(B);
@@ -249,7 +483,12 @@ int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs,
     p.M = (int)M; p.N = (int)N; p.K = (int)K; p.kbytes = (int)(K / 2);
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
     p.lsa = ldsa; p.lsb = ldsb;
-    return launch_dense<MODE_MXFP4>(p, stream);
+    return launch_dense<MODE_MXFP4>(p, workspace, workspace_bytes, stream);
+}
+
+int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
+                   int64_t K, int64_t lda, int64_t ldb, int64_t ldsa, int64_t ldsb, int64_t ldc, hipStream_t stream) {
+    return hkq_gemm_mxfp4_ws(A, As, B, Bs, C, M, N, K, lda, ldb, ldsa, ldsb, ldc, nullptr, 0, stream);
 }
 
 }  // extern "C"

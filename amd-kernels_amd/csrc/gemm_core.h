@@ -135,8 +135,8 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 
 // Epilogue shared by the GEMMs: scale in registers, stage each wave's bf16
 // (TM*32) x (TN*32) sub-tile in LDS (row m, col n, row pitch TN*64 + 16 bytes),
-// then store whole 256-byte row segments of C (16-byte stores when C's rows are
-// 16-byte aligned, else two 8-byte stores; N % 4 == 0). The caller has retired
+// then store whole row segments of C (TN*64 bytes: 128 or 256; 16-byte stores
+// when C's rows are 16-byte aligned, else two 8-byte stores; N % 4 == 0). The caller has retired
 // every LDS use of the main loop (a vmcnt(0) barrier) before calling.
 //   acc[i][j]: accumulator of n-tile i, m-tile j, D[n][m] layout
 //   (lane: m = lane & 31; register r: n = 8*(r/4) + 4*(lane/32) + r%4);
@@ -148,7 +148,7 @@ __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uin
                                                 uint16_t* C, int64_t ldc, int M, int N, int mw, int nw, bool c16,
                                                 RowScale row_scale, ColScale4 col_scale4, ColBias4 col_bias4) {
     constexpr int PITCH = TN * 32 * 2 + 16;
-    static_assert((TN * 32 * 2) % 256 == 0, "rows are whole 256-byte segments");
+    static_assert((TN * 32 * 2) % 128 == 0, "rows are whole 128-byte segments");
     HKQ_LDS uint8_t* ep = smem + wave * (TM * 32) * PITCH;
     const int khalf = lane >> 5;
     float rs[TM];
@@ -174,7 +174,7 @@ __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uin
     constexpr int SEGS = TN * 32 * 2 / 16;  // 16-byte pieces per row
     constexpr int ROWS_PER_PASS = 64 / SEGS;
     constexpr int PASSES = TM * 32 / ROWS_PER_PASS;
-    constexpr int BATCH = 8;  // LDS reads in flight before their stores
+    constexpr int BATCH = PASSES < 8 ? PASSES : 8;  // LDS reads in flight before their stores
     static_assert(PASSES % BATCH == 0, "whole batches");
     const int rl = lane / SEGS, seg = lane % SEGS;
     if (c16 && mw + TM * 32 <= M && nw + TN * 32 <= N) {

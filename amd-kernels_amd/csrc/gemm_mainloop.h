@@ -52,7 +52,7 @@ struct DenseCfg {
     static_assert(!SK || (GA % NW == 0 || NW % GA == 0), "A scale groups vs waves");
     static_assert(!SK || (GB % NW == 0 || NW % GB == 0), "B scale groups vs waves");
     static_assert(!SBLK || (SB_GROUPS <= SB_KT * NW && BM % 32 == 0), "scale block groups vs load slots");
-    static_assert((TN * 32 * 2) % 256 == 0, "epilogue rows are whole 256-byte segments");
+    static_assert((TN * 32 * 2) % 128 == 0, "epilogue rows are whole 128-byte segments");
 };
 
 // Where one workgroup's K-tiles come from. `a`/`b` point at the tile's first

@@ -28,6 +28,10 @@ SIGNATURES = {
     "hkq_mx_dequant": (_I, [_P, _P, _P, _I64, _I64, _I, _P]),
     "hkq_gemm_a8w8": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "hkq_gemm_mxfp4": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "hkq_gemm_a8w8_workspace": (ctypes.c_size_t, [_I64, _I64, _I64]),
+    "hkq_gemm_a8w8_ws": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, ctypes.c_size_t, _P]),
+    "hkq_gemm_mxfp4_workspace": (ctypes.c_size_t, [_I64, _I64, _I64]),
+    "hkq_gemm_mxfp4_ws": (_I, [_P, _P, _P, _P, _P] + [_I64] * 8 + [_P, ctypes.c_size_t, _P]),
     "hkq_gemm_blockscale": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "hkq_moe_a8w8": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]
                      + [_I64] * 12 + [_P]),
@@ -134,29 +138,48 @@ def mx_dequant(q, s, K: int, is_fp4: bool = True, stream=None):
     return out
 
 
-def gemm_a8w8(A, B, sa, sb, C=None, stream=None):
-    """A [M, K], B [N, K] E4M3FN codes; sa [M], sb [N] fp32 -> C bf16 [M, N]."""
+def _workspace(nbytes: int, like):
+    import torch
+
+    return torch.empty(nbytes, dtype=torch.uint8, device=like.device) if nbytes else None
+
+
+def gemm_a8w8(A, B, sa, sb, C=None, stream=None, split: bool = True):
+    """A [M, K], B [N, K] E4M3FN codes; sa [M], sb [N] fp32 -> C bf16 [M, N].
+    split=False runs the plain entry point (no workspace, no split-K)."""
     import torch
 
     M, K = A.shape
     N = B.shape[0]
     if C is None:
         C = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
-    call("hkq_gemm_a8w8", _ptr(A), _ptr(B), _ptr(sa), _ptr(sb), _ptr(C), M, N, K, A.stride(0), B.stride(0),
-         C.stride(0), _stream(stream))
+    if not split:
+        call("hkq_gemm_a8w8", _ptr(A), _ptr(B), _ptr(sa), _ptr(sb), _ptr(C), M, N, K, A.stride(0), B.stride(0),
+             C.stride(0), _stream(stream))
+        return C
+    ws = _workspace(lib().hkq_gemm_a8w8_workspace(M, N, K), A)
+    call("hkq_gemm_a8w8_ws", _ptr(A), _ptr(B), _ptr(sa), _ptr(sb), _ptr(C), M, N, K, A.stride(0), B.stride(0),
+         C.stride(0), _ptr(ws) if ws is not None else None, ws.numel() if ws is not None else 0, _stream(stream))
     return C
 
 
-def gemm_mxfp4(A, As, B, Bs, C=None, stream=None):
-    """A u8 [M, K/2], As u8 [M, K/32], B u8 [N, K/2], Bs u8 [N, K/32] -> C bf16 [M, N]."""
+def gemm_mxfp4(A, As, B, Bs, C=None, stream=None, split: bool = True):
+    """A u8 [M, K/2], As u8 [M, K/32], B u8 [N, K/2], Bs u8 [N, K/32] -> C bf16 [M, N].
+    split=False runs the plain entry point (no workspace, no split-K)."""
     import torch
 
     M, K = A.shape[0], A.shape[1] * 2
     N = B.shape[0]
     if C is None:
         C = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
-    call("hkq_gemm_mxfp4", _ptr(A), _ptr(As), _ptr(B), _ptr(Bs), _ptr(C), M, N, K, A.stride(0), B.stride(0),
-         As.stride(0), Bs.stride(0), C.stride(0), _stream(stream))
+    if not split:
+        call("hkq_gemm_mxfp4", _ptr(A), _ptr(As), _ptr(B), _ptr(Bs), _ptr(C), M, N, K, A.stride(0), B.stride(0),
+             As.stride(0), Bs.stride(0), C.stride(0), _stream(stream))
+        return C
+    ws = _workspace(lib().hkq_gemm_mxfp4_workspace(M, N, K), A)
+    call("hkq_gemm_mxfp4_ws", _ptr(A), _ptr(As), _ptr(B), _ptr(Bs), _ptr(C), M, N, K, A.stride(0), B.stride(0),
+         As.stride(0), Bs.stride(0), C.stride(0), _ptr(ws) if ws is not None else None,
+         ws.numel() if ws is not None else 0, _stream(stream))
     return C
 
 

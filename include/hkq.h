@@ -20,6 +20,7 @@
 #ifndef HKQ_H
 #define HKQ_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -86,6 +87,21 @@ int hkq_mx_dequant(const void* q, const void* s, void* out, int64_t M, int64_t K
 int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M, int64_t N,
                   int64_t K, int64_t lda, int64_t ldb, int64_t ldc, hkq_stream_t stream);
 
+/* hkq_gemm_a8w8 with a caller-provided device workspace (16-byte aligned).
+ * Shapes whose tiles would fill at most half of the CUs (256 x 256 tiles
+ * become 128 x 128, or (32 or 64) x 256 for M <= 64, first) split K over
+ * several workgroups and add the fp32 partials in a second kernel; that needs
+ * hkq_gemm_a8w8_workspace(M, N, K) bytes (0: no split for this shape). With a smaller workspace (or NULL) the
+ * call runs unsplit. Same results either way up to fp32 summation order. The
+ * workspace is in use until the work queued on `stream` completes. No
+ * counterpart in the reference, whose kernels have no split path; the drop-in
+ * modules (gemm_a8w8_tk, gemm_a8w8_per_token_scale_tk) call it with a
+ * workspace from torch's allocator. */
+size_t hkq_gemm_a8w8_workspace(int64_t M, int64_t N, int64_t K);
+int hkq_gemm_a8w8_ws(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M, int64_t N,
+                     int64_t K, int64_t lda, int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes,
+                     hkq_stream_t stream);
+
 /* MXFP4 A4W4: C = bf16(sum_k e2m1(A) 2^(As-127) e2m1(B) 2^(Bs-127)).
  * A u8 [M, lda >= K/2], As u8 [M, ldsa >= K/32], B u8 [N, ldb], Bs u8 [N, ldsb].
  * K % 128 == 0, N % 4 == 0, ldc % 4 == 0. Replaces gemm_afp4wfp4_tk.dispatch (kernels/gemm-basic/gemm_afp4wfp4/kernel.cpp:147-159),
@@ -93,6 +109,14 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
  * pre-dequantized bf16. */
 int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
                    int64_t K, int64_t lda, int64_t ldb, int64_t ldsa, int64_t ldsb, int64_t ldc, hkq_stream_t stream);
+
+/* hkq_gemm_mxfp4 with a caller-provided workspace: the split-K plan of
+ * hkq_gemm_a8w8_ws for the MXFP4 GEMM (no counterpart in the reference;
+ * gemm_afp4wfp4_tk calls it with a workspace from torch's allocator). */
+size_t hkq_gemm_mxfp4_workspace(int64_t M, int64_t N, int64_t K);
+int hkq_gemm_mxfp4_ws(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
+                      int64_t K, int64_t lda, int64_t ldb, int64_t ldsa, int64_t ldsb, int64_t ldc, void* workspace,
+                      size_t workspace_bytes, hkq_stream_t stream);
 
 /* Block-scale FP8 GEMM (DeepSeek-V3 style):
  * C = bf16(sum_g (A_g . B_g^T) * sa[m, g] * sb[g, n / group_n]), g = 128-wide K group.

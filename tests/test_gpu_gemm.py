@@ -88,6 +88,44 @@ def test_gemm_a8w8_baseline_sizes_sampled(orc, M, N, K):
     assert np.isfinite(C).all()
 
 
+# Smaller-tile and split-K plans: M <= 128 uses (32..128) x 256 tiles, few
+# 256 x 256 tiles become 128 x 128 tiles, and if those are still few (with a
+# long enough K) K is split into fp32 partials added by a second kernel.
+SPLIT_SHAPES = [(1, 4096, 14336), (16, 2048, 4096), (48, 1024, 2048), (128, 4096, 4096), (96, 28672, 4096),
+                (1024, 4096, 14336), (640, 1000, 8192), (256, 1024, 8192), (300, 2052, 2048)]
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
+def test_gemm_a8w8_split_and_skinny(orc, M, N, K):
+    """The split plan, the same shape through the plain entry point (no
+    workspace) and the oracle on a sampled block agree."""
+    require_gpu()
+    A, B, sa, sb = a8w8_inputs(orc, M, N, K, seed=M + 3 * N + K)
+    Ad, Bd, sad, sbd = dev_u8(A), dev_u8(B), dev_f32(sa), dev_f32(sb)
+    C1 = hkq.gemm_a8w8(Ad, Bd, sad, sbd)
+    C0 = hkq.gemm_a8w8(Ad, Bd, sad, sbd, split=False)
+    torch.cuda.synchronize()
+    c1, c0 = host_bf16_f32(C1), host_bf16_f32(C0)
+    np.testing.assert_allclose(c1, c0, rtol=1e-2, atol=2e-2)
+    rng = np.random.default_rng(N)
+    rows = np.sort(rng.choice(M, min(M, 64), replace=False))
+    cols = np.sort(rng.choice(N, min(N, 96), replace=False))
+    rows[-1], cols[-1] = M - 1, N - 1
+    ref = orc.gemm_a8w8_ref(A[rows], B[cols], sa[rows], sb[cols])
+    assert_gemm_close(c1[np.ix_(rows, cols)], ref, f"a8w8 split {M}x{N}x{K}")
+
+
+def test_gemm_workspace_plans():
+    """Shapes that fill the GPU need no workspace; underfilled ones do."""
+    require_gpu()
+    L = hkq.lib()
+    assert L.hkq_gemm_a8w8_workspace(4096, 14336, 4096) == 0
+    assert L.hkq_gemm_a8w8_workspace(16, 4096, 14336) > 0
+    assert L.hkq_gemm_a8w8_workspace(256, 1024, 8192) > 0
+    assert L.hkq_gemm_mxfp4_workspace(4096, 8192, 8192) == 0
+    assert L.hkq_gemm_mxfp4_workspace(16, 8192, 8192) > 0
+
+
 def mx_inputs(orc, M, N, K, seed):
     xa = orc.randn_bf16((M, K), seed=seed)
     xw = orc.randn_bf16((N, K), seed=seed + 1, std=0.02)
@@ -199,3 +237,21 @@ def test_gemm_blockscale_baseline_sizes_sampled(orc, N, K):
     ref = orc.gemm_blockscale_ref(A[rows], B[cols], sa[rows], sb_cols, 128, 1)
     assert_gemm_close(C[np.ix_(rows, cols)], ref, f"blockscale {M}x{N}x{K} sampled")
     assert np.isfinite(C).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 8192), (32, 2048, 8192), (128, 8192, 8192), (512, 1024, 16384)])
+def test_gemm_mxfp4_split_and_skinny(orc, M, N, K):
+    require_gpu()
+    Aq, As, Bq, Bs = mx_inputs(orc, M, N, K, seed=M + K + 5)
+    args = [dev_u8(a) for a in (Aq, As, Bq, Bs)]
+    C1 = hkq.gemm_mxfp4(*args)
+    C0 = hkq.gemm_mxfp4(*args, split=False)
+    torch.cuda.synchronize()
+    c1, c0 = host_bf16_f32(C1), host_bf16_f32(C0)
+    np.testing.assert_allclose(c1, c0, rtol=1e-2, atol=2e-2)
+    rng = np.random.default_rng(K)
+    rows = np.sort(rng.choice(M, min(M, 48), replace=False))
+    cols = np.sort(rng.choice(N, 64, replace=False))
+    rows[-1], cols[-1] = M - 1, N - 1
+    ref = orc.gemm_mxfp4_ref(Aq[rows], As[rows], Bq[cols], Bs[cols])
+    assert_gemm_close(c1[np.ix_(rows, cols)], ref, f"mxfp4 split {M}x{N}x{K}")
