@@ -128,7 +128,10 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
         const bool isa = g * 32 < BM;
         const uint8_t* base = (isa ? src.as : src.bs) + blk * 32;
         const int64_t bytes = (isa ? src.as_bytes : src.bs_bytes) - blk * 32;
-        const uint32_t off = (uint32_t)((isa ? r : r - BM) * (isa ? src.lsa : src.lsb)) + (uint32_t)((lane & 1) * 16);
+        // row slot s = lane / 2 of the group; its two 16-byte halves are stored
+        // swapped when bit 3 of s is set (see read_scale)
+        const uint32_t half = (uint32_t)((lane & 1) ^ ((lane >> 4) & 1));
+        const uint32_t off = (uint32_t)((isa ? r : r - BM) * (isa ? src.lsa : src.lsb)) + half * 16u;
         lds_load16(base, live && bytes > 0 ? (uint32_t)bytes : 0u, sblk + (blk & 1) * Cfg::SB_SLOT + g * 1024, off);
     };
 
@@ -203,9 +206,13 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
             const int row = (isa ? arow : brow) + t * 32;
             int w;
             if constexpr (Cfg::SBLK) {
+                // byte o = 8 * (kt % 4) + 4h of the row's 32; the 16-byte halves of
+                // rows with bit 3 set are swapped, so the 32 lanes of a read (32
+                // consecutive rows, 32-byte pitch) hit 16 distinct bank pairs
                 const HKQ_LDS uint8_t* slot = sblk + ((kt / Cfg::SB_KT) & 1) * Cfg::SB_SLOT;
-                w = *reinterpret_cast<const HKQ_LDS int*>(slot + (isa ? row : BM + row) * 32 + (kt % Cfg::SB_KT) * 8 +
-                                                         khalf * 4);
+                const int ra = isa ? row : BM + row;
+                const int o = (kt % Cfg::SB_KT) * 8 + khalf * 4;
+                w = *reinterpret_cast<const HKQ_LDS int*>(slot + ra * 32 + (o ^ (((ra >> 3) & 1) << 4)));
             } else {
                 const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KTB + (isa ? 0 : SCA);
                 w = *reinterpret_cast<const HKQ_LDS uint16_t*>(sca + row * 4 + khalf * 2);

@@ -67,6 +67,22 @@ def call(name: str, *args) -> None:
         raise HkqError(f"{name} failed with code {rc}: {msg}")
 
 
+def bind(name: str, *args):
+    """Zero-argument callable that repeats one C-ABI call with fixed arguments:
+    the arguments are converted to ctypes once, so back-to-back launches of a
+    short kernel are not limited by Python-side argument handling."""
+    fn = getattr(lib(), name)
+    cargs = [t(a) if a is not None else None for t, a in zip(SIGNATURES[name][1], args)]
+
+    def run():
+        rc = fn(*cargs)
+        if rc != 0:
+            msg = lib().hkq_last_error().decode(errors="replace")
+            raise HkqError(f"{name} failed with code {rc}: {msg}")
+
+    return run
+
+
 # ----------------------------------------------------------------------------
 # torch-tensor conveniences over the C ABI (device pointers + current stream)
 # ----------------------------------------------------------------------------

@@ -38,6 +38,9 @@ HEADLINE = dict(M=4096, N=14336, K=4096)
 MXFP4 = dict(M=4096, N=8192, K=8192)
 BLOCKSCALE = [(2048, 24576, 1536), (2048, 7168, 18432), (2048, 7168, 2048)]
 MOE = dict(T=4096, E=8, topk=2, hidden=4096, ffn=14336)
+# A8W8 shape sweep (N, K) x M of the reference's GEMM benchmark configuration
+SWEEP_NK = [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)]
+SWEEP_M = [1, 16, 128, 1024, 4096]
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_a8w8_4096x14336x4096_pmc.txt")
 
 
@@ -63,10 +66,10 @@ def seeded_bf16_dev(shape, std, seed):
     return (torch.randn(*shape, generator=g, device="cuda") * std).to(torch.bfloat16)
 
 
-def time_launches(fn, steps, warmup):
+def time_launches(fn, steps, warmup, preheat=PREHEAT_S):
     """Average ms per launch over `steps` back-to-back launches on the current stream.
 
-    Before the `warmup` launches, the kernel runs untimed for PREHEAT_S seconds:
+    Before the `warmup` launches, the kernel runs untimed for `preheat` seconds:
     MI355X engine clocks take tens of milliseconds of sustained load to settle,
     and a handful of warmup launches would otherwise time a ramping clock."""
     import time
@@ -74,7 +77,7 @@ def time_launches(fn, steps, warmup):
     import torch
 
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < PREHEAT_S:
+    while time.perf_counter() - t0 < preheat:
         for _ in range(10):
             fn()
         torch.cuda.synchronize()
@@ -123,7 +126,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant", "blockscale", "moe", "copy"], default=None,
+    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant", "blockscale", "moe", "sweep", "copy"], default=None,
                     help="run one kernel only (for profiling); prints no JSON line. 'copy' is a plain "
                          "1 GiB device copy used to calibrate the HBM byte counters")
     args = ap.parse_args()
@@ -180,7 +183,11 @@ def main():
         q = torch.empty((4096, 4096), dtype=torch.float8_e4m3fn, device="cuda")
         s = torch.empty((4096,), dtype=torch.float32, device="cuda")
         log("per-token quant 4096x4096")
-        res["quant"] = time_launches(lambda: hkq.per_token_quant(xq, hkq.KIND_FP8, q, s), steps, warmup)
+        # pre-bound C-ABI call: a ~10 us kernel would otherwise be timed at the
+        # rate Python can enqueue it
+        launch = hkq.bind("hkq_per_token_quant", xq.data_ptr(), q.data_ptr(), s.data_ptr(), 4096, 4096, xq.stride(0),
+                          q.stride(0), hkq.KIND_FP8, torch.cuda.current_stream().cuda_stream)
+        res["quant"] = time_launches(launch, steps, warmup)
 
     # ---- block-scale FP8 GEMM at the DeepSeek-V3 shapes (1x128 act / 128x128 weight scales) ----
     bs_res = []
@@ -226,8 +233,49 @@ def main():
             del wq
         res["moe"] = sum(r["ms"] for r in moe_res)
 
+    # ---- A8W8 shape sweep and the MXFP4 M=128 configuration (plans with smaller tiles / split K) ----
+    sweep = []
+    if args.only in (None, "sweep"):
+        log("a8w8 sweep")
+        for (nn, kk) in SWEEP_NK:
+            wb = torch.randint(0, 0x70, (nn, kk), dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
+            wsb = torch.rand(nn, device="cuda") * 1e-3
+            for mm in SWEEP_M:
+                if (mm, nn, kk) == (M, N, K):
+                    continue
+                xa = torch.randint(0, 0x70, (mm, kk), dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
+                xsa = torch.rand(mm, device="cuda")
+                Cs = torch.empty((mm, nn), dtype=torch.bfloat16, device="cuda")
+                nws = hkq.lib().hkq_gemm_a8w8_workspace(mm, nn, kk)
+                wsp = torch.empty(max(nws, 16), dtype=torch.uint8, device="cuda")
+                launch = hkq.bind("hkq_gemm_a8w8_ws", xa.data_ptr(), wb.data_ptr(), xsa.data_ptr(), wsb.data_ptr(),
+                                  Cs.data_ptr(), mm, nn, kk, kk, kk, nn, wsp.data_ptr(), nws,
+                                  torch.cuda.current_stream().cuda_stream)
+                ms_s = time_launches(launch, 20, 3, preheat=0.05)
+                byts = mm * kk + nn * kk + 2 * mm * nn + 4 * (mm + nn)
+                sweep.append({"M": mm, "N": nn, "K": kk, "us": round(ms_s * 1e3, 2),
+                              "tflops": round(2.0 * mm * nn * kk / (ms_s * 1e-3) / 1e12, 1),
+                              "GB/s": round(byts / (ms_s * 1e-3) / 1e9, 1)})
+        m4, n4, k4 = 128, MXFP4["N"], MXFP4["K"]
+        xa4, xw4 = seeded_bf16((m4, k4), 1.0, 11), seeded_bf16((n4, k4), 0.02, 12)
+        Aq4, As4 = hkq.mx_quant(xa4, True)
+        Bq4, Bs4 = hkq.mx_quant(xw4, True)
+        C4s = torch.empty((m4, n4), dtype=torch.bfloat16, device="cuda")
+        nws = hkq.lib().hkq_gemm_mxfp4_workspace(m4, n4, k4)
+        wsp = torch.empty(max(nws, 16), dtype=torch.uint8, device="cuda")
+        launch = hkq.bind("hkq_gemm_mxfp4_ws", Aq4.data_ptr(), As4.data_ptr(), Bq4.data_ptr(), Bs4.data_ptr(),
+                          C4s.data_ptr(), m4, n4, k4, Aq4.stride(0), Bq4.stride(0), As4.stride(0), Bs4.stride(0), n4,
+                          wsp.data_ptr(), nws, torch.cuda.current_stream().cuda_stream)
+        ms_s = time_launches(launch, 20, 3, preheat=0.05)
+        sweep.append({"kind": "mxfp4", "M": m4, "N": n4, "K": k4, "us": round(ms_s * 1e3, 2),
+                      "tflops": round(2.0 * m4 * n4 * k4 / (ms_s * 1e-3) / 1e12, 1)})
+        res["sweep"] = sum(r["us"] for r in sweep) * 1e-3
+
     if args.only is not None:
         log(json.dumps({k: round(v * 1e3, 2) for k, v in res.items()}) + "  (us per launch)")
+        if sweep:
+            for r in sweep:
+                log(json.dumps(r))
         return
 
     ms = res["a8w8"]
@@ -271,6 +319,7 @@ def main():
                                 "pct_hbm_peak": round(100 * quant_gbs / PEAK_HBM_GBS, 2)},
         "blockscale": bs_res,
         "moe_mixtral": moe_res,
+        "sweep": sweep,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_FP8_TFLOPS, 4), "traffic": read_traffic()},
         "cpu_baseline": cpu,
