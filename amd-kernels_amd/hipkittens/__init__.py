@@ -9,6 +9,8 @@ the modules this build provides:
     hk.gemm.a8w8_per_token.dispatch(A, B, C, a_s, b_s)     # gemm_a8w8_per_token_scale_tk
     hk.gemm.afp4wfp4.dispatch(A, B, C, A_scale, B_scale)   # gemm_afp4wfp4_tk
     hk.moe_routing.quant.downcast_to_mxfp(...)             # quant_moe_tk
+    hk.moe_routing.topk.moe_topk(X, ...)                   # moe_topk_tk (also bitmatrix,
+                                                           # expt_data, align_block_size)
     hk.modules["gemm_a8w8_tk"]                             # any module by name
 
 Discovery contract (reference hipkittens/__init__.py:31-62): extension files
@@ -156,7 +158,13 @@ class _MoeGemmNamespace:
 
 
 class _MoeRoutingNamespace:
+    align_block_size = _SubModule("moe_align_block_size_tk")
+    bitmatrix = _SubModule("moe_bitmatrix_tk")
+    expt_data = _SubModule("moe_expt_data_tk")
+    topk = _SubModule("moe_topk_tk")
     quant = _SubModule("quant_moe_tk")
+    # extension: the gate placement the reference compiles without a binding
+    routing = _SubModule("moe_routing_tk")
 
 
 gemm = _GemmNamespace()

@@ -35,6 +35,16 @@ SIGNATURES = {
     "hkq_gemm_blockscale": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "hkq_moe_a8w8": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]
                      + [_I64] * 12 + [_P]),
+    "hkq_moe_topk": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _I, _P]),
+    "hkq_sum_bitmatrix_rows": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "hkq_sum_bitmatrix_rows_fused": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P]),
+    "hkq_expt_data_stage1": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P]),
+    "hkq_expt_data_stage2": (_I, [_P, _P, _P, _I64, _I, _P]),
+    "hkq_expt_data_stage2_fused": (_I, [_P, _P, _P, _I64, _P]),
+    "hkq_expt_data_compute": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P]),
+    "hkq_routing_compute_indx": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I, _P]),
+    "hkq_routing_compute_indx_fused": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _P]),
+    "hkq_moe_align_block_size": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
 }
 
 
@@ -239,3 +249,122 @@ def moe_a8w8(X, W, hist, offs, expt_data, topk, gather=None, x_scale=None, w_sca
          _ptr(hist), _ptr(offs), _ptr(expt_data), T, E, N, K, expt_data.numel(), topk, X.stride(0), W.stride(0),
          W.stride(1), Y.stride(0), rows, gather.numel() if gather is not None else 0, _stream(stream))
     return Y
+
+
+# ----------------------------------------------------------------------------
+# MoE routing metadata (GPU producers of the tensors moe_a8w8 consumes)
+# ----------------------------------------------------------------------------
+
+def _opt_ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def moe_topk(logits, K: int, softmax: bool = True, bitmatrix: bool = True, stream=None):
+    """Top-K experts per row of bf16 logits [T, E]: (values bf16 [T, K],
+    experts int32 [T, K], bitmatrix int32 [T, ceil(E/32)] or None)."""
+    import torch
+
+    T, E = logits.shape
+    Yv = torch.empty((T, K), dtype=torch.bfloat16, device=logits.device)
+    Yi = torch.empty((T, K), dtype=torch.int32, device=logits.device)
+    nw = (E + 31) // 32
+    bits = torch.empty((T, nw), dtype=torch.int32, device=logits.device) if bitmatrix else None
+    call("hkq_moe_topk", _ptr(logits), logits.stride(0), _ptr(Yv), _ptr(Yi), K, _opt_ptr(bits), nw, 1, T, E, K,
+         int(softmax), _stream(stream))
+    return Yv, Yi, bits
+
+
+def sum_bitmatrix_rows(bits, partials: bool = True, stream=None):
+    """Column sums of a row-major bitmatrix int32 [T, nw]: (hist int32 [32*nw],
+    partials int32 [ceil(T/128), 32*nw] (exclusive over 128-row tiles) or None)."""
+    import torch
+
+    T, nw = bits.shape
+    ret = torch.empty(32 * nw, dtype=torch.int32, device=bits.device)
+    if not partials:
+        call("hkq_sum_bitmatrix_rows_fused", _ptr(bits), T, bits.stride(0), 1, _ptr(ret), nw, _stream(stream))
+        return ret, None
+    part = torch.empty(((T + 127) // 128, 32 * nw), dtype=torch.int32, device=bits.device)
+    call("hkq_sum_bitmatrix_rows", _ptr(bits), T, bits.stride(0), 1, _ptr(ret), _ptr(part), part.stride(0), 1,
+         32 * nw, nw, _stream(stream))
+    return ret, part
+
+
+def expt_data(hist, n_gates: int, tile_log2: int = 7, max_tiles: int | None = None, stream=None):
+    """OGS expert data: (token_start int32 [E+1], tile_start int32 [E+1], tile
+    metadata int32 [max_tiles], -1 past the last tile). The default max_tiles,
+    n_gates // 2^tile_log2 + E, bounds the tile count for any histogram."""
+    import torch
+
+    E = hist.numel()
+    if max_tiles is None:
+        max_tiles = n_gates // (1 << tile_log2) + E
+    ts = torch.empty(E + 1, dtype=torch.int32, device=hist.device)
+    tl = torch.empty(E + 1, dtype=torch.int32, device=hist.device)
+    md = torch.empty(max(max_tiles, 1), dtype=torch.int32, device=hist.device)
+    call("hkq_expt_data_compute", _ptr(hist), _ptr(ts), _ptr(tl), _ptr(md), E, max_tiles, n_gates, tile_log2, 0,
+         _stream(stream))
+    return ts, tl, md[:max_tiles]
+
+
+def compute_indx(expt_indx, tokens_start, partial_offs=None, expt_scal=None, n_slots: int | None = None,
+                 stream=None):
+    """Gate placement for expert ids [T, K]: (gather int32 [n_slots], scatter
+    int32 [T*K], gate_scal bf16 [n_slots] or None); partial_offs int32
+    [ceil(T/128), E] from sum_bitmatrix_rows, or None (counted in one workgroup)."""
+    import torch
+
+    T, K = expt_indx.shape
+    n = T * K
+    n_slots = n if n_slots is None else n_slots
+    dev = expt_indx.device
+    gather = torch.empty(max(n_slots, 1), dtype=torch.int32, device=dev)
+    scatter = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    gs = torch.empty(max(n_slots, 1), dtype=torch.bfloat16, device=dev) if expt_scal is not None else None
+    if partial_offs is None:
+        call("hkq_routing_compute_indx_fused", _ptr(gather), _ptr(scatter), _opt_ptr(gs), _opt_ptr(expt_scal),
+             _ptr(expt_indx), _ptr(tokens_start), n, K, _stream(stream))
+    else:
+        call("hkq_routing_compute_indx", _ptr(gather), _ptr(scatter), _opt_ptr(gs), _opt_ptr(expt_scal),
+             _ptr(expt_indx), _ptr(partial_offs), partial_offs.stride(0), partial_offs.stride(1),
+             _ptr(tokens_start), n, K, _stream(stream))
+    return gather[:n_slots], scatter[:n], (None if gs is None else gs[:n_slots])
+
+
+def moe_routing(logits, topk: int, block_m: int = 128, softmax: bool = True, stream=None):
+    """Router logits bf16 [T, E] -> the OGS metadata of moe_a8w8, on the GPU and
+    without a host synchronisation: top-k (+ bitmatrix), its column sums with
+    per-128-token partials, expert data, and the gate placement. Returns a dict
+    with topk_vals, topk_idx, hist, offs, tile_start, expt_data (tiles of
+    block_m rows, -1 past the last), gather, scatter, gate_scal."""
+    T, E = logits.shape
+    yv, yi, bits = moe_topk(logits, topk, softmax, True, stream)
+    hist, part = sum_bitmatrix_rows(bits, True, stream)
+    hist = hist[:E]
+    log2 = block_m.bit_length() - 1
+    assert (1 << log2) == block_m, "block_m must be a power of two"
+    ts, tl, md = expt_data(hist, T * topk, log2, stream=stream)
+    gather, scatter, gs = compute_indx(yi, ts, part, yv, stream=stream)
+    return {"topk_vals": yv, "topk_idx": yi, "hist": hist, "offs": ts[:E], "tile_start": tl, "expt_data": md,
+            "gather": gather, "scatter": scatter, "gate_scal": gs}
+
+
+def align_block_size(topk_ids, num_experts: int, block_size: int, stream=None):
+    """moe_align_block_size over flattened expert ids: (sorted_token_ids int32
+    [numel + E*(block_size-1)], expert_ids int32 [len(sorted) // block_size],
+    cumsum int32 [E+1], total int32 [1]); only the first total entries of
+    sorted_token_ids (and total // block_size of expert_ids) are written."""
+    import torch
+
+    numel = topk_ids.numel()
+    dev = topk_ids.device
+    cap = numel + num_experts * (block_size - 1)
+    sorted_ids = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+    eids = torch.empty(max(cap // block_size, 1), dtype=torch.int32, device=dev)
+    cnts = torch.empty((num_experts + 1) * num_experts, dtype=torch.int32, device=dev)
+    cum = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    total = torch.empty(1, dtype=torch.int32, device=dev)
+    call("hkq_moe_align_block_size", _ptr(topk_ids), _ptr(sorted_ids), _ptr(eids), _ptr(cnts), _ptr(cum),
+         _ptr(total), num_experts, block_size, numel, _stream(stream))
+    return sorted_ids, eids, cum, total
+

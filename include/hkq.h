@@ -155,6 +155,88 @@ int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* x_scale, in
                  int64_t stride_xm, int64_t stride_we, int64_t stride_wn, int64_t stride_ym, int64_t y_rows,
                  int64_t gather_len, hkq_stream_t stream);
 
+/* ---- MoE routing metadata producers --------------------------------------- */
+/* All index outputs are deterministic: gates of one expert keep their input
+ * order (the order of the reference's test formulas, tests/test_moe.py:97-128,
+ * 229-256), and no output needs to be cleared beforehand. */
+
+/* Top-K of each row of bf16 logits X [n_rows, stride_xm] (n_expts_tot <= 1024,
+ * 1 <= K <= 16): Yi[r*stride_ym + k] = expert of the k-th largest logit (ties:
+ * lower expert first; -0 == +0; NaN and -inf never chosen; -1 when fewer than
+ * K are eligible), Yv = its logit (bf16, -inf for -1), or with apply_softmax
+ * expf(v_k - v_0) * (1 / sum_k expf(v_k - v_0)). Bits (NULL: skipped) gets
+ * ceil(n_expts_tot / 32) words per row at Bits[r*stride_bm + w*stride_bn],
+ * bit e%32 of word e/32 set for each chosen expert. Replaces launch_moe_topk
+ * (kernels/moe-routing/moe_topk/kernel.cpp:218-270), which always writes 8
+ * words and handles only K in {2, 4, 8} over the first 256 experts. */
+int hkq_moe_topk(const void* X, int64_t stride_xm, void* Yv, int32_t* Yi, int64_t stride_ym, uint32_t* Bits,
+                 int64_t stride_bm, int64_t stride_bn, int64_t n_rows, int64_t n_expts_tot, int K, int apply_softmax,
+                 hkq_stream_t stream);
+
+/* Column sums of the bitmatrix B (word w of row r at B[r*stride_bm + w*stride_bn],
+ * shape_bn words per row): Ret[e] = rows with bit e set (32*shape_bn entries);
+ * Partials[t*stride_pm + e*stride_pn] = the same count over the 128-row tiles
+ * before tile t, for t < ceil(shape_bm / 128) and e < shape_pn. Replaces
+ * launch_sum_bitmatrix_rows (kernels/moe-routing/moe_bitmatrix/kernel.cpp:208-241). */
+int hkq_sum_bitmatrix_rows(const uint32_t* B, int64_t shape_bm, int64_t stride_bm, int64_t stride_bn, uint32_t* Ret,
+                           uint32_t* Partials, int64_t stride_pm, int64_t stride_pn, int64_t shape_pn,
+                           int64_t shape_bn, hkq_stream_t stream);
+
+/* Ret only, over all shape_bm rows (the reference reads at most 128). Replaces
+ * launch_sum_bitmatrix_rows_fused (moe_bitmatrix/kernel.cpp:244-297). */
+int hkq_sum_bitmatrix_rows_fused(const uint32_t* B, int64_t shape_bm, int64_t stride_bm, int64_t stride_bn,
+                                 uint32_t* Ret, int64_t n_blks_bitmatrix, hkq_stream_t stream);
+
+/* OGS expert data from the per-expert histogram (n_expts_tot <= 4096), tiles of
+ * 2^tile_dim_log2 rows: TokenStart[e] / TileStart[e] = exclusive prefix sums of
+ * Hist and of ceil(Hist / tile), TokenStart[E] = n_gates, TileStart[E] = total
+ * tiles; MDTileInfo[t] = e | (i << 16) for the i-th tile of expert e and
+ * 0xFFFFFFFF for total <= t < max_num_tiles (entries past max_num_tiles are
+ * never written). Stage 1 writes the starts and the 0xFFFFFFFF tail; stage 2
+ * the tiles from the caller's TileStart; the fused stage 2 only each expert's
+ * first tile. Replace launch_expt_data_stage1 / _stage2 / _stage2_fused /
+ * _compute (kernels/moe-routing/moe_expt_data/kernel.cpp:110-196). */
+int hkq_expt_data_stage1(const int32_t* Hist, int32_t* TokenStart, int32_t* TileStart, uint32_t* MDTileInfo,
+                         int64_t n_expts_tot, int64_t max_num_tiles, int64_t n_gates, int tile_dim_log2,
+                         hkq_stream_t stream);
+int hkq_expt_data_stage2(const int32_t* Hist, const int32_t* TileStart, uint32_t* TileInfo, int64_t n_expts_tot,
+                         int tile_dim_log2, hkq_stream_t stream);
+int hkq_expt_data_stage2_fused(const int32_t* Hist, const int32_t* TileStart, uint32_t* TileInfo, int64_t n_expts_tot,
+                               hkq_stream_t stream);
+int hkq_expt_data_compute(const int32_t* Hist, int32_t* TokenStart, int32_t* TileStart, uint32_t* MDTileInfo,
+                          int64_t n_expts_tot, int64_t max_num_tiles, int64_t n_gates, int tile_dim_log2,
+                          int use_fused_stage2, hkq_stream_t stream);
+
+/* Gate placement (1 <= n_expts_act <= 16): gate g of ExptIndx (flattened
+ * [tokens, n_expts_act], expert ids < 1024) in 128-token block b = g / (128 *
+ * n_expts_act) goes to pos = TokensStart[e] + PartialOffs[b*stride_pm +
+ * e*stride_pn] + (gates of e before g in block b); ScatterIndx[g] = pos,
+ * GatherIndx[pos] = g, GateScal[pos] = ExptScal[g] (bf16; both NULL: skipped).
+ * Gates with an id outside [0, 1024) (e.g. -1) get ScatterIndx = -1. The fused
+ * form takes no PartialOffs and counts across blocks itself, for any n_gates
+ * (the reference's handles one block). Replace launch_routing_compute_indx /
+ * _fused (kernels/moe-routing/moe_routing/kernel.cpp:209-306). */
+int hkq_routing_compute_indx(int32_t* GatherIndx, int32_t* ScatterIndx, void* GateScal, const void* ExptScal,
+                             const int32_t* ExptIndx, const int32_t* PartialOffs, int64_t stride_pm,
+                             int64_t stride_pn, const int32_t* TokensStart, int64_t n_gates, int n_expts_act,
+                             hkq_stream_t stream);
+int hkq_routing_compute_indx_fused(int32_t* GatherIndx, int32_t* ScatterIndx, void* GateScal, const void* ExptScal,
+                                   const int32_t* ExptIndx, const int32_t* TokensStart, int64_t n_gates,
+                                   int n_expts_act, hkq_stream_t stream);
+
+/* Block-padded expert order of numel expert ids (num_experts <= 1024):
+ * cumsum_buffer[e] = sum_{e' < e} ceil(c[e'] / block_size) * block_size with
+ * c = per-expert counts, total_tokens_post_pad[0] = cumsum_buffer[E];
+ * sorted_token_ids[cumsum[e] + i] = index of the i-th id equal to e (input
+ * order), padded slots = numel; expert_ids[j] = e for the blocks of expert e.
+ * Ids outside [0, E) are skipped. tokens_cnts_buffer ((E + 1) * E int32) is
+ * scratch. sorted_token_ids needs total entries (at most numel + E *
+ * (block_size - 1)). Replaces launch_moe_align_block_size
+ * (kernels/moe-routing/moe_align_block_size/kernel.cpp:131-181). */
+int hkq_moe_align_block_size(const int32_t* topk_ids, int32_t* sorted_token_ids, int32_t* expert_ids,
+                             int32_t* tokens_cnts_buffer, int32_t* cumsum_buffer, int32_t* total_tokens_post_pad,
+                             int64_t num_experts, int64_t block_size, int64_t numel, hkq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

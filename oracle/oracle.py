@@ -35,6 +35,17 @@ gemm refs              reference formulas (tests/test_gemm.py:116,148-153,
 moe_ref / ogs_routing  tests/test_moe.py:97-128,733-753 restated; invariants
                        (histogram sum, exclusive scan, gather permutation) and
                        agreement with per-expert dense GEMMs.
+topk                   torch.topk + torch.softmax (fp64) on tie-free logits;
+                       brute-force sort by (-value, expert) on logits with many
+                       ties, signed zeros, -inf and NaN (tests/test_oracle_routing.py).
+sum_bitmatrix_rows     numpy unpackbits column sums and an exclusive cumsum of
+                       per-tile sums; known answer of tests/test_moe.py:323-370.
+expt_data              numpy cumsum / repeat construction; the reference test's
+                       known-answer case (tests/test_moe.py:385-436).
+compute_indx           numpy stable argsort (gather) and its inverse (scatter)
+                       with the true per-block partials; carried == partial form.
+align_block_size       numpy stable argsort per expert plus padding; the
+                       reference test's own check (tests/test_moe.py:167-226).
 =====================  ==========================================================
 """
 from __future__ import annotations
@@ -92,6 +103,17 @@ def lib():
         for name in ("orc_e4m3fn_encode_array", "orc_e2m1_encode_array", "orc_mx_scale_exp_array"):
             getattr(L, name).restype = None
             getattr(L, name).argtypes = [P, I64, P]
+        I = ctypes.c_int
+        L.orc_topk.restype = None
+        L.orc_topk.argtypes = [P, I64, I64, I64, I, I, P, P, I64, P]
+        L.orc_sum_bitmatrix_rows.restype = None
+        L.orc_sum_bitmatrix_rows.argtypes = [P, I64, I64, P, P]
+        L.orc_expt_data.restype = None
+        L.orc_expt_data.argtypes = [P, I64, I64, I64, I, I, P, P, P]
+        L.orc_compute_indx.restype = None
+        L.orc_compute_indx.argtypes = [P, P, I64, I, P, I64, P, P, P, P]
+        L.orc_align_block_size.restype = I64
+        L.orc_align_block_size.argtypes = [P, I64, I64, I64, P, P, P]
         _lib = L
     return _lib
 
@@ -348,6 +370,82 @@ def moe_ref(X, W, x_scale, w_scale, bias, gather, hist, offs, expt_data, topk,
             r = r + np.asarray(bias, np.float64)[e][None, :]
         Y[sidx] = r
     return Y
+
+
+# ----------------------------------------------------------------------------
+# MoE routing metadata producers (routing_oracle.c)
+# ----------------------------------------------------------------------------
+
+def _opt(a):
+    return None if a is None else _p(a)
+
+
+def topk(x_bits: np.ndarray, K: int, softmax: bool, bitmatrix: bool = True):
+    """moe_topk: x_bits bf16 bits [rows, E] -> (Yv bf16 bits [rows, K],
+    Yi int32 [rows, K], bits uint32 [rows, ceil(E/32)] or None)."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    rows, E = x.shape
+    yv = np.zeros((rows, K), np.uint16)
+    yi = np.zeros((rows, K), np.int32)
+    bits = np.zeros((rows, (E + 31) // 32), np.uint32) if bitmatrix else None
+    lib().orc_topk(_p(x), E, rows, E, K, int(softmax), _p(yv), _p(yi), K, _opt(bits))
+    return yv, yi, bits
+
+
+def sum_bitmatrix_rows(bits: np.ndarray, partials: bool = True):
+    """bits uint32 [rows, nwords] -> (ret uint32 [32*nwords], partials uint32
+    [ceil(rows/128), 32*nwords] (exclusive over 128-row tiles) or None)."""
+    b = np.ascontiguousarray(bits, dtype=np.uint32)
+    rows, nw = b.shape
+    ret = np.zeros(32 * nw, np.uint32)
+    part = np.zeros(((rows + 127) // 128, 32 * nw), np.uint32) if partials else None
+    lib().orc_sum_bitmatrix_rows(_p(b), rows, nw, _p(ret), _opt(part))
+    return ret, part
+
+
+def expt_data(hist: np.ndarray, max_tiles: int, n_gates: int, log2: int, mode: int, md_init: int = 0x5A5A5A5A):
+    """mode 0: stage 1; 1: stage 1 + 2; 2: stage 1 + fused stage 2.
+    Returns (token_start [E+1], tile_start [E+1], md uint32 [max_tiles]) with md
+    pre-filled with md_init where the mode writes nothing."""
+    h = np.ascontiguousarray(hist, dtype=np.int32)
+    E = h.shape[0]
+    ts = np.zeros(E + 1, np.int32)
+    tl = np.zeros(E + 1, np.int32)
+    md = np.full(max(max_tiles, 1), md_init, np.uint32)
+    lib().orc_expt_data(_p(h), E, max_tiles, n_gates, log2, mode, _p(ts), _p(tl), _p(md))
+    return ts, tl, md[:max_tiles]
+
+
+def compute_indx(indx: np.ndarray, scal_bits, K: int, tokens_start: np.ndarray, partial_offs=None,
+                 n_slots: int | None = None):
+    """routing_compute_indx over flattened gates indx [n_gates]; partial_offs
+    int32 [nblocks, E] or None (counts carried). Returns (gather [n_slots],
+    scatter [n_gates], gate_scal bits [n_slots] or None); untouched gather
+    slots hold -7."""
+    ind = np.ascontiguousarray(indx, dtype=np.int32).ravel()
+    n = ind.shape[0]
+    n_slots = n if n_slots is None else n_slots
+    ts = np.ascontiguousarray(tokens_start, dtype=np.int32)
+    gather = np.full(max(n_slots, 1), -7, np.int32)
+    scatter = np.zeros(max(n, 1), np.int32)
+    sc = None if scal_bits is None else np.ascontiguousarray(scal_bits, dtype=np.uint16).ravel()
+    gs = None if sc is None else np.zeros(max(n_slots, 1), np.uint16)
+    po = None if partial_offs is None else np.ascontiguousarray(partial_offs, dtype=np.int32)
+    E = 0 if po is None else po.shape[1]
+    lib().orc_compute_indx(_p(ind), _opt(sc), n, K, _opt(po), E, _p(ts), _p(gather), _p(scatter), _opt(gs))
+    return gather[:n_slots], scatter[:n], (None if gs is None else gs[:n_slots])
+
+
+def align_block_size(ids: np.ndarray, E: int, bs: int):
+    """moe_align_block_size -> (sorted [total], expert_ids [total/bs], cumsum [E+1], total)."""
+    x = np.ascontiguousarray(ids, dtype=np.int32).ravel()
+    n = x.shape[0]
+    cap = n + E * (bs - 1) + 1
+    sorted_ = np.zeros(cap, np.int32)
+    eids = np.zeros(cap // bs + 1, np.int32)
+    cum = np.zeros(E + 1, np.int32)
+    total = int(lib().orc_align_block_size(_p(x), n, E, bs, _p(sorted_), _p(eids), _p(cum)))
+    return sorted_[:total], eids[: total // bs], cum, total
 
 
 # ----------------------------------------------------------------------------
