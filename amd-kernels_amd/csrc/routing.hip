@@ -29,6 +29,25 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// dst[i] = src[i] for i < n by the whole workgroup (NT threads), eight
+// independent loads in flight per thread before the LDS stores.
+template <int NT>
+__device__ __forceinline__ void copy_to_lds(int* dst, const int32_t* src, int n) {
+    for (int i0 = 0; i0 < n; i0 += NT * 8) {
+        int v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = i0 + j * NT + (int)threadIdx.x;
+            v[j] = i < n ? src[i] : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = i0 + j * NT + (int)threadIdx.x;
+            if (i < n) dst[i] = v[j];
+        }
+    }
+}
+
 // Mask of the lanes of this wave whose key equals this lane's key (lanes with
 // ok == false match nothing and are matched by nothing). Keys are < 2^nbits.
 // Called with all 64 lanes active.
@@ -68,6 +87,25 @@ __device__ __forceinline__ uint32_t order16(uint32_t h) {
 }
 __device__ __forceinline__ uint32_t unorder16(uint32_t k) { return (k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu); }
 
+// Maximum over aligned groups of L lanes (L a power of two <= 64), the result
+// in every lane of the group. Within a row of 16 lanes the exchanges are DPP
+// moves (quad_perm xor 1 / xor 2, half-row mirror, row mirror: each pairs the
+// two halves of the current group); wider groups use ds_swizzle / bpermute.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int L>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t m) {
+    if constexpr (L >= 2) m = max(m, dpp_u32<0xB1>(m));   // quad_perm [1,0,3,2]
+    if constexpr (L >= 4) m = max(m, dpp_u32<0x4E>(m));   // quad_perm [2,3,0,1]
+    if constexpr (L >= 8) m = max(m, dpp_u32<0x141>(m));  // row_half_mirror
+    if constexpr (L >= 16) m = max(m, dpp_u32<0x140>(m)); // row_mirror
+    if constexpr (L >= 32) m = max(m, (uint32_t)__builtin_amdgcn_ds_swizzle((int)m, 0x401F));  // xor 16
+    if constexpr (L >= 64) m = max(m, (uint32_t)__shfl_xor((int)m, 32, 64));
+    return m;
+}
+
 // L lanes per row, V logits per lane (lane j holds experts j, j + L, ...),
 // KMAX >= K winners kept in registers. A logit and its expert pack into one
 // 32-bit key, order16(bf16) << 16 | (0xFFFF - expert): the largest key is the
@@ -98,8 +136,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const TopkParams p) {
             uint32_t m = key[0];
 #pragma unroll
             for (int v = 1; v < V; ++v) m = max(m, key[v]);
-#pragma unroll
-            for (int o = 1; o < L; o <<= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+            m = group_max_u32<L>(m);
             win[k] = m;
 #pragma unroll
             for (int v = 0; v < V; ++v) key[v] = key[v] == m ? 0u : key[v];
@@ -172,6 +209,19 @@ constexpr int BS_TILE = 128;
 constexpr int BS_CHUNK = 256;  // tiles per LDS pass
 constexpr int BS_TPT = BS_CHUNK / 32;  // tiles per scanning thread
 
+__device__ __forceinline__ uint32_t tile_bit_count(const uint32_t* col, int64_t sbm, int rows, int r0, int lane) {
+    const int ra = r0 + lane, rb = ra + 64;
+    const uint32_t w0 = ra < rows ? col[(int64_t)ra * sbm] : 0u;
+    const uint32_t w1 = rb < rows ? col[(int64_t)rb * sbm] : 0u;
+    uint32_t mine = 0;
+#pragma unroll
+    for (int bit = 0; bit < 32; ++bit) {
+        const uint32_t c = (uint32_t)__popcll(__ballot((w0 >> bit) & 1u)) + (uint32_t)__popcll(__ballot((w1 >> bit) & 1u));
+        mine = lane == bit ? c : mine;
+    }
+    return mine;  // lane b < 32: rows of the tile with bit b set
+}
+
 __global__ __launch_bounds__(1024) void bitsum_kernel(const BitsumParams p) {
     __shared__ uint32_t cnt[BS_CHUNK][32];
     __shared__ uint32_t gsum[32][33];
@@ -186,17 +236,8 @@ __global__ __launch_bounds__(1024) void bitsum_kernel(const BitsumParams p) {
     for (int c0 = 0; c0 < ntiles; c0 += BS_CHUNK) {
         const int nt = min(BS_CHUNK, ntiles - c0);
         for (int t = wave; t < nt; t += 16) {
-            const int r0 = (c0 + t) * BS_TILE + lane, r1 = r0 + 64;
-            const uint32_t w0 = r0 < p.rows ? col[(int64_t)r0 * p.sbm] : 0u;
-            const uint32_t w1 = r1 < p.rows ? col[(int64_t)r1 * p.sbm] : 0u;
-            uint32_t mine = 0;
-#pragma unroll
-            for (int bit = 0; bit < 32; ++bit) {
-                const uint32_t c = (uint32_t)__popcll(__ballot((w0 >> bit) & 1u)) +
-                                   (uint32_t)__popcll(__ballot((w1 >> bit) & 1u));
-                mine = lane == bit ? c : mine;
-            }
-            if (lane < 32) cnt[t][lane] = mine;
+            const uint32_t c = tile_bit_count(col, p.sbm, p.rows, (c0 + t) * BS_TILE, lane);
+            if (lane < 32) cnt[t][lane] = c;
         }
         __syncthreads();
         // thread (g, b): tiles [g*BS_TPT, (g+1)*BS_TPT) of bit b
@@ -230,6 +271,62 @@ __global__ __launch_bounds__(1024) void bitsum_kernel(const BitsumParams p) {
     if (threadIdx.x < 32) p.ret[word * 32 + threadIdx.x] = carry[threadIdx.x];
 }
 
+// Wide form of the same sums when every expert column has a partials column:
+// bitcount_kernel counts one 128-row tile per wave (16 tiles per workgroup,
+// grid over tiles x words) into partials; bitscan_kernel then turns each
+// expert's column of tile counts into its exclusive prefix, in place, and
+// writes ret.
+__global__ __launch_bounds__(1024) void bitcount_kernel(const BitsumParams p) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int word = blockIdx.y;
+    const int t = blockIdx.x * 16 + wave;
+    const int ntiles = (p.rows + BS_TILE - 1) / BS_TILE;
+    if (t >= ntiles) return;  // wave-uniform
+    const uint32_t c = tile_bit_count(p.B + (int64_t)word * p.sbn, p.sbm, p.rows, t * BS_TILE, lane);
+    if (lane < 32) p.partials[(int64_t)t * p.spm + ((int64_t)word * 32 + lane) * p.spn] = c;
+}
+
+__global__ __launch_bounds__(1024) void bitscan_kernel(const BitsumParams p) {
+    __shared__ uint32_t gsum[32][33];
+    __shared__ uint32_t carry[32];
+    const int word = blockIdx.x;
+    const int b = threadIdx.x & 31, g = threadIdx.x >> 5;
+    const int ntiles = (p.rows + BS_TILE - 1) / BS_TILE;
+    uint32_t* colp = p.partials + ((int64_t)word * 32 + b) * p.spn;
+    if (threadIdx.x < 32) carry[threadIdx.x] = 0;
+    for (int c0 = 0; c0 < ntiles; c0 += BS_CHUNK) {
+        const int nt = min(BS_CHUNK, ntiles - c0);
+        uint32_t v[BS_TPT], loc[BS_TPT], s = 0;
+#pragma unroll
+        for (int i = 0; i < BS_TPT; ++i) {
+            const int t = g * BS_TPT + i;
+            v[i] = t < nt ? colp[(int64_t)(c0 + t) * p.spm] : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < BS_TPT; ++i) {
+            loc[i] = s;
+            s += v[i];
+        }
+        gsum[g][b] = s;
+        __syncthreads();
+        uint32_t pre = carry[b], tot = 0;
+        for (int q = 0; q < 32; ++q) {
+            const uint32_t x = gsum[q][b];
+            pre += q < g ? x : 0u;
+            tot += x;
+        }
+#pragma unroll
+        for (int i = 0; i < BS_TPT; ++i) {
+            const int t = g * BS_TPT + i;
+            if (t < nt) colp[(int64_t)(c0 + t) * p.spm] = pre + loc[i];
+        }
+        __syncthreads();
+        if (g == 0) carry[b] += tot;
+        __syncthreads();
+    }
+    if (threadIdx.x < 32) p.ret[word * 32 + threadIdx.x] = carry[threadIdx.x];
+}
+
 // ---------------------------------------------------------------------------
 // expt_data (moe-routing/moe_expt_data/kernel.cpp:25-106):
 //   token_start[e] = sum_{e' < e} hist[e'], token_start[E] = n_gates;
@@ -249,11 +346,12 @@ struct ExptDataParams {
 };
 
 constexpr int ED_MAX_EXPTS = 4096;
-constexpr int ED_TILES_PER_BLOCK = 2048;
+constexpr int ED_TILES_PER_BLOCK = 512;
 
-// Exclusive block-wide scan of one value per thread (256 threads); returns the
-// prefix and stores the total in *total.
-__device__ __forceinline__ int block_scan_256(int v, int* wsum, int* total) {
+// Exclusive block-wide scan of one value per thread (NW waves); returns the
+// prefix and stores the total in *total. wsum holds NW ints.
+template <int NW>
+__device__ __forceinline__ int block_scan(int v, int* wsum, int* total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int incl = v;
 #pragma unroll
@@ -265,7 +363,7 @@ __device__ __forceinline__ int block_scan_256(int v, int* wsum, int* total) {
     __syncthreads();
     int pre = 0, tot = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < NW; ++q) {
         pre += q < wave ? wsum[q] : 0;
         tot += wsum[q];
     }
@@ -276,21 +374,24 @@ __device__ __forceinline__ int block_scan_256(int v, int* wsum, int* total) {
 
 __global__ __launch_bounds__(256) void expt_data_kernel(const ExptDataParams p) {
     __shared__ int tstart[ED_MAX_EXPTS + 1];
+    __shared__ int hist[ED_MAX_EXPTS];
     __shared__ int wsum[4];
+    copy_to_lds<256>(hist, p.hist, p.E);
+    __syncthreads();
     const int per = (p.E + 255) / 256;
     const int e0 = threadIdx.x * per, e1 = min(p.E, e0 + per);
     int ntok = 0, ntile = 0;
     for (int e = e0; e < e1; ++e) {
-        const int h = p.hist[e];
+        const int h = hist[e];
         ntok += h;
         ntile += (h + (1 << p.log2) - 1) >> p.log2;
     }
     int tok_total, tile_total;
-    int tok = block_scan_256(ntok, wsum, &tok_total);
-    int tile = block_scan_256(ntile, wsum, &tile_total);
+    int tok = block_scan<4>(ntok, wsum, &tok_total);
+    int tile = block_scan<4>(ntile, wsum, &tile_total);
     const bool lead = blockIdx.x == 0 && p.starts;
     for (int e = e0; e < e1; ++e) {
-        const int h = p.hist[e];
+        const int h = hist[e];
         tstart[e] = tile;
         if (lead) {
             p.token_start[e] = tok;
@@ -364,44 +465,52 @@ struct IndxParams {
 
 constexpr int CI_TOKENS = 128;  // tokens per block (moe_routing/kernel.cpp:222)
 
-template <int CH>  // chunks of 64 gates per wave: 4 * CH * 64 >= 128 * K
-__global__ __launch_bounds__(256) void compute_indx_kernel(const IndxParams p) {
-    __shared__ int cnt[4][RT_MAX_EXPTS];
+// CH chunks of 64 gates per wave (4 * CH * 64 >= 128 * K); NB blocks in
+// flight per workgroup (4 waves each). With partial_offs the grid has one
+// workgroup per block (NB = 1); without, one workgroup walks all blocks NB at
+// a time and carries the per-expert counts.
+template <int CH, int NB>
+__global__ __launch_bounds__(256 * NB) void compute_indx_kernel(const IndxParams p) {
+    __shared__ int cnt[NB][4][RT_MAX_EXPTS];
     __shared__ int run[RT_MAX_EXPTS];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) & 3, slot = threadIdx.x >> 8;
     const int G = CI_TOKENS * p.K;
     const bool carry = p.partial_offs == nullptr;
     if (carry)
-        for (int e = threadIdx.x; e < RT_MAX_EXPTS; e += 256) run[e] = 0;
+        for (int e = threadIdx.x; e < RT_MAX_EXPTS; e += 256 * NB) run[e] = 0;
 
     const int b0 = carry ? 0 : blockIdx.x, b1 = carry ? p.nblocks : blockIdx.x + 1;
-    for (int blk = b0; blk < b1; ++blk) {
-        for (int i = threadIdx.x; i < 4 * RT_MAX_EXPTS; i += 256) (&cnt[0][0])[i] = 0;
+    for (int it = b0; it < b1; it += NB) {
+        const int blk = it + slot;  // may be >= b1: then every gate is out of range
+        for (int i = threadIdx.x; i < NB * 4 * RT_MAX_EXPTS; i += 256 * NB) (&cnt[0][0][0])[i] = 0;
         __syncthreads();
         int ex[CH], rk[CH];
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int gl = (wave * CH + c) * 64 + lane;
             const int64_t g = (int64_t)blk * G + gl;
-            const bool in = gl < G && g < p.n_gates;
+            const bool in = blk < b1 && gl < G && g < p.n_gates;
             const int e = in ? p.expt_indx[g] : -1;
             const bool ok = (uint32_t)e < (uint32_t)RT_MAX_EXPTS;
             const uint64_t m = match_key((uint32_t)e, ok, RT_EBITS);
             const int r = (int)lanes_below(m), n = __popcll(m);
-            const int base = ok ? cnt[wave][e] : 0;
-            if (ok && r == n - 1) cnt[wave][e] = base + n;
+            const int base = ok ? cnt[slot][wave][e] : 0;
+            if (ok && r == n - 1) cnt[slot][wave][e] = base + n;
             ex[c] = ok ? e : (in ? -2 : -1);
             rk[c] = base + r;
         }
         __syncthreads();
-        for (int e = threadIdx.x; e < RT_MAX_EXPTS; e += 256) {
+        // exclusive prefix over (block in flight, wave), starting from the carry
+        for (int e = threadIdx.x; e < RT_MAX_EXPTS; e += 256 * NB) {
             int s = carry ? run[e] : 0;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const int v = cnt[w][e];
-                cnt[w][e] = s;
-                s += v;
-            }
+            for (int j = 0; j < NB; ++j)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const int v = cnt[j][w][e];
+                    cnt[j][w][e] = s;
+                    s += v;
+                }
             if (carry) run[e] = s;
         }
         __syncthreads();
@@ -411,7 +520,7 @@ __global__ __launch_bounds__(256) void compute_indx_kernel(const IndxParams p) {
             const int64_t g = (int64_t)blk * G + gl;
             const int e = ex[c];
             if (e >= 0) {
-                int pos = p.tokens_start[e] + cnt[wave][e] + rk[c];
+                int pos = p.tokens_start[e] + cnt[slot][wave][e] + rk[c];
                 if (!carry) pos += p.partial_offs[(int64_t)blk * p.spm + (int64_t)e * p.spn];
                 p.scatter[g] = pos;
                 p.gather[pos] = (int32_t)g;
@@ -434,6 +543,8 @@ __global__ __launch_bounds__(256) void compute_indx_kernel(const IndxParams p) {
 // segment ranks and scatters its own ids (the cumsum is recomputed per
 // workgroup from the counts). Ids outside [0, E) are skipped.
 // ---------------------------------------------------------------------------
+constexpr int AL_MAX_COUNTS = 16384;  // segments x experts staged in LDS
+
 struct AlignParams {
     const int32_t* ids;
     int32_t* sorted;
@@ -444,96 +555,127 @@ struct AlignParams {
     int E, bs, numel, seg, nseg, ebits;
 };
 
-__global__ __launch_bounds__(256) void align_count_kernel(const AlignParams p) {
+constexpr int AL_NW = 16;  // waves per workgroup
+
+__global__ __launch_bounds__(64 * AL_NW) void align_count_kernel(const AlignParams p) {
     __shared__ int cnt[RT_MAX_EXPTS];
-    for (int e = threadIdx.x; e < p.E; e += 256) cnt[e] = 0;
+    for (int e = threadIdx.x; e < p.E; e += 64 * AL_NW) cnt[e] = 0;
     __syncthreads();
     const int i0 = blockIdx.x * p.seg, i1 = min(p.numel, i0 + p.seg);
-    for (int i = i0 + threadIdx.x; i < i1; i += 256) {
-        const int e = p.ids[i];
-        if ((uint32_t)e < (uint32_t)p.E) atomicAdd(&cnt[e], 1);
+    for (int b = i0; b < i1; b += 4 * 64 * AL_NW) {
+        int e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = b + j * 64 * AL_NW + (int)threadIdx.x;
+            e[j] = i < i1 ? p.ids[i] : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if ((uint32_t)e[j] < (uint32_t)p.E) atomicAdd(&cnt[e[j]], 1);
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < p.E; e += 256) p.counts[(int64_t)blockIdx.x * p.E + e] = cnt[e];
+    for (int e = threadIdx.x; e < p.E; e += 64 * AL_NW) p.counts[(int64_t)blockIdx.x * p.E + e] = cnt[e];
 }
 
-__global__ __launch_bounds__(256) void align_scatter_kernel(const AlignParams p) {
-    __shared__ int tot[RT_MAX_EXPTS];
-    __shared__ int pre[RT_MAX_EXPTS];
-    __shared__ int cum[RT_MAX_EXPTS + 1];
-    __shared__ int wcnt[4][RT_MAX_EXPTS];
-    __shared__ int wsum[4];
+// Dynamic LDS: tot[E], pre[E], cum[E + 1], segc[nseg * E], wcnt[AL_NW][E].
+__global__ __launch_bounds__(64 * AL_NW) void align_scatter_kernel(const AlignParams p) {
+    extern __shared__ int lds[];
+    int* tot = lds;
+    int* pre = tot + p.E;
+    int* cum = pre + p.E;
+    int* segc = cum + p.E + 1;
+    int* wcnt = segc + p.nseg * p.E;  // [AL_NW][E]
+    __shared__ int wsum[AL_NW];
+    constexpr int NT = 64 * AL_NW;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int seg = blockIdx.x;
 
     // per expert: the total count and the count in the segments before this one
-    for (int e = threadIdx.x; e < p.E; e += 256) {
+    copy_to_lds<NT>(segc, p.counts, p.nseg * p.E);
+    for (int i = threadIdx.x; i < AL_NW * p.E; i += NT) wcnt[i] = 0;
+    __syncthreads();
+    for (int e = threadIdx.x; e < p.E; e += NT) {
         int t = 0, before = 0;
         for (int s = 0; s < p.nseg; ++s) {
-            const int c = p.counts[(int64_t)s * p.E + e];
+            const int c = segc[s * p.E + e];
             before += s < seg ? c : 0;
             t += c;
         }
         tot[e] = t;
         pre[e] = before;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) wcnt[w][e] = 0;
     }
     __syncthreads();
     // padded exclusive cumsum over experts (thread-contiguous expert ranges)
-    const int per = (p.E + 255) / 256;
+    const int per = (p.E + NT - 1) / NT;
     const int e0 = threadIdx.x * per, e1 = min(p.E, e0 + per);
     int acc = 0;
     for (int e = e0; e < e1; ++e) acc += (tot[e] + p.bs - 1) / p.bs * p.bs;
     int all;
-    int run = block_scan_256(acc, wsum, &all);
+    int run = block_scan<AL_NW>(acc, wsum, &all);
     for (int e = e0; e < e1; ++e) {
         cum[e] = run;
         run += (tot[e] + p.bs - 1) / p.bs * p.bs;
     }
     if (threadIdx.x == 0) cum[p.E] = all;
 
-    // per-wave counts of this segment (wave w takes a contiguous quarter)
+    // per-wave counts of this segment (wave w takes a contiguous share, a
+    // multiple of 64 ids)
     const int i0 = seg * p.seg, i1 = min(p.numel, i0 + p.seg);
-    const int q = (p.seg / 4 + 63) / 64 * 64;
+    const int q = (p.seg / AL_NW + 63) / 64 * 64;
     const int w0 = min(i1, i0 + wave * q), w1 = min(i1, w0 + q);
-    for (int i = w0 + lane; i < w1; i += 64) {
-        const int e = p.ids[i];
-        if ((uint32_t)e < (uint32_t)p.E) atomicAdd(&wcnt[wave][e], 1);
+    int* mine = wcnt + wave * p.E;
+    for (int b = w0; b < w1; b += 4 * 64) {
+        int e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = b + j * 64 + lane;
+            e[j] = i < w1 ? p.ids[i] : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if ((uint32_t)e[j] < (uint32_t)p.E) atomicAdd(&mine[e[j]], 1);
     }
     __syncthreads();
     // base of (wave, expert) = cum[e] + earlier segments + earlier waves
-    for (int e = threadIdx.x; e < p.E; e += 256) {
+    for (int e = threadIdx.x; e < p.E; e += NT) {
         int s = cum[e] + pre[e];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const int v = wcnt[w][e];
-            wcnt[w][e] = s;
+        for (int w = 0; w < AL_NW; ++w) {
+            const int v = wcnt[w * p.E + e];
+            wcnt[w * p.E + e] = s;
             s += v;
         }
     }
     __syncthreads();
-    // per chunk of 64 ids: each id takes base + its rank among the chunk's ids
-    // of the same expert, and the last of them advances the base
-    for (int c0 = w0; c0 < w1; c0 += 64) {
-        const int i = c0 + lane;
-        const int e = i < w1 ? p.ids[i] : -1;
-        const bool ok = (uint32_t)e < (uint32_t)p.E;
-        const uint64_t m = match_key((uint32_t)e, ok, p.ebits);
-        const int r = (int)lanes_below(m), n = __popcll(m);
-        const int base = ok ? wcnt[wave][e] : 0;
-        if (ok && r == n - 1) wcnt[wave][e] = base + n;
-        if (ok) p.sorted[base + r] = i;
+    // chunks of 64 ids, four loads in flight: each id takes base + its rank
+    // among the chunk's ids of the same expert, and the last of them
+    // advances the base
+    for (int b = w0; b < w1; b += 4 * 64) {
+        int e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = b + j * 64 + lane;
+            e[j] = i < w1 ? p.ids[i] : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = b + j * 64 + lane;
+            const bool ok = (uint32_t)e[j] < (uint32_t)p.E;
+            const uint64_t m = match_key((uint32_t)e[j], ok, p.ebits);
+            const int r = (int)lanes_below(m), n = __popcll(m);
+            const int base = ok ? mine[e[j]] : 0;
+            if (ok && r == n - 1) mine[e[j]] = base + n;
+            if (ok) p.sorted[base + r] = i;
+        }
     }
 
     // padding, expert ids of the blocks, cumsum and total: experts e == seg (mod nseg)
     for (int e = seg; e < p.E; e += p.nseg) {
         const int pad0 = cum[e] + tot[e], end = cum[e + 1];
-        for (int s = pad0 + threadIdx.x; s < end; s += 256) p.sorted[s] = p.numel;
-        for (int blk = cum[e] / p.bs + threadIdx.x; blk < end / p.bs; blk += 256) p.expert_ids[blk] = e;
+        for (int x = pad0 + threadIdx.x; x < end; x += NT) p.sorted[x] = p.numel;
+        for (int blk = cum[e] / p.bs + threadIdx.x; blk < end / p.bs; blk += NT) p.expert_ids[blk] = e;
     }
     if (seg == 0) {
-        for (int e = threadIdx.x; e <= p.E; e += 256) p.cumsum[e] = cum[e];
+        for (int e = threadIdx.x; e <= p.E; e += NT) p.cumsum[e] = cum[e];
         if (threadIdx.x == 0) *p.total = all;
     }
 }
@@ -559,8 +701,9 @@ int launch_topk(const TopkParams& p, int kmax, hipStream_t s) {
 }
 
 template <int CH>
-int launch_indx(const IndxParams& p, int grid, hipStream_t s) {
-    compute_indx_kernel<CH><<<grid, 256, 0, s>>>(p);
+int launch_indx(const IndxParams& p, hipStream_t s) {
+    if (p.partial_offs) compute_indx_kernel<CH, 1><<<p.nblocks, 256, 0, s>>>(p);
+    else compute_indx_kernel<CH, 4><<<1, 1024, 0, s>>>(p);
     return hkq_launch_status();
 }
 
@@ -594,11 +737,10 @@ int indx(int32_t* gather, int32_t* scatter, void* gate_scal, const void* expt_sc
     p.K = K;
     const int64_t G = (int64_t)CI_TOKENS * K;
     p.nblocks = (int)((n_gates + G - 1) / G);
-    const int grid = partial_offs ? p.nblocks : 1;
-    if (K <= 2) return launch_indx<1>(p, grid, stream);
-    if (K <= 4) return launch_indx<2>(p, grid, stream);
-    if (K <= 8) return launch_indx<4>(p, grid, stream);
-    return launch_indx<8>(p, grid, stream);
+    if (K <= 2) return launch_indx<1>(p, stream);
+    if (K <= 4) return launch_indx<2>(p, stream);
+    if (K <= 8) return launch_indx<4>(p, stream);
+    return launch_indx<8>(p, stream);
 }
 
 int expt_data(const int32_t* hist, int32_t* token_start, int32_t* tile_start, uint32_t* md, int64_t E,
@@ -659,6 +801,15 @@ int bitsum(const uint32_t* B, int64_t rows, int64_t sbm, int64_t sbn, uint32_t* 
     p.rows = (int)rows;
     p.nwords = (int)nwords;
     p.pcols = (int)std::min<int64_t>(pcols, INT32_MAX);
+    const int64_t ntiles = (rows + BS_TILE - 1) / BS_TILE;
+    if (partials && pcols >= 32 * nwords && ntiles > 16) {
+        // every expert has a partials column to hold its tile counts
+        bitcount_kernel<<<dim3((unsigned)((ntiles + 15) / 16), (unsigned)nwords), 1024, 0, stream>>>(p);
+        const int rc = hkq_launch_status();
+        if (rc) return rc;
+        bitscan_kernel<<<(unsigned)nwords, 1024, 0, stream>>>(p);
+        return hkq_launch_status();
+    }
     bitsum_kernel<<<(unsigned)nwords, 1024, 0, stream>>>(p);
     return hkq_launch_status();
 }
@@ -696,10 +847,14 @@ extern "C" int hkq_moe_topk(const void* X, int64_t stride_xm, void* Yv, int32_t*
     p.nwords = (int)((n_expts_tot + 31) / 32);
     const int kmax = K <= 2 ? 2 : K <= 4 ? 4 : K <= 8 ? 8 : 16;
     const hipStream_t s = (hipStream_t)stream;
+    // lanes per row: enough for at most 8 (E <= 32) or 16 logits per lane
     if (n_expts_tot <= 8) return launch_topk<1, 8>(p, kmax, s);
+    if (n_expts_tot <= 16) return launch_topk<2, 8>(p, kmax, s);
     if (n_expts_tot <= 32) return launch_topk<4, 8>(p, kmax, s);
-    if (n_expts_tot <= 128) return launch_topk<16, 8>(p, kmax, s);
-    if (n_expts_tot <= 512) return launch_topk<64, 8>(p, kmax, s);
+    if (n_expts_tot <= 64) return launch_topk<4, 16>(p, kmax, s);
+    if (n_expts_tot <= 128) return launch_topk<8, 16>(p, kmax, s);
+    if (n_expts_tot <= 256) return launch_topk<16, 16>(p, kmax, s);
+    if (n_expts_tot <= 512) return launch_topk<32, 16>(p, kmax, s);
     return launch_topk<64, 16>(p, kmax, s);
 }
 
@@ -778,9 +933,11 @@ extern "C" int hkq_moe_align_block_size(const int32_t* topk_ids, int32_t* sorted
     HKQ_CHECK_ALIGN(cumsum_buffer, 4);
     HKQ_CHECK_ALIGN(total_tokens_post_pad, 4);
     const int64_t E = num_experts;
-    // segments of a multiple of 256 ids; at most min(64, E + 1) of them, so the
-    // per-segment counts fit the reference's (E + 1) * E workspace
-    int64_t seg = std::max<int64_t>(1024, (numel + std::min<int64_t>(64, E + 1) - 1) / std::min<int64_t>(64, E + 1));
+    // segments of a multiple of 256 ids; at most min(64, E + 1, 16384 / E) of
+    // them, so the per-segment counts fit the reference's (E + 1) * E
+    // workspace and the scatter kernel's LDS copy of them
+    const int64_t maxseg = std::max<int64_t>(1, std::min<int64_t>({64, E + 1, AL_MAX_COUNTS / E}));
+    int64_t seg = std::max<int64_t>(1024, (numel + maxseg - 1) / maxseg);
     seg = (seg + 255) / 256 * 256;
     const int64_t nseg = std::max<int64_t>(1, (numel + seg - 1) / seg);
     AlignParams p{};
@@ -798,9 +955,21 @@ extern "C" int hkq_moe_align_block_size(const int32_t* topk_ids, int32_t* sorted
     p.ebits = 0;
     while ((1ll << p.ebits) < E) ++p.ebits;
     const hipStream_t s = (hipStream_t)stream;
-    align_count_kernel<<<(unsigned)nseg, 256, 0, s>>>(p);
+    const size_t lds = sizeof(int) * (size_t)(3 * E + 1 + nseg * E + AL_NW * E);
+    static bool lds_set = false;  // the largest size any call can need, set once
+    if (!lds_set) {
+        const int most = (int)sizeof(int) * (3 * RT_MAX_EXPTS + 1 + AL_MAX_COUNTS + AL_NW * RT_MAX_EXPTS);
+        const hipError_t e = hipFuncSetAttribute((const void*)align_scatter_kernel,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, most);
+        if (e != hipSuccess) {
+            ::hkq::set_error("hipFuncSetAttribute(align_scatter_kernel) failed: %s", hipGetErrorString(e));
+            return (int)e;
+        }
+        lds_set = true;
+    }
+    align_count_kernel<<<(unsigned)nseg, 64 * AL_NW, 0, s>>>(p);
     int rc = hkq_launch_status();
     if (rc) return rc;
-    align_scatter_kernel<<<(unsigned)nseg, 256, 0, s>>>(p);
+    align_scatter_kernel<<<(unsigned)nseg, 64 * AL_NW, lds, s>>>(p);
     return hkq_launch_status();
 }

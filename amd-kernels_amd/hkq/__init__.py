@@ -331,22 +331,66 @@ def compute_indx(expt_indx, tokens_start, partial_offs=None, expt_scal=None, n_s
     return gather[:n_slots], scatter[:n], (None if gs is None else gs[:n_slots])
 
 
+def moe_routing_plan(logits, topk: int, block_m: int = 128, softmax: bool = True, stream=None):
+    """Allocate the routing outputs for router logits bf16 [T, E] and bind the
+    five launches that fill them (top-k + bitmatrix, tile counts and their
+    scan, expert data, gate placement). Returns (outputs, run): run() enqueues
+    the launches on the stream, with no host synchronisation and no
+    allocation. outputs: topk_vals, topk_idx, bits, hist, partials, offs,
+    token_start, tile_start, expt_data (tiles of block_m rows, -1 past the
+    last), gather, scatter, gate_scal."""
+    import torch
+
+    T, E = logits.shape
+    K = topk
+    log2 = block_m.bit_length() - 1
+    if (1 << log2) != block_m:
+        raise ValueError("block_m must be a power of two")
+    dev = logits.device
+    nw = (E + 31) // 32
+    ntiles = (T + 127) // 128
+    max_tiles = T * K // block_m + E
+    o = {
+        "topk_vals": torch.empty((T, K), dtype=torch.bfloat16, device=dev),
+        "topk_idx": torch.empty((T, K), dtype=torch.int32, device=dev),
+        "bits": torch.empty((T, nw), dtype=torch.int32, device=dev),
+        "hist_all": torch.empty(32 * nw, dtype=torch.int32, device=dev),
+        "partials": torch.empty((ntiles, 32 * nw), dtype=torch.int32, device=dev),
+        "token_start": torch.empty(E + 1, dtype=torch.int32, device=dev),
+        "tile_start": torch.empty(E + 1, dtype=torch.int32, device=dev),
+        "expt_data": torch.empty(max(max_tiles, 1), dtype=torch.int32, device=dev),
+        "gather": torch.empty(max(T * K, 1), dtype=torch.int32, device=dev),
+        "scatter": torch.empty(max(T * K, 1), dtype=torch.int32, device=dev),
+        "gate_scal": torch.empty(max(T * K, 1), dtype=torch.bfloat16, device=dev),
+    }
+    st = _stream(stream)
+    P = {k: v.data_ptr() for k, v in o.items()}
+    calls = [
+        bind("hkq_moe_topk", logits.data_ptr(), logits.stride(0), P["topk_vals"], P["topk_idx"], K, P["bits"], nw, 1,
+             T, E, K, int(softmax), st),
+        bind("hkq_sum_bitmatrix_rows", P["bits"], T, nw, 1, P["hist_all"], P["partials"], 32 * nw, 1, 32 * nw, nw, st),
+        bind("hkq_expt_data_compute", P["hist_all"], P["token_start"], P["tile_start"], P["expt_data"], E, max_tiles,
+             T * K, log2, 0, st),
+        bind("hkq_routing_compute_indx", P["gather"], P["scatter"], P["gate_scal"], P["topk_vals"], P["topk_idx"],
+             P["partials"], 32 * nw, 1, P["token_start"], T * K, K, st),
+    ]
+
+    def run():
+        for c in calls:
+            c()
+
+    o["hist"] = o["hist_all"][:E]
+    o["offs"] = o["token_start"][:E]
+    o["expt_data"] = o["expt_data"][:max_tiles]
+    return o, run
+
+
 def moe_routing(logits, topk: int, block_m: int = 128, softmax: bool = True, stream=None):
     """Router logits bf16 [T, E] -> the OGS metadata of moe_a8w8, on the GPU and
-    without a host synchronisation: top-k (+ bitmatrix), its column sums with
-    per-128-token partials, expert data, and the gate placement. Returns a dict
-    with topk_vals, topk_idx, hist, offs, tile_start, expt_data (tiles of
-    block_m rows, -1 past the last), gather, scatter, gate_scal."""
-    T, E = logits.shape
-    yv, yi, bits = moe_topk(logits, topk, softmax, True, stream)
-    hist, part = sum_bitmatrix_rows(bits, True, stream)
-    hist = hist[:E]
-    log2 = block_m.bit_length() - 1
-    assert (1 << log2) == block_m, "block_m must be a power of two"
-    ts, tl, md = expt_data(hist, T * topk, log2, stream=stream)
-    gather, scatter, gs = compute_indx(yi, ts, part, yv, stream=stream)
-    return {"topk_vals": yv, "topk_idx": yi, "hist": hist, "offs": ts[:E], "tile_start": tl, "expt_data": md,
-            "gather": gather, "scatter": scatter, "gate_scal": gs}
+    without a host synchronisation (see moe_routing_plan for the outputs)."""
+    o, run = moe_routing_plan(logits, topk, block_m, softmax, stream)
+    run()
+    return o
 
 
 def align_block_size(topk_ids, num_experts: int, block_size: int, stream=None):

@@ -38,6 +38,8 @@ HEADLINE = dict(M=4096, N=14336, K=4096)
 MXFP4 = dict(M=4096, N=8192, K=8192)
 BLOCKSCALE = [(2048, 24576, 1536), (2048, 7168, 18432), (2048, 7168, 2048)]
 MOE = dict(T=4096, E=8, topk=2, hidden=4096, ffn=14336)
+# routing pipelines timed beside the Mixtral one: (tokens, experts, top-k)
+ROUTING_EXTRA = [(4096, 256, 8), (32768, 256, 8)]
 # A8W8 shape sweep (N, K) x M of the reference's GEMM benchmark configuration
 SWEEP_NK = [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)]
 SWEEP_M = [1, 16, 128, 1024, 4096]
@@ -92,24 +94,6 @@ def time_launches(fn, steps, warmup, preheat=PREHEAT_S):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
-
-
-def ogs_routing(assigns, num_experts, block_m=128):
-    """OGS routing metadata (int32 device tensors) from top-k assignments [T, topk]:
-    per-expert counts and exclusive offsets, the sorted-slot -> t*topk+k gather
-    index (token-major within an expert) and one e | (block << 16) entry per
-    block_m rows of each expert -- the contract of the reference's
-    tests/test_moe.py:97-128."""
-    import torch
-
-    flat = assigns.reshape(-1).to(torch.int64)
-    hist = torch.bincount(flat, minlength=num_experts).to(torch.int32)
-    offs = torch.zeros(num_experts, dtype=torch.int32)
-    offs[1:] = torch.cumsum(hist, 0)[:-1].to(torch.int32)
-    gather = torch.argsort(flat, stable=True).to(torch.int32)
-    tiles = [e | (b << 16) for e in range(num_experts) for b in range((int(hist[e]) + block_m - 1) // block_m)]
-    dev = lambda t: t.cuda()
-    return dev(hist), dev(offs), dev(gather), dev(torch.tensor(tiles, dtype=torch.int32))
 
 
 def read_traffic():
@@ -209,12 +193,19 @@ def main():
         res["blockscale"] = sum(r["ms"] for r in bs_res)
 
     # ---- A8W8 MoE grouped GEMM, Mixtral-8x7B (E=8, top-2, 4096 tokens, 4096 -> 14336 gate/up, down) ----
-    moe_res = []
+    moe_res, routing_res = [], []
     if args.only in (None, "moe"):
         T, E, topk, hidden, ffn = MOE["T"], MOE["E"], MOE["topk"], MOE["hidden"], MOE["ffn"]
-        g = torch.Generator(device="cpu").manual_seed(8)
-        assigns = torch.topk(torch.softmax(torch.randn(T, E, generator=g), -1), topk, dim=-1).indices
-        hist, offs, gather, expt_data = ogs_routing(assigns, E, 128)
+        # routing on the GPU from seeded router logits ~N(0,1): top-2 (with softmax over
+        # the chosen logits), tile counts, expert data and gate placement
+        logits = seeded_bf16((T, E), 1.0, 8)
+        rt, route = hkq.moe_routing_plan(logits, topk, 128)
+        route()
+        hist, offs, gather, expt_data = rt["hist"], rt["offs"], rt["gather"], rt["expt_data"]
+        torch.cuda.synchronize()
+        log(f"moe routing T={T} E={E} top-{topk}")
+        ms_r = time_launches(route, steps, warmup, preheat=0.05)
+        routing_res.append({"T": T, "E": E, "topk": topk, "us": round(ms_r * 1e3, 2), "calls": 4})
         xm = seeded_bf16((T, hidden), 1.0, 9)
         qx, sx = hkq.per_token_quant(xm)
         for name, (nn, kk) in (("gate_up", (2 * ffn, hidden)), ("down", (hidden, ffn))):
@@ -232,6 +223,11 @@ def main():
                             "tflops": round(2.0 * T * topk * nn * kk / (ms_m * 1e-3) / 1e12, 2)})
             del wq
         res["moe"] = sum(r["ms"] for r in moe_res)
+        for (Tr, Er, Kr) in ROUTING_EXTRA:
+            lg = seeded_bf16((Tr, Er), 1.0, 30)
+            _, route = hkq.moe_routing_plan(lg, Kr, 128)
+            ms_r = time_launches(route, steps, warmup, preheat=0.05)
+            routing_res.append({"T": Tr, "E": Er, "topk": Kr, "us": round(ms_r * 1e3, 2), "calls": 4})
 
     # ---- A8W8 shape sweep and the MXFP4 M=128 configuration (plans with smaller tiles / split K) ----
     sweep = []
@@ -273,6 +269,8 @@ def main():
 
     if args.only is not None:
         log(json.dumps({k: round(v * 1e3, 2) for k, v in res.items()}) + "  (us per launch)")
+        for r in routing_res:
+            log(json.dumps({"routing": r}))
         if sweep:
             for r in sweep:
                 log(json.dumps(r))
@@ -319,6 +317,7 @@ def main():
                                 "pct_hbm_peak": round(100 * quant_gbs / PEAK_HBM_GBS, 2)},
         "blockscale": bs_res,
         "moe_mixtral": moe_res,
+        "moe_routing": routing_res,
         "sweep": sweep,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_FP8_TFLOPS, 4), "traffic": read_traffic()},

@@ -52,7 +52,8 @@ def ulp_close(a_bits, b_bits):
 
 
 @pytest.mark.parametrize("T,E,K", [(4096, 8, 2), (1000, 64, 6), (4096, 256, 8), (333, 128, 4), (257, 512, 10),
-                                   (100, 1024, 16), (50, 5, 8), (64, 20, 1)])
+                                   (100, 1024, 16), (50, 5, 8), (64, 20, 1), (700, 16, 3), (129, 60, 8),
+                                   (200, 384, 8), (90, 1000, 2)])
 def test_topk(orc, T, E, K):
     require_gpu()
     xb = logits_with_specials(orc, T, E, T + E + K)
