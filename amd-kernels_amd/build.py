@@ -40,7 +40,7 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-HIP_SOURCES = ["quant.hip", "gemm.hip", "gemm_blockscale.hip", "moe.hip", "routing.hip"]
+HIP_SOURCES = ["quant.hip", "gemm.hip", "gemm_blockscale.hip", "moe.hip", "routing.hip", "norm_quant.hip"]
 CPP_SOURCES = ["hkq_error.cpp"]
 
 # pybind11 module name -> binding source (module names are the reference's)
@@ -53,6 +53,8 @@ MODULES = {
     "gemm_a8w8_blockscale_tk": "bind_gemm_a8w8_blockscale.cpp",
     "moe_op_gemm_a8w8_tk": "bind_moe_op_gemm_a8w8.cpp",
     "moe_op_gemm_a8w8_blockscale_tk": "bind_moe_op_gemm_a8w8_blockscale.cpp",
+    "fused_fp8_quant_tk": "bind_fused_fp8_quant.cpp",
+    "fused_mxfp4_quant_tk": "bind_fused_mxfp4_quant.cpp",
     "moe_topk_tk": "bind_moe_topk.cpp",
     "moe_bitmatrix_tk": "bind_moe_bitmatrix.cpp",
     "moe_expt_data_tk": "bind_moe_expt_data.cpp",

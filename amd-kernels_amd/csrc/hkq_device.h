@@ -52,14 +52,23 @@ __device__ __forceinline__ uint32_t cvt_pk_e4m3(float a, float b) {
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
 }
 
-// E2M1 code of q (round to nearest even on the grid {0,.5,1,1.5,2,3,4,6},
-// saturating at 6; sign from the sign bit; NaN -> +6). Branch-free compares.
-__device__ __forceinline__ uint32_t e2m1_encode(float q) {
-    float a = __builtin_fabsf(q);
-    uint32_t m = (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) + (a > 5.0f);
-    m = (q != q) ? 7u : m;
-    uint32_t s = (q != q) ? 0u : ((__float_as_uint(q) >> 28) & 8u);
-    return s | m;
+// Eight values (already multiplied by the block's 2^-e) -> eight E2M1 codes,
+// value j in nibble j. The rule: round to nearest even on the grid
+// {0, .5, 1, 1.5, 2, 3, 4, 6}, saturating at 6, sign from the sign bit, NaN ->
+// +6 (code 0x7). v_cvt_scalef32_pk_fp4_f32 with scale 1.0 implements it except
+// for NaN, whose sign it keeps (checked on the GPU against a compare-based
+// encoder over every tie +-3 ulp and 2^20 random values), so NaN is mapped to
+// +6 first.
+__device__ __forceinline__ uint32_t e2m1_encode8(const float* v) {
+    uint32_t w = 0;
+    float a[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = v[j] != v[j] ? 6.0f : v[j];
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a[0], a[1], 1.0f, 0);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a[2], a[3], 1.0f, 1);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a[4], a[5], 1.0f, 2);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a[6], a[7], 1.0f, 3);
+    return w;
 }
 
 // Unbiased shared exponent of the MXFP4 scale rule: P = (bits(amax) + 0x200000)
@@ -90,11 +99,45 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// Wave-level reductions over groups of W adjacent lanes (W a power of two <= 64).
+// Value of v in the partner lane of a butterfly step over aligned groups of
+// 2*H lanes (H = 1, 2, 4, 8: DPP quad_perm [1,0,3,2] / [2,3,0,1], half-row
+// mirror, row mirror; 16: ds_swizzle xor 16; 32: bpermute xor 32). The mirror
+// steps pair lane i with 2H-1-i instead of i^H; once the previous steps have
+// made every H-lane subgroup uniform, both pairings combine the same values.
+template <int H>
+__device__ __forceinline__ float butterfly_partner(float v) {
+    const int x = __float_as_int(v);
+    if constexpr (H == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+    else if constexpr (H == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+    else if constexpr (H == 4) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false));
+    else if constexpr (H == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false));
+    else if constexpr (H == 16) return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x401F));
+    else return __shfl_xor(v, 32, 64);
+}
+
+// Wave-level reductions over groups of W adjacent lanes (W a power of two <= 64),
+// the result in every lane of the group. Called with all lanes active.
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = 1; o < W; o <<= 1) v = max_num(v, __shfl_xor(v, o, 64));
+    if constexpr (W >= 2) v = max_num(v, butterfly_partner<1>(v));
+    if constexpr (W >= 4) v = max_num(v, butterfly_partner<2>(v));
+    if constexpr (W >= 8) v = max_num(v, butterfly_partner<4>(v));
+    if constexpr (W >= 16) v = max_num(v, butterfly_partner<8>(v));
+    if constexpr (W >= 32) v = max_num(v, butterfly_partner<16>(v));
+    if constexpr (W >= 64) v = max_num(v, butterfly_partner<32>(v));
+    return v;
+}
+
+// Sum by the same butterfly: every lane of the group ends with the same bits,
+// equal to the xor butterfly (v += v[lane ^ o] for o = 1, 2, ..., W/2).
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (W >= 2) v = v + butterfly_partner<1>(v);
+    if constexpr (W >= 4) v = v + butterfly_partner<2>(v);
+    if constexpr (W >= 8) v = v + butterfly_partner<4>(v);
+    if constexpr (W >= 16) v = v + butterfly_partner<8>(v);
+    if constexpr (W >= 32) v = v + butterfly_partner<16>(v);
+    if constexpr (W >= 64) v = v + butterfly_partner<32>(v);
     return v;
 }
 

@@ -171,13 +171,13 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(const uint16_t* __restric
         if (FP4) {
             const int e = mx_scale_exp(m);
             const float mul = exp2i(-e);  // exact: ldexp(x, -e)
-            uint32_t packed = 0;
+            float t[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                uint32_t lo = e2m1_encode(bf16_to_f32(w[j] & 0xFFFF) * mul);
-                uint32_t hi = e2m1_encode(bf16_to_f32(w[j] >> 16) * mul);
-                packed |= (lo | (hi << 4)) << (8 * j);
+                t[2 * j] = bf16_to_f32(w[j] & 0xFFFF) * mul;
+                t[2 * j + 1] = bf16_to_f32(w[j] >> 16) * mul;
             }
+            const uint32_t packed = e2m1_encode8(t);
             if (ok) {
                 reinterpret_cast<uint32_t*>(q + row * (K >> 1))[col] = packed;
                 if ((threadIdx.x & 3) == 0) s[row * (K >> 5) + (col >> 2)] = (uint8_t)(e + 127);

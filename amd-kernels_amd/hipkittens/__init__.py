@@ -123,6 +123,22 @@ def per_token_quant_fwd(*args, **kwargs):
     return _call("quant_tk", "per_token_quant_fwd", *args, **kwargs)
 
 
+def fused_rmsnorm_fp8_quant_fwd(*args, **kwargs):
+    """fused_rmsnorm_fp8_quant_fwd(input bf16 [M,D], weight bf16 [D], output e4m3 [M,D], scales f32 [M,D/128], eps)"""
+    return _call("fused_fp8_quant_tk", "fused_rmsnorm_fp8_quant_fwd", *args, **kwargs)
+
+
+def fused_rmsnorm_mxfp4_quant_fwd(*args, **kwargs):
+    """fused_rmsnorm_mxfp4_quant_fwd(input bf16 [M,D], weight bf16 [D], output u8 [M,D/2], scales u8 [M,D/32], eps)"""
+    return _call("fused_mxfp4_quant_tk", "fused_rmsnorm_mxfp4_quant_fwd", *args, **kwargs)
+
+
+def swiglu_quant_fwd(*args, **kwargs):
+    """swiglu_quant_fwd(input bf16 [M,2F], output e4m3 [M,F], scales f32 [M] or [M,F/128], alpha=1.0,
+    interleaved=False, group_size=0) (extension)"""
+    return _call("quant_tk", "swiglu_quant_fwd", *args, **kwargs)
+
+
 def group_quant_fwd(*args, **kwargs):
     """group_quant_fwd(input bf16 [M,K], output [M,K], scales f32 [M,K/g], group_size=128) (extension)"""
     return _call("quant_tk", "group_quant_fwd", *args, **kwargs)

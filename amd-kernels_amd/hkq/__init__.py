@@ -35,6 +35,8 @@ SIGNATURES = {
     "hkq_gemm_blockscale": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "hkq_moe_a8w8": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]
                      + [_I64] * 12 + [_P]),
+    "hkq_rmsnorm_quant": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _P]),
+    "hkq_swiglu_quant": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _I, _P]),
     "hkq_moe_topk": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _I, _P]),
     "hkq_sum_bitmatrix_rows": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "hkq_sum_bitmatrix_rows_fused": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P]),
@@ -162,6 +164,40 @@ def mx_dequant(q, s, K: int, is_fp4: bool = True, stream=None):
     out = torch.empty((M, K), dtype=torch.bfloat16, device=q.device)
     call("hkq_mx_dequant", _ptr(q), _ptr(s), _ptr(out), M, K, int(is_fp4), _stream(stream))
     return out
+
+
+def rmsnorm_quant(x, w, eps: float = 1e-6, kind: int = 0, q=None, s=None, stream=None):
+    """RMSNorm + quantization of bf16 [M, D] with weight bf16 [D]. kind 0: 1x128
+    FP8 -> (q float8_e4m3fn [M, D], s fp32 [M, D/128]); kind 1: MXFP4 ->
+    (q uint8 [M, D/2], s uint8 e8m0 [M, D/32])."""
+    import torch
+
+    M, D = x.shape
+    if q is None:
+        q = (torch.empty((M, D), dtype=torch.float8_e4m3fn, device=x.device) if kind == 0
+             else torch.empty((M, D // 2), dtype=torch.uint8, device=x.device))
+    if s is None:
+        s = (torch.empty((M, D // 128), dtype=torch.float32, device=x.device) if kind == 0
+             else torch.empty((M, D // 32), dtype=torch.uint8, device=x.device))
+    call("hkq_rmsnorm_quant", _ptr(x), _ptr(w), _ptr(q), _ptr(s), M, D, x.stride(0), q.stride(0), s.stride(0),
+         eps, kind, _stream(stream))
+    return q, s
+
+
+def swiglu_quant(y, alpha: float = 1.0, interleaved: bool = False, group: int = 0, q=None, s=None, stream=None):
+    """SiLU-and-mul of a gate/up output bf16 [M, 2F] + FP8 quantization:
+    (q float8_e4m3fn [M, F], s fp32 [M] (group 0) or [M, F/128] (group 128))."""
+    import torch
+
+    M, F2 = y.shape
+    F = F2 // 2
+    if q is None:
+        q = torch.empty((M, F), dtype=torch.float8_e4m3fn, device=y.device)
+    if s is None:
+        s = torch.empty((M,) if group == 0 else (M, F // 128), dtype=torch.float32, device=y.device)
+    call("hkq_swiglu_quant", _ptr(y), _ptr(q), _ptr(s), M, F, y.stride(0), q.stride(0),
+         s.stride(0) if group else 0, alpha, int(interleaved), group, _stream(stream))
+    return q, s
 
 
 def _workspace(nbytes: int, like):

@@ -40,6 +40,8 @@ BLOCKSCALE = [(2048, 24576, 1536), (2048, 7168, 18432), (2048, 7168, 2048)]
 MOE = dict(T=4096, E=8, topk=2, hidden=4096, ffn=14336)
 # routing pipelines timed beside the Mixtral one: (tokens, experts, top-k)
 ROUTING_EXTRA = [(4096, 256, 8), (32768, 256, 8)]
+# fused RMSNorm + quantizer cases: (rows, hidden, kind 0 = FP8 1x128 / 1 = MXFP4)
+RMSNORM_CASES = [(4096, 4096, 0), (16384, 7168, 0), (4096, 8192, 1), (16384, 7168, 1)]
 # A8W8 shape sweep (N, K) x M of the reference's GEMM benchmark configuration
 SWEEP_NK = [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)]
 SWEEP_M = [1, 16, 128, 1024, 4096]
@@ -110,7 +112,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant", "blockscale", "moe", "sweep", "copy"], default=None,
+    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant", "blockscale", "moe", "fused", "sweep", "copy"],
+                    default=None,
                     help="run one kernel only (for profiling); prints no JSON line. 'copy' is a plain "
                          "1 GiB device copy used to calibrate the HBM byte counters")
     args = ap.parse_args()
@@ -193,7 +196,7 @@ def main():
         res["blockscale"] = sum(r["ms"] for r in bs_res)
 
     # ---- A8W8 MoE grouped GEMM, Mixtral-8x7B (E=8, top-2, 4096 tokens, 4096 -> 14336 gate/up, down) ----
-    moe_res, routing_res = [], []
+    moe_res, routing_res, fused_res = [], [], []
     if args.only in (None, "moe"):
         T, E, topk, hidden, ffn = MOE["T"], MOE["E"], MOE["topk"], MOE["hidden"], MOE["ffn"]
         # routing on the GPU from seeded router logits ~N(0,1): top-2 (with softmax over
@@ -208,26 +211,95 @@ def main():
         routing_res.append({"T": T, "E": E, "topk": topk, "us": round(ms_r * 1e3, 2), "calls": 4})
         xm = seeded_bf16((T, hidden), 1.0, 9)
         qx, sx = hkq.per_token_quant(xm)
-        for name, (nn, kk) in (("gate_up", (2 * ffn, hidden)), ("down", (hidden, ffn))):
+
+        def expert_weights(nn, kk, seed):
             wq = torch.empty((E, nn, kk), dtype=torch.float8_e4m3fn, device="cuda")
             ws_m = torch.empty((E, nn), dtype=torch.float32, device="cuda")
             for e in range(E):  # per-channel quantization of each expert's [N, K] weights
-                hkq.per_token_quant(seeded_bf16_dev((nn, kk), 0.02, 10 + e), hkq.KIND_FP8, wq[e], ws_m[e])
-            xin, sin = (qx, sx) if kk == hidden else hkq.per_token_quant(seeded_bf16_dev((T, kk), 1.0, 20))
-            Ym = torch.empty((T * topk, nn), dtype=torch.bfloat16, device="cuda")
-            torch.cuda.synchronize()
+                hkq.per_token_quant(seeded_bf16_dev((nn, kk), 0.02, seed + e), hkq.KIND_FP8, wq[e], ws_m[e])
+            return wq, ws_m
+
+        # the layer: gate/up over gathered tokens -> SwiGLU + per-token FP8 of the
+        # expert-sorted rows -> down over those rows (no gather)
+        w1, ws1 = expert_weights(2 * ffn, hidden, 10)
+        w2, ws2 = expert_weights(hidden, ffn, 40)
+        Y1 = torch.empty((T * topk, 2 * ffn), dtype=torch.bfloat16, device="cuda")
+        Y2 = torch.empty((T * topk, hidden), dtype=torch.bfloat16, device="cuda")
+        q2 = torch.empty((T * topk, ffn), dtype=torch.float8_e4m3fn, device="cuda")
+        s2 = torch.empty((T * topk,), dtype=torch.float32, device="cuda")
+        hkq.moe_a8w8(qx, w1, hist, offs, expt_data, topk, gather=gather, x_scale=sx, w_scale=ws1, Y=Y1)
+        hkq.swiglu_quant(Y1, q=q2, s=s2)
+        torch.cuda.synchronize()
+        steps_fns = (
+            ("gate_up", 2 * ffn, hidden, lambda: hkq.moe_a8w8(qx, w1, hist, offs, expt_data, topk, gather=gather,
+                                                              x_scale=sx, w_scale=ws1, Y=Y1)),
+            ("down", hidden, ffn, lambda: hkq.moe_a8w8(q2, w2, hist, offs, expt_data, 1, gather=None, x_scale=s2,
+                                                       w_scale=ws2, Y=Y2)),
+        )
+        for name, nn, kk, fn in steps_fns:
             log(f"moe {name} N={nn} K={kk}")
-            ms_m = time_launches(lambda: hkq.moe_a8w8(xin, wq, hist, offs, expt_data, topk, gather=gather,
-                                                      x_scale=sin, w_scale=ws_m, Y=Ym), steps, warmup)
+            ms_m = time_launches(fn, steps, warmup)
             moe_res.append({"proj": name, "N": nn, "K": kk, "ms": round(ms_m, 5),
                             "tflops": round(2.0 * T * topk * nn * kk / (ms_m * 1e-3) / 1e12, 2)})
-            del wq
-        res["moe"] = sum(r["ms"] for r in moe_res)
+        log(f"swiglu + FP8 [{T * topk}, 2x{ffn}]")
+        launch = hkq.bind("hkq_swiglu_quant", Y1.data_ptr(), q2.data_ptr(), s2.data_ptr(), T * topk, ffn, 2 * ffn, ffn,
+                          0, 1.0, 0, 0, torch.cuda.current_stream().cuda_stream)
+        ms_sw = time_launches(launch, steps, warmup)
+        sw_bytes = T * topk * (4 * ffn + ffn + 4)
+        fused_res.append({"op": "swiglu_fp8_per_token", "M": T * topk, "F": ffn, "us": round(ms_sw * 1e3, 2),
+                          "GB/s": round(sw_bytes / (ms_sw * 1e-3) / 1e9, 1),
+                          "pct_hbm_peak": round(100 * sw_bytes / (ms_sw * 1e-3) / 1e9 / PEAK_HBM_GBS, 1)})
+        layer_ms = ms_r + sum(r["ms"] for r in moe_res) + ms_sw
+        moe_res.append({"proj": "layer (routing + gate_up + swiglu/quant + down)", "ms": round(layer_ms, 5)})
+        del w1, w2
+        res["moe"] = layer_ms
         for (Tr, Er, Kr) in ROUTING_EXTRA:
             lg = seeded_bf16((Tr, Er), 1.0, 30)
             _, route = hkq.moe_routing_plan(lg, Kr, 128)
             ms_r = time_launches(route, steps, warmup, preheat=0.05)
             routing_res.append({"T": Tr, "E": Er, "topk": Kr, "us": round(ms_r * 1e3, 2), "calls": 4})
+
+    # ---- fused RMSNorm + quantizers (HBM-bound) ----
+    if args.only in (None, "fused"):
+        for (mm, dd, kind) in RMSNORM_CASES:
+            xr = seeded_bf16((mm, dd), 1.0, 50)
+            wr = seeded_bf16((dd,), 1.0, 51)
+            qr, sr = hkq.rmsnorm_quant(xr, wr, 1e-6, kind)
+            torch.cuda.synchronize()
+            log(f"rmsnorm + {'fp8 1x128' if kind == 0 else 'mxfp4'} [{mm}, {dd}]")
+            launch = hkq.bind("hkq_rmsnorm_quant", xr.data_ptr(), wr.data_ptr(), qr.data_ptr(), sr.data_ptr(), mm, dd,
+                              dd, qr.stride(0), sr.stride(0), 1e-6, kind, torch.cuda.current_stream().cuda_stream)
+            ms_n = time_launches(launch, steps, warmup)
+            nb = mm * dd * (2 + (1 + 4 / 128 if kind == 0 else 0.5 + 1 / 32)) + 2 * dd
+            fused_res.append({"op": "rmsnorm_fp8_1x128" if kind == 0 else "rmsnorm_mxfp4", "M": mm, "D": dd,
+                              "us": round(ms_n * 1e3, 2), "GB/s": round(nb / (ms_n * 1e-3) / 1e9, 1),
+                              "pct_hbm_peak": round(100 * nb / (ms_n * 1e-3) / 1e9 / PEAK_HBM_GBS, 1)})
+            del xr, qr, sr
+        # the plain quantizers of the same family, for comparison
+        for (mm, dd) in ((4096, 8192), (16384, 7168)):
+            xr = seeded_bf16((mm, dd), 1.0, 52)
+            q4 = torch.empty((mm, dd // 2), dtype=torch.uint8, device="cuda")
+            s4 = torch.empty((mm, dd // 32), dtype=torch.uint8, device="cuda")
+            log(f"mx quant fp4 [{mm}, {dd}]")
+            launch = hkq.bind("hkq_mx_quant", xr.data_ptr(), q4.data_ptr(), s4.data_ptr(), mm, dd, dd, 1,
+                              torch.cuda.current_stream().cuda_stream)
+            ms_q = time_launches(launch, steps, warmup)
+            nb = mm * dd * (2 + 0.5 + 1 / 32)
+            fused_res.append({"op": "mx_quant_fp4", "M": mm, "D": dd, "us": round(ms_q * 1e3, 2),
+                              "GB/s": round(nb / (ms_q * 1e-3) / 1e9, 1),
+                              "pct_hbm_peak": round(100 * nb / (ms_q * 1e-3) / 1e9 / PEAK_HBM_GBS, 1)})
+            qg = torch.empty((mm, dd), dtype=torch.float8_e4m3fn, device="cuda")
+            sg = torch.empty((mm, dd // 128), dtype=torch.float32, device="cuda")
+            log(f"group quant fp8 1x128 [{mm}, {dd}]")
+            launch = hkq.bind("hkq_group_quant", xr.data_ptr(), qg.data_ptr(), sg.data_ptr(), mm, dd, dd, dd,
+                              dd // 128, 128, hkq.KIND_FP8, torch.cuda.current_stream().cuda_stream)
+            ms_g = time_launches(launch, steps, warmup)
+            nb = mm * dd * (2 + 1 + 4 / 128)
+            fused_res.append({"op": "group_quant_fp8_1x128", "M": mm, "D": dd, "us": round(ms_g * 1e3, 2),
+                              "GB/s": round(nb / (ms_g * 1e-3) / 1e9, 1),
+                              "pct_hbm_peak": round(100 * nb / (ms_g * 1e-3) / 1e9 / PEAK_HBM_GBS, 1)})
+            del xr, qg, sg, q4, s4
+        res["fused"] = sum(r["us"] for r in fused_res) * 1e-3
 
     # ---- A8W8 shape sweep and the MXFP4 M=128 configuration (plans with smaller tiles / split K) ----
     sweep = []
@@ -271,6 +343,8 @@ def main():
         log(json.dumps({k: round(v * 1e3, 2) for k, v in res.items()}) + "  (us per launch)")
         for r in routing_res:
             log(json.dumps({"routing": r}))
+        for r in moe_res + fused_res:
+            log(json.dumps(r))
         if sweep:
             for r in sweep:
                 log(json.dumps(r))
@@ -318,6 +392,7 @@ def main():
         "blockscale": bs_res,
         "moe_mixtral": moe_res,
         "moe_routing": routing_res,
+        "fused_quant": fused_res,
         "sweep": sweep,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_FP8_TFLOPS, 4), "traffic": read_traffic()},

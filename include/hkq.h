@@ -76,6 +76,35 @@ int hkq_mx_quant(const void* x, void* q, void* s, int64_t M, int64_t K, int64_t 
  * Replaces quant_moe_tk.upcast_from_mxfp (kernels/moe-misc/quant_moe/kernel.cpp:433-450). */
 int hkq_mx_dequant(const void* q, const void* s, void* out, int64_t M, int64_t K, int is_fp4, hkq_stream_t stream);
 
+/* ---- quantizers fused with their producer -------------------------------- */
+
+/* RMSNorm + quantization of x bf16 [M, ldx] with weight w bf16 [D] (D <= 8192):
+ * r = 1 / sqrt(sum(x^2) / D + eps), y = (x * r) * w, with sum(x^2) reduced in a
+ * fixed order (per lane of a wave: fma chain over the 16-byte chunks
+ * c = lane + 64 i, then an xor butterfly over the 64 lanes), then
+ * kind 0: 1x128 FP8, s[m, g] = max(amax/448, 1e-10) fp32 [M, lds],
+ *         q = E4M3FN(clamp(y / s)) [M, ldq] (D % 128 == 0);
+ * kind 1: MXFP4, s = e8m0 of the MX shared exponent [M, lds] bytes, q = two
+ *         E2M1 codes per byte [M, ldq] (D % 32 == 0).
+ * Replaces fused_rmsnorm_fp8_quant_fwd (kernels/quantization/fused_fp8_quant/
+ * kernel.cpp:251-268) and fused_rmsnorm_mxfp4_quant_fwd (fused_mxfp4_quant/
+ * kernel.cpp:291-308), which accept only D in {4096, 8192} and write an affine
+ * byte instead of E4M3 codes (fused_fp8_quant/kernel.cpp:206). */
+int hkq_rmsnorm_quant(const void* x, const void* w, void* q, void* s, int64_t M, int64_t D, int64_t ldx, int64_t ldq,
+                      int64_t lds, float eps, int kind, hkq_stream_t stream);
+
+/* SwiGLU + FP8 quantization of a gate/up GEMM output y bf16 [M, ldy] (2F
+ * columns used): act = silu(g) * u with silu(g) = g / (1 + 2^(-log2(e) * alpha * g))
+ * (the silu of kernels/moe-gemm/moe_op_gemm_a8w8/kernel.cpp:57-59);
+ * (g, u) = columns (k, F + k), or (2k, 2k + 1) when interleaved (the column
+ * order of kernels/moe-gemm/moe_op_silu_fused/kernel.cpp:9-12). group 0: one
+ * scale per row s[m]; group 128: s[m * lds + k / 128]; s = max(amax/448, 1e-10),
+ * q = E4M3FN(clamp(act / s)) [M, ldq]. No counterpart in the reference, which
+ * leaves the activation to a separate kernel (moe_op_gemm_a8w8/kernel.cpp:162);
+ * this feeds the per-token FP8 down projection of hkq_moe_a8w8. */
+int hkq_swiglu_quant(const void* y, void* q, float* s, int64_t M, int64_t F, int64_t ldy, int64_t ldq, int64_t lds,
+                     float alpha, int interleaved, int group, hkq_stream_t stream);
+
 /* ---- dense GEMMs (A [M, K], B [N, K], both K-contiguous; C bf16 [M, ldc]) ---- */
 
 /* C = bf16((A . B^T) * sa[m] * sb[n]); A, B E4M3FN; sa fp32 [M], sb fp32 [N].

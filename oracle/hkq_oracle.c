@@ -12,6 +12,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 static inline float bits2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
@@ -257,4 +258,97 @@ void orc_e2m1_encode_array(const float* x, int64_t n, uint8_t* out) {
 
 void orc_mx_scale_exp_array(const float* amax, int64_t n, int32_t* out) {
     for (int64_t i = 0; i < n; ++i) out[i] = orc_mx_scale_exp(amax[i]);
+}
+
+/* ---- quantizers fused with their producer ---------------------------------- */
+
+/* RMSNorm + quantization (quantization/fused_fp8_quant/kernel.cpp:37-204,
+ * fused_mxfp4_quant/kernel.cpp:40-243): y = x * rsqrt(mean(x^2) + eps) * w,
+ * then the 1x128 FP8 rule (kind 0) or the MXFP4 rule (kind 1). The reference
+ * leaves the summation order and the rsqrt rounding open (a 256-thread tree,
+ * an approximate rsqrtf); this restatement fixes both as the product does so
+ * the codes can be compared bit for bit: 64 partial sums, partial l an fmaf
+ * chain over columns 8c .. 8c+7 of the chunks c = l, l + 64, ..., then an xor
+ * butterfly (partial l += partial l^o for o = 1, 2, ..., 32); r = 1 / sqrtf(sum
+ * / D + eps) correctly rounded; y = (x * r) * w. x, w bf16 bits; q, s as the
+ * product writes them (s fp32 per 128 columns, or e8m0 bytes per 32). */
+void orc_rmsnorm_quant(const uint16_t* x, const uint16_t* w, int64_t M, int64_t D, float eps, int kind, uint8_t* q,
+                       void* s) {
+    const int64_t nch = D / 8;
+    float* y = (float*)malloc(sizeof(float) * (size_t)D);
+    for (int64_t m = 0; m < M; ++m) {
+        const uint16_t* xr = x + m * D;
+        float part[64];
+        for (int l = 0; l < 64; ++l) {
+            float acc = 0.0f;
+            for (int64_t c = l; c < nch; c += 64)
+                for (int j = 0; j < 8; ++j) {
+                    const float v = orc_bf16_to_f32(xr[c * 8 + j]);
+                    acc = fmaf(v, v, acc);
+                }
+            part[l] = acc;
+        }
+        for (int o = 1; o < 64; o <<= 1) {
+            float nxt[64];
+            for (int l = 0; l < 64; ++l) nxt[l] = part[l] + part[l ^ o];
+            memcpy(part, nxt, sizeof(part));
+        }
+        const float r = 1.0f / sqrtf(part[0] / (float)D + eps);
+        for (int64_t k = 0; k < D; ++k) y[k] = (orc_bf16_to_f32(xr[k]) * r) * orc_bf16_to_f32(w[k]);
+        if (kind == 0) {
+            for (int64_t g0 = 0; g0 < D; g0 += 128) {
+                float amax = 0.0f;
+                for (int64_t k = g0; k < g0 + 128; ++k) amax = max_num(amax, fabsf(y[k]));
+                const float sc = max_num(amax / 448.0f, 1e-10f);
+                const float rc = 1.0f / sc;
+                ((float*)s)[m * (D / 128) + g0 / 128] = sc;
+                for (int64_t k = g0; k < g0 + 128; ++k)
+                    q[m * D + k] = orc_e4m3fn_encode(max_num(min_num(y[k] * rc, 448.0f), -448.0f));
+            }
+        } else {
+            for (int64_t g0 = 0; g0 < D; g0 += 32) {
+                float amax = 0.0f;
+                for (int64_t k = g0; k < g0 + 32; ++k) amax = max_num(amax, fabsf(y[k]));
+                const int e = orc_mx_scale_exp(amax);
+                const float mul = ldexpf(1.0f, -e);
+                ((uint8_t*)s)[m * (D / 32) + g0 / 32] = (uint8_t)(e + 127);
+                for (int64_t k = g0; k < g0 + 32; k += 2) {
+                    const uint8_t lo = orc_e2m1_encode(y[k] * mul), hi = orc_e2m1_encode(y[k + 1] * mul);
+                    q[m * (D / 2) + k / 2] = (uint8_t)(lo | (hi << 4));
+                }
+            }
+        }
+    }
+    free(y);
+}
+
+/* SwiGLU + FP8 quantization: act = silu(g) * u, silu(g) = g / (1 + exp2f(-1.44269504089f
+ * * alpha * g)) (moe-gemm/moe_op_gemm_a8w8/kernel.cpp:57-59), (g, u) = columns (k, F + k)
+ * or (2k, 2k + 1) when interleaved (moe-gemm/moe_op_silu_fused/kernel.cpp:9-12);
+ * then per row (group 0) or per 128 columns s = max(amax/448, 1e-10),
+ * q = E4M3FN(clamp(act * (1/s), +-448)). y bf16 bits [M, 2F]; act fp32 [M, F]
+ * is returned too (NULL: not). */
+void orc_swiglu_quant(const uint16_t* y, int64_t M, int64_t F, float alpha, int interleaved, int group, uint8_t* q,
+                      float* s, float* act_out) {
+    float* act = (float*)malloc(sizeof(float) * (size_t)F);
+    const int64_t G = group ? group : F;
+    for (int64_t m = 0; m < M; ++m) {
+        const uint16_t* yr = y + m * 2 * F;
+        for (int64_t k = 0; k < F; ++k) {
+            const float g = orc_bf16_to_f32(interleaved ? yr[2 * k] : yr[k]);
+            const float u = orc_bf16_to_f32(interleaved ? yr[2 * k + 1] : yr[F + k]);
+            act[k] = g / (1.0f + exp2f(-1.44269504089f * alpha * g)) * u;
+            if (act_out) act_out[m * F + k] = act[k];
+        }
+        for (int64_t g0 = 0; g0 < F; g0 += G) {
+            float amax = 0.0f;
+            for (int64_t k = g0; k < g0 + G; ++k) amax = max_num(amax, fabsf(act[k]));
+            const float sc = max_num(amax / 448.0f, 1e-10f);
+            const float rc = 1.0f / sc;
+            s[group ? m * (F / G) + g0 / G : m] = sc;
+            for (int64_t k = g0; k < g0 + G; ++k)
+                q[m * F + k] = orc_e4m3fn_encode(max_num(min_num(act[k] * rc, 448.0f), -448.0f));
+        }
+    }
+    free(act);
 }

@@ -35,6 +35,15 @@ gemm refs              reference formulas (tests/test_gemm.py:116,148-153,
 moe_ref / ogs_routing  tests/test_moe.py:97-128,733-753 restated; invariants
                        (histogram sum, exclusive scan, gather permutation) and
                        agreement with per-expert dense GEMMs.
+rmsnorm_quant          fp64 numpy RMSNorm (the test_parity.py formula of
+                       fused_fp8_quant) then the pinned group / MX quantizers:
+                       codes equal except where y sits within an ulp of a
+                       rounding boundary; known answers for constant rows
+                       (rms = |c| exactly); the fixed-order sum against math.fsum.
+swiglu_quant           torch.nn.functional.silu(g) * u in fp64 then the pinned
+                       per-token quantizer (codes within one step; scales within
+                       4 ulp); alpha scaling; interleaved == split after a
+                       column permutation.
 topk                   torch.topk + torch.softmax (fp64) on tie-free logits;
                        brute-force sort by (-value, expert) on logits with many
                        ties, signed zeros, -inf and NaN (tests/test_oracle_routing.py).
@@ -104,6 +113,10 @@ def lib():
             getattr(L, name).restype = None
             getattr(L, name).argtypes = [P, I64, P]
         I = ctypes.c_int
+        L.orc_rmsnorm_quant.restype = None
+        L.orc_rmsnorm_quant.argtypes = [P, P, I64, I64, ctypes.c_float, I, P, P]
+        L.orc_swiglu_quant.restype = None
+        L.orc_swiglu_quant.argtypes = [P, I64, I64, ctypes.c_float, I, I, P, P, P]
         L.orc_topk.restype = None
         L.orc_topk.argtypes = [P, I64, I64, I64, I, I, P, P, I64, P]
         L.orc_sum_bitmatrix_rows.restype = None
@@ -370,6 +383,39 @@ def moe_ref(X, W, x_scale, w_scale, bias, gather, hist, offs, expt_data, topk,
             r = r + np.asarray(bias, np.float64)[e][None, :]
         Y[sidx] = r
     return Y
+
+
+# ----------------------------------------------------------------------------
+# Quantizers fused with their producer
+# ----------------------------------------------------------------------------
+
+def rmsnorm_quant(xb: np.ndarray, wb: np.ndarray, eps: float, kind: int):
+    """RMSNorm + quantization of bf16 bits [M, D] (weight bits [D]); kind 0:
+    (E4M3FN codes [M, D], fp32 scales [M, D/128]); kind 1: (packed E2M1 [M, D/2],
+    e8m0 [M, D/32])."""
+    x = np.ascontiguousarray(xb, dtype=np.uint16)
+    w = np.ascontiguousarray(wb, dtype=np.uint16)
+    M, D = x.shape
+    if kind == 0:
+        q = np.zeros((M, D), np.uint8)
+        s = np.zeros((M, D // 128), np.float32)
+    else:
+        q = np.zeros((M, D // 2), np.uint8)
+        s = np.zeros((M, D // 32), np.uint8)
+    lib().orc_rmsnorm_quant(_p(x), _p(w), M, D, eps, kind, _p(q), _p(s))
+    return q, s
+
+
+def swiglu_quant(yb: np.ndarray, alpha: float = 1.0, interleaved: bool = False, group: int = 0):
+    """SwiGLU + FP8 of bf16 bits [M, 2F] -> (codes [M, F], scales [M] or [M, F/128], act fp32 [M, F])."""
+    y = np.ascontiguousarray(yb, dtype=np.uint16)
+    M, F2 = y.shape
+    F = F2 // 2
+    q = np.zeros((M, F), np.uint8)
+    s = np.zeros((M,) if group == 0 else (M, F // group), np.float32)
+    act = np.zeros((M, F), np.float32)
+    lib().orc_swiglu_quant(_p(y), M, F, alpha, int(interleaved), group, _p(q), _p(s), _p(act))
+    return q, s, act
 
 
 # ----------------------------------------------------------------------------
