@@ -53,6 +53,7 @@ MODULES = {
     "gemm_a8w8_blockscale_tk": "bind_gemm_a8w8_blockscale.cpp",
     "moe_op_gemm_a8w8_tk": "bind_moe_op_gemm_a8w8.cpp",
     "moe_op_gemm_a8w8_blockscale_tk": "bind_moe_op_gemm_a8w8_blockscale.cpp",
+    "moe_op_mxfp4_tk": "bind_moe_op_mxfp4.cpp",
     "fused_fp8_quant_tk": "bind_fused_fp8_quant.cpp",
     "fused_mxfp4_quant_tk": "bind_fused_mxfp4_quant.cpp",
     "moe_topk_tk": "bind_moe_topk.cpp",

@@ -143,10 +143,12 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 //   row_scale(j) -> scale of the lane's m in m-tile j; col_scale4(i, g) -> the
 //   4 scales of n = i*32 + 8g + 4*(lane/32) + 0..3 (both relative to the wave);
 //   col_bias4(i, g) -> the 4 values added after scaling (zero when unused).
+// Scale, convert and stage the wave's (TM*32) x (TN*32) sub-tile in LDS as bf16
+// rows of PITCH bytes (returns the wave's staging area).
 template <int TM, int TN, typename RowScale, typename ColScale4, typename ColBias4>
-__device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uint8_t* smem, int wave, int lane,
-                                                uint16_t* C, int64_t ldc, int M, int N, int mw, int nw, bool c16,
-                                                RowScale row_scale, ColScale4 col_scale4, ColBias4 col_bias4) {
+__device__ __forceinline__ HKQ_LDS uint8_t* stage_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uint8_t* smem, int wave,
+                                                            int lane, RowScale row_scale, ColScale4 col_scale4,
+                                                            ColBias4 col_bias4) {
     constexpr int PITCH = TN * 32 * 2 + 16;
     static_assert((TN * 32 * 2) % 128 == 0, "rows are whole 128-byte segments");
     HKQ_LDS uint8_t* ep = smem + wave * (TM * 32) * PITCH;
@@ -170,6 +172,30 @@ __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uin
             }
         }
     }
+    return ep;
+}
+
+// One 16-byte piece (8 bf16) of a staged row to dst, of which n_left columns
+// are inside C (N % 4 == 0: a piece is whole, half or out of range).
+__device__ __forceinline__ void store_piece_bf16(uint16_t* dst, const v4i& v, int n_left, bool c16) {
+    if (n_left >= 8) {
+        if (c16) {
+            __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(dst));
+        } else {
+            __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
+            __builtin_nontemporal_store(v2i{v[2], v[3]}, reinterpret_cast<v2i*>(dst + 4));
+        }
+    } else if (n_left > 0) {
+        __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
+    }
+}
+
+template <int TM, int TN, typename RowScale, typename ColScale4, typename ColBias4>
+__device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uint8_t* smem, int wave, int lane,
+                                                uint16_t* C, int64_t ldc, int M, int N, int mw, int nw, bool c16,
+                                                RowScale row_scale, ColScale4 col_scale4, ColBias4 col_bias4) {
+    constexpr int PITCH = TN * 32 * 2 + 16;
+    HKQ_LDS uint8_t* ep = stage_tile_bf16<TM, TN>(acc, smem, wave, lane, row_scale, col_scale4, col_bias4);
     // LDS operations of a wave complete in order: the reads below see the writes above.
     constexpr int SEGS = TN * 32 * 2 / 16;  // 16-byte pieces per row
     constexpr int ROWS_PER_PASS = 64 / SEGS;
@@ -198,20 +224,28 @@ __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uin
         const v4i v = lds_read16(ep + r * PITCH + seg * 16);
         const int m = mw + r;
         const int n = nw + seg * 8;
-        if (m < M) {
-            // N % 4 == 0: a piece is whole, half (4 values) or out of range
-            uint16_t* dst = C + (int64_t)m * ldc + n;
-            if (n + 8 <= N) {
-                if (c16) {
-                    __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(dst));
-                } else {
-                    __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
-                    __builtin_nontemporal_store(v2i{v[2], v[3]}, reinterpret_cast<v2i*>(dst + 4));
-                }
-            } else if (n < N) {
-                __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
-            }
-        }
+        if (m < M) store_piece_bf16(C + (int64_t)m * ldc + n, v, N - n, c16);
+    }
+}
+
+// As store_tile_bf16, with the rows scattered: wave row r (0 .. TM*32-1) goes
+// to C row row_of(r), or nowhere when row_of(r) < 0.
+template <int TM, int TN, typename RowOf, typename RowScale, typename ColScale4, typename ColBias4>
+__device__ __forceinline__ void store_tile_bf16_rows(v16f (&acc)[TN][TM], HKQ_LDS uint8_t* smem, int wave, int lane,
+                                                     uint16_t* C, int64_t ldc, int N, int nw, bool c16, RowOf row_of,
+                                                     RowScale row_scale, ColScale4 col_scale4, ColBias4 col_bias4) {
+    constexpr int PITCH = TN * 32 * 2 + 16;
+    HKQ_LDS uint8_t* ep = stage_tile_bf16<TM, TN>(acc, smem, wave, lane, row_scale, col_scale4, col_bias4);
+    constexpr int SEGS = TN * 32 * 2 / 16;
+    constexpr int ROWS_PER_PASS = 64 / SEGS;
+    const int rl = lane / SEGS, seg = lane % SEGS;
+#pragma unroll 4
+    for (int r0 = 0; r0 < TM * 32; r0 += ROWS_PER_PASS) {
+        const int r = r0 + rl;
+        const v4i v = lds_read16(ep + r * PITCH + seg * 16);
+        const int64_t m = row_of(r);
+        const int n = nw + seg * 8;
+        if (m >= 0) store_piece_bf16(C + m * ldc + n, v, N - n, c16);
     }
 }
 

@@ -64,6 +64,9 @@ struct LoopSrc {
     const uint8_t *as, *bs;
     int64_t as_bytes, bs_bytes, lsa, lsb;
     int KT;  // K-tiles
+    // FP4 with gathered A rows: byte offset of tile row r's scale row inside
+    // `as` (beyond as_bytes for rows that read zero); nullptr: row r * lsa
+    const HKQ_LDS uint32_t* sa_rows = nullptr;
 };
 
 // Byte offset (row and logical chunk, excluding the K position) of LDS-direct
@@ -131,7 +134,9 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
         // row slot s = lane / 2 of the group; its two 16-byte halves are stored
         // swapped when bit 3 of s is set (see read_scale)
         const uint32_t half = (uint32_t)((lane & 1) ^ ((lane >> 4) & 1));
-        const uint32_t off = (uint32_t)((isa ? r : r - BM) * (isa ? src.lsa : src.lsb)) + half * 16u;
+        const uint32_t row_off = isa ? (src.sa_rows ? src.sa_rows[r] : (uint32_t)(r * src.lsa))
+                                     : (uint32_t)((r - BM) * src.lsb);
+        const uint32_t off = row_off + half * 16u;
         lds_load16(base, live && bytes > 0 ? (uint32_t)bytes : 0u, sblk + (blk & 1) * Cfg::SB_SLOT + g * 1024, off);
     };
 
@@ -162,7 +167,7 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
         } else if (idx < LA + LB + LSA) {
             const int g = ((idx - LA - LB) * NW + wave) % GA;
             const int kb4 = kt * 4;
-            const uint32_t off = (uint32_t)((g * 64 + lane) * src.lsa);
+            const uint32_t off = src.sa_rows ? src.sa_rows[g * 64 + lane] : (uint32_t)((g * 64 + lane) * src.lsa);
             lds_load4(src.as + kb4, live ? (uint32_t)(src.as_bytes - kb4) : 0u, st + (BM + BN) * KTB + g * 256, off);
         } else {
             const int g = ((idx - LA - LB - LSA) * NW + wave) % GB;

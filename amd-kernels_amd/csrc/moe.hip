@@ -152,6 +152,147 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
     return hkq_launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// MXFP4 MoE GEMM over the block-sorted routing of moe_align_block_size
+// (moe-gemm/moe_op_mxfp4/kernel.cpp:90-237): tile row r of 128-row block pm
+// is gate id = sorted_token_ids[pm*128 + r] (valid when < num_valid_tokens),
+// its A row is id / top_k, its expert expert_ids[pm] (-1: the block's valid
+// rows are written as zeros), and
+//   C[id, n] = bf16((sum_k A[id/topk, k] B[e, n, k]) * a_scale[0] * b_scale[e]
+//                   * (mul_routed_weight ? topk_weights[id] : 1))
+// with A, B E2M1 pairs and e8m0 scales per 32 K values on both. Output rows
+// are written at the gate id (the reference's C[token_id]).
+// ---------------------------------------------------------------------------
+struct MoeFp4Params {
+    const uint8_t* A;       // [tokens, sam] bytes, K/2 used
+    const uint8_t* As;      // [tokens, sas] e8m0, K/32 used
+    const uint8_t* B;       // expert e at B + e*sbe, row n at + n*sbn (K/2 bytes)
+    const uint8_t* Bs;      // expert e at Bs + e*sbse, row n at + n*sbsn (K/32 bytes)
+    uint16_t* C;            // row id at C + id*scm
+    const float* a_scale;   // nullptr: 1
+    const float* b_scale;   // nullptr: 1
+    const float* topk_w;    // nullptr: no routed weight
+    const int32_t* sorted;  // [grid_m * 128]
+    const int32_t* expert;  // [grid_m]
+    int tokens, E, N, K, topk, num_valid, grid_m, tiles_n, group_m, c16;
+    int64_t sam, sas, sbe, sbn, sbse, sbsn, scm;
+};
+
+constexpr uint32_t FP4_OOB = 0x7FFF0000u;  // a row offset past every operand's bounds
+
+template <int KTB, int NS>
+__global__ __launch_bounds__(256, 1) void moe_mxfp4_kernel(const MoeFp4Params p) {
+    constexpr int WAVES_M = 1, WAVES_N = 4, TM = 4, TN = 2;
+    using Cfg = DenseCfg<MODE_MXFP4, WAVES_M, WAVES_N, TM, TN, KTB>;
+    constexpr int NW = Cfg::NW, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
+    static_assert(Cfg::BM == MOE_BM, "one tile row block per routing block");
+
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
+    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+    HKQ_LDS uint32_t* sa_rows = (HKQ_LDS uint32_t*)(smem + Cfg::lds_bytes(NS));
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wn = wave % WAVES_N;
+    const int khalf = lane >> 5;
+
+    int pm, tn;
+    tile_coords(blockIdx.x, p.grid_m, p.tiles_n, p.group_m, pm, tn);
+    const int e = p.expert[pm];
+    const int n0 = tn * BN;
+    const int nw = n0 + wn * TN * 32;
+    const int32_t* ids = p.sorted + (int64_t)pm * MOE_BM;
+    // gate id of tile row r, or -1 when it is padding
+    auto gate_of = [&](int r) {
+        const int id = ids[r];
+        return (id >= 0 && id < p.num_valid) ? id : -1;
+    };
+    // A row of tile row r, or -1 (padding, or a row past the activations)
+    auto arow_of = [&](int r) {
+        const int id = gate_of(r);
+        const int t = id < 0 ? -1 : id / p.topk;
+        return t < p.tokens ? t : -1;
+    };
+
+    if (e < 0 || e >= p.E) {
+        if (e != -1) return;  // an expert id past E: nothing to compute or write
+        // the reference writes zeros to the valid rows of a block without expert
+        for (int r = wave; r < MOE_BM; r += NW) {
+            const int id = gate_of(r);
+            if (id < 0) continue;
+            for (int n = n0 + lane * 4; n < min(p.N, n0 + BN); n += 256)
+                *reinterpret_cast<v2i*>(p.C + (int64_t)id * p.scm + n) = v2i{0, 0};
+        }
+        return;
+    }
+
+    for (int r = threadIdx.x; r < MOE_BM; r += 256) {
+        const int t = arow_of(r);
+        sa_rows[r] = t < 0 ? FP4_OOB : (uint32_t)(t * p.sas);
+    }
+    __syncthreads();
+
+    const int rows_b = min(p.N - n0, BN);
+    LoopSrc src;
+    src.a = p.A;
+    src.a_bytes = min((int64_t)p.tokens * p.sam, (int64_t)FP4_OOB);
+    src.b = p.B + (int64_t)e * p.sbe + (int64_t)n0 * p.sbn;
+    src.b_bytes = min((int64_t)rows_b * p.sbn, (int64_t)FP4_OOB);
+    src.as = p.As;
+    src.as_bytes = min((int64_t)p.tokens * p.sas, (int64_t)FP4_OOB);
+    src.bs = p.Bs + (int64_t)e * p.sbse + (int64_t)n0 * p.sbsn;
+    src.bs_bytes = min((int64_t)rows_b * p.sbsn, (int64_t)FP4_OOB);
+    src.lsa = p.sas;
+    src.lsb = p.sbsn;
+    src.KT = (p.K / 2) / KTB;
+    src.sa_rows = sa_rows;
+    uint32_t a_off[LA], b_off[LB];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+        const int r = (i * NW + wave) * Cfg::RPL + lane / Cfg::KT::CHUNKS;
+        const int t = arow_of(r);
+        a_off[i] = t < 0 ? FP4_OOB : (uint32_t)(t * p.sam) + (uint32_t)(Cfg::KT::load_chunk(lane, r) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.sbn);
+
+    v16f acc[TN][TM];
+    gemm_mainloop<MODE_MXFP4, WAVES_M, WAVES_N, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
+
+    const float g = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
+    store_tile_bf16_rows<TM, TN>(
+        acc, smem, wave, lane, p.C, p.scm, p.N, nw, p.c16 != 0, [&](int r) { return (int64_t)gate_of(r); },
+        [&](int j) {
+            const int id = gate_of(j * 32 + (lane & 31));
+            return (p.topk_w && id >= 0) ? g * p.topk_w[id] : g;
+        },
+        [&](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); },
+        [&](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); });
+}
+
+template <int KTB, int NS>
+static int launch_moe_fp4(MoeFp4Params& p, hipStream_t stream) {
+    using Cfg = DenseCfg<MODE_MXFP4, 1, 4, 4, 2, KTB>;
+    constexpr int LDS = Cfg::lds_bytes(NS) + MOE_BM * 4;
+    static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
+    auto kern = moe_mxfp4_kernel<KTB, NS>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
+        if (err != hipSuccess) {
+            set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", LDS, hipGetErrorString(err));
+            return (int)err;
+        }
+        attr_set = true;
+    }
+    p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
+    if (p.group_m <= 0) p.group_m = 8;
+    const int64_t nblk = (int64_t)p.grid_m * p.tiles_n;
+    if (nblk == 0) return 0;
+    kern<<<dim3((unsigned)nblk), 256, LDS, stream>>>(p);
+    return hkq_launch_status();
+}
+
 }  // namespace hkq
 
 using namespace hkq;
@@ -198,4 +339,58 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     // 128-byte K-tiles (2-stage ring) when every row has whole ones: a partial
     // last K-tile would read the next row's bytes instead of zeros
     return K % 128 == 0 ? launch_moe<4, 4, 128, 2>(p, stream) : launch_moe<4, 4, 64, 3>(p, stream);
+}
+
+extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* A_mx_scale, const void* B_mx_scale,
+                             const float* A_scale, const float* B_scale, const float* topk_weights,
+                             const int32_t* sorted_token_ids, const int32_t* expert_ids, int64_t N, int64_t K,
+                             int64_t num_valid_tokens, int64_t top_k, int mul_routed_weight, int64_t stride_am,
+                             int64_t stride_be, int64_t stride_bn, int64_t stride_cm, int64_t stride_amxm,
+                             int64_t stride_bmxe, int64_t stride_bmxn, int64_t num_tokens, int64_t num_experts,
+                             int64_t grid_m, hipStream_t stream) {
+    HKQ_CHECK_ARG(N >= 0 && K > 0 && num_valid_tokens >= 0 && top_k > 0 && num_tokens >= 0 && num_experts > 0 &&
+                      grid_m >= 0,
+                  "N, num_valid_tokens, num_tokens, grid_m >= 0; K, top_k, num_experts > 0");
+    HKQ_CHECK_ARG(N < (1 << 30) && K < (1 << 30) && grid_m < (1 << 22) && num_tokens < (1 << 30) &&
+                      num_valid_tokens < (1 << 30),
+                  "dimensions out of range");
+    HKQ_CHECK_ARG(K % 128 == 0, "K must be a multiple of 128 (64 bytes of E2M1 pairs)");
+    HKQ_CHECK_ARG(N % 4 == 0, "N must be a multiple of 4");
+    HKQ_CHECK_ARG(stride_am >= K / 2 && stride_am % 16 == 0, "stride_am must be >= K/2 bytes and a multiple of 16");
+    HKQ_CHECK_ARG(stride_bn >= K / 2 && stride_bn % 16 == 0,
+                  "stride_bn must be >= K/2 bytes and a multiple of 16 (B[e] is [N, K/2], K contiguous)");
+    HKQ_CHECK_ARG(stride_be >= 0 && stride_be % 16 == 0, "stride_be must be a non-negative multiple of 16");
+    HKQ_CHECK_ARG(stride_amxm >= K / 32 && stride_bmxn >= K / 32 && stride_bmxe >= 0,
+                  "scale strides must cover K/32 bytes per row (scales [rows, K/32], K contiguous)");
+    HKQ_CHECK_ARG((K / 2) % 128 == 0 || (stride_amxm % 4 == 0 && stride_bmxn % 4 == 0),
+                  "with K % 256 != 0 the scale row strides must be multiples of 4");
+    HKQ_CHECK_ARG((int64_t)num_tokens * stride_am < (int64_t)FP4_OOB &&
+                      (int64_t)num_tokens * stride_amxm < (int64_t)FP4_OOB,
+                  "the activations must span less than 2^31 - 2^16 bytes");
+    HKQ_CHECK_ARG(stride_cm >= N && stride_cm % 4 == 0, "stride_cm must be >= N and a multiple of 4");
+    HKQ_CHECK_ARG(grid_m == 0 || (sorted_token_ids && expert_ids), "sorted_token_ids and expert_ids are required");
+    HKQ_CHECK_ARG(!mul_routed_weight || topk_weights, "topk_weights is required with mul_routed_weight");
+    HKQ_CHECK_ALIGN(A, 16);
+    HKQ_CHECK_ALIGN(B, 16);
+    HKQ_CHECK_ALIGN(A_mx_scale, 4);
+    HKQ_CHECK_ALIGN(B_mx_scale, 4);
+    HKQ_CHECK_ALIGN(C, 8);
+    MoeFp4Params p{};
+    p.A = static_cast<const uint8_t*>(A);
+    p.As = static_cast<const uint8_t*>(A_mx_scale);
+    p.B = static_cast<const uint8_t*>(B);
+    p.Bs = static_cast<const uint8_t*>(B_mx_scale);
+    p.C = static_cast<uint16_t*>(C);
+    p.a_scale = A_scale;
+    p.b_scale = B_scale;
+    p.topk_w = mul_routed_weight ? topk_weights : nullptr;
+    p.sorted = sorted_token_ids;
+    p.expert = expert_ids;
+    p.tokens = (int)num_tokens; p.E = (int)num_experts; p.N = (int)N; p.K = (int)K; p.topk = (int)top_k;
+    p.num_valid = (int)num_valid_tokens; p.grid_m = (int)grid_m;
+    p.sam = stride_am; p.sas = stride_amxm; p.sbe = stride_be; p.sbn = stride_bn; p.sbse = stride_bmxe;
+    p.sbsn = stride_bmxn; p.scm = stride_cm;
+    p.c16 = (stride_cm % 8 == 0) && (reinterpret_cast<uintptr_t>(C) % 16 == 0);
+    // 128-byte K-tiles when rows have whole ones (K % 256 == 0), else 64-byte ones
+    return (K / 2) % 128 == 0 ? launch_moe_fp4<128, 2>(p, stream) : launch_moe_fp4<64, 4>(p, stream);
 }

@@ -171,6 +171,7 @@ class _GemmNamespace:
 class _MoeGemmNamespace:
     a8w8 = _SubModule("moe_op_gemm_a8w8_tk")
     a8w8_blockscale = _SubModule("moe_op_gemm_a8w8_blockscale_tk")
+    mxfp4 = _SubModule("moe_op_mxfp4_tk")
 
 
 class _MoeRoutingNamespace:

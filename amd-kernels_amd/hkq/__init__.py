@@ -37,6 +37,7 @@ SIGNATURES = {
                      + [_I64] * 12 + [_P]),
     "hkq_rmsnorm_quant": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _P]),
     "hkq_swiglu_quant": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _I, _P]),
+    "hkq_moe_mxfp4": (_I, [_P] * 10 + [_I64, _I64, _I64, _I64, _I] + [_I64] * 10 + [_P]),
     "hkq_moe_topk": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _I, _P]),
     "hkq_sum_bitmatrix_rows": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "hkq_sum_bitmatrix_rows_fused": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P]),
@@ -101,6 +102,10 @@ def bind(name: str, *args):
 
 def _ptr(t) -> int:
     return t.data_ptr()
+
+
+def _opt_ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
 
 
 def _stream(stream=None) -> int:
@@ -287,13 +292,32 @@ def moe_a8w8(X, W, hist, offs, expt_data, topk, gather=None, x_scale=None, w_sca
     return Y
 
 
+def moe_mxfp4(A, As, B, Bs, sorted_ids, expert_ids, num_valid: int, topk: int, a_scale=None, b_scale=None,
+              topk_weights=None, C=None, c_rows=None, stream=None):
+    """MXFP4 MoE over block-sorted routing (align_block_size output, 128-row
+    blocks). A uint8 [T, K/2], As uint8 [T, K/32], B uint8 [E, N, K/2], Bs uint8
+    [E, N, K/32] (K contiguous); topk_weights (fp32, indexed by gate id) turns on
+    the routed-weight multiply. Returns C bf16 [c_rows (default num_valid), N]
+    with row = gate id."""
+    import torch
+
+    T, Kh = A.shape
+    E, N = B.shape[0], B.shape[1]
+    K = 2 * Kh
+    rows = num_valid if c_rows is None else c_rows
+    if C is None:
+        C = torch.zeros((rows, N), dtype=torch.bfloat16, device=A.device)
+    grid_m = sorted_ids.numel() // 128
+    call("hkq_moe_mxfp4", _ptr(A), _ptr(B), _ptr(C), _ptr(As), _ptr(Bs), _opt_ptr(a_scale), _opt_ptr(b_scale),
+         _opt_ptr(topk_weights), _ptr(sorted_ids), _ptr(expert_ids), N, K, num_valid, topk,
+         int(topk_weights is not None), A.stride(0), B.stride(0), B.stride(1), C.stride(0), As.stride(0),
+         Bs.stride(0), Bs.stride(1), T, E, grid_m, _stream(stream))
+    return C
+
+
 # ----------------------------------------------------------------------------
 # MoE routing metadata (GPU producers of the tensors moe_a8w8 consumes)
 # ----------------------------------------------------------------------------
-
-def _opt_ptr(t) -> int:
-    return 0 if t is None else t.data_ptr()
-
 
 def moe_topk(logits, K: int, softmax: bool = True, bitmatrix: bool = True, stream=None):
     """Top-K experts per row of bf16 logits [T, E]: (values bf16 [T, K],

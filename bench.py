@@ -252,6 +252,32 @@ def main():
         layer_ms = ms_r + sum(r["ms"] for r in moe_res) + ms_sw
         moe_res.append({"proj": "layer (routing + gate_up + swiglu/quant + down)", "ms": round(layer_ms, 5)})
         del w1, w2
+
+        # MXFP4 experts over the block-sorted routing of the same top-2 choice
+        # (moe_align_block_size, 128-row blocks)
+        sids, eids, _, tot = hkq.align_block_size(rt["topk_idx"], E, 128)
+        total = int(tot.item())
+        sids, eids = sids[:total], eids[: total // 128]
+        a4, as4 = hkq.mx_quant(xm, True)
+        for name, (nn, kk) in (("gate_up", (2 * ffn, hidden)), ("down", (hidden, ffn))):
+            xa4, xs4 = (a4, as4) if kk == hidden else hkq.mx_quant(seeded_bf16((T, kk), 1.0, 60), True)
+            wq4 = torch.empty((E, nn, kk // 2), dtype=torch.uint8, device="cuda")
+            ws4 = torch.empty((E, nn, kk // 32), dtype=torch.uint8, device="cuda")
+            for e in range(E):
+                hkq.call("hkq_mx_quant", seeded_bf16_dev((nn, kk), 0.02, 70 + e).data_ptr(), wq4[e].data_ptr(),
+                         ws4[e].data_ptr(), nn, kk, kk, 1, torch.cuda.current_stream().cuda_stream)
+            C4 = torch.empty((T * topk, nn), dtype=torch.bfloat16, device="cuda")
+            launch = hkq.bind("hkq_moe_mxfp4", xa4.data_ptr(), wq4.data_ptr(), C4.data_ptr(), xs4.data_ptr(),
+                              ws4.data_ptr(), None, None, None,
+                              sids.data_ptr(), eids.data_ptr(), nn, kk, T * topk, topk, 0, xa4.stride(0),
+                              wq4.stride(0), wq4.stride(1), C4.stride(0), xs4.stride(0), ws4.stride(0), ws4.stride(1),
+                              T, E, total // 128, torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            log(f"moe mxfp4 {name} N={nn} K={kk}")
+            ms_4 = time_launches(launch, steps, warmup)
+            moe_res.append({"proj": f"mxfp4 {name}", "N": nn, "K": kk, "ms": round(ms_4, 5),
+                            "tflops": round(2.0 * T * topk * nn * kk / (ms_4 * 1e-3) / 1e12, 2)})
+            del wq4, ws4, C4
         res["moe"] = layer_ms
         for (Tr, Er, Kr) in ROUTING_EXTRA:
             lg = seeded_bf16((Tr, Er), 1.0, 30)

@@ -184,6 +184,26 @@ int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* x_scale, in
                  int64_t stride_xm, int64_t stride_we, int64_t stride_wn, int64_t stride_ym, int64_t y_rows,
                  int64_t gather_len, hkq_stream_t stream);
 
+/* MXFP4 MoE over block-sorted routing (the output of hkq_moe_align_block_size):
+ * tile row r of 128-row block pm is gate id = sorted_token_ids[pm*128 + r]
+ * (rows with id >= num_valid_tokens are padding), expert e = expert_ids[pm]:
+ *   C[id, n] = bf16((sum_k A[id / top_k, k] B[e, n, k]) * A_scale[0] * B_scale[e]
+ *                   * (mul_routed_weight ? topk_weights[id] : 1))
+ * (A_scale / B_scale NULL: 1); a block with e == -1 writes zeros to its valid
+ * rows. A [num_tokens, stride_am] bytes and B[e] [N, stride_bn] bytes hold E2M1
+ * pairs, K contiguous (even k in the low nibble); A_mx_scale [num_tokens,
+ * stride_amxm] and B_mx_scale[e] [N, stride_bmxn] hold e8m0 bytes per 32 K
+ * values; expert e at B + e*stride_be, B_mx_scale + e*stride_bmxe; C bf16 rows
+ * of stride_cm. K % 128 == 0, N % 4 == 0. Replaces moe_op_mxfp4_tk.moe_mxfp4
+ * (kernels/moe-gemm/moe_op_mxfp4/kernel.cpp:263-330), whose weights are
+ * [E, K/2, N] (N contiguous): pass them transposed. */
+int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* A_mx_scale, const void* B_mx_scale,
+                  const float* A_scale, const float* B_scale, const float* topk_weights,
+                  const int32_t* sorted_token_ids, const int32_t* expert_ids, int64_t N, int64_t K,
+                  int64_t num_valid_tokens, int64_t top_k, int mul_routed_weight, int64_t stride_am,
+                  int64_t stride_be, int64_t stride_bn, int64_t stride_cm, int64_t stride_amxm, int64_t stride_bmxe,
+                  int64_t stride_bmxn, int64_t num_tokens, int64_t num_experts, int64_t grid_m, hkq_stream_t stream);
+
 /* ---- MoE routing metadata producers --------------------------------------- */
 /* All index outputs are deterministic: gates of one expert keep their input
  * order (the order of the reference's test formulas, tests/test_moe.py:97-128,

@@ -35,6 +35,8 @@ gemm refs              reference formulas (tests/test_gemm.py:116,148-153,
 moe_ref / ogs_routing  tests/test_moe.py:97-128,733-753 restated; invariants
                        (histogram sum, exclusive scan, gather permutation) and
                        agreement with per-expert dense GEMMs.
+moe_mxfp4_ref          per-expert dense gemm_mxfp4_ref on the gathered rows
+                       (tests/test_oracle_moe.py); routed-weight and -1 block cases.
 rmsnorm_quant          fp64 numpy RMSNorm (the test_parity.py formula of
                        fused_fp8_quant) then the pinned group / MX quantizers:
                        codes equal except where y sits within an ulp of a
@@ -492,6 +494,36 @@ def align_block_size(ids: np.ndarray, E: int, bs: int):
     cum = np.zeros(E + 1, np.int32)
     total = int(lib().orc_align_block_size(_p(x), n, E, bs, _p(sorted_), _p(eids), _p(cum)))
     return sorted_[:total], eids[: total // bs], cum, total
+
+
+def moe_mxfp4_ref(Aq, As, Bq, Bs, a_scale, b_scale, topk_w, sorted_ids, expert_ids, N, num_valid, topk,
+                  mul_routed_weight, c_rows):
+    """The MXFP4 MoE of moe-gemm/moe_op_mxfp4/kernel.cpp:90-237 on the block-sorted
+    routing of moe_align_block_size: for 128-row block pm with expert e =
+    expert_ids[pm] and row id = sorted_ids[pm*128 + r] < num_valid,
+    C[id] = (A[id // topk] . B[e]^T) * a_scale * b_scale[e] * (w[id] if mul), or 0
+    when e == -1. Aq [T, K/2], As [T, K/32], Bq [E, N, K/2], Bs [E, N, K/32]
+    (K contiguous). fp64 [c_rows, N], rows never written are NaN."""
+    a = mx_fp4_dequant_f32(Aq, As).astype(np.float64)
+    E = Bq.shape[0]
+    b = [mx_fp4_dequant_f32(Bq[e], Bs[e]).astype(np.float64) for e in range(E)]
+    C = np.full((c_rows, N), np.nan)
+    sorted_ids = np.asarray(sorted_ids)
+    for pm, e in enumerate(np.asarray(expert_ids).tolist()):
+        ids = sorted_ids[pm * 128:(pm + 1) * 128]
+        ids = ids[(ids >= 0) & (ids < num_valid)]
+        if len(ids) == 0:
+            continue
+        if e == -1:
+            C[ids] = 0.0
+            continue
+        r = a[ids // topk] @ b[e].T
+        g = (1.0 if a_scale is None else float(np.float32(a_scale))) * (1.0 if b_scale is None else float(b_scale[e]))
+        r = r * g
+        if mul_routed_weight:
+            r = r * np.asarray(topk_w, np.float64)[ids][:, None]
+        C[ids] = r
+    return C
 
 
 # ----------------------------------------------------------------------------
