@@ -34,7 +34,36 @@ struct DenseParams {
     int splits;           // K splits of the split/skinny path (1: none)
     int kt_split;         // K-tiles per split
     float* ws;            // split partials (splits > 1)
+    // batched A8W8 GEMMs: grid.y walks the batch; the operands of batch z start
+    // z * bs_* further (bytes for A/B, elements for the others); bias bf16 [N]
+    // per batch (nullptr: none), added after the scales
+    int batch;  // 0 or 1: one GEMM
+    const uint16_t* bias;
+    int64_t bs_a, bs_b, bs_c, bs_sa, bs_sb, bs_bias;
 };
+
+// The parameters of this workgroup's batch (blockIdx.y).
+__device__ __forceinline__ DenseParams batch_slice(const DenseParams& p) {
+    DenseParams q = p;
+    if (gridDim.y > 1) {
+        const int64_t z = blockIdx.y;
+        q.A += z * p.bs_a;
+        q.B += z * p.bs_b;
+        q.C += z * p.bs_c;
+        q.sa = static_cast<const float*>(p.sa) + z * p.bs_sa;
+        q.sb = static_cast<const float*>(p.sb) + z * p.bs_sb;
+        if (p.bias) q.bias += z * p.bs_bias;
+    }
+    return q;
+}
+
+// bias of columns n .. n+3 (zero when there is none or n is past N; N % 4 == 0)
+__device__ __forceinline__ float4 bias4(const DenseParams& p, int n) {
+    if (!p.bias || n >= p.N) return make_float4(0.f, 0.f, 0.f, 0.f);
+    const uint2 b = *reinterpret_cast<const uint2*>(p.bias + n);
+    return make_float4(bf16_to_f32(b.x & 0xFFFF), bf16_to_f32(b.x >> 16), bf16_to_f32(b.y & 0xFFFF),
+                       bf16_to_f32(b.y >> 16));
+}
 
 // Tile geometry of the dense GEMMs: 256 x 256 tiles computed by 4 waves of
 // 128 x 128 (whole tiles) or 64 x 128 (M halves of a tile, 128 x 256). K-tiles
@@ -69,7 +98,7 @@ template <int MODE, int WM, int WN, int TM, int TN, int KTB>
 __device__ __forceinline__ void dense_kloop(const DenseParams& p, int m0, int n0, int kt0, int kt1, HKQ_LDS uint8_t* smem,
                                             v16f (&acc)[TN][TM]) {
     using Cfg = DenseCfg<MODE, WM, WN, TM, TN, KTB>;
-    constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
+    constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN;
     constexpr bool FP4 = Cfg::FP4;
     constexpr int SCB_PER_KT = KTB / 16;  // FP4 scale bytes per row per K-tile
     const int lane = threadIdx.x & 63;
@@ -89,11 +118,8 @@ __device__ __forceinline__ void dense_kloop(const DenseParams& p, int m0, int n0
     src.lsa = p.lsa;
     src.lsb = p.lsb;
     src.KT = kt1 - kt0;
-    uint32_t a_off[LA], b_off[LB];
-#pragma unroll
-    for (int i = 0; i < LA; ++i) a_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.lda);
-#pragma unroll
-    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.ldb);
+    const auto a_off = dense_offs<NW, KTB, Cfg::LA>(wave, lane, p.lda);
+    const auto b_off = dense_offs<NW, KTB, Cfg::LB>(wave, lane, p.ldb);
     gemm_mainloop<MODE, WM, WN, TM, TN, KTB, dense_ns<KTB>()>(src, a_off, b_off, smem, lane, wave, acc);
 }
 
@@ -145,7 +171,7 @@ __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn
             }
             return make_float4(1.f, 1.f, 1.f, 1.f);
         },
-        [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); });
+        [&](int i, int g) { return bias4(p, nw + i * 32 + 8 * g + 4 * khalf); });
 }
 
 // Workgroup u < n_whole computes tile u. When the last round of tiles would
@@ -155,9 +181,10 @@ __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn
 // n_whole + 8 * (v >> 4) + (v & 7), so both halves of a tile run on one XCD.
 // Tile ids then go through tile_coords' XCD-aware order.
 template <int MODE, int KTB>
-__global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_gemm_kernel(const DenseParams p) {
+__global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_gemm_kernel(const DenseParams pb) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+    const DenseParams p = batch_slice(pb);
     const int u = blockIdx.x;
     int whole = -1, t = -1, half = 0;
     if (u < p.n_whole) {
@@ -204,16 +231,17 @@ __device__ __forceinline__ void dense_epilogue_global(const DenseParams& p, v16f
             const int n = nw + i * 32 + 8 * g + 4 * khalf;
             return (MODE == MODE_A8W8 && n < p.N) ? *reinterpret_cast<const float4*>(sb + n) : make_float4(1.f, 1.f, 1.f, 1.f);
         },
-        [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); });
+        [&](int i, int g) { return bias4(p, nw + i * 32 + 8 * g + 4 * khalf); });
 }
 
 template <int MODE, int WM, int WN, int TM, int TN, int KTB, int MINB>
-__global__ __launch_bounds__(64 * WM * WN, MINB) void dense_tile_kernel(const DenseParams p) {
+__global__ __launch_bounds__(64 * WM * WN, MINB) void dense_tile_kernel(const DenseParams pb) {
     using Cfg = DenseCfg<MODE, WM, WN, TM, TN, KTB>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::NW;
     constexpr int NQ = TN * TM * 4;  // float4 of accumulators per lane
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+    const DenseParams p = batch_slice(pb);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tiles = p.tiles_m * p.tiles_n;
@@ -301,12 +329,13 @@ struct DensePlan {
     size_t ws_bytes;
 };
 
-static DensePlan dense_plan(int64_t M, int64_t N, int64_t kbytes, bool allow_split) {
+static DensePlan dense_plan(int64_t M, int64_t N, int64_t kbytes, bool allow_split, int64_t batch = 1) {
     DensePlan pl{};
     const int ktb = kbytes % 128 == 0 ? 128 : 64;
     const int64_t KT = kbytes / ktb;
     const int ncu = cu_count() > 0 ? cu_count() : 256;
-    auto ntiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    // tiles of the whole launch (all batches)
+    auto ntiles = [&](int64_t bm, int64_t bn) { return batch * ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     int64_t bm = DENSE_BM, bn = DENSE_BN;
     pl.geo = GEO_256;
     if (ktb == 128 && M <= 64) {
@@ -351,7 +380,7 @@ static int launch_dense_tiles(DenseParams& p, const DensePlan& pl, hipStream_t s
     p.kt_split = pl.kt_split;
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     if (tiles == 0) return 0;
-    kern<<<dim3((unsigned)(tiles * p.splits)), 64 * WM * WN, LDS, stream>>>(p);
+    kern<<<dim3((unsigned)(tiles * p.splits), (unsigned)std::max(1, p.batch)), 64 * WM * WN, LDS, stream>>>(p);
     if (int e = hkq_launch_status()) return e;
     if (p.splits == 1) return 0;
     const int64_t total = tiles * Cfg::NW * (TN * TM * 4) * 64;  // float4 per split
@@ -376,11 +405,12 @@ static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
     // CUs and the tiles have rows in both halves.
     const int ncu = cu_count();
     const int64_t last = ncu > 0 ? tiles % ncu : 0;
-    const int64_t split = (last > 0 && 2 * last <= ncu && p.M > DENSE_BM / 2) ? last : 0;
+    const bool batched = p.batch > 1;  // a batch fills the GPU by itself: no half tiles
+    const int64_t split = (!batched && last > 0 && 2 * last <= ncu && p.M > DENSE_BM / 2) ? last : 0;
     p.n_whole = (int)(tiles - split);
     p.n_split = (int)split;
     const int64_t nblk = p.n_whole + 2 * ((split + 7) / 8 * 8);
-    kern<<<dim3((unsigned)nblk), 64 * DENSE_WAVES_M * DENSE_WAVES_N, LDS, stream>>>(p);
+    kern<<<dim3((unsigned)nblk, (unsigned)std::max(1, p.batch)), 64 * DENSE_WAVES_M * DENSE_WAVES_N, LDS, stream>>>(p);
     return hkq_launch_status();
 }
 
@@ -389,8 +419,11 @@ static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
 template <int MODE, int KTB>
 static int launch_dense_ktb(DenseParams& p, void* ws, size_t ws_bytes, hipStream_t stream) {
     p.c16 = (p.ldc % 8 == 0) && (reinterpret_cast<uintptr_t>(p.C) % 16 == 0);
-    DensePlan pl = dense_plan(p.M, p.N, p.kbytes, true);
-    if (pl.splits > 1 && (ws == nullptr || ws_bytes < pl.ws_bytes)) pl = dense_plan(p.M, p.N, p.kbytes, false);
+    // batches and bias run unsplit (the split partials and their reduction are per 2-D GEMM)
+    const bool plain = p.batch <= 1 && p.bias == nullptr;
+    DensePlan pl = dense_plan(p.M, p.N, p.kbytes, plain, std::max(1, p.batch));
+    if (pl.splits > 1 && (ws == nullptr || ws_bytes < pl.ws_bytes))
+        pl = dense_plan(p.M, p.N, p.kbytes, false, std::max(1, p.batch));
     p.ws = static_cast<float*>(ws);
     if constexpr (KTB == 128) {  // smaller tiles need a full 16-byte load per lane for their A rows
         if (pl.geo == GEO_SKINNY) {
@@ -489,6 +522,40 @@ int hkq_gemm_mxfp4_ws(const void* A, const void* As, const void* B, const void* 
 int hkq_gemm_mxfp4(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
                    int64_t K, int64_t lda, int64_t ldb, int64_t ldsa, int64_t ldsb, int64_t ldc, hipStream_t stream) {
     return hkq_gemm_mxfp4_ws(A, As, B, Bs, C, M, N, K, lda, ldb, ldsa, ldsb, ldc, nullptr, 0, stream);
+}
+
+int hkq_batched_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb, const void* bias, void* C,
+                          int64_t batch, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                          int64_t batch_stride_a, int64_t batch_stride_b, int64_t batch_stride_c,
+                          int64_t batch_stride_sa, int64_t batch_stride_sb, int64_t batch_stride_bias,
+                          hipStream_t stream) {
+    if (int e = check_common(M, N, K, ldc, C)) return e;
+    HKQ_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535]");
+    HKQ_CHECK_ARG(K % 64 == 0, "K must be a multiple of 64");
+    HKQ_CHECK_ARG(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0,
+                  "lda/ldb must be >= K and multiples of 16");
+    HKQ_CHECK_ARG(batch <= 1 || (batch_stride_a % 16 == 0 && batch_stride_b % 16 == 0 && batch_stride_c % 8 == 0 &&
+                                 batch_stride_sb % 4 == 0 && batch_stride_bias % 4 == 0),
+                  "batch strides must keep every batch's operands aligned (A, B: 16 bytes; C: 8 elements; "
+                  "b_scale, bias: 4 elements)");
+    HKQ_CHECK_ALIGN(A, 16);
+    HKQ_CHECK_ALIGN(B, 16);
+    HKQ_CHECK_ALIGN(sb, 16);
+    HKQ_CHECK_ALIGN(bias, 8);
+    if (batch == 0) return 0;
+    DenseParams p{};
+    p.A = static_cast<const uint8_t*>(A);
+    p.B = static_cast<const uint8_t*>(B);
+    p.C = static_cast<uint16_t*>(C);
+    p.sa = sa;
+    p.sb = sb;
+    p.M = (int)M; p.N = (int)N; p.K = (int)K; p.kbytes = (int)K;
+    p.lda = lda; p.ldb = ldb; p.ldc = ldc;
+    p.batch = (int)batch;
+    p.bias = static_cast<const uint16_t*>(bias);
+    p.bs_a = batch_stride_a; p.bs_b = batch_stride_b; p.bs_c = batch_stride_c;
+    p.bs_sa = batch_stride_sa; p.bs_sb = batch_stride_sb; p.bs_bias = batch_stride_bias;
+    return launch_dense<MODE_A8W8>(p, nullptr, 0, stream);
 }
 
 }  // extern "C"

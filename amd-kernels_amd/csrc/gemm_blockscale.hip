@@ -27,7 +27,20 @@ struct BlockScaleParams {
     int M, N, K;
     int64_t lda, ldb, ldc, lsa, lsb;
     int tiles_m, tiles_n, group_m, c16;
+    // multiply-add epilogue C = ca * GEMM + cb, ca / cb bf16 [M, ldca] / [M, ldcb]
+    // (nullptr: plain GEMM)
+    const uint16_t* ca;
+    const uint16_t* cb;
+    int64_t ldca, ldcb;
 };
+
+// ca / cb of row m, columns n .. n+3 (rows past M, columns past N: 1 and 0)
+__device__ __forceinline__ float4 load_bf16x4(const uint16_t* t, int64_t ld, int m, int n, int M, int N, float dflt) {
+    if (m >= M || n >= N) return make_float4(dflt, dflt, dflt, dflt);
+    const uint2 v = *reinterpret_cast<const uint2*>(t + (int64_t)m * ld + n);
+    return make_float4(bf16_to_f32(v.x & 0xFFFF), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFF),
+                       bf16_to_f32(v.y >> 16));
+}
 
 constexpr int BS_KT = 128;  // K-tile bytes per row = one 128-wide scale group
 
@@ -191,10 +204,21 @@ __global__ __launch_bounds__(256, 1) void blockscale_gemm_kernel(const BlockScal
     tile_barrier<0>();
 
     const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
-    store_tile_bf16<TM, TN>(
-        acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, [](int) { return 1.0f; },
-        [](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); },
-        [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); });
+    auto one = [](int) { return 1.0f; };
+    auto ones = [](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); };
+    auto zeros = [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); };
+    if (p.ca) {
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, zeros,
+                                [&](int j, int i, int g, float4 v) {
+                                    const int m = mw + j * 32 + (lane & 31), n = nw + i * 32 + 8 * g + 4 * khalf;
+                                    const float4 a = load_bf16x4(p.ca, p.ldca, m, n, p.M, p.N, 1.0f);
+                                    const float4 b = load_bf16x4(p.cb, p.ldcb, m, n, p.M, p.N, 0.0f);
+                                    return make_float4(a.x * v.x + b.x, a.y * v.y + b.y, a.z * v.z + b.z,
+                                                       a.w * v.w + b.w);
+                                });
+    } else {
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, zeros);
+    }
 }
 
 template <bool GN1>
@@ -228,9 +252,32 @@ static int launch_blockscale(BlockScaleParams& p, hipStream_t stream) {
 
 using namespace hkq;
 
+static int blockscale_call(const void* A, const void* B, const float* sa, const float* sb, void* C, const void* ca,
+                           const void* cb, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t lsa,
+                           int64_t lsb, int64_t ldc, int64_t ldca, int64_t ldcb, int64_t group_n, hipStream_t stream);
+
 extern "C" int hkq_gemm_blockscale(const void* A, const void* B, const float* sa, const float* sb, void* C,
                                    int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t lsa,
                                    int64_t lsb, int64_t ldc, int64_t group_n, hipStream_t stream) {
+    return blockscale_call(A, B, sa, sb, C, nullptr, nullptr, M, N, K, lda, ldb, lsa, lsb, ldc, 0, 0, group_n,
+                           stream);
+}
+
+extern "C" int hkq_gemm_blockscale_mul_add(const void* A, const void* B, const float* sa, const float* sb, void* C,
+                                           const void* c_a, const void* c_b, int64_t M, int64_t N, int64_t K,
+                                           int64_t lda, int64_t ldb, int64_t lsa, int64_t lsb, int64_t ldc,
+                                           int64_t ldca, int64_t ldcb, int64_t group_n, hipStream_t stream) {
+    HKQ_CHECK_ARG(c_a && c_b, "c_a and c_b are required");
+    HKQ_CHECK_ARG(ldca >= N && ldcb >= N && ldca % 4 == 0 && ldcb % 4 == 0,
+                  "c_a / c_b row strides must be >= N and multiples of 4");
+    HKQ_CHECK_ALIGN(c_a, 8);
+    HKQ_CHECK_ALIGN(c_b, 8);
+    return blockscale_call(A, B, sa, sb, C, c_a, c_b, M, N, K, lda, ldb, lsa, lsb, ldc, ldca, ldcb, group_n, stream);
+}
+
+static int blockscale_call(const void* A, const void* B, const float* sa, const float* sb, void* C, const void* ca,
+                           const void* cb, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t lsa,
+                           int64_t lsb, int64_t ldc, int64_t ldca, int64_t ldcb, int64_t group_n, hipStream_t stream) {
     HKQ_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "M, N must be >= 0 and K > 0");
     HKQ_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), "dimensions must be < 2^30");
     HKQ_CHECK_ARG(K % 128 == 0, "K must be a multiple of the 128-wide scale group");
@@ -255,5 +302,8 @@ extern "C" int hkq_gemm_blockscale(const void* A, const void* B, const float* sa
     p.sb = sb;
     p.M = (int)M; p.N = (int)N; p.K = (int)K;
     p.lda = lda; p.ldb = ldb; p.ldc = ldc; p.lsa = lsa; p.lsb = lsb;
+    p.ca = static_cast<const uint16_t*>(ca);
+    p.cb = static_cast<const uint16_t*>(cb);
+    p.ldca = ldca; p.ldcb = ldcb;
     return group_n == 1 ? launch_blockscale<true>(p, stream) : launch_blockscale<false>(p, stream);
 }

@@ -143,12 +143,18 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 //   row_scale(j) -> scale of the lane's m in m-tile j; col_scale4(i, g) -> the
 //   4 scales of n = i*32 + 8g + 4*(lane/32) + 0..3 (both relative to the wave);
 //   col_bias4(i, g) -> the 4 values added after scaling (zero when unused).
+// Element-wise step after scaling: elem(j, i, g, v) maps the lane's 4 values v
+// of m-tile j, n-tile i, register group g; the default leaves them unchanged.
+struct NoElem {
+    __device__ float4 operator()(int, int, int, float4 v) const { return v; }
+};
+
 // Scale, convert and stage the wave's (TM*32) x (TN*32) sub-tile in LDS as bf16
 // rows of PITCH bytes (returns the wave's staging area).
-template <int TM, int TN, typename RowScale, typename ColScale4, typename ColBias4>
+template <int TM, int TN, typename RowScale, typename ColScale4, typename ColBias4, typename Elem = NoElem>
 __device__ __forceinline__ HKQ_LDS uint8_t* stage_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uint8_t* smem, int wave,
                                                             int lane, RowScale row_scale, ColScale4 col_scale4,
-                                                            ColBias4 col_bias4) {
+                                                            ColBias4 col_bias4, Elem elem = Elem{}) {
     constexpr int PITCH = TN * 32 * 2 + 16;
     static_assert((TN * 32 * 2) % 128 == 0, "rows are whole 128-byte segments");
     HKQ_LDS uint8_t* ep = smem + wave * (TM * 32) * PITCH;
@@ -166,8 +172,11 @@ __device__ __forceinline__ HKQ_LDS uint8_t* stage_tile_bf16(v16f (&acc)[TN][TM],
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const float a = rs[j];
-                const uint32_t lo = pk_bf16(acc[i][j][4 * g + 0] * a * cs.x + cb.x, acc[i][j][4 * g + 1] * a * cs.y + cb.y);
-                const uint32_t hi = pk_bf16(acc[i][j][4 * g + 2] * a * cs.z + cb.z, acc[i][j][4 * g + 3] * a * cs.w + cb.w);
+                const float4 v = elem(j, i, g,
+                                      make_float4(acc[i][j][4 * g + 0] * a * cs.x + cb.x, acc[i][j][4 * g + 1] * a * cs.y + cb.y,
+                                                  acc[i][j][4 * g + 2] * a * cs.z + cb.z, acc[i][j][4 * g + 3] * a * cs.w + cb.w));
+                const uint32_t lo = pk_bf16(v.x, v.y);
+                const uint32_t hi = pk_bf16(v.z, v.w);
                 *reinterpret_cast<HKQ_LDS v2i*>(ep + (j * 32 + (lane & 31)) * PITCH + nl * 2) = v2i{(int)lo, (int)hi};
             }
         }
@@ -190,12 +199,13 @@ __device__ __forceinline__ void store_piece_bf16(uint16_t* dst, const v4i& v, in
     }
 }
 
-template <int TM, int TN, typename RowScale, typename ColScale4, typename ColBias4>
+template <int TM, int TN, typename RowScale, typename ColScale4, typename ColBias4, typename Elem = NoElem>
 __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uint8_t* smem, int wave, int lane,
                                                 uint16_t* C, int64_t ldc, int M, int N, int mw, int nw, bool c16,
-                                                RowScale row_scale, ColScale4 col_scale4, ColBias4 col_bias4) {
+                                                RowScale row_scale, ColScale4 col_scale4, ColBias4 col_bias4,
+                                                Elem elem = Elem{}) {
     constexpr int PITCH = TN * 32 * 2 + 16;
-    HKQ_LDS uint8_t* ep = stage_tile_bf16<TM, TN>(acc, smem, wave, lane, row_scale, col_scale4, col_bias4);
+    HKQ_LDS uint8_t* ep = stage_tile_bf16<TM, TN>(acc, smem, wave, lane, row_scale, col_scale4, col_bias4, elem);
     // LDS operations of a wave complete in order: the reads below see the writes above.
     constexpr int SEGS = TN * 32 * 2 / 16;  // 16-byte pieces per row
     constexpr int ROWS_PER_PASS = 64 / SEGS;

@@ -78,6 +78,29 @@ __device__ __forceinline__ uint32_t dense_row_off(int i, int wave, int lane, int
     return (uint32_t)(r * ld) + (uint32_t)(KT::load_chunk(lane, r) << 4);
 }
 
+// Per-lane source offsets of an operand's LDS-direct loads within a K-tile:
+// load i reads at byte v[i] (row and logical chunk; out of bounds for rows that
+// must read zero). Loop-invariant, so the K loop keeps them in VGPRs.
+template <int N>
+struct TableOff {
+    uint32_t v[N];
+};
+template <int NW, int KTB, int N>
+__device__ __forceinline__ TableOff<N> dense_offs(int wave, int lane, int64_t ld) {
+    TableOff<N> o;
+#pragma unroll
+    for (int i = 0; i < N; ++i) o.v[i] = dense_row_off<NW, KTB>(i, wave, lane, ld);
+    return o;
+}
+
+// Issue load i of a K-tile: `base` / `bytes` already start at the K-tile (bytes
+// <= 0: read zero).
+template <int N>
+__device__ __forceinline__ void issue_rows16(const uint8_t* base, int64_t bytes, const TableOff<N>& o, int i,
+                                             HKQ_LDS uint8_t* dst) {
+    lds_load16(base, bytes > 0 ? (uint32_t)(bytes < 0x7FFFFFFF ? bytes : 0x7FFFFFFF) : 0u, dst, o.v[i]);
+}
+
 // Pipeline (per wave; one barrier per K-tile, NS ring stages):
 //   K-tile kt lives in stage kt % NS. Its SUB K-steps run their MFMAs with
 //   double-buffered fragments: the LDS reads of the next step are issued between
@@ -97,14 +120,12 @@ __device__ __forceinline__ uint32_t dense_row_off(int i, int wave, int lane, int
 // contiguous (2 bytes for KTB 64, one 4-byte plane for KTB 128), and the MFMA's
 // opsel picks byte 2ks + part.
 //
-// a_off/b_off: per load instruction, the byte offset of the lane's row and
-// logical chunk inside src.a / src.b (OOB for rows that must read zero).
+// a_off/b_off: the lane's row and logical chunk offsets inside src.a / src.b of
+// each load instruction (TableOff; out of bounds for rows that must read zero).
 // On return acc holds the tile's fp32 sums and every wave is past a vmcnt(0)
 // barrier, so the caller may reuse the LDS.
-template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int KTB, int NS>
-__device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
-                                              const uint32_t (&a_off)[DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>::LA],
-                                              const uint32_t (&b_off)[DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>::LB],
+template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int KTB, int NS, typename AOff, typename BOff>
+__device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_off, const BOff& b_off,
                                               HKQ_LDS uint8_t* smem, int lane, int wave, v16f (&acc)[TN][TM]) {
     using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>;
     using KT = KTile<KTB>;
@@ -134,8 +155,12 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
         // row slot s = lane / 2 of the group; its two 16-byte halves are stored
         // swapped when bit 3 of s is set (see read_scale)
         const uint32_t half = (uint32_t)((lane & 1) ^ ((lane >> 4) & 1));
-        const uint32_t row_off = isa ? (src.sa_rows ? src.sa_rows[r] : (uint32_t)(r * src.lsa))
-                                     : (uint32_t)((r - BM) * src.lsb);
+        // both row offsets are formed and one is selected: a branch here would
+        // split the loop body into blocks, and the compiler then sinks the
+        // MFMAs of the earlier blocks past the loads they should overlap
+        const uint32_t a_row = src.sa_rows ? src.sa_rows[isa ? r : 0] : (uint32_t)(r * src.lsa);
+        const uint32_t b_row = (uint32_t)((r - BM) * src.lsb);
+        const uint32_t row_off = isa ? a_row : b_row;
         const uint32_t off = row_off + half * 16u;
         lds_load16(base, live && bytes > 0 ? (uint32_t)bytes : 0u, sblk + (blk & 1) * Cfg::SB_SLOT + g * 1024, off);
     };
@@ -159,11 +184,10 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
             }
         }
         if (idx < LA) {
-            lds_load16(src.a + kb, live ? (uint32_t)(src.a_bytes - kb) : 0u, st + (idx * NW + wave) * 1024, a_off[idx]);
+            issue_rows16(src.a + kb, live ? src.a_bytes - kb : 0, a_off, idx, st + (idx * NW + wave) * 1024);
         } else if (idx < LA + LB) {
             const int i = idx - LA;
-            lds_load16(src.b + kb, live ? (uint32_t)(src.b_bytes - kb) : 0u, st + BM * KTB + (i * NW + wave) * 1024,
-                       b_off[i]);
+            issue_rows16(src.b + kb, live ? src.b_bytes - kb : 0, b_off, i, st + BM * KTB + (i * NW + wave) * 1024);
         } else if (idx < LA + LB + LSA) {
             const int g = ((idx - LA - LB) * NW + wave) % GA;
             const int kb4 = kt * 4;
@@ -177,9 +201,20 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
         }
     };
 
-    const int arow = wm * TM * 32 + (lane & 31);
-    const int brow = wn * TN * 32 + (lane & 31);
     const int khalf = lane >> 5;
+
+    // LDS addresses of the fragment reads. The lane reads rows
+    // (wave's first row) + t*32 + lane%32; rows 32 apart share the chunk
+    // swizzle, so the address is a per-lane part that depends only on the
+    // K-step and part (frag_lo), a wave-uniform part (stage, operand, wave
+    // rows) and the constant t*32*KTB, which the reads carry as their offset.
+    int frag_lo[SUB][PARTS];
+#pragma unroll
+    for (int ks = 0; ks < SUB; ++ks)
+#pragma unroll
+        for (int part = 0; part < PARTS; ++part)
+            frag_lo[ks][part] = KT::swz(lane & 31, khalf * HCH + 2 * ks + part);
+    const int a_wave_off = wm * TM * 32 * KTB, b_wave_off = BM * KTB + wn * TN * 32 * KTB;
 
     struct Frags {
         v4i a[TM][PARTS], b[TN][PARTS];
@@ -188,12 +223,10 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
     // (a0 b0 a1 b1 ...) so the first MFMAs' operands arrive first; slots past
     // TM (A) or TN (B) tiles are empty.
     auto read_piece = [&](int stage, int ks, Frags& f, int idx) {
-        const HKQ_LDS uint8_t* At = smem + stage * STAGE;
         const int t = idx / (2 * PARTS), isb = (idx / PARTS) & 1, part = idx % PARTS;
         if ((isb ? TN : TM) <= t) return;
-        const int row = (isb ? brow : arow) + t * 32;
-        const int chunk = khalf * HCH + 2 * ks + part;
-        const v4i v = lds_read16(At + (isb ? BM * KTB : 0) + KT::swz(row, chunk));
+        const HKQ_LDS uint8_t* base = smem + stage * STAGE + (isb ? b_wave_off : a_wave_off) + frag_lo[ks][part];
+        const v4i v = lds_read16(base + t * 32 * KTB);
         if (isb) f.b[t][part] = v;
         else f.a[t][part] = v;
     };
@@ -204,23 +237,27 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src,
     struct Scales {
         int a[TM], b[TN];
     };
+    // Scale reads: row ra = (wave's first row) + t*32 + lane%32 keeps bit 3 of
+    // lane%32, so the swapped-half XOR below is a per-lane constant.
+    const int sc_lo = (lane & 31) * 32 + khalf * 4, sc_x = (((lane & 31) >> 3) & 1) << 4;
+    const int sk_lo = (lane & 31) * 4 + khalf * 2;
     auto read_scale = [&](int stage, int kt, Scales& s, int idx) {
         if constexpr (FP4) {
             const bool isa = idx < TM;
             const int t = isa ? idx : idx - TM;
-            const int row = (isa ? arow : brow) + t * 32;
             int w;
             if constexpr (Cfg::SBLK) {
                 // byte o = 8 * (kt % 4) + 4h of the row's 32; the 16-byte halves of
                 // rows with bit 3 set are swapped, so the 32 lanes of a read (32
                 // consecutive rows, 32-byte pitch) hit 16 distinct bank pairs
                 const HKQ_LDS uint8_t* slot = sblk + ((kt / Cfg::SB_KT) & 1) * Cfg::SB_SLOT;
-                const int ra = isa ? row : BM + row;
-                const int o = (kt % Cfg::SB_KT) * 8 + khalf * 4;
-                w = *reinterpret_cast<const HKQ_LDS int*>(slot + ra * 32 + (o ^ (((ra >> 3) & 1) << 4)));
+                const int wave_row = isa ? wm * TM * 32 : BM + wn * TN * 32;
+                const int o = ((kt % Cfg::SB_KT) * 8) ^ sc_x;
+                w = *reinterpret_cast<const HKQ_LDS int*>(slot + wave_row * 32 + sc_lo + o + t * 1024);
             } else {
                 const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KTB + (isa ? 0 : SCA);
-                w = *reinterpret_cast<const HKQ_LDS uint16_t*>(sca + row * 4 + khalf * 2);
+                const int wave_row = isa ? wm * TM * 32 : wn * TN * 32;
+                w = *reinterpret_cast<const HKQ_LDS uint16_t*>(sca + wave_row * 4 + sk_lo + t * 128);
             }
             if (isa) s.a[t] = w;
             else s.b[t] = w;

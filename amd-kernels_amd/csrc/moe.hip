@@ -85,15 +85,14 @@ __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoePara
     src.as = src.bs = nullptr;
     src.as_bytes = src.bs_bytes = src.lsa = src.lsb = 0;
     src.KT = p.K / KTB;
-    uint32_t a_off[LA], b_off[LB];
+    TableOff<LA> a_off;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
         const int r = (i * NW + wave) * Cfg::RPL + lane / Cfg::KT::CHUNKS;
         const int t = token_of(r);
-        a_off[i] = t < 0 ? OOB : (uint32_t)(t * p.sxm) + (uint32_t)(Cfg::KT::load_chunk(lane, r) << 4);
+        a_off.v[i] = t < 0 ? OOB : (uint32_t)(t * p.sxm) + (uint32_t)(Cfg::KT::load_chunk(lane, r) << 4);
     }
-#pragma unroll
-    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.swn);
+    const auto b_off = dense_offs<NW, KTB, LB>(wave, lane, p.swn);
 
     v16f acc[TN][TM];
     gemm_mainloop<MODE_A8W8, WAVES_M, WAVES_N, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
@@ -246,15 +245,14 @@ __global__ __launch_bounds__(256, 1) void moe_mxfp4_kernel(const MoeFp4Params p)
     src.lsb = p.sbsn;
     src.KT = (p.K / 2) / KTB;
     src.sa_rows = sa_rows;
-    uint32_t a_off[LA], b_off[LB];
+    TableOff<LA> a_off;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
         const int r = (i * NW + wave) * Cfg::RPL + lane / Cfg::KT::CHUNKS;
         const int t = arow_of(r);
-        a_off[i] = t < 0 ? FP4_OOB : (uint32_t)(t * p.sam) + (uint32_t)(Cfg::KT::load_chunk(lane, r) << 4);
+        a_off.v[i] = t < 0 ? FP4_OOB : (uint32_t)(t * p.sam) + (uint32_t)(Cfg::KT::load_chunk(lane, r) << 4);
     }
-#pragma unroll
-    for (int i = 0; i < LB; ++i) b_off[i] = dense_row_off<NW, KTB>(i, wave, lane, p.sbn);
+    const auto b_off = dense_offs<NW, KTB, LB>(wave, lane, p.sbn);
 
     v16f acc[TN][TM];
     gemm_mainloop<MODE_MXFP4, WAVES_M, WAVES_N, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
