@@ -51,6 +51,11 @@ MODULES = {
     "gemm_a8w8_per_token_scale_tk": "bind_gemm_a8w8_per_token_scale.cpp",
     "gemm_afp4wfp4_tk": "bind_gemm_afp4wfp4.cpp",
     "gemm_a8w8_blockscale_tk": "bind_gemm_a8w8_blockscale.cpp",
+    "gemm_a16w16_tk": "bind_gemm_a16w16.cpp",
+    "batched_gemm_a8w8_tk": "bind_batched_gemm_a8w8.cpp",
+    "batched_gemm_bf16_tk": "bind_batched_gemm_bf16.cpp",
+    "fused_gemm_a8w8_blockscale_mul_add_tk": "bind_fused_gemm_a8w8_blockscale_mul_add.cpp",
+    "fused_gemm_a8w8_blockscale_a16w16_tk": "bind_fused_gemm_a8w8_blockscale_a16w16.cpp",
     "moe_op_gemm_a8w8_tk": "bind_moe_op_gemm_a8w8.cpp",
     "moe_op_gemm_a8w8_blockscale_tk": "bind_moe_op_gemm_a8w8_blockscale.cpp",
     "moe_op_mxfp4_tk": "bind_moe_op_mxfp4.cpp",

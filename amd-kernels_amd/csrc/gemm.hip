@@ -8,7 +8,12 @@
 //                        e8m0 scales per 32 K-values fed to the MFMA scale
 //                        operands (gemm-basic/gemm_afp4wfp4/kernel.cpp:1-12 for
 //                        the data format; the reference kernel itself consumes
-//                        pre-dequantized bf16).
+//                        pre-dequantized bf16);
+//   hkq_gemm_bf16,       C = bf16(A . B^T (+ bias[n])), bf16 operands
+//   hkq_batched_gemm_*   (gemm-basic/gemm_a16w16/kernel.cpp; formula
+//                        tests/test_gemm.py:21-42), batched over grid.y
+//                        (gemm-batched/batched_gemm_a8w8, batched_gemm_bf16;
+//                        formulas tests/test_gemm.py:316-390).
 #include <algorithm>
 
 #include "gemm_mainloop.h"
@@ -556,6 +561,46 @@ int hkq_batched_gemm_a8w8(const void* A, const void* B, const float* sa, const f
     p.bs_a = batch_stride_a; p.bs_b = batch_stride_b; p.bs_c = batch_stride_c;
     p.bs_sa = batch_stride_sa; p.bs_sb = batch_stride_sb; p.bs_bias = batch_stride_bias;
     return launch_dense<MODE_A8W8>(p, nullptr, 0, stream);
+}
+
+size_t hkq_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 32 != 0) return 0;
+    return dense_plan(M, N, 2 * K, true).ws_bytes;
+}
+
+int hkq_batched_gemm_bf16(const void* A, const void* B, const void* bias, void* C, int64_t batch, int64_t M, int64_t N,
+                          int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch_stride_a,
+                          int64_t batch_stride_b, int64_t batch_stride_c, int64_t batch_stride_bias, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream) {
+    if (int e = check_common(M, N, K, ldc, C)) return e;
+    HKQ_CHECK_ARG(batch >= 0 && batch <= 65535, "batch must be in [0, 65535]");
+    HKQ_CHECK_ARG(K % 32 == 0, "K must be a multiple of 32");
+    HKQ_CHECK_ARG(lda >= K && ldb >= K && lda % 8 == 0 && ldb % 8 == 0,
+                  "lda/ldb (elements) must be >= K and multiples of 8");
+    HKQ_CHECK_ARG(batch <= 1 || (batch_stride_a % 8 == 0 && batch_stride_b % 8 == 0 && batch_stride_c % 8 == 0 &&
+                                 batch_stride_bias % 4 == 0),
+                  "batch strides must keep every batch's operands aligned (A, B, C: 8 elements; bias: 4)");
+    HKQ_CHECK_ALIGN(A, 16);
+    HKQ_CHECK_ALIGN(B, 16);
+    HKQ_CHECK_ALIGN(bias, 8);
+    HKQ_CHECK_ALIGN(workspace, 16);
+    if (batch == 0) return 0;
+    DenseParams p{};
+    p.A = static_cast<const uint8_t*>(A);
+    p.B = static_cast<const uint8_t*>(B);
+    p.C = static_cast<uint16_t*>(C);
+    p.M = (int)M; p.N = (int)N; p.K = (int)K; p.kbytes = (int)(2 * K);
+    p.lda = 2 * lda; p.ldb = 2 * ldb; p.ldc = ldc;
+    p.batch = (int)batch;
+    p.bias = static_cast<const uint16_t*>(bias);
+    p.bs_a = 2 * batch_stride_a; p.bs_b = 2 * batch_stride_b; p.bs_c = batch_stride_c;
+    p.bs_bias = batch_stride_bias;
+    return launch_dense<MODE_BF16>(p, workspace, workspace_bytes, stream);
+}
+
+int hkq_gemm_bf16(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                  int64_t ldc, hipStream_t stream) {
+    return hkq_batched_gemm_bf16(A, B, nullptr, C, 1, M, N, K, lda, ldb, ldc, 0, 0, 0, 0, nullptr, 0, stream);
 }
 
 }  // extern "C"

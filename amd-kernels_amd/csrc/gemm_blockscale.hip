@@ -34,13 +34,35 @@ struct BlockScaleParams {
     int64_t ldca, ldcb;
 };
 
-// ca / cb of row m, columns n .. n+3 (rows past M, columns past N: 1 and 0)
-__device__ __forceinline__ float4 load_bf16x4(const uint16_t* t, int64_t ld, int m, int n, int M, int N, float dflt) {
-    if (m >= M || n >= N) return make_float4(dflt, dflt, dflt, dflt);
-    const uint2 v = *reinterpret_cast<const uint2*>(t + (int64_t)m * ld + n);
-    return make_float4(bf16_to_f32(v.x & 0xFFFF), bf16_to_f32(v.x >> 16), bf16_to_f32(v.y & 0xFFFF),
-                       bf16_to_f32(v.y >> 16));
-}
+// Multiply-add epilogue hook: v -> ca[m, n] * v + cb[m, n] on the fp32 sums.
+// prefetch(i) loads the lane's 4 x TM groups of 4 bf16 of both operands for
+// n-tile i in one batch (rows past M / columns past N: ca = 1, cb = 0).
+template <int TM>
+struct MulAddElem {
+    const uint16_t *ca, *cb;
+    int64_t ldca, ldcb;
+    int M, N, mw, nw, lane;
+    uint2 a[4][TM], b[4][TM];
+    __device__ void prefetch(int i) {
+        const int m0 = mw + (lane & 31), n0 = nw + i * 32 + 4 * (lane >> 5);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int m = m0 + j * 32, n = n0 + 8 * g;
+                const bool in = m < M && n < N;
+                a[g][j] = in ? *reinterpret_cast<const uint2*>(ca + (int64_t)m * ldca + n) : make_uint2(0x3F803F80u, 0x3F803F80u);
+                b[g][j] = in ? *reinterpret_cast<const uint2*>(cb + (int64_t)m * ldcb + n) : make_uint2(0u, 0u);
+            }
+    }
+    __device__ float4 operator()(int j, int, int g, float4 v) const {
+        const uint2 x = a[g][j], y = b[g][j];
+        return make_float4(bf16_to_f32(x.x & 0xFFFF) * v.x + bf16_to_f32(y.x & 0xFFFF),
+                           bf16_to_f32(x.x >> 16) * v.y + bf16_to_f32(y.x >> 16),
+                           bf16_to_f32(x.y & 0xFFFF) * v.z + bf16_to_f32(y.y & 0xFFFF),
+                           bf16_to_f32(x.y >> 16) * v.w + bf16_to_f32(y.y >> 16));
+    }
+};
 
 constexpr int BS_KT = 128;  // K-tile bytes per row = one 128-wide scale group
 
@@ -208,14 +230,17 @@ __global__ __launch_bounds__(256, 1) void blockscale_gemm_kernel(const BlockScal
     auto ones = [](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); };
     auto zeros = [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); };
     if (p.ca) {
-        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, zeros,
-                                [&](int j, int i, int g, float4 v) {
-                                    const int m = mw + j * 32 + (lane & 31), n = nw + i * 32 + 8 * g + 4 * khalf;
-                                    const float4 a = load_bf16x4(p.ca, p.ldca, m, n, p.M, p.N, 1.0f);
-                                    const float4 b = load_bf16x4(p.cb, p.ldcb, m, n, p.M, p.N, 0.0f);
-                                    return make_float4(a.x * v.x + b.x, a.y * v.y + b.y, a.z * v.z + b.z,
-                                                       a.w * v.w + b.w);
-                                });
+        MulAddElem<TM> e;
+        e.ca = p.ca;
+        e.cb = p.cb;
+        e.ldca = p.ldca;
+        e.ldcb = p.ldcb;
+        e.M = p.M;
+        e.N = p.N;
+        e.mw = mw;
+        e.nw = nw;
+        e.lane = lane;
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, zeros, e);
     } else {
         store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, zeros);
     }

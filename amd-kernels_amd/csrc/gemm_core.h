@@ -36,7 +36,7 @@ namespace hkq {
 
 constexpr uint32_t OOB = 0x80000000u;  // buffer offset that always reads zero (num_records <= 2^31 - 1)
 
-enum GemmMode { MODE_A8W8 = 0, MODE_BLOCKSCALE = 1, MODE_MXFP4 = 2 };
+enum GemmMode { MODE_A8W8 = 0, MODE_BLOCKSCALE = 1, MODE_MXFP4 = 2, MODE_BF16 = 3 };
 
 template <int KTB>
 struct KTile {
@@ -88,6 +88,13 @@ template <bool FP4, int OPA, int OPB>
 __device__ __forceinline__ v16f mfma_sel(const v8i& a, const v8i& b, const v16f& c, int sa, int sb) {
     if (FP4) return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 4, 4, OPA, sa, OPB, sb);
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, OPA, sa, OPB, sb);
+}
+
+// bf16 operands: 8 values (16 bytes) per lane, one 16-deep MFMA.
+typedef __bf16 v8bf16 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ v16f mfma_bf16(const v4i& a, const v4i& b, const v16f& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf16, a), __builtin_bit_cast(v8bf16, b), c, 0, 0,
+                                                  0);
 }
 
 // s_waitcnt immediate (gfx9 encoding): vmcnt in [3:0] and [15:14], expcnt in
@@ -145,7 +152,12 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 //   col_bias4(i, g) -> the 4 values added after scaling (zero when unused).
 // Element-wise step after scaling: elem(j, i, g, v) maps the lane's 4 values v
 // of m-tile j, n-tile i, register group g; the default leaves them unchanged.
+// Element-wise hook of the epilogue: prefetch(i) runs before the values of
+// n-tile i are formed (so a hook that reads memory can issue all of that
+// tile's loads at once), then operator()(j, i, g, v) maps the scaled fp32
+// values v of m-tile j, column group g before the bf16 conversion.
 struct NoElem {
+    __device__ void prefetch(int) {}
     __device__ float4 operator()(int, int, int, float4 v) const { return v; }
 };
 
@@ -164,6 +176,7 @@ __device__ __forceinline__ HKQ_LDS uint8_t* stage_tile_bf16(v16f (&acc)[TN][TM],
     for (int j = 0; j < TM; ++j) rs[j] = row_scale(j);
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
+        elem.prefetch(i);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int nl = i * 32 + 8 * g + 4 * khalf;

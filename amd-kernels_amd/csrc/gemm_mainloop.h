@@ -15,7 +15,8 @@ struct DenseCfg {
     static constexpr int BM = WAVES_M * TM * 32, BN = WAVES_N * TN * 32;
     static constexpr bool FP4 = MODE == MODE_MXFP4;
     // K-steps per K-tile: 64 bytes of K per row each (FP8: one 64-deep MFMA per
-    // output sub-tile; FP4: two, one per 32-byte half of the lane's fragment)
+    // output sub-tile; FP4: two, one per 32-byte half of the lane's fragment;
+    // BF16: two 16-deep MFMAs, one per 16-byte part)
     static constexpr int SUB = KTB / 64;
     static constexpr int RPL = KT::ROWS_PER_LOAD;
     static constexpr int LA = BM / RPL / NW, LB = BN / RPL / NW;
@@ -114,8 +115,8 @@ __device__ __forceinline__ void issue_rows16(const uint8_t* base, int64_t bytes,
 //
 // Fragments: lane half h (lane / 32) owns logical chunks [h * KTB/32, (h+1) *
 // KTB/32) of every row; K-step ks uses chunks h*KTB/32 + 2ks + {0, 1}, read as
-// two 16-byte parts (FP8: the two halves of one MFMA operand; FP4: one MFMA
-// each). The order in which K enters the sums is the same for A and B, so the
+// two 16-byte parts (FP8: the two halves of one MFMA operand; FP4 and BF16:
+// one MFMA each). The order in which K enters the sums is the same for A and B, so the
 // products are unchanged; for FP4 it makes the lane's e8m0 bytes of one K-tile
 // contiguous (2 bytes for KTB 64, one 4-byte plane for KTB 128), and the MFMA's
 // opsel picks byte 2ks + part.
@@ -270,11 +271,14 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
         for (int j = 0; j < TM; ++j) acc[i][j] = v16f{};
 
     // MFMA slot idx (accumulator i*TM + j) of K-step ks: one FP8 MFMA on the
-    // 32-byte fragments, or two FP4 MFMAs (one per 16-byte half, scale bytes
-    // 2ks and 2ks + 1 of the lane's scale word)
+    // 32-byte fragments, two FP4 MFMAs (one per 16-byte half, scale bytes 2ks
+    // and 2ks + 1 of the lane's scale word) or two BF16 MFMAs (one per half)
     auto mfma_one = [&](const Frags& f, int ks, const Scales& s, int idx) {
         const int i = idx / TM, j = idx % TM;
-        if constexpr (FP4) {
+        if constexpr (MODE == MODE_BF16) {
+            acc[i][j] = mfma_bf16(f.b[i][0], f.a[j][0], acc[i][j]);
+            acc[i][j] = mfma_bf16(f.b[i][1], f.a[j][1], acc[i][j]);
+        } else if constexpr (FP4) {
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const v8i b = v8i{f.b[i][q][0], f.b[i][q][1], f.b[i][q][2], f.b[i][q][3], 0, 0, 0, 0};

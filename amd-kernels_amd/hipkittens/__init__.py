@@ -8,6 +8,10 @@ the modules this build provides:
     hk.gemm.a8w8.dispatch(A, B, a_scale, b_scale, C)       # gemm_a8w8_tk
     hk.gemm.a8w8_per_token.dispatch(A, B, C, a_s, b_s)     # gemm_a8w8_per_token_scale_tk
     hk.gemm.afp4wfp4.dispatch(A, B, C, A_scale, B_scale)   # gemm_afp4wfp4_tk
+    hk.gemm.a16w16.dispatch(A, B, C)                       # gemm_a16w16_tk
+    hk.batched_gemm.a8w8.dispatch(A, B, a_s, b_s, C, bias) # batched_gemm_a8w8_tk (also .bf16)
+    hk.fused_gemm.a8w8_blockscale_mul_add.dispatch(a, b, c, a_s, b_s, c_a, c_b)
+                                                           # (also .a8w8_blockscale_a16w16)
     hk.moe_routing.quant.downcast_to_mxfp(...)             # quant_moe_tk
     hk.moe_routing.topk.moe_topk(X, ...)                   # moe_topk_tk (also bitmatrix,
                                                            # expt_data, align_block_size)
@@ -162,10 +166,21 @@ class _SubModule:
 
 
 class _GemmNamespace:
+    a16w16 = _SubModule("gemm_a16w16_tk")
     a8w8 = _SubModule("gemm_a8w8_tk")
     a8w8_per_token = _SubModule("gemm_a8w8_per_token_scale_tk")
     a8w8_blockscale = _SubModule("gemm_a8w8_blockscale_tk")
     afp4wfp4 = _SubModule("gemm_afp4wfp4_tk")
+
+
+class _BatchedGemmNamespace:
+    bf16 = _SubModule("batched_gemm_bf16_tk")
+    a8w8 = _SubModule("batched_gemm_a8w8_tk")
+
+
+class _FusedGemmNamespace:
+    a8w8_blockscale_a16w16 = _SubModule("fused_gemm_a8w8_blockscale_a16w16_tk")
+    a8w8_blockscale_mul_add = _SubModule("fused_gemm_a8w8_blockscale_mul_add_tk")
 
 
 class _MoeGemmNamespace:
@@ -185,5 +200,7 @@ class _MoeRoutingNamespace:
 
 
 gemm = _GemmNamespace()
+batched_gemm = _BatchedGemmNamespace()
+fused_gemm = _FusedGemmNamespace()
 moe = _MoeGemmNamespace()
 moe_routing = _MoeRoutingNamespace()

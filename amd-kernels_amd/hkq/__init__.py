@@ -33,6 +33,11 @@ SIGNATURES = {
     "hkq_gemm_mxfp4_workspace": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "hkq_gemm_mxfp4_ws": (_I, [_P, _P, _P, _P, _P] + [_I64] * 8 + [_P, ctypes.c_size_t, _P]),
     "hkq_gemm_blockscale": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "hkq_gemm_blockscale_mul_add": (_I, [_P] * 7 + [_I64] * 11 + [_P]),
+    "hkq_batched_gemm_a8w8": (_I, [_P] * 6 + [_I64] * 13 + [_P]),
+    "hkq_gemm_bf16": (_I, [_P, _P, _P] + [_I64] * 6 + [_P]),
+    "hkq_gemm_bf16_workspace": (ctypes.c_size_t, [_I64, _I64, _I64]),
+    "hkq_batched_gemm_bf16": (_I, [_P] * 4 + [_I64] * 11 + [_P, ctypes.c_size_t, _P]),
     "hkq_moe_a8w8": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]
                      + [_I64] * 12 + [_P]),
     "hkq_rmsnorm_quant": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _P]),
@@ -261,6 +266,63 @@ def gemm_blockscale(A, B, sa, sb, C=None, group_n: int = 128, stream=None):
         C = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
     call("hkq_gemm_blockscale", _ptr(A), _ptr(B), _ptr(sa), _ptr(sb), _ptr(C), M, N, K, A.stride(0), B.stride(0),
          sa.stride(0), sb.stride(0), C.stride(0), group_n, _stream(stream))
+    return C
+
+
+def gemm_blockscale_mul_add(A, B, sa, sb, c_a, c_b, C=None, group_n: int = 128, stream=None):
+    """C = bf16(c_a * G + c_b), G the fp32 block-scale GEMM of gemm_blockscale;
+    c_a, c_b bf16 [M, N]."""
+    import torch
+
+    M, K = A.shape
+    N = B.shape[0]
+    if C is None:
+        C = torch.empty(M, N, dtype=torch.bfloat16, device=A.device)
+    call("hkq_gemm_blockscale_mul_add", _ptr(A), _ptr(B), _ptr(sa), _ptr(sb), _ptr(C), _ptr(c_a), _ptr(c_b), M, N, K,
+         A.stride(0), B.stride(0), sa.stride(0), sb.stride(0), C.stride(0), c_a.stride(0), c_b.stride(0), group_n,
+         _stream(stream))
+    return C
+
+
+def batched_gemm_a8w8(A, B, sa, sb, bias=None, C=None, stream=None):
+    """A [Z, M, K], B [Z, N, K] E4M3FN codes; sa fp32 [Z, M], sb fp32 [Z, N];
+    bias bf16 [Z, N] or None -> C bf16 [Z, M, N]."""
+    import torch
+
+    Z, M, K = A.shape
+    N = B.shape[1]
+    if C is None:
+        C = torch.empty(Z, M, N, dtype=torch.bfloat16, device=A.device)
+    call("hkq_batched_gemm_a8w8", _ptr(A), _ptr(B), _ptr(sa), _ptr(sb), _opt_ptr(bias), _ptr(C), Z, M, N, K,
+         A.stride(1), B.stride(1), C.stride(1), A.stride(0), B.stride(0), C.stride(0), sa.stride(0), sb.stride(0),
+         bias.stride(0) if bias is not None else 0, _stream(stream))
+    return C
+
+
+def gemm_bf16(A, B, C=None, bias=None, stream=None, split: bool = True):
+    """A [M, K] or [Z, M, K], B [N, K] or [Z, N, K] bf16; bias bf16 [N] / [Z, N]
+    or None -> C bf16 [M, N] / [Z, M, N]. split=False (or a batch or bias) runs
+    without a workspace, so without split-K."""
+    import torch
+
+    batched = A.dim() == 3
+    A3 = A if batched else A.unsqueeze(0)
+    B3 = B if batched else B.unsqueeze(0)
+    Z, M, K = A3.shape
+    N = B3.shape[1]
+    if C is None:
+        C = torch.empty(Z, M, N, dtype=torch.bfloat16, device=A.device)
+        if not batched:
+            C = C[0]
+    C3 = C if batched else C.unsqueeze(0)
+    b2 = None if bias is None else (bias if bias.dim() == 2 else bias.unsqueeze(0))
+    ws = None
+    if split and Z == 1 and bias is None:
+        n = int(lib().hkq_gemm_bf16_workspace(M, N, K))
+        ws = torch.empty(n, dtype=torch.uint8, device=A.device) if n else None
+    call("hkq_batched_gemm_bf16", _ptr(A3), _ptr(B3), _opt_ptr(b2), _ptr(C3), Z, M, N, K, A3.stride(1),
+         B3.stride(1), C3.stride(1), A3.stride(0), B3.stride(0), C3.stride(0), b2.stride(0) if b2 is not None else 0,
+         _ptr(ws) if ws is not None else None, ws.numel() if ws is not None else 0, _stream(stream))
     return C
 
 

@@ -33,11 +33,14 @@ for _p in (ROOT, PKG):
 PEAK_FP8_TFLOPS = 5000.0   # MI355X dense FP8 (e4m3) MFMA
 PEAK_FP4_TFLOPS = 10100.0  # MI355X dense MXFP4 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 HEADLINE = dict(M=4096, N=14336, K=4096)
 MXFP4 = dict(M=4096, N=8192, K=8192)
 BLOCKSCALE = [(2048, 24576, 1536), (2048, 7168, 18432), (2048, 7168, 2048)]
 MOE = dict(T=4096, E=8, topk=2, hidden=4096, ffn=14336)
+# batched A8W8 (batch, M, N, K)
+BATCHED = (8, 1024, 4096, 4096)
 # routing pipelines timed beside the Mixtral one: (tokens, experts, top-k)
 ROUTING_EXTRA = [(4096, 256, 8), (32768, 256, 8)]
 # fused RMSNorm + quantizer cases: (rows, hidden, kind 0 = FP8 1x128 / 1 = MXFP4)
@@ -112,7 +115,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant", "blockscale", "moe", "fused", "sweep", "copy"],
+    ap.add_argument("--only", choices=["a8w8", "mxfp4", "quant", "blockscale", "moe", "fused", "ext", "sweep", "copy"],
                     default=None,
                     help="run one kernel only (for profiling); prints no JSON line. 'copy' is a plain "
                          "1 GiB device copy used to calibrate the HBM byte counters")
@@ -327,6 +330,54 @@ def main():
             del xr, qg, sg, q4, s4
         res["fused"] = sum(r["us"] for r in fused_res) * 1e-3
 
+    # ---- bf16, batched A8W8 and block-scale multiply-add GEMMs ----
+    ext_res = []
+    if args.only in (None, "ext"):
+        stream = torch.cuda.current_stream().cuda_stream
+        mm, nn, kk = HEADLINE["M"], HEADLINE["N"], HEADLINE["K"]
+        a16 = seeded_bf16((mm, kk), 1.0, 80)
+        b16 = seeded_bf16((nn, kk), 0.02, 81)
+        c16 = torch.empty((mm, nn), dtype=torch.bfloat16, device="cuda")
+        log(f"bf16 gemm {mm}x{nn}x{kk}")
+        launch = hkq.bind("hkq_gemm_bf16", a16.data_ptr(), b16.data_ptr(), c16.data_ptr(), mm, nn, kk, kk, kk, nn,
+                          stream)
+        ms_e = time_launches(launch, steps, warmup)
+        tf = 2.0 * mm * nn * kk / (ms_e * 1e-3) / 1e12
+        ext_res.append({"op": "gemm_bf16", "M": mm, "N": nn, "K": kk, "ms": round(ms_e, 5), "tflops": round(tf, 1),
+                        "pct_bf16_peak": round(100 * tf / PEAK_BF16_TFLOPS, 1)})
+        del a16, b16, c16
+        zb, mb, nb_, kb_ = BATCHED
+        xb = seeded_bf16((zb * mb, kb_), 1.0, 82)
+        wb = seeded_bf16((zb * nb_, kb_), 0.02, 83)
+        qxb, sxb = hkq.per_token_quant(xb)
+        qwb, swb = hkq.per_token_quant(wb)
+        biasb = seeded_bf16((zb, nb_), 1.0, 84)
+        cb = torch.empty((zb, mb, nb_), dtype=torch.bfloat16, device="cuda")
+        log(f"batched a8w8 {zb}x{mb}x{nb_}x{kb_}")
+        launch = hkq.bind("hkq_batched_gemm_a8w8", qxb.data_ptr(), qwb.data_ptr(), sxb.data_ptr(), swb.data_ptr(),
+                          biasb.data_ptr(), cb.data_ptr(), zb, mb, nb_, kb_, kb_, kb_, nb_, mb * kb_, nb_ * kb_,
+                          mb * nb_, mb, nb_, nb_, stream)
+        ms_e = time_launches(launch, steps, warmup)
+        tf = 2.0 * zb * mb * nb_ * kb_ / (ms_e * 1e-3) / 1e12
+        ext_res.append({"op": "batched_gemm_a8w8", "batch": zb, "M": mb, "N": nb_, "K": kb_, "ms": round(ms_e, 5),
+                        "tflops": round(tf, 1), "pct_fp8_peak": round(100 * tf / PEAK_FP8_TFLOPS, 1)})
+        del xb, wb, qxb, qwb, cb
+        bm, bn, bk = BLOCKSCALE[2]
+        qa_b, sa_b = hkq.group_quant(seeded_bf16((bm, bk), 1.0, 85), 128)
+        qw_b, sw_rows = hkq.group_quant(seeded_bf16((bn, bk), 0.02, 86), 128)
+        sb_b = sw_rows.view(bn // 128, 128, bk // 128).amax(dim=1).t().contiguous()
+        ca = seeded_bf16((bm, bn), 1.0, 87)
+        cbb = seeded_bf16((bm, bn), 1.0, 88)
+        Cm = torch.empty((bm, bn), dtype=torch.bfloat16, device="cuda")
+        log(f"blockscale mul_add {bm}x{bn}x{bk}")
+        launch = hkq.bind("hkq_gemm_blockscale_mul_add", qa_b.data_ptr(), qw_b.data_ptr(), sa_b.data_ptr(),
+                          sb_b.data_ptr(), Cm.data_ptr(), ca.data_ptr(), cbb.data_ptr(), bm, bn, bk, bk, bk,
+                          sa_b.stride(0), sb_b.stride(0), bn, bn, bn, 128, stream)
+        ms_e = time_launches(launch, steps, warmup)
+        ext_res.append({"op": "gemm_blockscale_mul_add", "M": bm, "N": bn, "K": bk, "ms": round(ms_e, 5),
+                        "tflops": round(2.0 * bm * bn * bk / (ms_e * 1e-3) / 1e12, 1)})
+        res["ext"] = sum(r["ms"] for r in ext_res)
+
     # ---- A8W8 shape sweep and the MXFP4 M=128 configuration (plans with smaller tiles / split K) ----
     sweep = []
     if args.only in (None, "sweep"):
@@ -369,7 +420,7 @@ def main():
         log(json.dumps({k: round(v * 1e3, 2) for k, v in res.items()}) + "  (us per launch)")
         for r in routing_res:
             log(json.dumps({"routing": r}))
-        for r in moe_res + fused_res:
+        for r in moe_res + fused_res + ext_res:
             log(json.dumps(r))
         if sweep:
             for r in sweep:
@@ -419,6 +470,7 @@ def main():
         "moe_mixtral": moe_res,
         "moe_routing": routing_res,
         "fused_quant": fused_res,
+        "gemm_ext": ext_res,
         "sweep": sweep,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_FP8_TFLOPS, 4), "traffic": read_traffic()},

@@ -159,6 +159,53 @@ int hkq_gemm_blockscale(const void* A, const void* B, const float* sa, const flo
                         int64_t K, int64_t lda, int64_t ldb, int64_t lsa, int64_t lsb, int64_t ldc, int64_t group_n,
                         hkq_stream_t stream);
 
+/* Block-scale FP8 GEMM with a multiply-add epilogue:
+ * C = bf16(c_a[m, n] * G[m, n] + c_b[m, n]), G the fp32 block-scale sum of
+ * hkq_gemm_blockscale (not rounded before the multiply-add); c_a / c_b bf16
+ * rows of ldca / ldcb elements (>= N, multiples of 4). Replaces
+ * fused_gemm_a8w8_blockscale_mul_add_tk.dispatch(a, b, c, a_scale, b_scale, c_a, c_b)
+ * (kernels/gemm-fused/fused_gemm_a8w8_blockscale_mul_add/kernel.cpp; formula
+ * tests/test_gemm.py:498-533). */
+int hkq_gemm_blockscale_mul_add(const void* A, const void* B, const float* sa, const float* sb, void* C,
+                                const void* c_a, const void* c_b, int64_t M, int64_t N, int64_t K, int64_t lda,
+                                int64_t ldb, int64_t lsa, int64_t lsb, int64_t ldc, int64_t ldca, int64_t ldcb,
+                                int64_t group_n, hkq_stream_t stream);
+
+/* ---- batched and bf16 GEMMs ---------------------------------------------- */
+
+/* Batched A8W8 GEMM: for z < batch,
+ * C_z = bf16((A_z . B_z^T) * sa_z[m] * sb_z[n] + bias_z[n]),
+ * operand z at z * batch_stride_* (bytes for A/B, elements for C, sa, sb and
+ * bias); bias bf16 [N] per batch or NULL. Shapes and strides as hkq_gemm_a8w8;
+ * batch <= 65535. Replaces batched_gemm_a8w8_tk.dispatch(A, B, a_scale, b_scale, C, bias)
+ * (kernels/gemm-batched/batched_gemm_a8w8/kernel.cpp; formula
+ * tests/test_gemm.py:349-390), with E4M3FN codes for A and B. */
+int hkq_batched_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb, const void* bias, void* C,
+                          int64_t batch, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                          int64_t batch_stride_a, int64_t batch_stride_b, int64_t batch_stride_c,
+                          int64_t batch_stride_sa, int64_t batch_stride_sb, int64_t batch_stride_bias,
+                          hkq_stream_t stream);
+
+/* bf16 GEMM C = bf16(A . B^T), A [M, K], B [N, K], C [M, N] bf16 with row
+ * strides lda, ldb, ldc in elements (lda, ldb multiples of 8; K % 32 == 0).
+ * Replaces gemm_a16w16_tk.dispatch(A, B, C)
+ * (kernels/gemm-basic/gemm_a16w16/kernel.cpp; formula tests/test_gemm.py:21-42)
+ * and the bf16 half of fused_gemm_a8w8_blockscale_a16w16_tk.dispatch
+ * (kernels/gemm-fused/fused_gemm_a8w8_blockscale_a16w16/kernel.cpp; tests/test_gemm.py:454-496). */
+int hkq_gemm_bf16(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                  int64_t ldc, hkq_stream_t stream);
+
+/* Batched bf16 GEMM with bias: C_z = bf16(A_z . B_z^T + bias_z[n]), strides in
+ * elements, bias bf16 [N] per batch or NULL; with batch == 1 and no bias a
+ * workspace of hkq_gemm_bf16_workspace bytes lets small grids split K (the
+ * plan of hkq_gemm_a8w8_ws). Replaces batched_gemm_bf16_tk.dispatch(A, B, C, bias)
+ * (kernels/gemm-batched/batched_gemm_bf16/kernel.cpp; formula tests/test_gemm.py:316-347). */
+size_t hkq_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K);
+int hkq_batched_gemm_bf16(const void* A, const void* B, const void* bias, void* C, int64_t batch, int64_t M, int64_t N,
+                          int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch_stride_a,
+                          int64_t batch_stride_b, int64_t batch_stride_c, int64_t batch_stride_bias, void* workspace,
+                          size_t workspace_bytes, hkq_stream_t stream);
+
 /* ---- MoE grouped GEMM over OGS routing metadata -------------------------- */
 
 /* For every routing tile ExptData[pm] = e | (b << 16) (-1: skipped), pm < grid_m,

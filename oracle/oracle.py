@@ -32,6 +32,11 @@ static_fp8             torch reference formula (tests/test_moe.py:997-999).
 gemm refs              reference formulas (tests/test_gemm.py:116,148-153,
                        gemm_a8w8_blockscale/test_parity.py:57-76), torch fp32,
                        plus closed forms (rank-1 / identity operands).
+gemm_bf16_ref,         torch fp32 matmul / bmm on the same decoded values (the
+batched_gemm_a8w8_ref, reference tests' formulas, tests/test_gemm.py:21-42,
+gemm_blockscale_mul_   316-390, 498-533); identity and all-ones closed forms;
+add_ref                c_a = 1, c_b = 0 reduces to the block-scale GEMM and
+                       c_a = 0 to c_b exactly.
 moe_ref / ogs_routing  tests/test_moe.py:97-128,733-753 restated; invariants
                        (histogram sum, exclusive scan, gather permutation) and
                        agreement with per-expert dense GEMMs.
@@ -319,6 +324,39 @@ def gemm_blockscale_ref(A, B, sa, sb, group_k: int = 128, group_n: int = 128) ->
         bs = np.repeat(sb[kg], group_n)[:N]
         C += part * sa[:, kg:kg + 1] * bs[None, :]
     return C
+
+
+def gemm_bf16_ref(A_bits, B_bits, bias_bits=None) -> np.ndarray:
+    """C = A . B^T (+ bias[n]) on bf16 bit patterns A [M, K], B [N, K]
+    (tests/test_gemm.py:21-42 and, with bias, :316-347); fp64 [M, N]."""
+    a = bf16_bits_to_f32(np.asarray(A_bits)).astype(np.float64)
+    b = bf16_bits_to_f32(np.asarray(B_bits)).astype(np.float64)
+    C = a @ b.T
+    if bias_bits is not None:
+        C = C + bf16_bits_to_f32(np.asarray(bias_bits)).astype(np.float64).reshape(1, -1)
+    return C
+
+
+def batched_gemm_a8w8_ref(A, B, sa, sb, bias_bits=None) -> np.ndarray:
+    """C[z] = (A[z] . B[z]^T) * sa[z][m] * sb[z][n] (+ bias[z][n]) over E4M3FN
+    codes A [Z, M, K], B [Z, N, K] (tests/test_gemm.py:349-390); fp64 [Z, M, N]."""
+    a = e4m3_decode(A).astype(np.float64)
+    b = e4m3_decode(B).astype(np.float64)
+    C = np.einsum("zmk,znk->zmn", a, b)
+    Z = a.shape[0]
+    C = C * np.asarray(sa, np.float64).reshape(Z, -1, 1) * np.asarray(sb, np.float64).reshape(Z, 1, -1)
+    if bias_bits is not None:
+        C = C + bf16_bits_to_f32(np.asarray(bias_bits)).astype(np.float64).reshape(Z, 1, -1)
+    return C
+
+
+def gemm_blockscale_mul_add_ref(A, B, sa, sb, ca_bits, cb_bits, group_k: int = 128, group_n: int = 128) -> np.ndarray:
+    """C = c_a * G + c_b with G = gemm_blockscale_ref (unrounded), c_a / c_b
+    bf16 bits [M, N] (tests/test_gemm.py:498-533); fp64 [M, N]."""
+    G = gemm_blockscale_ref(A, B, sa, sb, group_k, group_n)
+    ca = bf16_bits_to_f32(np.asarray(ca_bits)).astype(np.float64)
+    cb = bf16_bits_to_f32(np.asarray(cb_bits)).astype(np.float64)
+    return ca * G + cb
 
 
 def gemm_mxfp4_ref(Aq, As, Bq, Bs) -> np.ndarray:
