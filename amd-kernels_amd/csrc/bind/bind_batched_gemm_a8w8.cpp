@@ -1,5 +1,5 @@
 // batched_gemm_a8w8_tk -- the reference module of
-// kernels/gemm-batched/batched_gemm_a8w8/kernel.cpp:
+// kernels/gemm-batched/batched_gemm_a8w8/kernel.cpp:186-203:
 // dispatch(A, B, a_scale, b_scale, C, bias) over the HipKittens 4-D layout
 // (tests/test_gemm.py:349-390):
 //   A (1, B, M, K) and B (1, B, N, K): E4M3FN codes (float8_e4m3fn or uint8)

@@ -1,5 +1,5 @@
 // batched_gemm_bf16_tk -- the reference module of
-// kernels/gemm-batched/batched_gemm_bf16/kernel.cpp: dispatch(A, B, C, bias)
+// kernels/gemm-batched/batched_gemm_bf16/kernel.cpp:172-187: dispatch(A, B, C, bias)
 // over the HipKittens 4-D layout (tests/test_gemm.py:316-347):
 //   A (1, B, M, K), B (1, B, N, K), C (1, B, M, N): bf16; bias (1, B, 1, N)
 //   bf16 or None; C[z] = bf16(A[z] . B[z]^T + bias[z][n]).

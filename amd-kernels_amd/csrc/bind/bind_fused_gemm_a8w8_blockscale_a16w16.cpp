@@ -1,5 +1,5 @@
 // fused_gemm_a8w8_blockscale_a16w16_tk -- the reference module of
-// kernels/gemm-fused/fused_gemm_a8w8_blockscale_a16w16/kernel.cpp:
+// kernels/gemm-fused/fused_gemm_a8w8_blockscale_a16w16/kernel.cpp:251-270:
 // dispatch(a_fp8, b_fp8, c_fp8, a_scale, b_scale, a_bf16, b_bf16, c_bf16)
 // (tests/test_gemm.py:454-496): two independent GEMMs sharing M,
 //   c_fp8  = block-scale FP8 GEMM of a_fp8 [M, K], b_fp8 [N8, K] (E4M3FN codes,

@@ -1,5 +1,5 @@
 // fused_gemm_a8w8_blockscale_mul_add_tk -- the reference module of
-// kernels/gemm-fused/fused_gemm_a8w8_blockscale_mul_add/kernel.cpp:
+// kernels/gemm-fused/fused_gemm_a8w8_blockscale_mul_add/kernel.cpp:176-192:
 // dispatch(a, b, c, a_scale, b_scale, c_a, c_b) (tests/test_gemm.py:498-533):
 //   c = c_a * (sum_g (a_g . b_g^T) * a_scale[:, g] * b_scale[g, n / group_n]) + c_b
 // with a [M, K], b [N, K] E4M3FN codes, the block-scale GEMM's scale layouts,

@@ -1,6 +1,6 @@
-// gemm_a16w16_tk -- the reference module of kernels/gemm-basic/gemm_a16w16/kernel.cpp:
-// dispatch(A, B, C): A [M, K], B [N, K], C [M, N], all bf16; C = bf16(A . B^T)
-// (tests/test_gemm.py:21-42).
+// gemm_a16w16_tk -- the reference module of kernels/gemm-basic/gemm_a16w16 (no kernel
+// source in the reference tree; its test is tests/test_gemm.py:21-42):
+// dispatch(A, B, C): A [M, K], B [N, K], C [M, N], all bf16; C = bf16(A . B^T).
 #include "gemm_bind.h"
 
 using namespace hkqbind;

@@ -10,9 +10,9 @@
 //                        the data format; the reference kernel itself consumes
 //                        pre-dequantized bf16);
 //   hkq_gemm_bf16,       C = bf16(A . B^T (+ bias[n])), bf16 operands
-//   hkq_batched_gemm_*   (gemm-basic/gemm_a16w16/kernel.cpp; formula
-//                        tests/test_gemm.py:21-42), batched over grid.y
-//                        (gemm-batched/batched_gemm_a8w8, batched_gemm_bf16;
+//   hkq_batched_gemm_*   (gemm_a16w16, formula tests/test_gemm.py:21-42),
+//                        batched over grid.y (gemm-batched/batched_gemm_a8w8/
+//                        kernel.cpp:59-203, batched_gemm_bf16/kernel.cpp:53-187;
 //                        formulas tests/test_gemm.py:316-390).
 #include <algorithm>
 

@@ -164,7 +164,7 @@ int hkq_gemm_blockscale(const void* A, const void* B, const float* sa, const flo
  * hkq_gemm_blockscale (not rounded before the multiply-add); c_a / c_b bf16
  * rows of ldca / ldcb elements (>= N, multiples of 4). Replaces
  * fused_gemm_a8w8_blockscale_mul_add_tk.dispatch(a, b, c, a_scale, b_scale, c_a, c_b)
- * (kernels/gemm-fused/fused_gemm_a8w8_blockscale_mul_add/kernel.cpp; formula
+ * (kernels/gemm-fused/fused_gemm_a8w8_blockscale_mul_add/kernel.cpp:47-194; formula
  * tests/test_gemm.py:498-533). */
 int hkq_gemm_blockscale_mul_add(const void* A, const void* B, const float* sa, const float* sb, void* C,
                                 const void* c_a, const void* c_b, int64_t M, int64_t N, int64_t K, int64_t lda,
@@ -178,7 +178,7 @@ int hkq_gemm_blockscale_mul_add(const void* A, const void* B, const float* sa, c
  * operand z at z * batch_stride_* (bytes for A/B, elements for C, sa, sb and
  * bias); bias bf16 [N] per batch or NULL. Shapes and strides as hkq_gemm_a8w8;
  * batch <= 65535. Replaces batched_gemm_a8w8_tk.dispatch(A, B, a_scale, b_scale, C, bias)
- * (kernels/gemm-batched/batched_gemm_a8w8/kernel.cpp; formula
+ * (kernels/gemm-batched/batched_gemm_a8w8/kernel.cpp:59-203; formula
  * tests/test_gemm.py:349-390), with E4M3FN codes for A and B. */
 int hkq_batched_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb, const void* bias, void* C,
                           int64_t batch, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
@@ -189,9 +189,9 @@ int hkq_batched_gemm_a8w8(const void* A, const void* B, const float* sa, const f
 /* bf16 GEMM C = bf16(A . B^T), A [M, K], B [N, K], C [M, N] bf16 with row
  * strides lda, ldb, ldc in elements (lda, ldb multiples of 8; K % 32 == 0).
  * Replaces gemm_a16w16_tk.dispatch(A, B, C)
- * (kernels/gemm-basic/gemm_a16w16/kernel.cpp; formula tests/test_gemm.py:21-42)
+ * (kernels/gemm-basic/gemm_a16w16, which holds no kernel source in the reference tree; formula tests/test_gemm.py:21-42)
  * and the bf16 half of fused_gemm_a8w8_blockscale_a16w16_tk.dispatch
- * (kernels/gemm-fused/fused_gemm_a8w8_blockscale_a16w16/kernel.cpp; tests/test_gemm.py:454-496). */
+ * (kernels/gemm-fused/fused_gemm_a8w8_blockscale_a16w16/kernel.cpp:60-270; tests/test_gemm.py:454-496). */
 int hkq_gemm_bf16(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                   int64_t ldc, hkq_stream_t stream);
 
@@ -199,7 +199,7 @@ int hkq_gemm_bf16(const void* A, const void* B, void* C, int64_t M, int64_t N, i
  * elements, bias bf16 [N] per batch or NULL; with batch == 1 and no bias a
  * workspace of hkq_gemm_bf16_workspace bytes lets small grids split K (the
  * plan of hkq_gemm_a8w8_ws). Replaces batched_gemm_bf16_tk.dispatch(A, B, C, bias)
- * (kernels/gemm-batched/batched_gemm_bf16/kernel.cpp; formula tests/test_gemm.py:316-347). */
+ * (kernels/gemm-batched/batched_gemm_bf16/kernel.cpp:53-187; formula tests/test_gemm.py:316-347). */
 size_t hkq_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K);
 int hkq_batched_gemm_bf16(const void* A, const void* B, const void* bias, void* C, int64_t batch, int64_t M, int64_t N,
                           int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t batch_stride_a,
