@@ -162,21 +162,24 @@ __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn
 
     // Epilogue (scales of A8W8 applied in registers; MXFP4 has none left)
     const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
-    store_tile_bf16<TM, TN>(
-        acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0,
-        [&](int j) {
-            const int r = wm * TM * 32 + j * 32 + (lane & 31);
-            return MODE == MODE_A8W8 ? *reinterpret_cast<const HKQ_LDS float*>(scl + r * 4) : 1.0f;
-        },
-        [&](int i, int g) {
-            const int n = wn * TN * 32 + i * 32 + 8 * g + 4 * khalf;
-            if constexpr (MODE == MODE_A8W8) {
-                const v4f c = *reinterpret_cast<const HKQ_LDS v4f*>(scl + DENSE_BM * 4 + n * 4);
-                return make_float4(c[0], c[1], c[2], c[3]);
-            }
-            return make_float4(1.f, 1.f, 1.f, 1.f);
-        },
-        [&](int i, int g) { return bias4(p, nw + i * 32 + 8 * g + 4 * khalf); });
+    auto row_scale = [&](int j) {
+        const int r = wm * TM * 32 + j * 32 + (lane & 31);
+        return MODE == MODE_A8W8 ? *reinterpret_cast<const HKQ_LDS float*>(scl + r * 4) : 1.0f;
+    };
+    auto col_scale4 = [&](int i, int g) {
+        const int n = wn * TN * 32 + i * 32 + 8 * g + 4 * khalf;
+        if constexpr (MODE == MODE_A8W8) {
+            const v4f c = *reinterpret_cast<const HKQ_LDS v4f*>(scl + DENSE_BM * 4 + n * 4);
+            return make_float4(c[0], c[1], c[2], c[3]);
+        }
+        return make_float4(1.f, 1.f, 1.f, 1.f);
+    };
+    if (p.bias)
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, row_scale, col_scale4,
+                                [&](int i, int g) { return bias4(p, nw + i * 32 + 8 * g + 4 * khalf); });
+    else
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, row_scale, col_scale4,
+                                NoBias{});
 }
 
 // Workgroup u < n_whole computes tile u. When the last round of tiles would
@@ -226,17 +229,20 @@ __device__ __forceinline__ void dense_epilogue_global(const DenseParams& p, v16f
     const float* sa = static_cast<const float*>(p.sa);
     const float* sb = static_cast<const float*>(p.sb);
     const int khalf = lane >> 5;
-    store_tile_bf16<TM, TN>(
-        acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0,
-        [&](int j) {
-            const int m = mw + j * 32 + (lane & 31);
-            return (MODE == MODE_A8W8 && m < p.M) ? sa[m] : 1.0f;
-        },
-        [&](int i, int g) {
-            const int n = nw + i * 32 + 8 * g + 4 * khalf;
-            return (MODE == MODE_A8W8 && n < p.N) ? *reinterpret_cast<const float4*>(sb + n) : make_float4(1.f, 1.f, 1.f, 1.f);
-        },
-        [&](int i, int g) { return bias4(p, nw + i * 32 + 8 * g + 4 * khalf); });
+    auto row_scale = [&](int j) {
+        const int m = mw + j * 32 + (lane & 31);
+        return (MODE == MODE_A8W8 && m < p.M) ? sa[m] : 1.0f;
+    };
+    auto col_scale4 = [&](int i, int g) {
+        const int n = nw + i * 32 + 8 * g + 4 * khalf;
+        return (MODE == MODE_A8W8 && n < p.N) ? *reinterpret_cast<const float4*>(sb + n) : make_float4(1.f, 1.f, 1.f, 1.f);
+    };
+    if (p.bias)
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, row_scale, col_scale4,
+                                [&](int i, int g) { return bias4(p, nw + i * 32 + 8 * g + 4 * khalf); });
+    else
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, row_scale, col_scale4,
+                                NoBias{});
 }
 
 template <int MODE, int WM, int WN, int TM, int TN, int KTB, int MINB>
@@ -403,7 +409,8 @@ static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
     if (int e = set_lds(kern, LDS, attr_set)) return e;
     p.tiles_m = (p.M + DENSE_BM - 1) / DENSE_BM;
     p.tiles_n = (p.N + DENSE_BN - 1) / DENSE_BN;
-    if (p.group_m <= 0) p.group_m = 8;
+    // tile rows per group of the walk (measured best: 8 for FP8, 4 for FP4)
+    if (p.group_m <= 0) p.group_m = MODE == MODE_MXFP4 ? 4 : 8;
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     if (tiles == 0) return 0;
     // Split the last round into M halves when it would fill at most half of the

@@ -228,7 +228,6 @@ __global__ __launch_bounds__(256, 1) void blockscale_gemm_kernel(const BlockScal
     const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
     auto one = [](int) { return 1.0f; };
     auto ones = [](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); };
-    auto zeros = [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); };
     if (p.ca) {
         MulAddElem<TM> e;
         e.ca = p.ca;
@@ -240,9 +239,9 @@ __global__ __launch_bounds__(256, 1) void blockscale_gemm_kernel(const BlockScal
         e.mw = mw;
         e.nw = nw;
         e.lane = lane;
-        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, zeros, e);
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, NoBias{}, e);
     } else {
-        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, zeros);
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, NoBias{});
     }
 }
 

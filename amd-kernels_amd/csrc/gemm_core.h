@@ -152,6 +152,12 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 //   col_bias4(i, g) -> the 4 values added after scaling (zero when unused).
 // Element-wise step after scaling: elem(j, i, g, v) maps the lane's 4 values v
 // of m-tile j, n-tile i, register group g; the default leaves them unchanged.
+// Bias of an epilogue without one: -0 is the additive identity for every
+// value (x + -0 == x, also for x = -0), so the compiler drops the add.
+struct NoBias {
+    __device__ float4 operator()(int, int) const { return make_float4(-0.f, -0.f, -0.f, -0.f); }
+};
+
 // Element-wise hook of the epilogue: prefetch(i) runs before the values of
 // n-tile i are formed (so a hook that reads memory can issue all of that
 // tile's loads at once), then operator()(j, i, g, v) maps the scaled fp32
@@ -202,13 +208,13 @@ __device__ __forceinline__ HKQ_LDS uint8_t* stage_tile_bf16(v16f (&acc)[TN][TM],
 __device__ __forceinline__ void store_piece_bf16(uint16_t* dst, const v4i& v, int n_left, bool c16) {
     if (n_left >= 8) {
         if (c16) {
-            __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(dst));
+            *reinterpret_cast<v4i*>(dst) = v;
         } else {
-            __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
-            __builtin_nontemporal_store(v2i{v[2], v[3]}, reinterpret_cast<v2i*>(dst + 4));
+            *reinterpret_cast<v2i*>(dst) = v2i{v[0], v[1]};
+            *reinterpret_cast<v2i*>(dst + 4) = v2i{v[2], v[3]};
         }
     } else if (n_left > 0) {
-        __builtin_nontemporal_store(v2i{v[0], v[1]}, reinterpret_cast<v2i*>(dst));
+        *reinterpret_cast<v2i*>(dst) = v2i{v[0], v[1]};
     }
 }
 
@@ -236,8 +242,7 @@ __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uin
 #pragma unroll
             for (int k = 0; k < BATCH; ++k) v[k] = lds_read16(ep + ((b + k) * ROWS_PER_PASS + rl) * PITCH + seg * 16);
 #pragma unroll
-            for (int k = 0; k < BATCH; ++k)
-                __builtin_nontemporal_store(v[k], reinterpret_cast<v4i*>(dst + (b + k) * step));
+            for (int k = 0; k < BATCH; ++k) *reinterpret_cast<v4i*>(dst + (b + k) * step) = v[k];
         }
         return;
     }

@@ -264,8 +264,7 @@ __global__ __launch_bounds__(256, 1) void moe_mxfp4_kernel(const MoeFp4Params p)
             const int id = gate_of(j * 32 + (lane & 31));
             return (p.topk_w && id >= 0) ? g * p.topk_w[id] : g;
         },
-        [&](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); },
-        [&](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); });
+        [&](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); }, NoBias{});
 }
 
 template <int KTB, int NS>
