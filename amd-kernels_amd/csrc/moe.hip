@@ -37,6 +37,9 @@ struct MoeParams {
     int64_t sxm, swe, swn, sym;
     int64_t xs_tok, ws_e, ws_n, ws_gn, bias_e;
     int tiles_n, group_m, c16;
+    // per-channel scales / bias readable as float4 (16-byte aligned rows of
+    // contiguous channels, one scale per channel)
+    int ws_vec, bias_vec;
 };
 
 constexpr int MOE_BM = 128;  // rows per OGS routing block
@@ -94,6 +97,15 @@ __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoePara
     }
     const auto b_off = dense_offs<NW, KTB, LB>(wave, lane, p.swn);
 
+    // the epilogue's row scales, fetched before the K loop so that their
+    // dependent loads (gather index, then scale) are not on the tile's tail
+    float rs[TM];
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const int t = p.xs ? token_of(j * 32 + (lane & 31)) : -1;
+        rs[j] = !p.xs ? 1.0f : (t < 0 ? 0.0f : p.xs[(int64_t)t * p.xs_tok]);
+    }
+
     v16f acc[TN][TM];
     gemm_mainloop<MODE_A8W8, WAVES_M, WAVES_N, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
 
@@ -102,29 +114,25 @@ __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoePara
     const int out_rows = min(rows, p.y_rows - s0);
     store_tile_bf16<TM, TN>(
         acc, smem, wave, lane, p.Y + (int64_t)s0 * p.sym, p.sym, out_rows, p.N, 0, nw, p.c16 != 0,
-        [&](int j) {
-            if (!p.xs) return 1.0f;
-            const int t = token_of(j * 32 + (lane & 31));
-            return t < 0 ? 0.0f : p.xs[(int64_t)t * p.xs_tok];
-        },
+        [&](int j) { return rs[j]; },
         [&](int i, int g) {
+            // n .. n+3 lie inside C together (N % 4 == 0)
             const int n = nw + i * 32 + 8 * g + 4 * khalf;
-            float v[4] = {1.f, 1.f, 1.f, 1.f};
-            if (p.ws) {
+            if (!p.ws) return make_float4(1.f, 1.f, 1.f, 1.f);
+            if (n >= p.N) return make_float4(0.f, 0.f, 0.f, 0.f);
+            const float* w = p.ws + (int64_t)e * p.ws_e;
+            if (p.ws_vec) return *reinterpret_cast<const float4*>(w + n);
+            float v[4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    v[c] = n + c < p.N ? p.ws[(int64_t)e * p.ws_e + (int64_t)((n + c) / p.ws_gn) * p.ws_n] : 0.f;
-            }
+            for (int c = 0; c < 4; ++c) v[c] = w[(int64_t)((n + c) / p.ws_gn) * p.ws_n];
             return make_float4(v[0], v[1], v[2], v[3]);
         },
         [&](int i, int g) {
             const int n = nw + i * 32 + 8 * g + 4 * khalf;
-            float v[4] = {0.f, 0.f, 0.f, 0.f};
-            if (p.bias) {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) v[c] = n + c < p.N ? p.bias[(int64_t)e * p.bias_e + n + c] : 0.f;
-            }
-            return make_float4(v[0], v[1], v[2], v[3]);
+            if (!p.bias || n >= p.N) return make_float4(-0.f, -0.f, -0.f, -0.f);
+            const float* b = p.bias + (int64_t)e * p.bias_e + n;
+            if (p.bias_vec) return *reinterpret_cast<const float4*>(b);
+            return make_float4(b[0], b[1], b[2], b[3]);
         });
 }
 
@@ -332,6 +340,9 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     p.g_len = gather ? (int)gather_len : (int)y_rows;
     p.sxm = stride_xm; p.swe = stride_we; p.swn = stride_wn; p.sym = stride_ym;
     p.xs_tok = xs_stride_tok; p.ws_e = ws_stride_e; p.ws_n = ws_stride_n; p.ws_gn = ws_group_n; p.bias_e = bias_stride_e;
+    p.ws_vec = w_scale && ws_stride_n == 1 && ws_group_n == 1 && ws_stride_e % 4 == 0 &&
+               reinterpret_cast<uintptr_t>(w_scale) % 16 == 0;
+    p.bias_vec = bias && bias_stride_e % 4 == 0 && reinterpret_cast<uintptr_t>(bias) % 16 == 0;
     p.c16 = (stride_ym % 8 == 0) && (reinterpret_cast<uintptr_t>(Y) % 16 == 0);
     // 128-byte K-tiles (2-stage ring) when every row has whole ones: a partial
     // last K-tile would read the next row's bytes instead of zeros
