@@ -44,6 +44,40 @@ struct MoeParams {
 
 constexpr int MOE_BM = 128;  // rows per OGS routing block
 
+// Workgroup id -> (routing entry pm, column tile tn). The ids are first
+// spread over the XCDs as in tile_coords (a contiguous range per XCD); the
+// routing entries are then cut into groups of consecutive entries of one
+// expert inside aligned blocks of 16 entries, and each group walks its columns
+// with all of its entries side by side, so the workgroups resident on an XCD
+// share one expert's weight columns (and their gathered token rows) in its L2.
+__device__ __forceinline__ void moe_tile_coords(int bid, const int32_t* expt_data, int grid_m, int tiles_n, int E,
+                                                int& pm, int& tn) {
+    const int nblk = grid_m * tiles_n;
+    const int q = nblk >> 3, rem = nblk & 7;
+    const int xcd = bid & 7, idx = bid >> 3;
+    bid = xcd < rem ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
+    const int row = bid / tiles_n;
+    const int blk0 = row & ~15, nb = min(grid_m - blk0, 16);
+    const int lane = threadIdx.x & 63;
+    // expert of entries blk0 .. blk0+15 (-1: an empty entry or one naming no expert)
+    int key = -2;
+    if (lane < nb) {
+        const int ed = expt_data[blk0 + lane];
+        key = (ed == -1 || (ed & 0xFFFF) >= E) ? -1 : (ed & 0xFFFF);
+    }
+    const int s = row - blk0;
+    const int kstar = __shfl(key, s);
+    const uint32_t same = (uint32_t)__ballot(lane < nb && key == kstar) & 0xFFFFu;
+    const uint32_t below = ~same & ((1u << s) - 1u);          // entries before s of another expert
+    const uint32_t above = ~same & 0xFFFFu & ~((2u << s) - 1u);  // entries after s of another expert
+    const int start = blk0 + (below ? 32 - __builtin_clz(below) : 0);
+    const int end = blk0 + (above ? __builtin_ctz(above) : nb);
+    const int size = end - start;
+    const int l = bid - start * tiles_n;
+    pm = start + l % size;
+    tn = l / size;
+}
+
 template <int WAVES_N, int TN, int KTB, int NS>
 __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoeParams p) {
     constexpr int WAVES_M = 1, TM = 4;
@@ -60,7 +94,7 @@ __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoePara
     const int khalf = lane >> 5;
 
     int pm, tn;
-    tile_coords(blockIdx.x, p.grid_m, p.tiles_n, p.group_m, pm, tn);
+    moe_tile_coords(blockIdx.x, p.expt_data, p.grid_m, p.tiles_n, p.E, pm, tn);
     const int ed = p.expt_data[pm];
     if (ed == -1) return;
     const int e = ed & 0xFFFF, blk = ed >> 16;
