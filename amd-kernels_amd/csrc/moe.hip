@@ -12,11 +12,13 @@
 // expert (ws[e]) or per output channel group (ws[e * ws_e + (n / ws_gn) * ws_n]).
 // Output rows stay in expert-sorted order, as in the reference (no combine).
 //
-// Tiles are 128 rows (one OGS block) x 512 columns; the K loop is the shared
-// pipelined main loop with the A rows gathered per lane through the routing
-// index (rows of other tokens never enter LDS). Metadata is bounds-checked:
-// entries naming an expert >= E, rows past the gather index or tokens past T
-// read zero or are skipped instead of faulting.
+// Tiles are 256 columns by two consecutive OGS blocks of one expert (256 rows,
+// the dense GEMM's tile) or, where a pair of blocks straddles two experts, by
+// one block (128 rows); the K loop is the shared pipelined main loop with the
+// A rows gathered per lane through the routing index (rows of other tokens
+// never enter LDS). Metadata is bounds-checked: entries naming an expert >= E,
+// rows past the gather index or tokens past T read zero or are skipped instead
+// of faulting.
 #include "gemm_mainloop.h"
 #include "hkq_host.h"
 
@@ -44,66 +46,26 @@ struct MoeParams {
 
 constexpr int MOE_BM = 128;  // rows per OGS routing block
 
-// Workgroup id -> (routing entry pm, column tile tn). The ids are first
-// spread over the XCDs as in tile_coords (a contiguous range per XCD); the
-// routing entries are then cut into groups of consecutive entries of one
-// expert inside aligned blocks of 16 entries, and each group walks its columns
-// with all of its entries side by side, so the workgroups resident on an XCD
-// share one expert's weight columns (and their gathered token rows) in its L2.
-__device__ __forceinline__ void moe_tile_coords(int bid, const int32_t* expt_data, int grid_m, int tiles_n, int E,
-                                                int& pm, int& tn) {
-    const int nblk = grid_m * tiles_n;
-    const int q = nblk >> 3, rem = nblk & 7;
-    const int xcd = bid & 7, idx = bid >> 3;
-    bid = xcd < rem ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
-    const int row = bid / tiles_n;
-    const int blk0 = row & ~15, nb = min(grid_m - blk0, 16);
-    const int lane = threadIdx.x & 63;
-    // expert of entries blk0 .. blk0+15 (-1: an empty entry or one naming no expert)
-    int key = -2;
-    if (lane < nb) {
-        const int ed = expt_data[blk0 + lane];
-        key = (ed == -1 || (ed & 0xFFFF) >= E) ? -1 : (ed & 0xFFFF);
-    }
-    const int s = row - blk0;
-    const int kstar = __shfl(key, s);
-    const uint32_t same = (uint32_t)__ballot(lane < nb && key == kstar) & 0xFFFFu;
-    const uint32_t below = ~same & ((1u << s) - 1u);          // entries before s of another expert
-    const uint32_t above = ~same & 0xFFFFu & ~((2u << s) - 1u);  // entries after s of another expert
-    const int start = blk0 + (below ? 32 - __builtin_clz(below) : 0);
-    const int end = blk0 + (above ? __builtin_ctz(above) : nb);
-    const int size = end - start;
-    const int l = bid - start * tiles_n;
-    pm = start + l % size;
-    tn = l / size;
-}
+// Tiles: 256 columns x 256 rows = two consecutive routing blocks of one expert
+// (4 waves of 128 x 128, the dense GEMM's geometry), or x 128 rows = one block
+// (4 waves of 64 x 128) where a pair of blocks straddles two experts.
+constexpr int MOE_WM = 2, MOE_WN = 2, MOE_TN = 4, MOE_BN = MOE_WN * MOE_TN * 32;
 
-template <int WAVES_N, int TN, int KTB, int NS>
-__global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoeParams p) {
-    constexpr int WAVES_M = 1, TM = 4;
-    using Cfg = DenseCfg<MODE_A8W8, WAVES_M, WAVES_N, TM, TN, KTB>;
-    constexpr int NW = Cfg::NW, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
-    static_assert(Cfg::BM == MOE_BM, "one tile row block per routing entry");
-
-    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
-    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
-
+// Rows [row0, row0 + TM*64) of expert e (sorted rows start + row0 + r) times
+// columns [n0, n0 + 256).
+template <int TM, int KTB, int NS>
+__device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, int n0, HKQ_LDS uint8_t* smem) {
+    constexpr int TN = MOE_TN;
+    using Cfg = DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, TM, TN, KTB>;
+    constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wn = wave % WAVES_N;
+    const int wm = wave / MOE_WN, wn = wave % MOE_WN;
     const int khalf = lane >> 5;
 
-    int pm, tn;
-    moe_tile_coords(blockIdx.x, p.expt_data, p.grid_m, p.tiles_n, p.E, pm, tn);
-    const int ed = p.expt_data[pm];
-    if (ed == -1) return;
-    const int e = ed & 0xFFFF, blk = ed >> 16;
-    if (e >= p.E) return;
     const int m_e = p.hist[e], start = p.offs[e];
-    const int row0 = blk * MOE_BM;
-    const int rows = min(m_e - row0, MOE_BM);
-    if (rows <= 0 || start < 0) return;
-    const int n0 = tn * BN;
+    const int rows = min(m_e - row0, BM);
+    if (rows <= 0 || start < 0) return;  // uniform over the workgroup
     const int rows_b = min(p.N - n0, BN);
 
     // token of tile row r (-1 when the row is past the expert's rows or the metadata)
@@ -136,46 +98,84 @@ __global__ __launch_bounds__(64 * WAVES_N, 1) void moe_gemm_kernel(const MoePara
     float rs[TM];
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
-        const int t = p.xs ? token_of(j * 32 + (lane & 31)) : -1;
+        const int t = p.xs ? token_of(wm * TM * 32 + j * 32 + (lane & 31)) : -1;
         rs[j] = !p.xs ? 1.0f : (t < 0 ? 0.0f : p.xs[(int64_t)t * p.xs_tok]);
     }
 
     v16f acc[TN][TM];
-    gemm_mainloop<MODE_A8W8, WAVES_M, WAVES_N, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
+    gemm_mainloop<MODE_A8W8, MOE_WM, MOE_WN, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
 
     const int s0 = start + row0;
     const int nw = n0 + wn * TN * 32;
     const int out_rows = min(rows, p.y_rows - s0);
-    store_tile_bf16<TM, TN>(
-        acc, smem, wave, lane, p.Y + (int64_t)s0 * p.sym, p.sym, out_rows, p.N, 0, nw, p.c16 != 0,
-        [&](int j) { return rs[j]; },
-        [&](int i, int g) {
-            // n .. n+3 lie inside C together (N % 4 == 0)
-            const int n = nw + i * 32 + 8 * g + 4 * khalf;
-            if (!p.ws) return make_float4(1.f, 1.f, 1.f, 1.f);
-            if (n >= p.N) return make_float4(0.f, 0.f, 0.f, 0.f);
-            const float* w = p.ws + (int64_t)e * p.ws_e;
-            if (p.ws_vec) return *reinterpret_cast<const float4*>(w + n);
-            float v[4];
+    auto col_scale4 = [&](int i, int g) {
+        // n .. n+3 lie inside C together (N % 4 == 0)
+        const int n = nw + i * 32 + 8 * g + 4 * khalf;
+        if (!p.ws) return make_float4(1.f, 1.f, 1.f, 1.f);
+        if (n >= p.N) return make_float4(0.f, 0.f, 0.f, 0.f);
+        const float* w = p.ws + (int64_t)e * p.ws_e;
+        if (p.ws_vec) return *reinterpret_cast<const float4*>(w + n);
+        float v[4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v[c] = w[(int64_t)((n + c) / p.ws_gn) * p.ws_n];
-            return make_float4(v[0], v[1], v[2], v[3]);
-        },
-        [&](int i, int g) {
-            const int n = nw + i * 32 + 8 * g + 4 * khalf;
-            if (!p.bias || n >= p.N) return make_float4(-0.f, -0.f, -0.f, -0.f);
-            const float* b = p.bias + (int64_t)e * p.bias_e + n;
-            if (p.bias_vec) return *reinterpret_cast<const float4*>(b);
-            return make_float4(b[0], b[1], b[2], b[3]);
-        });
+        for (int c = 0; c < 4; ++c) v[c] = w[(int64_t)((n + c) / p.ws_gn) * p.ws_n];
+        return make_float4(v[0], v[1], v[2], v[3]);
+    };
+    auto row_scale = [&](int j) { return rs[j]; };
+    uint16_t* Y = p.Y + (int64_t)s0 * p.sym;
+    if (p.bias)
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, Y, p.sym, out_rows, p.N, wm * TM * 32, nw, p.c16 != 0, row_scale,
+                                col_scale4, [&](int i, int g) {
+                                    const int n = nw + i * 32 + 8 * g + 4 * khalf;
+                                    if (n >= p.N) return make_float4(0.f, 0.f, 0.f, 0.f);
+                                    const float* b = p.bias + (int64_t)e * p.bias_e + n;
+                                    if (p.bias_vec) return *reinterpret_cast<const float4*>(b);
+                                    return make_float4(b[0], b[1], b[2], b[3]);
+                                });
+    else
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, Y, p.sym, out_rows, p.N, wm * TM * 32, nw, p.c16 != 0, row_scale,
+                                col_scale4, NoBias{});
 }
 
-template <int WAVES_N, int TN, int KTB, int NS>
+// Workgroup: routing entries (2q, 2q + 1) x column tile tn. Two consecutive
+// blocks of one expert form one 256-row tile; otherwise each valid entry is a
+// 128-row tile, one after the other. Workgroup ids walk the columns of
+// group_m pairs at a time in dispatch order, so the CUs of every XCD work on
+// the same few pairs (one expert) together: the experts' tile counts differ,
+// and giving each XCD its own range of experts (as tile_coords would) left
+// XCDs idle and made the gate/up and down projections 9% and 31% slower.
+template <int KTB, int NS>
+__global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const MoeParams p) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
+    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+    const int pairs = (p.grid_m + 1) / 2;
+    const int per = p.group_m * p.tiles_n;
+    const int grp = blockIdx.x / per, first = grp * p.group_m;
+    const int gsize = min(pairs - first, p.group_m), in_g = blockIdx.x - grp * per;
+    const int q = first + in_g % gsize, tn = in_g / gsize;
+    const int n0 = tn * MOE_BN;
+    const int pm0 = 2 * q, pm1 = 2 * q + 1;
+    const int ed0 = p.expt_data[pm0], ed1 = pm1 < p.grid_m ? p.expt_data[pm1] : -1;
+    const int e0 = ed0 & 0xFFFF, e1 = ed1 & 0xFFFF;
+    const bool v0 = ed0 != -1 && e0 < p.E, v1 = ed1 != -1 && e1 < p.E;
+    const int b0 = ed0 >> 16, b1 = ed1 >> 16;
+    if (v0 && v1 && e0 == e1 && b1 == b0 + 1) {
+        moe_block<4, KTB, NS>(p, e0, b0 * MOE_BM, n0, smem);
+        return;
+    }
+    if (v0) moe_block<2, KTB, NS>(p, e0, b0 * MOE_BM, n0, smem);
+    if (v1) {
+        __syncthreads();  // every wave is done with the first block's epilogue staging
+        moe_block<2, KTB, NS>(p, e1, b1 * MOE_BM, n0, smem);
+    }
+}
+
+template <int KTB, int NS>
 static int launch_moe(MoeParams& p, hipStream_t stream) {
-    using Cfg = DenseCfg<MODE_A8W8, 1, WAVES_N, 4, TN, KTB>;
-    constexpr int LDS = Cfg::lds_bytes(NS);
+    using Whole = DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 4, MOE_TN, KTB>;
+    using Half = DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 2, MOE_TN, KTB>;
+    constexpr int LDS = Whole::lds_bytes(NS) > Half::lds_bytes(NS) ? Whole::lds_bytes(NS) : Half::lds_bytes(NS);
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
-    auto kern = moe_gemm_kernel<WAVES_N, TN, KTB, NS>;
+    auto kern = moe_gemm_kernel<KTB, NS>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
@@ -185,11 +185,11 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
         }
         attr_set = true;
     }
-    p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
-    if (p.group_m <= 0) p.group_m = 8;
-    const int64_t nblk = (int64_t)p.grid_m * p.tiles_n;
+    p.tiles_n = (p.N + MOE_BN - 1) / MOE_BN;
+    if (p.group_m <= 0) p.group_m = 2;
+    const int64_t nblk = (int64_t)((p.grid_m + 1) / 2) * p.tiles_n;
     if (nblk == 0) return 0;
-    kern<<<dim3((unsigned)nblk), 64 * WAVES_N, LDS, stream>>>(p);
+    kern<<<dim3((unsigned)nblk), 64 * MOE_WM * MOE_WN, LDS, stream>>>(p);
     return hkq_launch_status();
 }
 
@@ -380,7 +380,7 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     p.c16 = (stride_ym % 8 == 0) && (reinterpret_cast<uintptr_t>(Y) % 16 == 0);
     // 128-byte K-tiles (2-stage ring) when every row has whole ones: a partial
     // last K-tile would read the next row's bytes instead of zeros
-    return K % 128 == 0 ? launch_moe<4, 4, 128, 2>(p, stream) : launch_moe<4, 4, 64, 3>(p, stream);
+    return K % 128 == 0 ? launch_moe<128, 2>(p, stream) : launch_moe<64, 4>(p, stream);
 }
 
 extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* A_mx_scale, const void* B_mx_scale,

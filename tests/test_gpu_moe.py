@@ -95,6 +95,21 @@ def test_moe_skewed_routing_and_padding(orc):
     check_rows(orc, Y, ref)
 
 
+def test_moe_entry_order_and_pairing(orc):
+    """ExptData in another order than the producers write it: consecutive
+    entries that are blocks b, b+1 of one expert run as one 256-row tile, any
+    other entry as a 128-row tile; every listed block is computed once either
+    way (an expert with an odd block count puts a pair across two experts)."""
+    require_gpu()
+    T, E, topk, K, N = 700, 5, 2, 256, 256
+    _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 17)
+    ref = orc.moe_ref(X, W, xs, ws, None, gather, hist, offs, ed, topk, 128, "enk")
+    rng = np.random.default_rng(3)
+    for order in (np.arange(len(ed))[::-1], rng.permutation(len(ed)), np.roll(np.arange(len(ed)), 1)):
+        Y = run_moe(X, W, hist, offs, gather, ed[order], topk, xs, ws)
+        check_rows(orc, Y, ref)
+
+
 def test_moe_without_gather(orc):
     """GatherIndx None: tile rows read X[start + gm] directly (pre-sorted X)."""
     require_gpu()
