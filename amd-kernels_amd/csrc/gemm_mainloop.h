@@ -65,9 +65,13 @@ struct LoopSrc {
     const uint8_t *as, *bs;
     int64_t as_bytes, bs_bytes, lsa, lsb;
     int KT;  // K-tiles
-    // FP4 with gathered A rows: byte offset of tile row r's scale row inside
-    // `as` (beyond as_bytes for rows that read zero); nullptr: row r * lsa
-    const HKQ_LDS uint32_t* sa_rows = nullptr;
+    // FP4 with gathered A rows (sa_gathered): the byte offset inside `as` of the
+    // A scale row this lane loads, per load slot (128-byte K-tiles: slot
+    // u % SB_KT of scale unit u; 64-byte K-tiles: the k-th A scale load of a
+    // K-tile), beyond as_bytes for rows that read zero. Otherwise tile row r's
+    // scale row is at r * lsa.
+    bool sa_gathered = false;
+    uint32_t sa_row[4] = {0u, 0u, 0u, 0u};
 };
 
 // Byte offset (row and logical chunk, excluding the K position) of LDS-direct
@@ -139,6 +143,7 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     constexpr int HCH = KTB / 32;  // logical chunks per lane half
     static_assert(NS >= 2 && (NS - 1) * NLD + 3 <= 63, "ring depth and vmcnt budget");
     static_assert(!Cfg::SBLK || NS == 2, "the scale-block schedule assumes a 2-stage ring");
+    static_assert(Cfg::SB_KT <= 4 && LSA <= 4, "gathered scale rows: at most 4 load slots per lane");
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int KTN = src.KT;
 
@@ -159,7 +164,9 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
         // both row offsets are formed and one is selected: a branch here would
         // split the loop body into blocks, and the compiler then sinks the
         // MFMAs of the earlier blocks past the loads they should overlap
-        const uint32_t a_row = src.sa_rows ? src.sa_rows[isa ? r : 0] : (uint32_t)(r * src.lsa);
+        const int k = u % Cfg::SB_KT;
+        const uint32_t ga = k == 0 ? src.sa_row[0] : k == 1 ? src.sa_row[1] : k == 2 ? src.sa_row[2] : src.sa_row[3];
+        const uint32_t a_row = src.sa_gathered ? ga : (uint32_t)(r * src.lsa);
         const uint32_t b_row = (uint32_t)((r - BM) * src.lsb);
         const uint32_t row_off = isa ? a_row : b_row;
         const uint32_t off = row_off + half * 16u;
@@ -192,7 +199,8 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
         } else if (idx < LA + LB + LSA) {
             const int g = ((idx - LA - LB) * NW + wave) % GA;
             const int kb4 = kt * 4;
-            const uint32_t off = src.sa_rows ? src.sa_rows[g * 64 + lane] : (uint32_t)((g * 64 + lane) * src.lsa);
+            const uint32_t off =
+                src.sa_gathered ? src.sa_row[(idx - LA - LB) & 3] : (uint32_t)((g * 64 + lane) * src.lsa);
             lds_load4(src.as + kb4, live ? (uint32_t)(src.as_bytes - kb4) : 0u, st + (BM + BN) * KTB + g * 256, off);
         } else {
             const int g = ((idx - LA - LB - LSA) * NW + wave) % GB;

@@ -136,22 +136,29 @@ __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, i
                                 col_scale4, NoBias{});
 }
 
+// Workgroup id -> (routing-block pair q, column tile tn): the ids walk the
+// columns of `group` pairs at a time in dispatch order, so the CUs of every XCD
+// work on the same few pairs (one expert) together. The experts' block counts
+// differ, and giving each XCD its own range of experts (as tile_coords does for
+// the dense GEMMs) left XCDs idle: the A8W8 gate/up and down projections ran
+// 9% and 31% slower that way, the MXFP4 ones 16% and 33%.
+__device__ __forceinline__ void pair_walk(int bid, int pairs, int tiles_n, int group, int& q, int& tn) {
+    const int per = group * tiles_n;
+    const int grp = bid / per, first = grp * group;
+    const int gsize = min(pairs - first, group), in_g = bid - grp * per;
+    q = first + in_g % gsize;
+    tn = in_g / gsize;
+}
+
 // Workgroup: routing entries (2q, 2q + 1) x column tile tn. Two consecutive
 // blocks of one expert form one 256-row tile; otherwise each valid entry is a
-// 128-row tile, one after the other. Workgroup ids walk the columns of
-// group_m pairs at a time in dispatch order, so the CUs of every XCD work on
-// the same few pairs (one expert) together: the experts' tile counts differ,
-// and giving each XCD its own range of experts (as tile_coords would) left
-// XCDs idle and made the gate/up and down projections 9% and 31% slower.
+// 128-row tile, one after the other.
 template <int KTB, int NS>
 __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const MoeParams p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
-    const int pairs = (p.grid_m + 1) / 2;
-    const int per = p.group_m * p.tiles_n;
-    const int grp = blockIdx.x / per, first = grp * p.group_m;
-    const int gsize = min(pairs - first, p.group_m), in_g = blockIdx.x - grp * per;
-    const int q = first + in_g % gsize, tn = in_g / gsize;
+    int q, tn;
+    pair_walk(blockIdx.x, (p.grid_m + 1) / 2, p.tiles_n, p.group_m, q, tn);
     const int n0 = tn * MOE_BN;
     const int pm0 = 2 * q, pm1 = 2 * q + 1;
     const int ed0 = p.expt_data[pm0], ed1 = pm1 < p.grid_m ? p.expt_data[pm1] : -1;
@@ -221,26 +228,16 @@ struct MoeFp4Params {
 
 constexpr uint32_t FP4_OOB = 0x7FFF0000u;  // a row offset past every operand's bounds
 
-template <int KTB, int NS>
-__global__ __launch_bounds__(256, 1) void moe_mxfp4_kernel(const MoeFp4Params p) {
-    constexpr int WAVES_M = 1, WAVES_N = 4, TM = 4, TN = 2;
-    using Cfg = DenseCfg<MODE_MXFP4, WAVES_M, WAVES_N, TM, TN, KTB>;
-    constexpr int NW = Cfg::NW, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
-    static_assert(Cfg::BM == MOE_BM, "one tile row block per routing block");
-
-    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
-    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
-    HKQ_LDS uint32_t* sa_rows = (HKQ_LDS uint32_t*)(smem + Cfg::lds_bytes(NS));
-
+// Rows [pm*128, pm*128 + TM*64) of the sorted routing (one block, or two
+// consecutive blocks of expert e) times columns [n0, n0 + 256), expert e >= 0.
+template <int TM, int KTB, int NS>
+__device__ __forceinline__ void moe_fp4_block(const MoeFp4Params& p, int pm, int e, int n0, HKQ_LDS uint8_t* smem) {
+    constexpr int TN = MOE_TN;
+    using Cfg = DenseCfg<MODE_MXFP4, MOE_WM, MOE_WN, TM, TN, KTB>;
+    constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wn = wave % WAVES_N;
-    const int khalf = lane >> 5;
-
-    int pm, tn;
-    tile_coords(blockIdx.x, p.grid_m, p.tiles_n, p.group_m, pm, tn);
-    const int e = p.expert[pm];
-    const int n0 = tn * BN;
+    const int wm = wave / MOE_WN, wn = wave % MOE_WN;
     const int nw = n0 + wn * TN * 32;
     const int32_t* ids = p.sorted + (int64_t)pm * MOE_BM;
     // gate id of tile row r, or -1 when it is padding
@@ -255,24 +252,6 @@ __global__ __launch_bounds__(256, 1) void moe_mxfp4_kernel(const MoeFp4Params p)
         return t < p.tokens ? t : -1;
     };
 
-    if (e < 0 || e >= p.E) {
-        if (e != -1) return;  // an expert id past E: nothing to compute or write
-        // the reference writes zeros to the valid rows of a block without expert
-        for (int r = wave; r < MOE_BM; r += NW) {
-            const int id = gate_of(r);
-            if (id < 0) continue;
-            for (int n = n0 + lane * 4; n < min(p.N, n0 + BN); n += 256)
-                *reinterpret_cast<v2i*>(p.C + (int64_t)id * p.scm + n) = v2i{0, 0};
-        }
-        return;
-    }
-
-    for (int r = threadIdx.x; r < MOE_BM; r += 256) {
-        const int t = arow_of(r);
-        sa_rows[r] = t < 0 ? FP4_OOB : (uint32_t)(t * p.sas);
-    }
-    __syncthreads();
-
     const int rows_b = min(p.N - n0, BN);
     LoopSrc src;
     src.a = p.A;
@@ -286,7 +265,22 @@ __global__ __launch_bounds__(256, 1) void moe_mxfp4_kernel(const MoeFp4Params p)
     src.lsa = p.sas;
     src.lsb = p.sbsn;
     src.KT = (p.K / 2) / KTB;
-    src.sa_rows = sa_rows;
+    // the A scale rows this lane loads (the main loop's slot order): 128-byte
+    // K-tiles: row g*32 + lane/2 of group g = (k*NW + wave) % SB_GROUPS for
+    // slot k; 64-byte K-tiles: row g*64 + lane of group g = (k*NW + wave) % GA
+    src.sa_gathered = true;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        int r;
+        if constexpr (Cfg::SBLK) {
+            const int g = (k * NW + wave) % Cfg::SB_GROUPS;
+            r = g * 32 < BM ? g * 32 + (lane >> 1) : -1;
+        } else {
+            r = k < Cfg::LSA ? ((k * NW + wave) % Cfg::GA) * 64 + lane : -1;
+        }
+        const int t = r < 0 ? -1 : arow_of(r);
+        src.sa_row[k] = t < 0 ? FP4_OOB : (uint32_t)(t * p.sas);
+    }
     TableOff<LA> a_off;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
@@ -296,23 +290,70 @@ __global__ __launch_bounds__(256, 1) void moe_mxfp4_kernel(const MoeFp4Params p)
     }
     const auto b_off = dense_offs<NW, KTB, LB>(wave, lane, p.sbn);
 
-    v16f acc[TN][TM];
-    gemm_mainloop<MODE_MXFP4, WAVES_M, WAVES_N, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
+    // the epilogue's row scales (routed weights), fetched before the K loop
+    const float gs = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
+    float rs[TM];
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const int id = gate_of(wm * TM * 32 + j * 32 + (lane & 31));
+        rs[j] = (p.topk_w && id >= 0) ? gs * p.topk_w[id] : gs;
+    }
 
-    const float g = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
+    v16f acc[TN][TM];
+    gemm_mainloop<MODE_MXFP4, MOE_WM, MOE_WN, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
+
     store_tile_bf16_rows<TM, TN>(
-        acc, smem, wave, lane, p.C, p.scm, p.N, nw, p.c16 != 0, [&](int r) { return (int64_t)gate_of(r); },
-        [&](int j) {
-            const int id = gate_of(j * 32 + (lane & 31));
-            return (p.topk_w && id >= 0) ? g * p.topk_w[id] : g;
-        },
+        acc, smem, wave, lane, p.C, p.scm, p.N, nw, p.c16 != 0,
+        [&](int r) { return (int64_t)gate_of(wm * TM * 32 + r); }, [&](int j) { return rs[j]; },
         [&](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); }, NoBias{});
+}
+
+// The valid rows of block pm, whose expert id is -1, are written as zeros (as
+// the reference does); columns [n0, n0 + 256).
+__device__ __forceinline__ void moe_fp4_zero_block(const MoeFp4Params& p, int pm, int n0) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int32_t* ids = p.sorted + (int64_t)pm * MOE_BM;
+    for (int r = wave; r < MOE_BM; r += 4) {
+        const int id = ids[r];
+        if (id < 0 || id >= p.num_valid) continue;
+        for (int n = n0 + lane * 4; n < min(p.N, n0 + MOE_BN); n += 256)
+            *reinterpret_cast<v2i*>(p.C + (int64_t)id * p.scm + n) = v2i{0, 0};
+    }
+}
+
+// Workgroup: routing blocks (2q, 2q + 1) x column tile tn; two blocks of one
+// expert form one 256-row tile, otherwise each block is its own 128-row tile
+// (or, with expert -1, zeros). Tile order: pair_walk, one pair at a time.
+template <int KTB, int NS>
+__global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_mxfp4_kernel(const MoeFp4Params p) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
+    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+    int q, tn;
+    pair_walk(blockIdx.x, (p.grid_m + 1) / 2, p.tiles_n, p.group_m, q, tn);
+    const int n0 = tn * MOE_BN;
+    const int pm0 = 2 * q, pm1 = 2 * q + 1;
+    const int e0 = p.expert[pm0], e1 = pm1 < p.grid_m ? p.expert[pm1] : -2;
+    if (e0 >= 0 && e0 < p.E && e1 == e0) {
+        moe_fp4_block<4, KTB, NS>(p, pm0, e0, n0, smem);
+        return;
+    }
+    // an expert id past E (or the missing partner, -2): nothing to compute or write
+    if (e0 == -1) moe_fp4_zero_block(p, pm0, n0);
+    else if (e0 >= 0 && e0 < p.E) moe_fp4_block<2, KTB, NS>(p, pm0, e0, n0, smem);
+    if (e1 == -1) {
+        moe_fp4_zero_block(p, pm1, n0);
+    } else if (e1 >= 0 && e1 < p.E) {
+        __syncthreads();  // every wave is done with the first block's epilogue staging
+        moe_fp4_block<2, KTB, NS>(p, pm1, e1, n0, smem);
+    }
 }
 
 template <int KTB, int NS>
 static int launch_moe_fp4(MoeFp4Params& p, hipStream_t stream) {
-    using Cfg = DenseCfg<MODE_MXFP4, 1, 4, 4, 2, KTB>;
-    constexpr int LDS = Cfg::lds_bytes(NS) + MOE_BM * 4;
+    using Whole = DenseCfg<MODE_MXFP4, MOE_WM, MOE_WN, 4, MOE_TN, KTB>;
+    using Half = DenseCfg<MODE_MXFP4, MOE_WM, MOE_WN, 2, MOE_TN, KTB>;
+    constexpr int LDS = Whole::lds_bytes(NS) > Half::lds_bytes(NS) ? Whole::lds_bytes(NS) : Half::lds_bytes(NS);
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
     auto kern = moe_mxfp4_kernel<KTB, NS>;
     static bool attr_set = false;
@@ -324,11 +365,11 @@ static int launch_moe_fp4(MoeFp4Params& p, hipStream_t stream) {
         }
         attr_set = true;
     }
-    p.tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
-    if (p.group_m <= 0) p.group_m = 8;
-    const int64_t nblk = (int64_t)p.grid_m * p.tiles_n;
+    p.tiles_n = (p.N + MOE_BN - 1) / MOE_BN;
+    if (p.group_m <= 0) p.group_m = 1;
+    const int64_t nblk = (int64_t)((p.grid_m + 1) / 2) * p.tiles_n;
     if (nblk == 0) return 0;
-    kern<<<dim3((unsigned)nblk), 256, LDS, stream>>>(p);
+    kern<<<dim3((unsigned)nblk), 64 * MOE_WM * MOE_WN, LDS, stream>>>(p);
     return hkq_launch_status();
 }
 
