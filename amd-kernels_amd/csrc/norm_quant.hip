@@ -51,11 +51,18 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
     const int nch = D >> 3;
     const uint4* xr = reinterpret_cast<const uint4*>(x + (int64_t)row * ldx);
     const uint4* wr = reinterpret_cast<const uint4*>(w);
-    uint4 xv[NC];
+    // x and the weight are both requested before the reduction, so the
+    // weight's (cache-resident) loads overlap the row's HBM loads
+    uint4 xv[NC], wv[NC];
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
         const int c = lane + 64 * i;
         xv[i] = c < nch ? ld_stream16(xr + c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + 64 * i;
+        wv[i] = c < nch ? wr[c] : make_uint4(0, 0, 0, 0);
     }
     float ss = 0.0f;
 #pragma unroll
@@ -74,7 +81,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
         if (64 * i >= nch) break;  // wave-uniform: no lane has a chunk here
         float xf[8], wf[8], y[8];
         unpack8(xv[i], xf);
-        unpack8(c < nch ? wr[c] : make_uint4(0, 0, 0, 0), wf);  // the weight stays in cache across rows
+        unpack8(wv[i], wf);
         float m = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
