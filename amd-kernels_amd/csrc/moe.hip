@@ -150,6 +150,37 @@ __device__ __forceinline__ void pair_walk(int bid, int pairs, int tiles_n, int g
     tn = in_g / gsize;
 }
 
+// Work unit of workgroup bid: tile t (pair q, column tn) in pair_walk order,
+// whole (half -1) or one of its two blocks (half 0 / 1). When the last round
+// of the launch's tiles would fill at most half of the CUs, each of its tiles
+// is cut into its two blocks, run by two workgroups (the padding entries come
+// last, so these are the last live tiles and the empty ones after them):
+//   units [0, s0): tile u; then block (u - s0) & 1 of tile s0 + (u - s0) / 2.
+// Returns false for the spare units past the last tile.
+__device__ __forceinline__ bool pair_unit(int bid, int pairs, int tiles_n, int group, int split, int& q, int& tn,
+                                          int& half) {
+    const int total = pairs * tiles_n;
+    const int s0 = total - split;
+    int t;
+    half = -1;
+    if (bid < s0) {
+        t = bid;
+    } else {
+        t = s0 + (bid - s0) / 2;
+        half = (bid - s0) & 1;
+        if (t >= total) return false;
+    }
+    pair_walk(t, pairs, tiles_n, group, q, tn);
+    return true;
+}
+
+// Tiles of the last round that pair_unit cuts in two (host side).
+static int64_t moe_tail_split(int64_t tiles) {
+    const int ncu = cu_count();
+    const int64_t last = ncu > 0 ? tiles % ncu : 0;
+    return (last > 0 && 2 * last <= ncu) ? last : 0;
+}
+
 // Workgroup: routing entries (2q, 2q + 1) x column tile tn. Two consecutive
 // blocks of one expert form one 256-row tile; otherwise each valid entry is a
 // 128-row tile, one after the other.
@@ -223,6 +254,7 @@ struct MoeFp4Params {
     const int32_t* sorted;  // [grid_m * 128]
     const int32_t* expert;  // [grid_m]
     int tokens, E, N, K, topk, num_valid, grid_m, tiles_n, group_m, c16;
+    int split;  // tiles of the last round cut into their two blocks (pair_unit)
     int64_t sam, sas, sbe, sbn, sbse, sbsn, scm;
 };
 
@@ -329,23 +361,29 @@ template <int KTB, int NS>
 __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_mxfp4_kernel(const MoeFp4Params p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
-    int q, tn;
-    pair_walk(blockIdx.x, (p.grid_m + 1) / 2, p.tiles_n, p.group_m, q, tn);
+    int q, tn, half;
+    if (!pair_unit(blockIdx.x, (p.grid_m + 1) / 2, p.tiles_n, p.group_m, p.split, q, tn, half)) return;
     const int n0 = tn * MOE_BN;
     const int pm0 = 2 * q, pm1 = 2 * q + 1;
     const int e0 = p.expert[pm0], e1 = pm1 < p.grid_m ? p.expert[pm1] : -2;
-    if (e0 >= 0 && e0 < p.E && e1 == e0) {
+    if (half < 0 && e0 >= 0 && e0 < p.E && e1 == e0) {
         moe_fp4_block<4, KTB, NS>(p, pm0, e0, n0, smem);
         return;
     }
-    // an expert id past E (or the missing partner, -2): nothing to compute or write
-    if (e0 == -1) moe_fp4_zero_block(p, pm0, n0);
-    else if (e0 >= 0 && e0 < p.E) moe_fp4_block<2, KTB, NS>(p, pm0, e0, n0, smem);
-    if (e1 == -1) {
-        moe_fp4_zero_block(p, pm1, n0);
-    } else if (e1 >= 0 && e1 < p.E) {
-        __syncthreads();  // every wave is done with the first block's epilogue staging
-        moe_fp4_block<2, KTB, NS>(p, pm1, e1, n0, smem);
+    // the pair's blocks one at a time (both, or the one this unit was given);
+    // expert -1: zeros; an expert id past E: nothing to compute or write
+    const int h0 = half < 0 ? 0 : half, h1 = half < 0 ? 1 : half;
+#pragma unroll 1
+    for (int h = h0; h <= h1; ++h) {
+        const int pm = pm0 + h;
+        if (pm >= p.grid_m) break;
+        const int e = p.expert[pm];
+        if (e == -1) {
+            moe_fp4_zero_block(p, pm, n0);
+        } else if (e >= 0 && e < p.E) {
+            __syncthreads();  // every wave is done with an earlier block's epilogue staging
+            moe_fp4_block<2, KTB, NS>(p, pm, e, n0, smem);
+        }
     }
 }
 
@@ -367,8 +405,10 @@ static int launch_moe_fp4(MoeFp4Params& p, hipStream_t stream) {
     }
     p.tiles_n = (p.N + MOE_BN - 1) / MOE_BN;
     if (p.group_m <= 0) p.group_m = 1;
-    const int64_t nblk = (int64_t)((p.grid_m + 1) / 2) * p.tiles_n;
-    if (nblk == 0) return 0;
+    const int64_t tiles = (int64_t)((p.grid_m + 1) / 2) * p.tiles_n;
+    if (tiles == 0) return 0;
+    p.split = (int)moe_tail_split(tiles);
+    const int64_t nblk = tiles + p.split;
     kern<<<dim3((unsigned)nblk), 64 * MOE_WM * MOE_WN, LDS, stream>>>(p);
     return hkq_launch_status();
 }
