@@ -316,6 +316,152 @@ __global__ __launch_bounds__(256) void dense_reduce_kernel(const DenseParams p, 
     *reinterpret_cast<v2i*>(p.C + (int64_t)m * p.ldc + n) = v2i{(int)lo, (int)hi};
 }
 
+// ---------------------------------------------------------------------------
+// Narrow M (M <= 32, FP8 and FP4): a streaming path on the 16x16x128 MFMA.
+// Workgroup u owns the 16*NT columns [16*NT*u, 16*NT*(u+1)) of C for all M
+// rows; its 4 waves split K (wave w takes the 128-value K-steps
+// [w*S/4, (w+1)*S/4) of S) and load their operand fragments from memory
+// straight into registers, DEPTH steps ahead. The waves' sums meet in LDS, and
+// wave 0 adds them in wave order, applies the scales and writes C. Each weight
+// byte is read once, by one workgroup, in a single launch (no split-K
+// partials, no second kernel). NT > 1 reuses each activation fragment for NT
+// weight tiles when N gives more workgroups than CUs.
+//
+// Fragment layout of the 16x16x128 MFMA (verified on gfx950): lane l supplies
+// row l % 16 and the 32 K-values [32*(l/16), 32*(l/16) + 32) of the 128-deep
+// slice (FP8: 32 bytes; FP4: 16 bytes in the low 4 VGPRs, scaled per lane by
+// its 32-value block's e8m0); lane l, register i of the result holds
+// D[4*(l/16) + i][l % 16]. The MFMA A operand is the weight rows (n), B the
+// activation rows (m): a lane holds 4 consecutive n of one m. An FP8 sum over
+// K does not depend on which lane supplies which K-value as long as both
+// operands agree, so an FP8 lane takes bytes [16q, 16q+16) and [64+16q,
+// 64+16q+16) of the step (q = l/16): each 16-byte load covers 64 contiguous
+// bytes of 16 rows.
+constexpr int NARROW_WAVES = 4, NARROW_MAX_M = 32;
+
+template <int MODE, int MT, int NT>
+struct NarrowFrag {
+    v4i b0[NT], b1[NT];  // weight rows (b1: FP8 only)
+    v4i a0[MT], a1[MT];  // activation rows (a1: FP8 only)
+    uint32_t sb[NT], sa[MT];  // FP4: e8m0 scales of the step's 4 blocks (byte q is the lane's)
+};
+
+template <int MT, int NT>
+constexpr int narrow_depth() { return NT >= 4 ? 4 : NT == 2 ? 6 : 8; }
+
+template <int MODE, int MT, int NT>
+__global__ __launch_bounds__(64 * NARROW_WAVES) void narrow_gemm_kernel(const DenseParams pb) {
+    constexpr bool FP4 = MODE == MODE_MXFP4;
+    constexpr int SB = FP4 ? 64 : 128;  // bytes of a row per 128-value K-step
+    constexpr int DEPTH = narrow_depth<MT, NT>();
+    __shared__ v4f red[NARROW_WAVES][NT][MT][64];
+    const DenseParams p = batch_slice(pb);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * 16 * NT;
+    const int S = p.kbytes / SB;
+    const int s0 = wave * S / NARROW_WAVES, s1 = (wave + 1) * S / NARROW_WAVES;
+    const int rows_b = min(16 * NT, p.N - n0);
+    const auto rb = make_rsrc(p.B + (int64_t)n0 * p.ldb, (uint32_t)(rows_b * p.ldb));
+    const auto ra = make_rsrc(p.A, (uint32_t)(p.M * p.lda));
+    const uint8_t* bs = static_cast<const uint8_t*>(p.sb);
+    const auto rsb = make_rsrc(FP4 ? bs + (int64_t)n0 * p.lsb : p.B, FP4 ? (uint32_t)(rows_b * p.lsb) : 0u);
+    const auto rsa = make_rsrc(FP4 ? p.sa : p.A, FP4 ? (uint32_t)(p.M * p.lsa) : 0u);
+    uint32_t b_off[NT], a_off[MT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) b_off[t] = (uint32_t)((t * 16 + r) * p.ldb + 16 * q);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) a_off[t] = (uint32_t)((t * 16 + r) * p.lda + 16 * q);
+
+    // Steps at or past s1 read zeros (their MFMAs add nothing): offsets with
+    // the OOB bit set are past every buffer's range.
+    auto load = [&](int s, NarrowFrag<MODE, MT, NT>& f) {
+        const uint32_t kb = (uint32_t)s * SB | (s < s1 ? 0u : OOB);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            f.b0[t] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[t] + kb, 0, 0);
+            if constexpr (!FP4) f.b1[t] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[t] + kb + 64, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            f.a0[t] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t] + kb, 0, 0);
+            if constexpr (!FP4) f.a1[t] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t] + kb + 64, 0, 0);
+        }
+        if constexpr (FP4) {
+            const uint32_t ks = 4 * (uint32_t)s | (s < s1 ? 0u : OOB);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                f.sb[t] = __builtin_amdgcn_raw_buffer_load_b32(rsb, (uint32_t)((t * 16 + r) * p.lsb) + ks, 0, 0);
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                f.sa[t] = __builtin_amdgcn_raw_buffer_load_b32(rsa, (uint32_t)((t * 16 + r) * p.lsa) + ks, 0, 0);
+        }
+    };
+    v4f acc[NT][MT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[i][t] = v4f{0.f, 0.f, 0.f, 0.f};
+    auto mma = [&](const NarrowFrag<MODE, MT, NT>& f) {
+#pragma unroll
+        for (int i = 0; i < NT; ++i)
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                if constexpr (FP4) {
+                    const v8i a = v8i{f.b0[i][0], f.b0[i][1], f.b0[i][2], f.b0[i][3], 0, 0, 0, 0};
+                    const v8i b = v8i{f.a0[t][0], f.a0[t][1], f.a0[t][2], f.a0[t][3], 0, 0, 0, 0};
+                    acc[i][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        a, b, acc[i][t], 4, 4, 0, (int)(f.sb[i] >> (8 * q)), 0, (int)(f.sa[t] >> (8 * q)));
+                } else {
+                    const v8i a = v8i{f.b0[i][0], f.b0[i][1], f.b0[i][2], f.b0[i][3],
+                                      f.b1[i][0], f.b1[i][1], f.b1[i][2], f.b1[i][3]};
+                    const v8i b = v8i{f.a0[t][0], f.a0[t][1], f.a0[t][2], f.a0[t][3],
+                                      f.a1[t][0], f.a1[t][1], f.a1[t][2], f.a1[t][3]};
+                    acc[i][t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[i][t], 0, 0, 0, 127, 0, 127);
+                }
+            }
+    };
+    NarrowFrag<MODE, MT, NT> f[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load(s0 + d, f[d]);
+    for (int s = s0; s < s1; s += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            mma(f[d]);
+            load(s + d + DEPTH, f[d]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) red[wave][i][t][lane] = acc[i][t];
+    __syncthreads();
+    if (wave != 0) return;
+    const float* sa = static_cast<const float*>(p.sa);
+    const float* sb = static_cast<const float*>(p.sb);
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const int n = n0 + 16 * i + 4 * q;
+        if (n >= p.N) break;  // N % 4 == 0: n .. n+3 all in or all out
+        float4 cs = make_float4(1.f, 1.f, 1.f, 1.f);
+        if constexpr (MODE == MODE_A8W8) cs = *reinterpret_cast<const float4*>(sb + n);
+        const float4 c = bias4(p, n);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int m = t * 16 + r;
+            if (m >= p.M) break;
+            v4f v = red[0][i][t][lane];
+#pragma unroll
+            for (int w = 1; w < NARROW_WAVES; ++w) v += red[w][i][t][lane];
+            const float a = MODE == MODE_A8W8 ? sa[m] : 1.f;
+            *reinterpret_cast<v2i*>(p.C + (int64_t)m * p.ldc + n) =
+                v2i{(int)pk_bf16(v[0] * a * cs.x + c.x, v[1] * a * cs.y + c.y),
+                    (int)pk_bf16(v[2] * a * cs.z + c.z, v[3] * a * cs.w + c.w)};
+        }
+    }
+}
+
 template <typename K>
 static int set_lds(K kern, int lds, bool& done) {
     if (done) return 0;
@@ -426,10 +572,56 @@ static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
     return hkq_launch_status();
 }
 
+// The narrow path serves the FP8 and FP4 GEMMs whose rows hold whole 128-value
+// K-steps: all of M <= 16, and M <= 32 while one round of 16-column
+// workgroups covers N and K is at most 32 steps (every workgroup re-reads
+// the activation rows, which then costs more than the tiled path's
+// LDS-shared activation tile; measured on MI355X). Its buffer offsets are
+// 32-bit: 16*NT weight rows and 32 activation rows must span less than 2 GiB.
+static bool use_narrow(int mode, int64_t M, int64_t N, int64_t kbytes, int64_t lda, int64_t ldb, int64_t batch) {
+    if (mode != MODE_A8W8 && mode != MODE_MXFP4) return false;
+    const int64_t step = mode == MODE_MXFP4 ? 64 : 128;
+    if (M < 1 || M > NARROW_MAX_M || kbytes % step != 0 || 64 * ldb >= (1ll << 31) || NARROW_MAX_M * lda >= (1ll << 31))
+        return false;
+    if (M <= 16) return true;
+    const int64_t ncu = cu_count() > 0 ? cu_count() : 256;
+    return std::max<int64_t>(1, batch) * ((N + 15) / 16) < 2 * ncu && kbytes / step <= 32;
+}
+
+template <int MODE, int MT, int NT>
+static int launch_narrow_nt(const DenseParams& p, hipStream_t stream) {
+    const dim3 grid((unsigned)((p.N + 16 * NT - 1) / (16 * NT)), (unsigned)std::max(1, p.batch));
+    narrow_gemm_kernel<MODE, MT, NT><<<grid, 64 * NARROW_WAVES, 0, stream>>>(p);
+    return hkq_launch_status();
+}
+
+// Columns per workgroup: 16 * NT. One round of 16-column workgroups: NT = 1;
+// up to three rounds: NT = 2 (one round, activation fragments used twice);
+// more: NT = 4 (measured on MI355X at N = 4096 .. 28672).
+template <int MODE>
+static int launch_narrow(const DenseParams& p, hipStream_t stream) {
+    if constexpr (MODE == MODE_A8W8 || MODE == MODE_MXFP4) {
+        if (p.N == 0) return 0;
+        const int64_t ncu = cu_count() > 0 ? cu_count() : 256;
+        const int64_t wgs16 = (int64_t)std::max(1, p.batch) * ((p.N + 15) / 16);
+        const int nt = wgs16 <= ncu ? 1 : wgs16 <= 3 * ncu ? 2 : 4;
+        if (p.M <= 16) {
+            if (nt == 4) return launch_narrow_nt<MODE, 1, 4>(p, stream);
+            if (nt == 2) return launch_narrow_nt<MODE, 1, 2>(p, stream);
+            return launch_narrow_nt<MODE, 1, 1>(p, stream);
+        }
+        if (nt == 4) return launch_narrow_nt<MODE, 2, 4>(p, stream);
+        if (nt == 2) return launch_narrow_nt<MODE, 2, 2>(p, stream);
+        return launch_narrow_nt<MODE, 2, 1>(p, stream);
+    }
+    return 0;
+}
+
 // 128-byte K-tiles need whole 128-byte K-tiles in every row: a partial last
 // K-tile would read the next row's bytes instead of zeros.
 template <int MODE, int KTB>
 static int launch_dense_ktb(DenseParams& p, void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (use_narrow(MODE, p.M, p.N, p.kbytes, p.lda, p.ldb, p.batch)) return launch_narrow<MODE>(p, stream);
     p.c16 = (p.ldc % 8 == 0) && (reinterpret_cast<uintptr_t>(p.C) % 16 == 0);
     // batches and bias run unsplit (the split partials and their reduction are per 2-D GEMM)
     const bool plain = p.batch <= 1 && p.bias == nullptr;
@@ -469,7 +661,7 @@ static int check_common(int64_t M, int64_t N, int64_t K, int64_t ldc, const void
 extern "C" {
 
 size_t hkq_gemm_a8w8_workspace(int64_t M, int64_t N, int64_t K) {
-    if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0) return 0;
+    if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0 || use_narrow(MODE_A8W8, M, N, K, K, K, 1)) return 0;
     return dense_plan(M, N, K, true).ws_bytes;
 }
 
@@ -501,7 +693,7 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
 }
 
 size_t hkq_gemm_mxfp4_workspace(int64_t M, int64_t N, int64_t K) {
-    if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return 0;
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0 || use_narrow(MODE_MXFP4, M, N, K / 2, K / 2, K / 2, 1)) return 0;
     return dense_plan(M, N, K / 2, true).ws_bytes;
 }
 

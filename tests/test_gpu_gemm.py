@@ -91,7 +91,7 @@ def test_gemm_a8w8_baseline_sizes_sampled(orc, M, N, K):
 # Smaller-tile and split-K plans: M <= 128 uses (32..128) x 256 tiles, few
 # 256 x 256 tiles become 128 x 128 tiles, and if those are still few (with a
 # long enough K) K is split into fp32 partials added by a second kernel.
-SPLIT_SHAPES = [(1, 4096, 14336), (16, 2048, 4096), (48, 1024, 2048), (128, 4096, 4096), (96, 28672, 4096),
+SPLIT_SHAPES = [(1, 4096, 14336), (16, 2048, 4096), (48, 1024, 2048), (128, 4096, 4096), (96, 28672, 4096), (24, 28672, 4096),
                 (1024, 4096, 14336), (640, 1000, 8192), (256, 1024, 8192), (300, 2052, 2048)]
 
 
@@ -116,14 +116,52 @@ def test_gemm_a8w8_split_and_skinny(orc, M, N, K):
 
 
 def test_gemm_workspace_plans():
-    """Shapes that fill the GPU need no workspace; underfilled ones do."""
+    """Shapes that fill the GPU and the narrow (M <= 16) path need no
+    workspace; underfilled tiled shapes do."""
     require_gpu()
     L = hkq.lib()
     assert L.hkq_gemm_a8w8_workspace(4096, 14336, 4096) == 0
-    assert L.hkq_gemm_a8w8_workspace(16, 4096, 14336) > 0
+    assert L.hkq_gemm_a8w8_workspace(16, 4096, 14336) == 0
+    assert L.hkq_gemm_a8w8_workspace(64, 4096, 14336) > 0
     assert L.hkq_gemm_a8w8_workspace(256, 1024, 8192) > 0
     assert L.hkq_gemm_mxfp4_workspace(4096, 8192, 8192) == 0
-    assert L.hkq_gemm_mxfp4_workspace(16, 8192, 8192) > 0
+    assert L.hkq_gemm_mxfp4_workspace(16, 8192, 8192) == 0
+    assert L.hkq_gemm_mxfp4_workspace(64, 8192, 8192) > 0
+
+
+# Narrow path (M <= 16, and M <= 32 with few columns and a short K): one
+# workgroup per 16 * NT columns, K split over its 4 waves (S = K/128 steps,
+# S < 4 leaves waves idle), NT = 1, 2 or 4 by the number of workgroups,
+# ragged N (rows past N read as zeros), ragged M.
+NARROW_SHAPES = [(1, 16, 128), (1, 64, 640), (5, 1000, 4096), (16, 4096, 4096), (13, 6144, 256), (16, 28672, 512),
+                 (32, 4096, 4096), (20, 6000, 1024), (3, 200, 384)]
+
+
+@pytest.mark.parametrize("M,N,K", NARROW_SHAPES)
+def test_gemm_a8w8_narrow(orc, M, N, K):
+    require_gpu()
+    A, B, sa, sb = a8w8_inputs(orc, M, N, K, seed=11 * M + N + K)
+    C = run_a8w8(A, B, sa, sb)
+    assert_gemm_close(C, orc.gemm_a8w8_ref(A, B, sa, sb), f"a8w8 narrow {M}x{N}x{K}")
+
+
+def test_gemm_a8w8_narrow_strided(orc):
+    """Narrow path with lda/ldb/ldc past K/N: bytes outside C untouched."""
+    require_gpu()
+    M, N, K = 7, 40, 512
+    A, B, sa, sb = a8w8_inputs(orc, M, N, K, seed=78)
+    Ad = torch.zeros((M, K + 256), dtype=torch.uint8, device="cuda")
+    Bd = torch.zeros((N, K + 48), dtype=torch.uint8, device="cuda")
+    Ad[:, :K] = dev_u8(A)
+    Bd[:, :K] = dev_u8(B)
+    Cd = torch.full((M, N + 20), 5.0, dtype=torch.bfloat16, device="cuda")
+    sad, sbd = dev_f32(sa), dev_f32(sb)
+    hkq.call("hkq_gemm_a8w8", Ad.data_ptr(), Bd.data_ptr(), sad.data_ptr(), sbd.data_ptr(),
+             Cd.data_ptr(), M, N, K, K + 256, K + 48, N + 20, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    C = host_bf16_f32(Cd)
+    assert_gemm_close(C[:, :N], orc.gemm_a8w8_ref(A, B, sa, sb), "narrow strided")
+    assert np.all(C[:, N:] == 5.0)
 
 
 def mx_inputs(orc, M, N, K, seed):
@@ -141,7 +179,8 @@ def run_mxfp4(Aq, As, Bq, Bs):
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 256, 128), (256, 256, 256), (1, 256, 512), (128, 512, 8192), (77, 300, 768),
-                                   (600, 1028, 1536), (260, 264, 384)])
+                                   (600, 1028, 1536), (260, 264, 384), (7, 1000, 256), (16, 8192, 1024), (32, 2048, 4096),
+                                   (2, 48, 128)])
 def test_gemm_mxfp4(orc, M, N, K):
     require_gpu()
     Aq, As, Bq, Bs = mx_inputs(orc, M, N, K, seed=M * 7 + K)
