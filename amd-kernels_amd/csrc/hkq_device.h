@@ -52,18 +52,26 @@ __device__ __forceinline__ uint32_t cvt_pk_e4m3(float a, float b) {
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
 }
 
+// Four values -> four E4M3FN codes, value j in byte j: the second pair is
+// converted into the high half of the first pair's result (word select), so no
+// shift or mask is needed.
+__device__ __forceinline__ uint32_t cvt_pk4_e4m3(float a, float b, float c, float d) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false), true);
+}
+
 // Eight values (already multiplied by the block's 2^-e) -> eight E2M1 codes,
 // value j in nibble j. The rule: round to nearest even on the grid
 // {0, .5, 1, 1.5, 2, 3, 4, 6}, saturating at 6, sign from the sign bit, NaN ->
 // +6 (code 0x7). v_cvt_scalef32_pk_fp4_f32 with scale 1.0 implements it except
 // for NaN, whose sign it keeps (checked on the GPU against a compare-based
-// encoder over every tie +-3 ulp and 2^20 random values), so NaN is mapped to
-// +6 first.
+// encoder over every tie +-3 ulp and 2^20 random values), so values go through
+// min(v, 6) first: NaN becomes +6 (the minimum of a NaN and a number is the
+// number), and values above 6 saturate to the same code either way.
 __device__ __forceinline__ uint32_t e2m1_encode8(const float* v) {
     uint32_t w = 0;
     float a[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) a[j] = v[j] != v[j] ? 6.0f : v[j];
+    for (int j = 0; j < 8; ++j) a[j] = min_num(v[j], 6.0f);
     w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a[0], a[1], 1.0f, 0);
     w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a[2], a[3], 1.0f, 1);
     w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a[4], a[5], 1.0f, 2);

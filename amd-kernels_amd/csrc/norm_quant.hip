@@ -95,8 +95,8 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
             float v[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] = max_num(min_num(y[j] * rc, 448.0f), -448.0f);
-            const uint32_t lo = cvt_pk_e4m3(v[0], v[1]) | (cvt_pk_e4m3(v[2], v[3]) << 16);
-            const uint32_t hi = cvt_pk_e4m3(v[4], v[5]) | (cvt_pk_e4m3(v[6], v[7]) << 16);
+            const uint32_t lo = cvt_pk4_e4m3(v[0], v[1], v[2], v[3]);
+            const uint32_t hi = cvt_pk4_e4m3(v[4], v[5], v[6], v[7]);
             if (c < nch) {
                 *reinterpret_cast<uint2*>(q + (int64_t)row * ldq + (int64_t)c * 8) = make_uint2(lo, hi);
                 if ((lane & 15) == 0) reinterpret_cast<float*>(s)[(int64_t)row * lds + (c >> 4)] = sc;
@@ -194,8 +194,8 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
         float v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = max_num(min_num(act[i][j] * rc, 448.0f), -448.0f);
-        const uint32_t lo = cvt_pk_e4m3(v[0], v[1]) | (cvt_pk_e4m3(v[2], v[3]) << 16);
-        const uint32_t hi = cvt_pk_e4m3(v[4], v[5]) | (cvt_pk_e4m3(v[6], v[7]) << 16);
+        const uint32_t lo = cvt_pk4_e4m3(v[0], v[1], v[2], v[3]);
+        const uint32_t hi = cvt_pk4_e4m3(v[4], v[5], v[6], v[7]);
         if (c < nch) {
             *reinterpret_cast<uint2*>(q + (int64_t)row * ldq + (int64_t)c * 8) = make_uint2(lo, hi);
             if (GROUP == 128 && (t & 15) == 0) s[(int64_t)row * lds + (c >> 4)] = sc;

@@ -33,7 +33,7 @@ __device__ __forceinline__ uint32_t encode4(float a, float b, float c, float d, 
     if (KIND == KIND_FP8) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = max_num(min_num(v[i], qmax), -qmax);
-        return cvt_pk_e4m3(v[0], v[1]) | (cvt_pk_e4m3(v[2], v[3]) << 16);
+        return cvt_pk4_e4m3(v[0], v[1], v[2], v[3]);
     } else {
         uint32_t out = 0;
 #pragma unroll
@@ -144,8 +144,8 @@ __global__ __launch_bounds__(256) void static_fp8_kernel(const uint16_t* __restr
             f[2 * j + 1] = max_num(-448.0f, min_num(448.0f, bf16_to_f32(w[j] >> 16) / sc));
         }
         uint2 o;
-        o.x = cvt_pk_e4m3(f[0], f[1]) | (cvt_pk_e4m3(f[2], f[3]) << 16);
-        o.y = cvt_pk_e4m3(f[4], f[5]) | (cvt_pk_e4m3(f[6], f[7]) << 16);
+        o.x = cvt_pk4_e4m3(f[0], f[1], f[2], f[3]);
+        o.y = cvt_pk4_e4m3(f[4], f[5], f[6], f[7]);
         reinterpret_cast<uint2*>(y)[i] = o;
     }
 }
@@ -195,8 +195,8 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(const uint16_t* __restric
             }
             if (ok) {
                 uint2 o;
-                o.x = cvt_pk_e4m3(f[0], f[1]) | (cvt_pk_e4m3(f[2], f[3]) << 16);
-                o.y = cvt_pk_e4m3(f[4], f[5]) | (cvt_pk_e4m3(f[6], f[7]) << 16);
+                o.x = cvt_pk4_e4m3(f[0], f[1], f[2], f[3]);
+                o.y = cvt_pk4_e4m3(f[4], f[5], f[6], f[7]);
                 reinterpret_cast<uint2*>(q + row * K)[col] = o;
                 if ((threadIdx.x & 3) == 0) s[row * (K >> 5) + (col >> 2)] = (uint8_t)code;
             }
