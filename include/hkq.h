@@ -120,8 +120,9 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
  * Shapes whose tiles would fill at most half of the CUs (256 x 256 tiles
  * become 128 x 128, or (32 or 64) x 256 for M <= 64, first) split K over
  * several workgroups and add the fp32 partials in a second kernel; that needs
- * hkq_gemm_a8w8_workspace(M, N, K) bytes (0: no split for this shape). With a smaller workspace (or NULL) the
- * call runs unsplit. Same results either way up to fp32 summation order. The
+ * hkq_gemm_a8w8_workspace(M, N, K) bytes (0: no split for this shape; M <= 16
+ * runs a single-launch streaming kernel that needs none). With a smaller
+ * workspace (or NULL) the call runs unsplit. Same results either way up to fp32 summation order. The
  * workspace is in use until the work queued on `stream` completes. No
  * counterpart in the reference, whose kernels have no split path; the drop-in
  * modules (gemm_a8w8_tk, gemm_a8w8_per_token_scale_tk) call it with a
