@@ -245,6 +245,155 @@ __global__ __launch_bounds__(256, 1) void blockscale_gemm_kernel(const BlockScal
     }
 }
 
+// ---------------------------------------------------------------------------
+// Narrow M (M <= 64): the streaming layout of the dense GEMMs' narrow path
+// (workgroup = 16*NT columns for all rows, 4 waves splitting K, fragments
+// loaded straight into registers for the 16x16x128 MFMA; lane l supplies row
+// l % 16, bytes [16q, 16q+16) and [64+16q, 64+16q+16) of the step, q = l/16,
+// and holds D[4q + i][l % 16]). A 128-value K-step is exactly one scale
+// group, so each step's MFMA starts from zero and is promoted at once:
+// acc += P * sa[m, g] * sb[g, n / GN]. Rows come in MT tiles of 16. The
+// 256 x 256 tiles of the main kernel would give M <= 64 only N/256
+// workgroups.
+constexpr int BSN_WAVES = 4, BSN_MAX_M = 64;
+
+template <bool GN1, int MT, int NT>
+struct BsNarrowFrag {
+    v4i b0[NT], b1[NT], a0[MT], a1[MT];
+    float sa[MT];                // sa[m, g] of the lane's rows
+    float sb[NT][GN1 ? 4 : 1];   // sb[g, n] of the lane's 4 columns (GN 1) or of the tile's column block
+};
+
+template <bool GN1, int MT, int NT>
+__global__ __launch_bounds__(64 * BSN_WAVES) void blockscale_narrow_kernel(const BlockScaleParams p) {
+    constexpr int DEPTH = MT * NT == 1 ? 6 : 4;
+    __shared__ v4f red[BSN_WAVES][NT][MT][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * 16 * NT;
+    const int S = p.K / 128;
+    const int s0 = wave * S / BSN_WAVES, s1 = (wave + 1) * S / BSN_WAVES;
+    const int rows_b = min(16 * NT, p.N - n0);
+    const auto rb = make_rsrc(p.B + (int64_t)n0 * p.ldb, (uint32_t)(rows_b * p.ldb));
+    const auto ra = make_rsrc(p.A, (uint32_t)(p.M * p.lda));
+    // scales: rows of sa past M and groups past S read zero
+    const auto rsa = make_rsrc(p.sa, (uint32_t)(((int64_t)(p.M - 1) * p.lsa + S) * 4));
+    const auto rsb = make_rsrc(p.sb, (uint32_t)(((int64_t)(S - 1) * p.lsb + (GN1 ? p.N : (p.N + 127) / 128)) * 4));
+    uint32_t a_off[MT], sa_row[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        a_off[t] = (uint32_t)((t * 16 + r) * p.lda + 16 * q);
+        sa_row[t] = t * 16 + r < p.M ? (uint32_t)((t * 16 + r) * p.lsa) * 4 : OOB;
+    }
+    uint32_t b_off[NT], sb_col[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        b_off[i] = (uint32_t)((i * 16 + r) * p.ldb + 16 * q);
+        sb_col[i] = (uint32_t)(GN1 ? n0 + 16 * i + 4 * q : (n0 + 16 * i) / 128) * 4;
+    }
+
+    auto load = [&](int s, BsNarrowFrag<GN1, MT, NT>& f) {
+        const uint32_t kill = s < s1 ? 0u : OOB;
+        const uint32_t kb = (uint32_t)s * 128 | kill;
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            f.b0[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[i] + kb, 0, 0);
+            f.b1[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[i] + kb + 64, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            f.a0[t] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t] + kb, 0, 0);
+            f.a1[t] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t] + kb + 64, 0, 0);
+            f.sa[t] = __builtin_bit_cast(float,
+                                         __builtin_amdgcn_raw_buffer_load_b32(rsa, (sa_row[t] + 4 * (uint32_t)s) | kill, 0, 0));
+        }
+        const uint32_t srow = ((uint32_t)s * (uint32_t)p.lsb * 4) | kill;
+#pragma unroll
+        for (int i = 0; i < NT; ++i)
+#pragma unroll
+            for (int e = 0; e < (GN1 ? 4 : 1); ++e)
+                f.sb[i][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsb, srow + sb_col[i] + 4 * e, 0, 0));
+    };
+    v4f acc[NT][MT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[i][t] = v4f{0.f, 0.f, 0.f, 0.f};
+    auto mma = [&](const BsNarrowFrag<GN1, MT, NT>& f) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const v8i b = v8i{f.a0[t][0], f.a0[t][1], f.a0[t][2], f.a0[t][3], f.a1[t][0], f.a1[t][1], f.a1[t][2], f.a1[t][3]};
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                const v8i a = v8i{f.b0[i][0], f.b0[i][1], f.b0[i][2], f.b0[i][3],
+                                  f.b1[i][0], f.b1[i][1], f.b1[i][2], f.b1[i][3]};
+                const v4f P =
+                    __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[i][t][e] = __builtin_fmaf(P[e], f.sa[t] * f.sb[i][GN1 ? e : 0], acc[i][t][e]);
+            }
+        }
+    };
+    BsNarrowFrag<GN1, MT, NT> f[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load(s0 + d, f[d]);
+    for (int s = s0; s < s1; s += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            mma(f[d]);
+            load(s + d + DEPTH, f[d]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) red[wave][i][t][lane] = acc[i][t];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int n = n0 + 16 * i + 4 * q, m = t * 16 + r;
+        if (n >= p.N || m >= p.M) continue;  // N % 4 == 0: n .. n+3 all in or all out
+        v4f v = red[0][i][t][lane];
+#pragma unroll
+        for (int w = 1; w < BSN_WAVES; ++w) v += red[w][i][t][lane];
+        if (p.ca) {
+            const uint2 x = *reinterpret_cast<const uint2*>(p.ca + (int64_t)m * p.ldca + n);
+            const uint2 y = *reinterpret_cast<const uint2*>(p.cb + (int64_t)m * p.ldcb + n);
+            v = v4f{bf16_to_f32(x.x & 0xFFFF) * v[0] + bf16_to_f32(y.x & 0xFFFF),
+                    bf16_to_f32(x.x >> 16) * v[1] + bf16_to_f32(y.x >> 16),
+                    bf16_to_f32(x.y & 0xFFFF) * v[2] + bf16_to_f32(y.y & 0xFFFF),
+                    bf16_to_f32(x.y >> 16) * v[3] + bf16_to_f32(y.y >> 16)};
+        }
+        *reinterpret_cast<v2i*>(p.C + (int64_t)m * p.ldc + n) = v2i{(int)pk_bf16(v[0], v[1]), (int)pk_bf16(v[2], v[3])};
+    }
+}
+
+// M <= 64 in MT = 1, 2 or 4 row tiles, with 16-column (NT = 1) or 32-column
+// (NT = 2, when N/16 workgroups exceed the CUs) slices; 32 weight rows and 64
+// activation rows must span less than 2 GiB (32-bit buffer offsets).
+template <bool GN1, int MT>
+static int launch_blockscale_narrow_mt(const BlockScaleParams& p, hipStream_t stream) {
+    const int64_t ncu = cu_count() > 0 ? cu_count() : 256;
+    const int64_t wgs16 = (p.N + 15) / 16;
+    if (wgs16 > ncu)
+        blockscale_narrow_kernel<GN1, MT, 2><<<dim3((unsigned)((p.N + 31) / 32)), 64 * BSN_WAVES, 0, stream>>>(p);
+    else
+        blockscale_narrow_kernel<GN1, MT, 1><<<dim3((unsigned)wgs16), 64 * BSN_WAVES, 0, stream>>>(p);
+    return hkq_launch_status();
+}
+
+template <bool GN1>
+static int launch_blockscale_narrow(const BlockScaleParams& p, hipStream_t stream) {
+    if (p.M <= 16) return launch_blockscale_narrow_mt<GN1, 1>(p, stream);
+    if (p.M <= 32) return launch_blockscale_narrow_mt<GN1, 2>(p, stream);
+    return launch_blockscale_narrow_mt<GN1, 4>(p, stream);
+}
+
 template <bool GN1>
 static int launch_blockscale(BlockScaleParams& p, hipStream_t stream) {
     constexpr int BM = 256, BN = 256;
@@ -329,5 +478,9 @@ static int blockscale_call(const void* A, const void* B, const float* sa, const 
     p.ca = static_cast<const uint16_t*>(ca);
     p.cb = static_cast<const uint16_t*>(cb);
     p.ldca = ldca; p.ldcb = ldcb;
+    if (M == 0 || N == 0) return 0;
+    if (M <= BSN_MAX_M && 32 * ldb < (1ll << 31) && BSN_MAX_M * lda < (1ll << 31) && (int64_t)M * lsa < (1ll << 28) &&
+        (K / 128) * lsb < (1ll << 28))
+        return group_n == 1 ? launch_blockscale_narrow<true>(p, stream) : launch_blockscale_narrow<false>(p, stream);
     return group_n == 1 ? launch_blockscale<true>(p, stream) : launch_blockscale<false>(p, stream);
 }

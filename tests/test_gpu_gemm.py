@@ -241,9 +241,13 @@ def run_blockscale(A, B, sa, sb, group_n):
     return host_bf16_f32(C)
 
 
+# (1, 256, 1024) and M <= 64 below run the narrow block-scale kernel: 16-row
+# tiles (MT = 1, 2, 4), 16- or 32-column slices (N/16 > CUs), one K group
+# (S = 1 < 4 waves), ragged N.
 @pytest.mark.parametrize("group_n", [128, 1])
 @pytest.mark.parametrize("M,N,K", [(128, 128, 256), (256, 256, 128), (333, 516, 384), (1, 256, 1024),
-                                   (600, 772, 2048)])
+                                   (600, 772, 2048), (5, 1000, 512), (16, 4160, 1536), (20, 136, 128),
+                                   (33, 300, 384), (64, 516, 640)])
 def test_gemm_blockscale(orc, M, N, K, group_n):
     require_gpu()
     A, B, sa, sb = blockscale_inputs(orc, M, N, K, M + N + K, group_n)
