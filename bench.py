@@ -195,8 +195,19 @@ def main():
             ms_b = time_launches(lambda: hkq.gemm_blockscale(qa_b, qw_b, sa_b, sb_b, Cb, 128), steps, warmup)
             bs_res.append({"M": bm, "N": bn, "K": bk, "ms": round(ms_b, 5),
                            "tflops": round(2.0 * bm * bn * bk / (ms_b * 1e-3) / 1e12, 2)})
+            # decode-size rows on the same weights (the narrow path): HBM-bound, GB/s of weights + activations
+            for dm in (1, 16):
+                qa_d, sa_d = qa_b[:dm].contiguous(), sa_b[:dm].contiguous()
+                Cd = torch.empty((dm, bn), dtype=torch.bfloat16, device="cuda")
+                launch = hkq.bind("hkq_gemm_blockscale", qa_d.data_ptr(), qw_b.data_ptr(), sa_d.data_ptr(),
+                                  sb_b.data_ptr(), Cd.data_ptr(), dm, bn, bk, bk, bk, sa_d.stride(0), sb_b.stride(0), bn,
+                                  128, torch.cuda.current_stream().cuda_stream)
+                ms_d = time_launches(launch, steps, warmup, preheat=0.05)
+                byts = dm * bk + bn * bk + 4 * (dm + bn // 128) * (bk // 128) + 2 * dm * bn
+                bs_res.append({"M": dm, "N": bn, "K": bk, "us": round(ms_d * 1e3, 2),
+                               "GB/s": round(byts / (ms_d * 1e-3) / 1e9, 1)})
             del xa, xw, qa_b, qw_b
-        res["blockscale"] = sum(r["ms"] for r in bs_res)
+        res["blockscale"] = sum(r.get("ms", 0.0) for r in bs_res)
 
     # ---- A8W8 MoE grouped GEMM, Mixtral-8x7B (E=8, top-2, 4096 tokens, 4096 -> 14336 gate/up, down) ----
     moe_res, routing_res, fused_res = [], [], []
@@ -420,7 +431,7 @@ def main():
         log(json.dumps({k: round(v * 1e3, 2) for k, v in res.items()}) + "  (us per launch)")
         for r in routing_res:
             log(json.dumps({"routing": r}))
-        for r in moe_res + fused_res + ext_res:
+        for r in bs_res + moe_res + fused_res + ext_res:
             log(json.dumps(r))
         if sweep:
             for r in sweep:
