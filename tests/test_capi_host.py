@@ -63,6 +63,21 @@ def test_argument_errors_are_reported_before_launch():
     assert "multiple of 128" in hkq.lib().hkq_last_error().decode()
 
 
+def test_gemm_workspace_queries():
+    """Host-side GEMM plans (no GPU needed): the narrow path (M <= 16, and
+    M <= 32 on narrow short shapes) and full grids need no workspace; split-K
+    plans of the tiled path do (sizes for 256 CUs when no GPU is visible)."""
+    L = hkq.lib()
+    assert L.hkq_gemm_a8w8_workspace(1, 4096, 4096) == 0
+    assert L.hkq_gemm_a8w8_workspace(16, 4096, 14336) == 0
+    assert L.hkq_gemm_a8w8_workspace(32, 4096, 4096) == 0
+    assert L.hkq_gemm_a8w8_workspace(4096, 14336, 4096) == 0
+    assert L.hkq_gemm_a8w8_workspace(32, 28672, 4096) > 0   # wide N: tiled skinny path, split K
+    assert L.hkq_gemm_a8w8_workspace(64, 4096, 14336) > 0
+    assert L.hkq_gemm_mxfp4_workspace(16, 8192, 8192) == 0
+    assert L.hkq_gemm_mxfp4_workspace(64, 8192, 8192) > 0
+
+
 def test_hipkittens_discovery_and_errors():
     import hipkittens as hk
 
