@@ -215,7 +215,8 @@ __global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_g
 
 // ---------------------------------------------------------------------------
 // Smaller tiles and split K. A grid of 256 x 256 tiles that would fill at most
-// half of the CUs runs on 128 x 128 tiles (4 waves of 64 x 64), and M <= 64
+// half of the CUs runs on 128 x 128 tiles (4 waves of 64 x 64; FP8 with
+// M <= 128 and K <= 8192: 128 x 64 tiles, 4 waves of 32 x 64), and M <= 64
 // on one row of (32 or 64) x 256 tiles (4 waves side by side); if that still
 // fills at most half of the CUs, K is split as well: workgroup u computes tile
 // u % tiles over K-tiles [s * kt_split, (s+1) * kt_split), s = u / tiles, and
@@ -477,7 +478,7 @@ static int set_lds(K kern, int lds, bool& done) {
 // Plan of a dense GEMM: the tile geometry, how many K splits, and the
 // workspace the splits need (bytes). The same function answers the workspace
 // query, so a caller's workspace always matches the launch.
-enum DenseGeo { GEO_256 = 0, GEO_128 = 1, GEO_SKINNY = 2 };
+enum DenseGeo { GEO_256 = 0, GEO_128 = 1, GEO_SKINNY = 2, GEO_128x64 = 3 };
 struct DensePlan {
     int geo;
     int skinny_tm;  // GEO_SKINNY: TM = 1 or 2
@@ -486,7 +487,7 @@ struct DensePlan {
     size_t ws_bytes;
 };
 
-static DensePlan dense_plan(int64_t M, int64_t N, int64_t kbytes, bool allow_split, int64_t batch = 1) {
+static DensePlan dense_plan(int mode, int64_t M, int64_t N, int64_t kbytes, bool allow_split, int64_t batch = 1) {
     DensePlan pl{};
     const int ktb = kbytes % 128 == 0 ? 128 : 64;
     const int64_t KT = kbytes / ktb;
@@ -503,6 +504,13 @@ static DensePlan dense_plan(int64_t M, int64_t N, int64_t kbytes, bool allow_spl
     } else if (ktb == 128 && 2 * ntiles(DENSE_BM, DENSE_BN) <= ncu) {
         pl.geo = GEO_128;
         bm = bn = 128;
+        // FP8 with M <= 128 and K <= 8192: 128 x 64 tiles (4 waves of 32 x 64),
+        // twice the workgroups for the same K split (measured faster on the
+        // BASELINE sweep's M = 96 / 128 shapes; not for FP4 or longer K)
+        if (mode == MODE_A8W8 && M <= 128 && KT <= 64) {
+            pl.geo = GEO_128x64;
+            bn = 64;
+        }
     }
     pl.tiles = ntiles(bm, bn);
     pl.splits = 1;
@@ -625,9 +633,9 @@ static int launch_dense_ktb(DenseParams& p, void* ws, size_t ws_bytes, hipStream
     p.c16 = (p.ldc % 8 == 0) && (reinterpret_cast<uintptr_t>(p.C) % 16 == 0);
     // batches and bias run unsplit (the split partials and their reduction are per 2-D GEMM)
     const bool plain = p.batch <= 1 && p.bias == nullptr;
-    DensePlan pl = dense_plan(p.M, p.N, p.kbytes, plain, std::max(1, p.batch));
+    DensePlan pl = dense_plan(MODE, p.M, p.N, p.kbytes, plain, std::max(1, p.batch));
     if (pl.splits > 1 && (ws == nullptr || ws_bytes < pl.ws_bytes))
-        pl = dense_plan(p.M, p.N, p.kbytes, false, std::max(1, p.batch));
+        pl = dense_plan(MODE, p.M, p.N, p.kbytes, false, std::max(1, p.batch));
     p.ws = static_cast<float*>(ws);
     if constexpr (KTB == 128) {  // smaller tiles need a full 16-byte load per lane for their A rows
         if (pl.geo == GEO_SKINNY) {
@@ -635,6 +643,8 @@ static int launch_dense_ktb(DenseParams& p, void* ws, size_t ws_bytes, hipStream
             return launch_dense_tiles<MODE, 1, SKINNY_WAVES_N, 2, SKINNY_TN, KTB, 1>(p, pl, stream);
         }
         if (pl.geo == GEO_128) return launch_dense_tiles<MODE, 2, 2, 2, 2, KTB, 2>(p, pl, stream);
+        if constexpr (MODE == MODE_A8W8)
+            if (pl.geo == GEO_128x64) return launch_dense_tiles<MODE, 4, 1, 1, 2, KTB, 2>(p, pl, stream);
     }
     return launch_dense_whole<MODE, KTB>(p, stream);
 }
@@ -662,7 +672,7 @@ extern "C" {
 
 size_t hkq_gemm_a8w8_workspace(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0 || use_narrow(MODE_A8W8, M, N, K, K, K, 1)) return 0;
-    return dense_plan(M, N, K, true).ws_bytes;
+    return dense_plan(MODE_A8W8, M, N, K, true).ws_bytes;
 }
 
 int hkq_gemm_a8w8_ws(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M, int64_t N,
@@ -694,7 +704,7 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
 
 size_t hkq_gemm_mxfp4_workspace(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0 || use_narrow(MODE_MXFP4, M, N, K / 2, K / 2, K / 2, 1)) return 0;
-    return dense_plan(M, N, K / 2, true).ws_bytes;
+    return dense_plan(MODE_MXFP4, M, N, K / 2, true).ws_bytes;
 }
 
 int hkq_gemm_mxfp4_ws(const void* A, const void* As, const void* B, const void* Bs, void* C, int64_t M, int64_t N,
@@ -764,7 +774,7 @@ int hkq_batched_gemm_a8w8(const void* A, const void* B, const float* sa, const f
 
 size_t hkq_gemm_bf16_workspace(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 32 != 0) return 0;
-    return dense_plan(M, N, 2 * K, true).ws_bytes;
+    return dense_plan(MODE_BF16, M, N, 2 * K, true).ws_bytes;
 }
 
 int hkq_batched_gemm_bf16(const void* A, const void* B, const void* bias, void* C, int64_t batch, int64_t M, int64_t N,

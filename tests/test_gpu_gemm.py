@@ -88,11 +88,13 @@ def test_gemm_a8w8_baseline_sizes_sampled(orc, M, N, K):
     assert np.isfinite(C).all()
 
 
-# Smaller-tile and split-K plans: M <= 128 uses (32..128) x 256 tiles, few
-# 256 x 256 tiles become 128 x 128 tiles, and if those are still few (with a
-# long enough K) K is split into fp32 partials added by a second kernel.
+# Smaller-tile and split-K plans: M <= 64 uses (32 or 64) x 256 tiles, few
+# 256 x 256 tiles become 128 x 128 tiles (128 x 64 for FP8 with M <= 128 and
+# K <= 8192), and if those are still few (with a long enough K) K is split
+# into fp32 partials added by a second kernel.
 SPLIT_SHAPES = [(1, 4096, 14336), (16, 2048, 4096), (48, 1024, 2048), (128, 4096, 4096), (96, 28672, 4096), (24, 28672, 4096),
-                (1024, 4096, 14336), (640, 1000, 8192), (256, 1024, 8192), (300, 2052, 2048)]
+                (1024, 4096, 14336), (640, 1000, 8192), (256, 1024, 8192), (300, 2052, 2048), (100, 1000, 2048),
+                (128, 6144, 4096)]
 
 
 @pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
