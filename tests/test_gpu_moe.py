@@ -65,8 +65,14 @@ def test_moe_reference_setup(orc):
     check_rows(orc, Y, ref)
 
 
+# At most 32 routed rows (or 64 with N <= 4096): the decode (streaming)
+# kernel, with 16 or 64 columns per workgroup (N > 4096), one, two or four
+# 16-row groups, ragged N and K-steps uneven over the 4 waves; (24, 2, 2, 384,
+# 4104) has 48 rows and a wide N, so it takes the tiled kernel.
 @pytest.mark.parametrize("T,E,topk,K,N", [(300, 4, 2, 512, 520), (1, 8, 2, 256, 512), (1000, 8, 2, 1024, 1024),
-                                          (257, 3, 1, 384, 260), (77, 4, 2, 320, 256)])
+                                          (257, 3, 1, 384, 260), (77, 4, 2, 320, 256), (5, 8, 2, 512, 4100),
+                                          (16, 8, 2, 384, 1000), (16, 4, 2, 640, 4200), (30, 8, 2, 256, 520),
+                                          (24, 2, 2, 384, 4104)])
 def test_moe_per_token_per_channel(orc, T, E, topk, K, N):
     require_gpu()
     _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, T + N)
@@ -110,11 +116,28 @@ def test_moe_entry_order_and_pairing(orc):
         check_rows(orc, Y, ref)
 
 
-def test_moe_without_gather(orc):
-    """GatherIndx None: tile rows read X[start + gm] directly (pre-sorted X)."""
+def test_moe_decode_reference_setup(orc):
+    """The reference test's scale and bias layout (per-tensor activation scale,
+    per-expert weight scale, bias) at a decode size (8 tokens, top-2)."""
+    require_gpu()
+    T, E, topk, K, N = 8, 8, 2, 256, 320
+    _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, T, E, topk, K, N, 21)
+    rng = np.random.default_rng(22)
+    xs = np.array([0.01], np.float32)
+    ws = (rng.random(E) * 0.01).astype(np.float32)
+    bias = (rng.standard_normal((E, N)) * 0.1).astype(np.float32)
+    Y = run_moe(X, W, hist, offs, gather, ed, topk, xs, ws, bias)
+    ref = orc.moe_ref(X, W, xs, ws, bias, gather, hist, offs, ed, topk, 128, "enk")
+    check_rows(orc, Y, ref)
+
+
+@pytest.mark.parametrize("hist", [[130, 0, 70, 256], [3, 0, 9, 8]])
+def test_moe_without_gather(orc, hist):
+    """GatherIndx None: tile rows read X[start + gm] directly (pre-sorted X);
+    20 rows in all take the decode kernel."""
     require_gpu()
     E, K, N = 4, 256, 256
-    hist = np.array([130, 0, 70, 256], np.int32)
+    hist = np.array(hist, np.int32)
     offs = np.concatenate([[0], np.cumsum(hist)[:-1]]).astype(np.int32)
     ed = np.array([e | (b << 16) for e in range(E) for b in range((hist[e] + 127) // 128)], np.int32)
     rows = int(hist.sum())
