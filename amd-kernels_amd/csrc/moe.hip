@@ -546,6 +546,132 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_mxfp4_kernel(cons
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode-size MXFP4 MoE (at most 32 valid gate ids): the streaming layout of
+// the narrow GEMM. Workgroup u takes block u / slices and the 16*NT columns of
+// slice u % slices; for every 16-entry group of the block that holds a valid
+// gate id (with the sorted layout that is the first one or two groups) its 4
+// waves stream K through the 16x16x128 MFMA with per-lane e8m0 scales (lane l:
+// entry l % 16 of the group, bytes [16q, 16q+16) of a 64-byte K-step and the
+// scale byte q of the step's 4 blocks, q = l/16). Blocks of expert -1 write
+// zeros to their valid rows, as the tiled kernel does.
+constexpr int MOE_FP4_NARROW_MAX_VALID = 32;
+
+template <int NT>
+__global__ __launch_bounds__(64 * MOE_NARROW_WAVES) void moe_fp4_narrow_kernel(const MoeFp4Params p, int slices) {
+    constexpr int DEPTH = NT >= 4 ? 4 : 8;
+    __shared__ v4f red[MOE_NARROW_WAVES][NT][64];
+    const int pm = blockIdx.x / slices, n0 = (blockIdx.x % slices) * 16 * NT;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, q = lane >> 4;
+    const int32_t* ids = p.sorted + (int64_t)pm * MOE_BM;
+    const int e = p.expert[pm];
+    if (e < 0 || e >= p.E) {
+        if (e < 0) {  // valid rows of an unassigned block are zeros
+            for (int rr = threadIdx.x; rr < MOE_BM; rr += 64 * MOE_NARROW_WAVES) {
+                const int id = ids[rr];
+                if (id < 0 || id >= p.num_valid) continue;
+                for (int n = n0; n < min(p.N, n0 + 16 * NT); n += 4)
+                    *reinterpret_cast<v2i*>(p.C + (int64_t)id * p.scm + n) = v2i{0, 0};
+            }
+        }
+        return;
+    }
+    const int S = p.K / 128;  // 64-byte K-steps
+    const int s0 = wave * S / MOE_NARROW_WAVES, s1 = (wave + 1) * S / MOE_NARROW_WAVES;
+    const int rows_b = min(16 * NT, p.N - n0);
+    const auto rb = make_rsrc(p.B + (int64_t)e * p.sbe + (int64_t)n0 * p.sbn, (uint32_t)(rows_b * p.sbn));
+    const auto rbs = make_rsrc(p.Bs + (int64_t)e * p.sbse + (int64_t)n0 * p.sbsn, (uint32_t)(rows_b * p.sbsn));
+    const auto ra = make_rsrc(p.A, (uint32_t)((int64_t)p.tokens * p.sam));
+    const auto ras = make_rsrc(p.As, (uint32_t)((int64_t)p.tokens * p.sas));
+    uint32_t b_off[NT], bs_off[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        b_off[i] = (uint32_t)((i * 16 + r) * p.sbn + 16 * q);
+        bs_off[i] = (uint32_t)((i * 16 + r) * p.sbsn);
+    }
+    const float gs = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
+
+    for (int g = 0; g < MOE_BM / 16; ++g) {
+        const int id0 = ids[g * 16 + r];
+        const int id = (id0 >= 0 && id0 < p.num_valid) ? id0 : -1;
+        if (__builtin_amdgcn_ballot_w64(id >= 0) == 0) continue;  // uniform: no valid entry in the group
+        const int tk = id < 0 ? -1 : id / p.topk;
+        const bool live = tk >= 0 && tk < p.tokens;
+        // Offsets stay below 2^32: valid ones are below 2^31, an invalid row's
+        // is OOB itself, and the K part is below 2^31.
+        const uint32_t a_off = live ? (uint32_t)(tk * p.sam + 16 * q) : OOB;
+        const uint32_t as_off = live ? (uint32_t)(tk * p.sas) : OOB;
+        struct Frag {
+            v4i b[NT], a;
+            uint32_t sb[NT], sa;
+        };
+        auto load = [&](int s, Frag& f) {
+            const uint32_t kb = (uint32_t)s * 64, ks = (uint32_t)s * 4, kill = s < s1 ? 0u : OOB;
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                f.b[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, (b_off[i] + kb) | kill, 0, 0);
+                f.sb[i] = __builtin_amdgcn_raw_buffer_load_b32(rbs, (bs_off[i] + ks) | kill, 0, 0);
+            }
+            f.a = __builtin_amdgcn_raw_buffer_load_b128(ra, (a_off + kb) | kill, 0, 0);
+            f.sa = __builtin_amdgcn_raw_buffer_load_b32(ras, (as_off + ks) | kill, 0, 0);
+        };
+        v4f acc[NT];
+#pragma unroll
+        for (int i = 0; i < NT; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+        auto mma = [&](const Frag& f) {
+            const v8i bb = v8i{f.a[0], f.a[1], f.a[2], f.a[3], 0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                const v8i aa = v8i{f.b[i][0], f.b[i][1], f.b[i][2], f.b[i][3], 0, 0, 0, 0};
+                acc[i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aa, bb, acc[i], 4, 4, 0, (int)(f.sb[i] >> (8 * q)),
+                                                                          0, (int)(f.sa >> (8 * q)));
+            }
+        };
+        Frag f[DEPTH];
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(s0 + d, f[d]);
+        for (int s = s0; s < s1; s += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                mma(f[d]);
+                load(s + d + DEPTH, f[d]);
+            }
+        }
+        __syncthreads();  // the previous group's sums have been read
+#pragma unroll
+        for (int i = 0; i < NT; ++i) red[wave][i][lane] = acc[i];
+        __syncthreads();
+        if (wave == 0 && id >= 0) {
+            const float rs = p.topk_w ? gs * p.topk_w[id] : gs;
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                const int n = n0 + 16 * i + 4 * q;
+                if (n >= p.N) break;  // N % 4 == 0: n .. n+3 all in or all out
+                v4f v = red[0][i][lane];
+#pragma unroll
+                for (int w = 1; w < MOE_NARROW_WAVES; ++w) v += red[w][i][lane];
+                *reinterpret_cast<v2i*>(p.C + (int64_t)id * p.scm + n) =
+                    v2i{(int)pk_bf16(v[0] * rs, v[1] * rs), (int)pk_bf16(v[2] * rs, v[3] * rs)};
+            }
+        }
+    }
+}
+
+static int launch_moe_fp4_narrow(const MoeFp4Params& p, hipStream_t stream) {
+    if (p.grid_m == 0 || p.N == 0) return 0;
+    const int threads = 64 * MOE_NARROW_WAVES;
+    if (p.N > 4096) {
+        const int slices = (p.N + 63) / 64;
+        moe_fp4_narrow_kernel<4><<<dim3((unsigned)((int64_t)p.grid_m * slices)), threads, 0, stream>>>(p, slices);
+    } else {
+        const int slices = (p.N + 15) / 16;
+        moe_fp4_narrow_kernel<1><<<dim3((unsigned)((int64_t)p.grid_m * slices)), threads, 0, stream>>>(p, slices);
+    }
+    return hkq_launch_status();
+}
+
 template <int KTB, int NS>
 static int launch_moe_fp4(MoeFp4Params& p, hipStream_t stream) {
     using Whole = DenseCfg<MODE_MXFP4, MOE_WM, MOE_WN, 4, MOE_TN, KTB>;
@@ -682,6 +808,12 @@ extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* 
     p.sam = stride_am; p.sas = stride_amxm; p.sbe = stride_be; p.sbn = stride_bn; p.sbse = stride_bmxe;
     p.sbsn = stride_bmxn; p.scm = stride_cm;
     p.c16 = (stride_cm % 8 == 0) && (reinterpret_cast<uintptr_t>(C) % 16 == 0);
+    // Decode sizes (at most 32 valid gate ids) take the streaming path; its
+    // scale loads are dwords, and 64 weight rows must span less than 2 GiB.
+    if (num_valid_tokens <= MOE_FP4_NARROW_MAX_VALID && stride_amxm % 4 == 0 && stride_bmxn % 4 == 0 &&
+        stride_bmxe % 4 == 0 && reinterpret_cast<uintptr_t>(A_mx_scale) % 4 == 0 &&
+        reinterpret_cast<uintptr_t>(B_mx_scale) % 4 == 0 && 64 * stride_bn < (1ll << 31) && 64 * stride_bmxn < (1ll << 31))
+        return launch_moe_fp4_narrow(p, stream);
     // 128-byte K-tiles when rows have whole ones (K % 256 == 0), else 64-byte ones
     return (K / 2) % 128 == 0 ? launch_moe_fp4<128, 2>(p, stream) : launch_moe_fp4<64, 4>(p, stream);
 }

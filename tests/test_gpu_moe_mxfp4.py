@@ -30,8 +30,12 @@ def problem(orc, T, E, K, N, seed):
     return Aq, As, Bq.reshape(E, N, K // 2), Bs.reshape(E, N, K // 32)
 
 
+# (1, ...), (5, ...) and (16, ...) have at most 32 valid gate ids: the decode
+# (streaming) kernel, with 16 or 64 (N > 4096) columns per workgroup and
+# K-steps uneven over its 4 waves.
 @pytest.mark.parametrize("T,E,topk,K,N", [(64, 8, 2, 256, 256), (1024, 8, 2, 2048, 1024), (300, 4, 1, 384, 520),
-                                          (77, 16, 4, 512, 64)])
+                                          (77, 16, 4, 512, 64), (1, 8, 2, 256, 512), (5, 8, 2, 384, 4160),
+                                          (16, 8, 2, 640, 1000)])
 def test_moe_mxfp4(orc, T, E, topk, K, N):
     require_gpu()
     Aq, As, Bq, Bs = problem(orc, T, E, K, N, T + K)
@@ -85,6 +89,29 @@ def test_moe_mxfp4_gpu_routing_and_special_blocks(orc):
     assert np.all(got[dropped] == 7.0) and np.all(got[~written] == 7.0)
     blk1 = s_h[128:256][s_h[128:256] < T * topk]
     assert len(blk1) and np.all(got[blk1] == 0.0)
+
+
+def test_moe_mxfp4_decode_layouts(orc):
+    """Decode kernel on hand-made blocks: a valid id past the first 16 entries
+    of its block (a later 16-entry group), a block of expert -1 (zeros for its
+    valid rows) and rows no block names (left untouched)."""
+    require_gpu()
+    T, E, topk, K, N = 4, 2, 2, 256, 96
+    Aq, As, Bq, Bs = problem(orc, T, E, K, N, 41)
+    nv = T * topk
+    s = np.full(3 * 128, nv, np.int32)
+    s[[0, 1, 2, 37]] = [0, 1, 2, 3]          # block 0, expert 0: entry 37 is in group 2
+    s[[128, 129]] = [4, 5]                   # block 1, expert -1: zeros
+    s[[256, 300]] = [6, 7]                   # block 2, expert 1
+    eids = np.array([0, -1, 1], np.int32)
+    C = torch.full((nv + 2, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    hkq.moe_mxfp4(dev_u8(Aq), dev_u8(As), dev_u8(Bq), dev_u8(Bs), dev_i32(s), dev_i32(eids), nv, topk, C=C)
+    torch.cuda.synchronize()
+    ref = orc.moe_mxfp4_ref(Aq, As, Bq, Bs, None, None, None, s, eids, N, nv, topk, False, nv)
+    got = C.float().cpu().numpy()
+    rows = [0, 1, 2, 3, 6, 7]
+    assert_gemm_close(got[rows], ref[rows], "moe mxfp4 decode layouts")
+    assert np.all(got[[4, 5]] == 0.0) and np.all(got[nv:] == 7.0)
 
 
 def test_moe_mxfp4_module_reference_call(orc):
