@@ -265,6 +265,28 @@ def main():
                           "pct_hbm_peak": round(100 * sw_bytes / (ms_sw * 1e-3) / 1e9 / PEAK_HBM_GBS, 1)})
         layer_ms = ms_r + sum(r["ms"] for r in moe_res) + ms_sw
         moe_res.append({"proj": "layer (routing + gate_up + swiglu/quant + down)", "ms": round(layer_ms, 5)})
+        # decode sizes (the streaming MoE kernel): HBM-bound, GB/s of the active experts' weights
+        for td in (1, 8):
+            rtd, route_d = hkq.moe_routing_plan(logits[:td].contiguous(), topk, 128)
+            route_d()
+            hd = rtd["hist"]
+            qd, sd = qx[:td].contiguous(), sx[:td].contiguous()
+            q2d = q2[: td * topk].contiguous()
+            s2d = s2[: td * topk].contiguous()
+            Y1d = torch.empty((td * topk, 2 * ffn), dtype=torch.bfloat16, device="cuda")
+            Y2d = torch.empty((td * topk, hidden), dtype=torch.bfloat16, device="cuda")
+            torch.cuda.synchronize()
+            act = int((hd[:E] > 0).sum().item())
+            for name, nn, kk, fn in (
+                ("gate_up", 2 * ffn, hidden, lambda: hkq.moe_a8w8(qd, w1, hd, rtd["offs"], rtd["expt_data"], topk,
+                                                                  gather=rtd["gather"], x_scale=sd, w_scale=ws1,
+                                                                  Y=Y1d)),
+                ("down", hidden, ffn, lambda: hkq.moe_a8w8(q2d, w2, hd, rtd["offs"], rtd["expt_data"], 1, gather=None,
+                                                           x_scale=s2d, w_scale=ws2, Y=Y2d))):
+                log(f"moe decode T={td} {name}")
+                ms_d = time_launches(fn, steps, warmup, preheat=0.05)
+                moe_res.append({"proj": f"decode {name}", "T": td, "active_experts": act, "N": nn, "K": kk,
+                                "us": round(ms_d * 1e3, 2), "GB/s": round(act * nn * kk / (ms_d * 1e-3) / 1e9, 1)})
         del w1, w2
 
         # MXFP4 experts over the block-sorted routing of the same top-2 choice
