@@ -264,8 +264,26 @@ struct BsNarrowFrag {
     float sb[NT][GN1 ? 4 : 1];   // sb[g, n] of the lane's 4 columns (GN 1) or of the tile's column block
 };
 
+// Rows [64 * blockIdx.y, 64 * blockIdx.y + 64) of the GEMM as a GEMM of their own.
+__device__ __forceinline__ BlockScaleParams bs_row_slice(const BlockScaleParams& pb) {
+    BlockScaleParams p = pb;
+    const int m0 = blockIdx.y * BSN_MAX_M;
+    if (m0 > 0) {
+        p.A += (int64_t)m0 * p.lda;
+        p.sa += (int64_t)m0 * p.lsa;
+        p.C += (int64_t)m0 * p.ldc;
+        if (p.ca) {
+            p.ca += (int64_t)m0 * p.ldca;
+            p.cb += (int64_t)m0 * p.ldcb;
+        }
+        p.M = min(BSN_MAX_M, p.M - m0);
+    }
+    return p;
+}
+
 template <bool GN1, int MT, int NT>
-__global__ __launch_bounds__(64 * BSN_WAVES) void blockscale_narrow_kernel(const BlockScaleParams p) {
+__global__ __launch_bounds__(64 * BSN_WAVES) void blockscale_narrow_kernel(const BlockScaleParams pb) {
+    const BlockScaleParams p = bs_row_slice(pb);
     constexpr int DEPTH = MT * NT == 1 ? 6 : 4;
     __shared__ v4f red[BSN_WAVES][NT][MT][64];
     const int lane = threadIdx.x & 63;
@@ -374,16 +392,18 @@ __global__ __launch_bounds__(64 * BSN_WAVES) void blockscale_narrow_kernel(const
 }
 
 // M <= 64 in MT = 1, 2 or 4 row tiles, with 16-column (NT = 1) or 32-column
-// (NT = 2, when N/16 workgroups exceed the CUs) slices; 32 weight rows and 64
+// (NT = 2, when N/16 workgroups exceed the CUs) slices; larger M in row groups
+// of 64 (grid.y), each streaming the weights again. 32 weight rows and 64
 // activation rows must span less than 2 GiB (32-bit buffer offsets).
 template <bool GN1, int MT>
 static int launch_blockscale_narrow_mt(const BlockScaleParams& p, hipStream_t stream) {
     const int64_t ncu = cu_count() > 0 ? cu_count() : 256;
     const int64_t wgs16 = (p.N + 15) / 16;
+    const unsigned row_groups = (unsigned)((p.M + BSN_MAX_M - 1) / BSN_MAX_M);
     if (wgs16 > ncu)
-        blockscale_narrow_kernel<GN1, MT, 2><<<dim3((unsigned)((p.N + 31) / 32)), 64 * BSN_WAVES, 0, stream>>>(p);
+        blockscale_narrow_kernel<GN1, MT, 2><<<dim3((unsigned)((p.N + 31) / 32), row_groups), 64 * BSN_WAVES, 0, stream>>>(p);
     else
-        blockscale_narrow_kernel<GN1, MT, 1><<<dim3((unsigned)wgs16), 64 * BSN_WAVES, 0, stream>>>(p);
+        blockscale_narrow_kernel<GN1, MT, 1><<<dim3((unsigned)wgs16, row_groups), 64 * BSN_WAVES, 0, stream>>>(p);
     return hkq_launch_status();
 }
 
@@ -479,8 +499,14 @@ static int blockscale_call(const void* A, const void* B, const float* sa, const 
     p.cb = static_cast<const uint16_t*>(cb);
     p.ldca = ldca; p.ldcb = ldcb;
     if (M == 0 || N == 0) return 0;
-    if (M <= BSN_MAX_M && 32 * ldb < (1ll << 31) && BSN_MAX_M * lda < (1ll << 31) && (int64_t)M * lsa < (1ll << 28) &&
-        (K / 128) * lsb < (1ll << 28))
+    // M <= 64; up to 192 rows (row groups of 64) while the 256 x 256 tiles
+    // would give fewer than a quarter of the CUs work (at N = 7168, 28 tiles:
+    // 16x7168x18432 took 321 us tiled, 31 us streamed; 128x7168x18432 325 vs
+    // 140 us; at 256 rows the tiles win for K <= 7168)
+    const int64_t ncu = cu_count() > 0 ? cu_count() : 256;
+    const bool few_tiles = M <= 192 && ((N + 255) / 256) * 4 < ncu;
+    if ((M <= BSN_MAX_M || few_tiles) && 32 * ldb < (1ll << 31) && BSN_MAX_M * lda < (1ll << 31) &&
+        (int64_t)M * lsa < (1ll << 28) && (K / 128) * lsb < (1ll << 28))
         return group_n == 1 ? launch_blockscale_narrow<true>(p, stream) : launch_blockscale_narrow<false>(p, stream);
     return group_n == 1 ? launch_blockscale<true>(p, stream) : launch_blockscale<false>(p, stream);
 }

@@ -245,11 +245,12 @@ def run_blockscale(A, B, sa, sb, group_n):
 
 # (1, 256, 1024) and M <= 64 below run the narrow block-scale kernel: 16-row
 # tiles (MT = 1, 2, 4), 16- or 32-column slices (N/16 > CUs), one K group
-# (S = 1 < 4 waves), ragged N.
+# (S = 1 < 4 waves), ragged N; (100, 1000, 512) and (192, 2112, 1024) run it in
+# row groups of 64 (few 256 x 256 tiles).
 @pytest.mark.parametrize("group_n", [128, 1])
 @pytest.mark.parametrize("M,N,K", [(128, 128, 256), (256, 256, 128), (333, 516, 384), (1, 256, 1024),
                                    (600, 772, 2048), (5, 1000, 512), (16, 4160, 1536), (20, 136, 128),
-                                   (33, 300, 384), (64, 516, 640)])
+                                   (33, 300, 384), (64, 516, 640), (100, 1000, 512), (192, 2112, 1024)])
 def test_gemm_blockscale(orc, M, N, K, group_n):
     require_gpu()
     A, B, sa, sb = blockscale_inputs(orc, M, N, K, M + N + K, group_n)

@@ -213,7 +213,7 @@ def blockscale_operands(orc, M, N, K, seed, group_n):
 
 @pytest.mark.parametrize("group_n", [1, 128])
 @pytest.mark.parametrize("M,N,K", [(256, 256, 256), (333, 516, 384), (1, 256, 1024), (600, 772, 2048), (9, 4160, 256),
-                                   (40, 200, 512)])
+                                   (40, 200, 512), (129, 264, 256)])
 def test_blockscale_mul_add(orc, M, N, K, group_n):
     require_gpu()
     A, B, sa, sb = blockscale_operands(orc, M, N, K, M + N, group_n)
