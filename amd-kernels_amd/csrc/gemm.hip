@@ -581,9 +581,9 @@ static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
 }
 
 // The narrow path serves the FP8 and FP4 GEMMs whose rows hold whole 128-value
-// K-steps: all of M <= 16, and M <= 32 while one round of 16-column
-// workgroups covers N and K is at most 32 steps (every workgroup re-reads
-// the activation rows, which then costs more than the tiled path's
+// K-steps: all of M <= 16, and M <= 32 while the 16-column workgroups number
+// fewer than two per CU and K is at most 32 steps (beyond that, every
+// workgroup re-reading the activation rows costs more than the tiled path's
 // LDS-shared activation tile; measured on MI355X). Its buffer offsets are
 // 32-bit: 16*NT weight rows and 32 activation rows must span less than 2 GiB.
 static bool use_narrow(int mode, int64_t M, int64_t N, int64_t kbytes, int64_t lda, int64_t ldb, int64_t batch) {
