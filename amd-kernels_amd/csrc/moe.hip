@@ -808,9 +808,14 @@ extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* 
     p.sam = stride_am; p.sas = stride_amxm; p.sbe = stride_be; p.sbn = stride_bn; p.sbse = stride_bmxe;
     p.sbsn = stride_bmxn; p.scm = stride_cm;
     p.c16 = (stride_cm % 8 == 0) && (reinterpret_cast<uintptr_t>(C) % 16 == 0);
-    // Decode sizes (at most 32 valid gate ids) take the streaming path; its
-    // scale loads are dwords, and 64 weight rows must span less than 2 GiB.
-    if (num_valid_tokens <= MOE_FP4_NARROW_MAX_VALID && stride_amxm % 4 == 0 && stride_bmxn % 4 == 0 &&
+    // The streaming path when the tiled grid would give fewer than a quarter
+    // of the CUs work and there are at most 32 valid gate ids (measured: one
+    // token's down projection, N = 4096, 56 -> 22 us; with N = 28672 or eight
+    // tokens the tiled kernel is faster). Its scale loads are dwords, and 64
+    // weight rows must span less than 2 GiB.
+    const int64_t ncu = cu_count() > 0 ? cu_count() : 256;
+    const bool few_tiles = ((grid_m + 1) / 2) * ((N + MOE_BN - 1) / MOE_BN) * 4 < ncu;
+    if (few_tiles && num_valid_tokens <= MOE_FP4_NARROW_MAX_VALID && stride_amxm % 4 == 0 && stride_bmxn % 4 == 0 &&
         stride_bmxe % 4 == 0 && reinterpret_cast<uintptr_t>(A_mx_scale) % 4 == 0 &&
         reinterpret_cast<uintptr_t>(B_mx_scale) % 4 == 0 && 64 * stride_bn < (1ll << 31) && 64 * stride_bmxn < (1ll << 31))
         return launch_moe_fp4_narrow(p, stream);

@@ -30,9 +30,9 @@ def problem(orc, T, E, K, N, seed):
     return Aq, As, Bq.reshape(E, N, K // 2), Bs.reshape(E, N, K // 32)
 
 
-# (1, ...), (5, ...) and (16, ...) have at most 32 valid gate ids: the decode
-# (streaming) kernel, with 16 or 64 (N > 4096) columns per workgroup and
-# K-steps uneven over its 4 waves.
+# (1, ...) and (16, ...) have at most 32 valid gate ids and a small tiled grid:
+# the decode (streaming) kernel, with K-steps uneven over its 4 waves;
+# (5, 8, 2, 384, 4160) has few ids but a large tiled grid, so it stays tiled.
 @pytest.mark.parametrize("T,E,topk,K,N", [(64, 8, 2, 256, 256), (1024, 8, 2, 2048, 1024), (300, 4, 1, 384, 520),
                                           (77, 16, 4, 512, 64), (1, 8, 2, 256, 512), (5, 8, 2, 384, 4160),
                                           (16, 8, 2, 640, 1000)])
