@@ -40,7 +40,8 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-HIP_SOURCES = ["quant.hip", "gemm.hip", "gemm_blockscale.hip", "moe.hip", "routing.hip", "norm_quant.hip"]
+HIP_SOURCES = ["quant.hip", "gemm.hip", "gemm_blockscale.hip", "moe.hip", "moe_blockscale.hip", "routing.hip",
+               "norm_quant.hip"]
 CPP_SOURCES = ["hkq_error.cpp"]
 
 # pybind11 module name -> binding source (module names are the reference's)

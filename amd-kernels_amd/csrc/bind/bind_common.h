@@ -107,6 +107,19 @@ inline void check(int rc, const char* what) {
     if (rc != 0) throw std::runtime_error(std::string(what) + ": " + hkq_last_error() + " (code " + std::to_string(rc) + ")");
 }
 
+// The K-contiguous copy [E, N, R] (strides R*N, R, 1) of E byte planes [R, N]
+// (plane e at src + e*src_e, row r at + r*src_r, N contiguous), made on the
+// current stream in a torch temporary that lives as long as the result:
+// how the MoE modules take the reference's N-contiguous weights.
+inline Workspace pack_kmajor(py::object like, uint64_t src, int64_t E, int64_t R, int64_t N, int64_t src_e,
+                             int64_t src_r, const char* what) {
+    Workspace w = workspace((size_t)(E * R * N), like);
+    if (E * R * N > 0 && w.ptr == nullptr)
+        throw py::value_error(std::string(what) + ": N-contiguous weights need torch for the K-major copy");
+    check(hkq_moe_pack_kmajor((const void*)src, w.ptr, E, R, N, src_e, src_r, R * N, R, current_stream()), what);
+    return w;
+}
+
 inline const char* kBF16 = "torch.bfloat16";
 inline const char* kF32 = "torch.float32";
 inline const char* kFP8 = "torch.float8_e4m3fn";

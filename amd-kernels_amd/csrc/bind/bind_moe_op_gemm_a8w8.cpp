@@ -2,8 +2,9 @@
 // kernels/moe-gemm/moe_op_gemm_a8w8/kernel.cpp:244-271 (same function, argument
 // names and order). X_scale: None, numel 1 (per tensor, the reference's) or T
 // (per token); W_scale: None, numel E (per expert, the reference's) or E*N (per
-// output channel). apply_swiglu / swiglu_alpha are accepted and, as in the
-// reference, do not change the output.
+// output channel). W may be K-contiguous ([E, N, K]) or the reference's
+// N-contiguous [E, K, N] (copied K-major first). apply_swiglu / swiglu_alpha
+// are accepted and, as in the reference, do not change the output.
 #include "moe_bind.h"
 
 using namespace hkqbind;

@@ -1,10 +1,11 @@
 // moe_op_gemm_a8w8_blockscale_tk -- the reference module of
 // kernels/moe-gemm/moe_op_gemm_a8w8_blockscale/kernel.cpp:244-280 (same
-// function, argument names and order). Supported granularity: group_k == K,
-// i.e. X_scale [T, 1] (per token, strides xsm/xsk) and W_scale
-// [E, 1, ceil(N/group_n)] (per expert x output-channel group, strides
-// wse/wsk/wsn) -- with group_n == 1 this is per-token x per-channel scaling.
-// group_k < K raises ValueError.
+// function, argument names and order): X_scale [T, K/group_k] (strides
+// xsm/xsk) and W_scale [E, K/group_k, ceil(N/group_n)] (strides wse/wsk/wsn),
+// any group_k that is a multiple of 64 and group_n >= 1. group_k == K
+// (per-token x per-channel-group scales) runs on the per-token MoE kernel,
+// smaller groups on the per-group promotion kernel. W may be K-contiguous
+// ([E, N, K]) or the reference's N-contiguous [E, K, N].
 #include "moe_bind.h"
 
 using namespace hkqbind;
@@ -16,33 +17,51 @@ void moe_a8w8_blockscale(py::object X, py::object W, py::object Y, py::object X_
                          int stride_wk, int stride_wn, int stride_xsm, int stride_xsk, int stride_wse,
                          int stride_wsk, int stride_wsn) {
     (void)grid_n;
-    (void)stride_xsk;
-    (void)stride_wsk;
-    expect(group_k == K, "group_k < K (per-K-group promotion) is not supported by this MoE kernel; "
-                         "use group_k == K (per-token x per-channel scales)");
     expect(group_n >= 1, "group_n must be >= 1");
-    MoeScales sc;
-    if (!X_scale.is_none()) {
-        auto v = view(X_scale, "X_scale");
-        expect_dtype(v, "X_scale", {kF32});
-        sc.xs = (const float*)v.ptr;
-        sc.xs_tok = stride_xsm;
+    expect(group_k == K || (group_k >= 64 && group_k % 64 == 0), "group_k must be K or a positive multiple of 64");
+    if (group_k == K) {
+        (void)stride_xsk;
+        (void)stride_wsk;
+        MoeScales sc;
+        if (!X_scale.is_none()) {
+            auto v = view(X_scale, "X_scale");
+            expect_dtype(v, "X_scale", {kF32});
+            sc.xs = (const float*)v.ptr;
+            sc.xs_tok = stride_xsm;
+        }
+        if (!W_scale.is_none()) {
+            auto v = view(W_scale, "W_scale");
+            expect_dtype(v, "W_scale", {kF32});
+            sc.ws = (const float*)v.ptr;
+            sc.ws_e = stride_wse;
+            sc.ws_n = stride_wsn;
+            sc.ws_gn = group_n;
+        }
+        moe_call(X, W, Y, sc, bias, GatherIndx, ExptHist, ExptOffs, ExptData, N, K, grid_m, n_expts_act, stride_ym,
+                 stride_yn, stride_xm, stride_xk, stride_we, stride_wk, stride_wn);
+        return;
     }
-    if (!W_scale.is_none()) {
-        auto v = view(W_scale, "W_scale");
-        expect_dtype(v, "W_scale", {kF32});
-        sc.ws = (const float*)v.ptr;
-        sc.ws_e = stride_wse;
-        sc.ws_n = stride_wsn;
-        sc.ws_gn = group_n;
-    }
-    moe_call(X, W, Y, sc, bias, GatherIndx, ExptHist, ExptOffs, ExptData, N, K, grid_m, n_expts_act, stride_ym,
-             stride_yn, stride_xm, stride_xk, stride_we, stride_wk, stride_wn);
+    auto xs = view(X_scale, "X_scale"), ws = view(W_scale, "W_scale");
+    expect_dtype(xs, "X_scale", {kF32});
+    expect_dtype(ws, "W_scale", {kF32});
+    MoeArgs a = moe_prepare(X, W, Y, bias, GatherIndx, ExptHist, ExptOffs, ExptData, N, K, grid_m, stride_ym,
+                            stride_yn, stride_xm, stride_xk, stride_we, stride_wk, stride_wn);
+    const int64_t G = (K + group_k - 1) / group_k, C = (N + group_n - 1) / group_n;
+    expect(a.T == 0 || xs.numel() >= (a.T - 1) * (int64_t)stride_xsm + (G - 1) * (int64_t)stride_xsk + 1,
+           "X_scale is smaller than its strides say");
+    expect(ws.numel() >= (a.E - 1) * (int64_t)stride_wse + (G - 1) * (int64_t)stride_wsk +
+                             (C - 1) * (int64_t)stride_wsn + 1,
+           "W_scale is smaller than its strides say");
+    check(hkq_moe_a8w8_blockscale(a.X, a.W, a.Y, (const float*)xs.ptr, stride_xsm, stride_xsk, (const float*)ws.ptr,
+                                  stride_wse, stride_wsk, stride_wsn, group_k, group_n, a.bias, N, a.gather, a.hist,
+                                  a.offs, a.ed, a.T, a.E, N, K, grid_m, n_expts_act, a.stride_xm, a.stride_we,
+                                  a.stride_wn, a.stride_ym, a.y_rows, a.glen, current_stream()),
+          "moe_a8w8_blockscale");
 }
 
 PYBIND11_MODULE(moe_op_gemm_a8w8_blockscale_tk, m) {
     m.def("moe_a8w8_blockscale", &moe_a8w8_blockscale,
-          "MoE E4M3FN grouped GEMM with strided per-token / per-channel-group scales (group_k == K)", py::arg("X"),
+          "MoE E4M3FN grouped GEMM with per-K-group activation and weight scales", py::arg("X"),
           py::arg("W"), py::arg("Y"), py::arg("X_scale"), py::arg("W_scale"), py::arg("bias"), py::arg("GatherIndx"),
           py::arg("ExptHist"), py::arg("ExptOffs"), py::arg("ExptData"), py::arg("N"), py::arg("K"),
           py::arg("group_k"), py::arg("group_n"), py::arg("grid_m"), py::arg("grid_n"), py::arg("n_expts_act"),

@@ -6,10 +6,11 @@
 //           stride_bn, stride_cm, stride_cn, stride_amxm, stride_amxk,
 //           stride_bmxe, stride_bmxk, stride_bmxn, grid_m, grid_n).
 // Strides are in elements of each tensor (bytes for the uint8 ones). B and
-// B_mx_scale must be K-contiguous (stride_bk == stride_bmxk == 1: B[e] is
-// [N, K/2]); the reference test's [E, K/2, N] layout raises ValueError naming
-// the transpose. Every index the call can reach is checked against the
-// tensors' sizes before the launch.
+// B_mx_scale may be K-contiguous (stride_bk == stride_bmxk == 1: B[e] is
+// [N, K/2]) or the reference test's N-contiguous [E, K/2, N] / [E, K/32, N]
+// (stride_bn == stride_bmxn == 1), which are copied K-major on the stream
+// before the GEMM (hkq_moe_pack_kmajor). Every index the call can reach is
+// checked against the tensors' sizes before the launch.
 #include "bind_common.h"
 
 using namespace hkqbind;
@@ -41,9 +42,10 @@ void moe_mxfp4(py::object A, py::object B, py::object C, py::object A_mx_scale, 
     expect_dtype(ids, "sorted_token_ids", {kI32});
     expect_dtype(eids, "expert_ids", {kI32});
     expect(stride_ak == 1 && stride_amxk == 1, "A and A_mx_scale must be K-contiguous (stride_ak == stride_amxk == 1)");
-    expect(stride_bk == 1 && stride_bmxk == 1,
-           "B and B_mx_scale must be K-contiguous (stride_bk == stride_bmxk == 1): pass B[e] as [N, K/2] and "
-           "B_mx_scale[e] as [N, K/32], e.g. B.transpose(1, 2).contiguous() with strides ((K/2)*N, 1, K/2)");
+    const bool kmajor = stride_bk == 1 && stride_bmxk == 1;
+    expect(kmajor || (stride_bn == 1 && stride_bmxn == 1),
+           "B and B_mx_scale must both be K-contiguous (stride_bk == stride_bmxk == 1) or both N-contiguous "
+           "(stride_bn == stride_bmxn == 1)");
     expect(stride_cn == 1, "C must be N-contiguous (stride_cn == 1)");
     expect(a.contiguous() && b.contiguous() && as.contiguous() && bs.contiguous() && c.contiguous() &&
                ids.contiguous() && eids.contiguous(),
@@ -52,9 +54,23 @@ void moe_mxfp4(py::object A, py::object B, py::object C, py::object A_mx_scale, 
     const int64_t tokens = a.dim(0), E = b.dim(0);
     expect(a.numel() >= extent({{tokens, stride_am}, {K / 2, 1}}), "A is smaller than its strides say");
     expect(as.numel() >= extent({{tokens, stride_amxm}, {K / 32, 1}}), "A_mx_scale is smaller than its strides say");
-    expect(b.numel() >= extent({{E, stride_be}, {N, stride_bn}, {K / 2, 1}}), "B is smaller than its strides say");
-    expect(bs.numel() >= extent({{E, stride_bmxe}, {N, stride_bmxn}, {K / 32, 1}}),
+    expect(b.numel() >= extent({{E, stride_be}, {N, stride_bn}, {K / 2, stride_bk}}), "B is smaller than its strides say");
+    expect(bs.numel() >= extent({{E, stride_bmxe}, {N, stride_bmxn}, {K / 32, stride_bmxk}}),
            "B_mx_scale is smaller than its strides say");
+    // N-contiguous weights and scales (tests/test_moe.py:909-925 of the
+    // reference): K-major copies [E, N, K/2] and [E, N, K/32] for this call
+    Workspace bp, bsp;
+    uint64_t b_ptr = b.ptr, bs_ptr = bs.ptr;
+    if (!kmajor) {
+        bp = pack_kmajor(B, b.ptr, E, K / 2, N, stride_be, stride_bk, "moe_mxfp4 weight prepack");
+        bsp = pack_kmajor(B, bs.ptr, E, K / 32, N, stride_bmxe, stride_bmxk, "moe_mxfp4 scale prepack");
+        b_ptr = (uint64_t)bp.ptr;
+        bs_ptr = (uint64_t)bsp.ptr;
+        stride_be = (K / 2) * N;
+        stride_bn = K / 2;
+        stride_bmxe = (K / 32) * N;
+        stride_bmxn = K / 32;
+    }
     expect(ids.numel() >= (int64_t)grid_m * 128, "sorted_token_ids must hold grid_m * 128 entries");
     expect(eids.numel() >= grid_m, "expert_ids must hold grid_m entries");
     expect(c.numel() >= extent({{num_valid_tokens, stride_cm}, {N, 1}}), "C must hold num_valid_tokens rows");
@@ -77,8 +93,8 @@ void moe_mxfp4(py::object A, py::object B, py::object C, py::object A_mx_scale, 
         expect(v.numel() >= num_valid_tokens && v.contiguous(), "topk_weights must hold num_valid_tokens values");
         tw = (const float*)v.ptr;
     }
-    check(hkq_moe_mxfp4((const void*)a.ptr, (const void*)b.ptr, (void*)c.ptr, (const void*)as.ptr,
-                        (const void*)bs.ptr, sa, sb, tw, (const int32_t*)ids.ptr, (const int32_t*)eids.ptr, N, K,
+    check(hkq_moe_mxfp4((const void*)a.ptr, (const void*)b_ptr, (void*)c.ptr, (const void*)as.ptr,
+                        (const void*)bs_ptr, sa, sb, tw, (const int32_t*)ids.ptr, (const int32_t*)eids.ptr, N, K,
                         num_valid_tokens, top_k, mul_routed_weight ? 1 : 0, stride_am, stride_be, stride_bn,
                         stride_cm, stride_amxm, stride_bmxe, stride_bmxn, tokens, E, grid_m, current_stream()),
           "moe_mxfp4");

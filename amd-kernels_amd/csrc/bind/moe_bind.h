@@ -1,4 +1,4 @@
-// moe_bind.h -- argument handling shared by the two MoE GEMM modules
+// moe_bind.h -- argument handling shared by the two A8W8 MoE GEMM modules
 // (reference argument names and orders; strides in elements).
 #pragma once
 #include "bind_common.h"
@@ -12,10 +12,24 @@ struct MoeScales {
     int64_t ws_e = 0, ws_n = 0, ws_gn = 1;
 };
 
-inline void moe_call(py::object X, py::object W, py::object Y, const MoeScales& sc, py::object bias,
-                     py::object GatherIndx, py::object ExptHist, py::object ExptOffs, py::object ExptData, int N,
-                     int K, int grid_m, int n_expts_act, int stride_ym, int stride_yn, int stride_xm, int stride_xk,
-                     int stride_we, int stride_wk, int stride_wn) {
+// Tensors and strides of one MoE call after validation; W points at K-contiguous
+// rows (the reference's N-contiguous [E, K, N] weights are copied K-major into
+// `packed`, which must outlive the launch).
+struct MoeArgs {
+    const void* X = nullptr;
+    const void* W = nullptr;
+    void* Y = nullptr;
+    const float* bias = nullptr;
+    const int32_t *gather = nullptr, *hist = nullptr, *offs = nullptr, *ed = nullptr;
+    int64_t T = 0, E = 0, glen = 0, y_rows = 0;
+    int64_t stride_xm = 0, stride_we = 0, stride_wn = 0, stride_ym = 0;
+    Workspace packed;
+};
+
+inline MoeArgs moe_prepare(py::object X, py::object W, py::object Y, py::object bias, py::object GatherIndx,
+                           py::object ExptHist, py::object ExptOffs, py::object ExptData, int N, int K, int grid_m,
+                           int stride_ym, int stride_yn, int stride_xm, int stride_xk, int stride_we, int stride_wk,
+                           int stride_wn) {
     auto x = view(X, "X"), w = view(W, "W"), y = view(Y, "Y");
     if (x.dtype == kBF16 || x.dtype == kI8 || w.dtype == kBF16 || w.dtype == kI8)
         throw py::type_error("X and W must hold E4M3FN codes (torch.float8_e4m3fn or uint8)");
@@ -24,37 +38,62 @@ inline void moe_call(py::object X, py::object W, py::object Y, const MoeScales& 
     expect_dtype(y, "Y", {kBF16});
     expect(stride_xk == 1, "X must be K-contiguous (stride_xk == 1)");
     expect(stride_yn == 1, "Y must be N-contiguous (stride_yn == 1)");
-    expect(stride_wk == 1,
-           "W must be K-contiguous (stride_wk == 1): pass W[e] as [N, K], e.g. W.transpose(1, 2).contiguous() "
-           "with strides (N*K, 1, K)");
+    expect(stride_wk == 1 || stride_wn == 1, "W must be K-contiguous (stride_wk == 1) or N-contiguous (stride_wn == 1)");
     auto hist = view(ExptHist, "ExptHist"), offs = view(ExptOffs, "ExptOffs"), ed = view(ExptData, "ExptData");
     expect_dtype(hist, "ExptHist", {kI32});
     expect_dtype(offs, "ExptOffs", {kI32});
     expect_dtype(ed, "ExptData", {kI32});
     expect(ed.numel() >= grid_m, "ExptData must hold grid_m entries");
-    const int64_t E = hist.numel();
-    expect(offs.numel() == E, "ExptHist and ExptOffs must have one entry per expert");
-    const int32_t* gather = nullptr;
-    int64_t glen = 0;
+    MoeArgs a;
+    a.E = hist.numel();
+    expect(offs.numel() == a.E, "ExptHist and ExptOffs must have one entry per expert");
     if (!GatherIndx.is_none()) {
         auto g = view(GatherIndx, "GatherIndx");
         expect_dtype(g, "GatherIndx", {kI32});
-        gather = (const int32_t*)g.ptr;
-        glen = g.numel();
+        a.gather = (const int32_t*)g.ptr;
+        a.glen = g.numel();
     }
-    const float* b = nullptr;
     if (!bias.is_none()) {
         auto bv = view(bias, "bias");
         expect_dtype(bv, "bias", {kF32});
-        expect(bv.numel() >= E * N && bv.contiguous(), "bias must be a contiguous [E, N] fp32 tensor");
-        b = (const float*)bv.ptr;
+        expect(bv.numel() >= a.E * N && bv.contiguous(), "bias must be a contiguous [E, N] fp32 tensor");
+        a.bias = (const float*)bv.ptr;
     }
-    const int64_t T = x.dim(0);
-    const int64_t y_rows = y.dim(0);
-    check(hkq_moe_a8w8((const void*)x.ptr, (const void*)w.ptr, (void*)y.ptr, sc.xs, sc.xs_tok, sc.ws, sc.ws_e,
-                       sc.ws_n, sc.ws_gn, b, N, gather, (const int32_t*)hist.ptr, (const int32_t*)offs.ptr,
-                       (const int32_t*)ed.ptr, T, E, N, K, grid_m, n_expts_act, stride_xm, stride_we, stride_wn,
-                       stride_ym, y_rows, glen, current_stream()),
+    a.X = (const void*)x.ptr;
+    a.Y = (void*)y.ptr;
+    a.hist = (const int32_t*)hist.ptr;
+    a.offs = (const int32_t*)offs.ptr;
+    a.ed = (const int32_t*)ed.ptr;
+    a.T = x.dim(0);
+    a.y_rows = y.dim(0);
+    a.stride_xm = stride_xm;
+    a.stride_ym = stride_ym;
+    if (stride_wk == 1) {
+        a.W = (const void*)w.ptr;
+        a.stride_we = stride_we;
+        a.stride_wn = stride_wn;
+    } else {
+        // the reference's [E, K, N] layout (tests/test_moe.py:723-729): rows of
+        // K per output channel are what the kernels stream, so copy it K-major
+        expect(w.numel() >= (a.E - 1) * (int64_t)stride_we + (int64_t)(K - 1) * stride_wk + N,
+               "W is smaller than its strides say");
+        a.packed = pack_kmajor(W, w.ptr, a.E, K, N, stride_we, stride_wk, "moe weight prepack");
+        a.W = a.packed.ptr;
+        a.stride_we = (int64_t)N * K;
+        a.stride_wn = K;
+    }
+    return a;
+}
+
+inline void moe_call(py::object X, py::object W, py::object Y, const MoeScales& sc, py::object bias,
+                     py::object GatherIndx, py::object ExptHist, py::object ExptOffs, py::object ExptData, int N,
+                     int K, int grid_m, int n_expts_act, int stride_ym, int stride_yn, int stride_xm, int stride_xk,
+                     int stride_we, int stride_wk, int stride_wn) {
+    MoeArgs a = moe_prepare(X, W, Y, bias, GatherIndx, ExptHist, ExptOffs, ExptData, N, K, grid_m, stride_ym,
+                            stride_yn, stride_xm, stride_xk, stride_we, stride_wk, stride_wn);
+    check(hkq_moe_a8w8(a.X, a.W, a.Y, sc.xs, sc.xs_tok, sc.ws, sc.ws_e, sc.ws_n, sc.ws_gn, a.bias, N, a.gather, a.hist,
+                       a.offs, a.ed, a.T, a.E, N, K, grid_m, n_expts_act, a.stride_xm, a.stride_we, a.stride_wn,
+                       a.stride_ym, a.y_rows, a.glen, current_stream()),
           "moe");
 }
 

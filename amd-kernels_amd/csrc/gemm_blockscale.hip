@@ -276,8 +276,10 @@ __device__ __forceinline__ BlockScaleParams bs_row_slice(const BlockScaleParams&
             p.ca += (int64_t)m0 * p.ldca;
             p.cb += (int64_t)m0 * p.ldcb;
         }
-        p.M = min(BSN_MAX_M, p.M - m0);
     }
+    // every row group (the first included) spans at most 64 rows, which keeps
+    // its buffer ranges within the host's 64-row 2^31-byte bound
+    p.M = min(BSN_MAX_M, p.M - m0);
     return p;
 }
 

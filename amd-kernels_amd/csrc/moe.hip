@@ -193,8 +193,10 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const
     const int n0 = tn * MOE_BN;
     const int pm0 = 2 * q, pm1 = 2 * q + 1;
     const int ed0 = p.expt_data[pm0], ed1 = pm1 < p.grid_m ? p.expt_data[pm1] : -1;
+    // an entry with bit 31 set (-1 or any malformed word) is skipped: its block
+    // id would be negative
     const int e0 = ed0 & 0xFFFF, e1 = ed1 & 0xFFFF;
-    const bool v0 = ed0 != -1 && e0 < p.E, v1 = ed1 != -1 && e1 < p.E;
+    const bool v0 = ed0 >= 0 && e0 < p.E, v1 = ed1 >= 0 && e1 < p.E;
     const int b0 = ed0 >> 16, b1 = ed1 >> 16;
     if (v0 && v1 && e0 == e1 && b1 == b0 + 1) {
         moe_block<4, KTB, NS>(p, e0, b0 * MOE_BM, n0, smem);
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(64 * MOE_NARROW_WAVES) void moe_narrow_kernel(const
     const int pm = blockIdx.x / slices, n0 = (blockIdx.x % slices) * 16 * NT;
     const int ed = p.expt_data[pm];
     const int e = ed & 0xFFFF, b = ed >> 16;
-    if (ed == -1 || e >= p.E) return;  // uniform over the workgroup
+    if (ed < 0 || e >= p.E) return;  // uniform over the workgroup (bit 31 set: -1 or malformed)
     const int m_e = p.hist[e], start = p.offs[e];
     const int rows = min(m_e - b * MOE_BM, 16 * MT);
     if (rows <= 0 || start < 0) return;
@@ -715,6 +717,8 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     HKQ_CHECK_ARG(K % 64 == 0, "K must be a multiple of 64");
     HKQ_CHECK_ARG(N % 4 == 0, "N must be a multiple of 4");
     HKQ_CHECK_ARG(stride_xm >= K && stride_xm % 16 == 0, "stride_xm must be >= K and a multiple of 16");
+    // the kernels address gathered X rows with 32-bit buffer offsets
+    HKQ_CHECK_ARG(T * stride_xm < (1ll << 31), "X must span less than 2^31 bytes (T * stride_xm)");
     HKQ_CHECK_ARG(stride_wn >= K && stride_wn % 16 == 0, "stride_wn must be >= K and a multiple of 16 (W[e] is [N, K])");
     HKQ_CHECK_ARG(stride_we >= 0 && stride_we % 16 == 0, "stride_we must be a non-negative multiple of 16");
     HKQ_CHECK_ARG(stride_ym >= N && stride_ym % 4 == 0, "stride_ym must be >= N and a multiple of 4");
@@ -751,7 +755,7 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     // a gather; every block then holds at most that many rows.
     const int64_t routed = gather ? T * topk : T;
     const bool decode = routed <= 32 || (routed <= MOE_NARROW_MAX_ROWS && N <= 4096);
-    if (decode && K % 128 == 0 && 64 * stride_wn < (1ll << 31) && T * stride_xm < (1ll << 31))
+    if (decode && K % 128 == 0 && 64 * stride_wn < (1ll << 31))
         return launch_moe_narrow(p, routed, stream);
     // 128-byte K-tiles (2-stage ring) when every row has whole ones: a partial
     // last K-tile would read the next row's bytes instead of zeros

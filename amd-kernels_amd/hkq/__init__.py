@@ -40,6 +40,9 @@ SIGNATURES = {
     "hkq_batched_gemm_bf16": (_I, [_P] * 4 + [_I64] * 11 + [_P, ctypes.c_size_t, _P]),
     "hkq_moe_a8w8": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]
                      + [_I64] * 12 + [_P]),
+    "hkq_moe_a8w8_blockscale": (_I, [_P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64,
+                                     _P, _P, _P, _P] + [_I64] * 12 + [_P]),
+    "hkq_moe_pack_kmajor": (_I, [_P, _P] + [_I64] * 7 + [_P]),
     "hkq_rmsnorm_quant": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _P]),
     "hkq_swiglu_quant": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _I, _P]),
     "hkq_moe_mxfp4": (_I, [_P] * 10 + [_I64, _I64, _I64, _I64, _I] + [_I64] * 10 + [_P]),
@@ -352,6 +355,41 @@ def moe_a8w8(X, W, hist, offs, expt_data, topk, gather=None, x_scale=None, w_sca
          _ptr(hist), _ptr(offs), _ptr(expt_data), T, E, N, K, expt_data.numel(), topk, X.stride(0), W.stride(0),
          W.stride(1), Y.stride(0), rows, gather.numel() if gather is not None else 0, _stream(stream))
     return Y
+
+
+def moe_a8w8_blockscale(X, W, hist, offs, expt_data, topk, x_scale, w_scale, group_k: int, group_n: int,
+                        gather=None, bias=None, Y=None, y_rows=None, stream=None):
+    """OGS-routed A8W8 MoE GEMM with per-K-group scales. X [T, K] E4M3FN;
+    W [E, N, K] E4M3FN (K contiguous); x_scale fp32 [T, ceil(K/group_k)];
+    w_scale fp32 [E, ceil(K/group_k), ceil(N/group_n)] (any strides); bias None
+    or fp32 [E, N]. Returns Y bf16 [y_rows (default T*topk), N]."""
+    import torch
+
+    T, K = X.shape
+    E, N = W.shape[0], W.shape[1]
+    rows = T * topk if y_rows is None else y_rows
+    if Y is None:
+        Y = torch.zeros((rows, N), dtype=torch.bfloat16, device=X.device)
+    call("hkq_moe_a8w8_blockscale", _ptr(X), _ptr(W), _ptr(Y), _ptr(x_scale), x_scale.stride(0), x_scale.stride(1),
+         _ptr(w_scale), w_scale.stride(0), w_scale.stride(1), w_scale.stride(2), group_k, group_n, _opt_ptr(bias), N,
+         _opt_ptr(gather), _ptr(hist), _ptr(offs), _ptr(expt_data), T, E, N, K, expt_data.numel(), topk,
+         X.stride(0), W.stride(0), W.stride(1), Y.stride(0), rows, gather.numel() if gather is not None else 0,
+         _stream(stream))
+    return Y
+
+
+def moe_pack_kmajor(W, out=None, stream=None):
+    """[E, R, N] byte planes (N contiguous, e.g. the reference's [E, K, N] MoE
+    weights) -> contiguous [E, N, R] (uint8 view of the same codes)."""
+    import torch
+
+    E, R, N = W.shape
+    assert W.stride(2) == 1, "the source's last dimension must be contiguous"
+    if out is None:
+        out = torch.empty((E, N, R), dtype=torch.uint8, device=W.device)
+    call("hkq_moe_pack_kmajor", _ptr(W), _ptr(out), E, R, N, W.stride(0), W.stride(1), out.stride(0), out.stride(1),
+         _stream(stream))
+    return out
 
 
 def moe_mxfp4(A, As, B, Bs, sorted_ids, expert_ids, num_valid: int, topk: int, a_scale=None, b_scale=None,

@@ -214,8 +214,8 @@ int hkq_batched_gemm_bf16(const void* A, const void* B, const void* bias, void* 
  * token = gather[s] / topk (gather == NULL: token = s):
  *   Y[s, n] = bf16((sum_k X[token, k] * W[e, n, k]) * xs(token) * ws(e, n) + bias[e, n]).
  * X E4M3FN [T, stride_xm], K contiguous; W E4M3FN with expert stride stride_we and
- * row (n) stride stride_wn, K contiguous (the reference's [E, K, N] layout has to
- * be passed transposed to [E, N, K]); Y bf16 rows of stride_ym, y_rows of them.
+ * row (n) stride stride_wn, K contiguous (the reference's [E, K, N] layout goes
+ * through hkq_moe_pack_kmajor first); Y bf16 rows of stride_ym, y_rows of them.
  * xs: NULL (1), x_scale[0] (xs_stride_tok 0) or x_scale[token * xs_stride_tok].
  * ws: NULL (1) or w_scale[e * ws_stride_e + (n / ws_group_n) * ws_stride_n]
  *   (per expert: ws_stride_n 0; per channel: ws_stride_e N, ws_stride_n 1, ws_group_n 1).
@@ -232,6 +232,38 @@ int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* x_scale, in
                  int64_t stride_xm, int64_t stride_we, int64_t stride_wn, int64_t stride_ym, int64_t y_rows,
                  int64_t gather_len, hkq_stream_t stream);
 
+/* The same grouped GEMM with per-K-group scales: for group g = k / group_k
+ * (group_k a multiple of 64),
+ *   Y[s, n] = bf16(sum_g (sum_{k in g} X[token, k] W[e, n, k])
+ *                  * x_scale[token * xs_stride_m + g * xs_stride_k]
+ *                  * w_scale[e * ws_stride_e + g * ws_stride_k + (n / group_n) * ws_stride_n]
+ *                  + bias[e * bias_stride_e + n]).
+ * Routing, X, W, Y, bias and the argument checks as hkq_moe_a8w8; x_scale and
+ * w_scale are required. Replaces moe_op_gemm_a8w8_blockscale_tk.moe_a8w8_blockscale
+ * (kernels/moe-gemm/moe_op_gemm_a8w8_blockscale/kernel.cpp:192-280; per-tile
+ * promotion :114-145) for any group_k; group_k == K is also served, faster, by
+ * hkq_moe_a8w8 with per-token x per-channel-group scales. */
+int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, const float* x_scale, int64_t xs_stride_m,
+                            int64_t xs_stride_k, const float* w_scale, int64_t ws_stride_e, int64_t ws_stride_k,
+                            int64_t ws_stride_n, int64_t group_k, int64_t group_n, const float* bias,
+                            int64_t bias_stride_e, const int32_t* gather, const int32_t* hist, const int32_t* offs,
+                            const int32_t* expt_data, int64_t T, int64_t E, int64_t N, int64_t K, int64_t grid_m,
+                            int64_t topk, int64_t stride_xm, int64_t stride_we, int64_t stride_wn, int64_t stride_ym,
+                            int64_t y_rows, int64_t gather_len, hkq_stream_t stream);
+
+/* Byte-plane transpose dst[e][n][r] = src[e][r][n] (src row r at
+ * src + e*src_stride_e + r*src_stride_r, N contiguous bytes; dst row n at
+ * dst + e*dst_stride_e + n*dst_stride_n, R contiguous bytes). Turns the
+ * reference's N-contiguous MoE weights -- E4M3FN [E, K, N], E2M1 pairs
+ * [E, K/2, N] and e8m0 weight scales [E, K/32, N] (tests/test_moe.py:723-729,
+ * 808-815, 909-925) -- into the K-contiguous rows the MoE GEMMs above read.
+ * The reference's kernels read W through stride_wk / stride_wn instead
+ * (kernels/moe-gemm/moe_op_gemm_a8w8/kernel.cpp:120,
+ * moe_op_gemm_a8w8_blockscale/kernel.cpp:108, moe_op_mxfp4/kernel.cpp:155);
+ * the reference-named modules call this on such weights before the GEMM. */
+int hkq_moe_pack_kmajor(const void* src, void* dst, int64_t E, int64_t R, int64_t N, int64_t src_stride_e,
+                        int64_t src_stride_r, int64_t dst_stride_e, int64_t dst_stride_n, hkq_stream_t stream);
+
 /* MXFP4 MoE over block-sorted routing (the output of hkq_moe_align_block_size):
  * tile row r of 128-row block pm is gate id = sorted_token_ids[pm*128 + r]
  * (rows with id >= num_valid_tokens are padding), expert e = expert_ids[pm]:
@@ -244,7 +276,8 @@ int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* x_scale, in
  * values; expert e at B + e*stride_be, B_mx_scale + e*stride_bmxe; C bf16 rows
  * of stride_cm. K % 128 == 0, N % 4 == 0. Replaces moe_op_mxfp4_tk.moe_mxfp4
  * (kernels/moe-gemm/moe_op_mxfp4/kernel.cpp:263-330), whose weights are
- * [E, K/2, N] (N contiguous): pass them transposed. */
+ * [E, K/2, N] (N contiguous): hkq_moe_pack_kmajor transposes them (and their
+ * [E, K/32, N] scales). */
 int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* A_mx_scale, const void* B_mx_scale,
                   const float* A_scale, const float* B_scale, const float* topk_weights,
                   const int32_t* sorted_token_ids, const int32_t* expert_ids, int64_t N, int64_t K,

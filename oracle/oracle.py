@@ -326,6 +326,52 @@ def gemm_blockscale_ref(A, B, sa, sb, group_k: int = 128, group_n: int = 128) ->
     return C
 
 
+# Full-output references at BASELINE sizes: the same formulas with the decoded
+# operands multiplied in fp32 by torch on all host threads (seconds instead of
+# minutes for 10^11-10^12 flops). Products of E4M3 / E2M1 values are exact in
+# fp32; the fp32 sums differ from the fp64 ones by ~sqrt(K) * 2^-24 of the sum
+# of |terms|, far inside the GEMM tolerance. Pinned against the fp64 functions
+# above on small shapes (tests/test_oracle_gemm_ext.py).
+
+def _matmul_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """a [M, K] . b[N, K]^T in fp32 on the host (torch CPU, all threads)."""
+    import torch
+    torch.set_num_threads(max(1, len(os.sched_getaffinity(0))))
+    ta = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    tb = torch.from_numpy(np.ascontiguousarray(b, dtype=np.float32))
+    return (ta @ tb.T).numpy()
+
+
+def gemm_a8w8_ref_f32(A, B, sa, sb) -> np.ndarray:
+    """gemm_a8w8_ref with an fp32 product: float32 [M, N]."""
+    C = _matmul_f32(e4m3_decode(A), e4m3_decode(B))
+    C *= np.asarray(sa, np.float32).reshape(-1, 1)
+    C *= np.asarray(sb, np.float32).reshape(1, -1)
+    return C
+
+
+def gemm_blockscale_ref_f32(A, B, sa, sb, group_k: int = 128, group_n: int = 128) -> np.ndarray:
+    """gemm_blockscale_ref as one fp32 product of pre-scaled operands:
+    sum_g (A_g sa[:, g]) . (B_g sb[g, n/gn])^T = (A * SA) . (B * SB)^T with
+    SA[m, k] = sa[m, k/gk], SB[n, k] = sb[k/gk, n/gn] (each scaled operand
+    rounds once to fp32: 2^-24 relative). float32 [M, N]."""
+    a = e4m3_decode(A)
+    b = e4m3_decode(B)
+    M, K = a.shape
+    N = b.shape[0]
+    sa = np.asarray(sa, np.float32).reshape(M, -1)
+    sb = np.asarray(sb, np.float32).reshape(sa.shape[1], -1)
+    kidx = np.arange(K) // group_k
+    a = a * sa[:, kidx]
+    b = b * sb[kidx][:, np.arange(N) // group_n].T
+    return _matmul_f32(a, b)
+
+
+def gemm_mxfp4_ref_f32(Aq, As, Bq, Bs) -> np.ndarray:
+    """gemm_mxfp4_ref with an fp32 product (decoded values are exact): float32 [M, N]."""
+    return _matmul_f32(mx_fp4_dequant_f32(Aq, As), mx_fp4_dequant_f32(Bq, Bs))
+
+
 def gemm_bf16_ref(A_bits, B_bits, bias_bits=None) -> np.ndarray:
     """C = A . B^T (+ bias[n]) on bf16 bit patterns A [M, K], B [N, K]
     (tests/test_gemm.py:21-42 and, with bias, :316-347); fp64 [M, N]."""
@@ -423,6 +469,108 @@ def moe_ref(X, W, x_scale, w_scale, bias, gather, hist, offs, expt_data, topk,
             r = r + np.asarray(bias, np.float64)[e][None, :]
         Y[sidx] = r
     return Y
+
+
+def _tiles_rows(gather, hist, offs, expt_data, topk, E, block_m=128):
+    """Per routing tile (e, sorted rows, tokens), skipping -1 / malformed entries."""
+    out = []
+    for ed in np.asarray(expt_data).tolist():
+        if ed < 0 or (ed & 0xFFFF) >= E:
+            continue
+        e, b = ed & 0xFFFF, ed >> 16
+        n = min(int(hist[e]) - b * block_m, block_m)
+        if n <= 0:
+            continue
+        sidx = int(offs[e]) + b * block_m + np.arange(n)
+        out.append((e, sidx, np.asarray(gather)[sidx] // topk))
+    return out
+
+
+def moe_blockscale_ref(X, W, x_scale, w_scale, bias, gather, hist, offs, expt_data, topk, group_k, group_n,
+                       block_m: int = 128, w_layout: str = "enk"):
+    """moe-gemm/moe_op_gemm_a8w8_blockscale/kernel.cpp:93-167 restated: for each
+    routing tile, Y[s, n] = sum_g (X[tok, g-part] . W[e, n, g-part]) *
+    x_scale[tok, g] * w_scale[e, g, n // group_n] + bias[e, n]. X e4m3 codes
+    [T, K]; W [E, N, K] ("enk") or [E, K, N] ("ekn"); x_scale [T, G];
+    w_scale [E, G, ceil(N / group_n)]. fp64 [T*topk, N], untouched rows NaN."""
+    x = e4m3_decode(X).astype(np.float64)
+    w = e4m3_decode(W).astype(np.float64)
+    if w_layout == "ekn":
+        w = np.transpose(w, (0, 2, 1))
+    E, N, K = w.shape
+    T = x.shape[0]
+    xs = np.asarray(x_scale, np.float64).reshape(T, -1)
+    ws = np.asarray(w_scale, np.float64).reshape(E, xs.shape[1], -1)
+    G = xs.shape[1]
+    Y = np.full((T * topk, N), np.nan)
+    for e, sidx, tok in _tiles_rows(gather, hist, offs, expt_data, topk, E, block_m):
+        acc = np.zeros((len(sidx), N))
+        for g in range(G):
+            ks = slice(g * group_k, min((g + 1) * group_k, K))
+            part = x[tok][:, ks] @ w[e][:, ks].T
+            wcol = ws[e, g][np.arange(N) // group_n]
+            acc += part * xs[tok, g][:, None] * wcol[None, :]
+        if bias is not None:
+            acc += np.asarray(bias, np.float64)[e][None, :]
+        Y[sidx] = acc
+    return Y
+
+
+def moe_ref_f32(X, W, x_scale, w_scale, gather, hist, offs, expt_data, topk, group_k=None, group_n=1,
+                block_m: int = 128):
+    """fp32 full-output MoE reference for BASELINE sizes: per expert one fp32
+    product of pre-scaled operands (W [E, N, K] e4m3 codes). x_scale: [T]
+    (per token) or [T, G]; w_scale: [E, N] (per channel) or [E, G, C] with
+    group_k / group_n. Rows of the listed tiles only; the rest NaN (float32)."""
+    E, N, K = W.shape
+    T = X.shape[0]
+    gk = K if group_k is None else group_k
+    xs = np.asarray(x_scale, np.float32).reshape(T, -1)      # [T, 1] or [T, G]
+    ws = np.asarray(w_scale, np.float32)
+    gn = 1 if ws.ndim == 2 else group_n
+    ws = ws.reshape(E, 1, N) if ws.ndim == 2 else ws          # [E, 1 or G, C]
+    kidx = np.arange(K) // gk
+    kx = kidx if xs.shape[1] > 1 else np.zeros(K, np.int64)
+    kw = kidx if ws.shape[1] > 1 else np.zeros(K, np.int64)
+    Y = np.full((T * topk, N), np.nan, np.float32)
+    rows = {}
+    for e, sidx, tok in _tiles_rows(gather, hist, offs, expt_data, topk, E, block_m):
+        s0, t0 = rows.get(e, (np.zeros(0, np.int64), np.zeros(0, np.int64)))
+        rows[e] = (np.concatenate([s0, sidx]), np.concatenate([t0, tok]))
+    for e, (sidx, tok) in rows.items():
+        a = e4m3_decode(X[tok]) * xs[tok][:, kx]
+        b = e4m3_decode(W[e]) * ws[e][kw][:, np.arange(N) // gn].T
+        Y[sidx] = _matmul_f32(a, b)
+    return Y
+
+
+def moe_mxfp4_ref_f32(Aq, As, Bq, Bs, a_scale, b_scale, topk_w, sorted_ids, expert_ids, N, num_valid, topk,
+                      mul_routed_weight, c_rows):
+    """moe_mxfp4_ref with one fp32 product per expert over all of its rows
+    (decoded E2M1 values are exact): float32 [c_rows, N], unwritten rows NaN."""
+    a = mx_fp4_dequant_f32(Aq, As)
+    E = Bq.shape[0]
+    C = np.full((c_rows, N), np.nan, np.float32)
+    sorted_ids = np.asarray(sorted_ids)
+    per_e = {}
+    for pm, e in enumerate(np.asarray(expert_ids).tolist()):
+        ids = sorted_ids[pm * 128:(pm + 1) * 128]
+        ids = ids[(ids >= 0) & (ids < num_valid)]
+        if len(ids) == 0:
+            continue
+        if e == -1:
+            C[ids] = 0.0
+        elif 0 <= e < E:
+            per_e.setdefault(e, []).append(ids)
+    for e, lst in per_e.items():
+        ids = np.concatenate(lst)
+        r = _matmul_f32(a[ids // topk], mx_fp4_dequant_f32(Bq[e], Bs[e]))
+        g = (1.0 if a_scale is None else float(np.float32(a_scale))) * (1.0 if b_scale is None else float(b_scale[e]))
+        r *= np.float32(g)
+        if mul_routed_weight:
+            r *= np.asarray(topk_w, np.float32)[ids][:, None]
+        C[ids] = r
+    return C
 
 
 # ----------------------------------------------------------------------------

@@ -103,3 +103,15 @@ def test_hipkittens_rejects_host_tensors_and_bf16_codes():
         hk.gemm.a8w8.dispatch(a, a, s, s, c)
     with pytest.raises(ValueError, match="GPU tensor"):
         hk.per_token_quant_fwd(a, a, s)
+
+
+def test_moe_a8w8_rejects_x_past_2gib():
+    """The MoE kernels address gathered X rows with 32-bit buffer offsets, so
+    an X spanning 2^31 bytes or more is rejected before any launch instead of
+    reading zeros or other tokens' rows."""
+    p = 0x1000  # never dereferenced: validation fails first
+    K = 4096
+    T = (1 << 31) // K  # T * K == 2^31
+    args = [p, p, p, None, 0, None, 0, 0, 1, None, 0, None, p, p, p,
+            T, 8, 4096, K, 16, 2, K, 4096 * K, K, 4096, T * 2, 0, None]
+    _expect_invalid("hkq_moe_a8w8", *args, match="2\\^31")

@@ -26,12 +26,15 @@ def rms_inputs(orc, M, D, seed):
     return xb, wb
 
 
-@pytest.mark.parametrize("kind", [0, 1])
-@pytest.mark.parametrize("M,D", [(1, 128), (7, 1024), (256, 4096), (33, 5120), (64, 7168), (130, 8192), (5, 2080)])
+# FP8 1x128 (kind 0) needs D % 128 == 0, MXFP4 (kind 1) D % 32 == 0: only
+# valid combinations are generated
+RMS_SHAPES = [(1, 128), (7, 1024), (256, 4096), (33, 5120), (64, 7168), (130, 8192), (5, 2080)]
+
+
+@pytest.mark.parametrize("kind,M,D", [(k, M, D) for k in (0, 1) for (M, D) in RMS_SHAPES
+                                      if D % (128 if k == 0 else 32) == 0])
 def test_rmsnorm_quant_bitexact(orc, kind, M, D):
     require_gpu()
-    if kind == 0 and D % 128:
-        pytest.skip("FP8 1x128 needs D % 128 == 0")
     xb, wb = rms_inputs(orc, M, D, M + D + kind)
     eps = 1e-6
     q, s = hkq.rmsnorm_quant(dev_bf16(xb), dev_bf16(wb), eps, kind)
@@ -97,14 +100,15 @@ def e4m3_step_diff(a, b):
     return np.where((sa == sb) | ((ma == 0) & (mb == 0)), d, np.where(ma + mb <= 1, 1, 99))
 
 
+# 1x128 groups need F % 128 == 0: only valid combinations are generated
+SWIGLU_SHAPES = [(1, 128, 1.0), (64, 14336, 1.0), (300, 1024, 1.702), (17, 6144, 1.0), (8, 32768, 1.0), (40, 200, 1.0)]
+
+
 @pytest.mark.parametrize("interleaved", [False, True])
-@pytest.mark.parametrize("group", [0, 128])
-@pytest.mark.parametrize("M,F,alpha", [(1, 128, 1.0), (64, 14336, 1.0), (300, 1024, 1.702), (17, 6144, 1.0),
-                                       (8, 32768, 1.0), (40, 200, 1.0)])
+@pytest.mark.parametrize("group,M,F,alpha", [(g, M, F, a) for g in (0, 128) for (M, F, a) in SWIGLU_SHAPES
+                                             if g == 0 or F % g == 0])
 def test_swiglu_quant(orc, interleaved, group, M, F, alpha):
     require_gpu()
-    if group and F % 128:
-        pytest.skip("1x128 groups need F % 128 == 0")
     yb = orc.randn_bf16((M, 2 * F), seed=M + F + group)
     q, s = hkq.swiglu_quant(dev_bf16(yb), alpha, interleaved, group)
     torch.cuda.synchronize()

@@ -156,7 +156,9 @@ def test_moe_malformed_metadata_does_not_fault(orc):
     require_gpu()
     T, E, topk, K, N = 128, 2, 1, 128, 256
     _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 11)
-    bad = np.concatenate([ed, np.array([7 | (0 << 16), 1 | (9 << 16)], np.int32)])  # expert 7, block 9
+    # expert 7, block 9 of expert 1, and words with bit 31 set other than -1
+    # (their block id would be negative)
+    bad = np.concatenate([ed, np.array([7 | (0 << 16), 1 | (9 << 16), -0x7FFFFFFF, -0x7FFF0000], np.int32)])
     g2 = gather.copy()
     g2[5] = T * topk + 40  # token past T: the row reads zero
     Y = run_moe(X, W, hist, offs, g2, bad, topk, xs, ws)
@@ -165,73 +167,175 @@ def test_moe_malformed_metadata_does_not_fault(orc):
     check_rows(orc, Y, ref)
 
 
-@pytest.mark.parametrize("K,N", [(4096, 28672), (14336, 4096)])
-def test_moe_mixtral_sampled(orc, K, N):
-    """BASELINE MoE shapes (Mixtral-8x7B: T=4096, E=8, top-2; gate/up K=4096,
-    N=28672 and down K=14336, N=4096), softmax top-2 routing from seeded logits;
-    weights quantized per channel on the GPU; sampled rows/columns vs the oracle."""
-    require_gpu()
-    T, E, topk = 4096, 8, 2
-    g = torch.Generator(device="cpu").manual_seed(K)
+def mixtral_routing(orc, T, E, topk, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
     logits = torch.randn(T, E, generator=g)
     assigns = torch.topk(torch.softmax(logits, -1), topk, dim=-1).indices.numpy()
-    hist, offs, gather, ed = orc.ogs_routing(assigns, E, 128)
-    xb = orc.randn_bf16((T, K), seed=K + 1)
-    X, xs = orc.quant_rowwise(xb, None, "fp8")
-    w = (torch.randn(E * N, K, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    return orc.ogs_routing(assigns, E, 128)
+
+
+def device_weights_fp8(E, N, K, seed):
+    """E*N x K weights ~N(0, 0.02) drawn on the device and quantized per row
+    by the GPU quantizer (bit-exact with the oracle's, tests/test_gpu_quant.py);
+    returns the codes [E, N, K] and scales [E, N] on the host."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn(E * N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
     Wq_d, ws_d = hkq.per_token_quant(w)
     torch.cuda.synchronize()
     del w
-    W = Wq_d.view(torch.uint8).cpu().numpy().reshape(E, N, K)
-    ws = ws_d.cpu().numpy().reshape(E, N)
-    Y = run_moe(X, W, hist, offs, gather, ed, topk, xs.reshape(-1), ws)
-    rng = np.random.default_rng(N)
-    srows = np.sort(rng.choice(T * topk, 64, replace=False))
-    cols = np.sort(rng.choice(N, 64, replace=False))
-    # sampled reference: expert of each sorted row from the offsets, token from the gather
-    e_of = np.searchsorted(offs, srows, side="right") - 1
-    tok = gather[srows] // topk
-    x = orc.e4m3_decode(X[tok]).astype(np.float64)
-    ref = np.empty((len(srows), len(cols)))
-    for i, (e, t) in enumerate(zip(e_of, tok)):
-        wcols = orc.e4m3_decode(W[e][cols]).astype(np.float64)
-        ref[i] = (wcols @ x[i]) * xs.reshape(-1)[t] * ws[e, cols]
-    assert_gemm_close(Y[np.ix_(srows, cols)], ref, f"moe K={K} N={N} sampled")
-    assert np.isfinite(Y).all()
+    return Wq_d.view(torch.uint8).cpu().numpy().reshape(E, N, K), ws_d.cpu().numpy().reshape(E, N)
+
+
+@pytest.mark.parametrize("K,N", [(4096, 28672), (14336, 4096)])
+def test_moe_mixtral_full(orc, K, N):
+    """BASELINE MoE shapes (Mixtral-8x7B: T=4096, E=8, top-2; gate/up K=4096,
+    N=28672 and down K=14336, N=4096), softmax top-2 routing from seeded logits,
+    per-token x per-channel scales: every routed output row against the fp32
+    oracle (oracle.moe_ref_f32, pinned in tests/test_oracle_moe.py)."""
+    require_gpu()
+    T, E, topk = 4096, 8, 2
+    hist, offs, gather, ed = mixtral_routing(orc, T, E, topk, K)
+    X, xs = orc.quant_rowwise(orc.randn_bf16((T, K), seed=K + 1), None, "fp8")
+    xs = xs.reshape(-1)
+    W, ws = device_weights_fp8(E, N, K, seed=K + 2)
+    Y = run_moe(X, W, hist, offs, gather, ed, topk, xs, ws)
+    ref = orc.moe_ref_f32(X, W, xs, ws, gather, hist, offs, ed, topk)
+    assert not np.isnan(ref).any()  # every (token, choice) routed
+    assert_gemm_close(Y, ref, f"moe mixtral K={K} N={N}")
+
+
+# ---------------------------------------------------------------------------
+# Block-scale MoE (per-K-group scales): moe_op_gemm_a8w8_blockscale with
+# group_k < K (kernel.cpp:114-145 of the reference)
+# ---------------------------------------------------------------------------
+
+def run_moe_bs(X, W, hist, offs, gather, ed, topk, xs, ws, gk, gn, bias=None, y_rows=None):
+    Y = hkq.moe_a8w8_blockscale(dev_u8(X), dev_u8(W), dev_i32(hist), dev_i32(offs), dev_i32(ed), topk, dev_f32(xs),
+                                dev_f32(ws), gk, gn, gather=dev_i32(gather) if gather is not None else None,
+                                bias=dev_f32(bias) if bias is not None else None, y_rows=y_rows)
+    torch.cuda.synchronize()
+    return host_bf16_f32(Y)
+
+
+# group_k 64 / 128 / 192 (one, two, three K-tiles per group), group_n 1 (per
+# column), 7 (groups across sub-tiles), 64 and 128 (one scale per sub-tile),
+# ragged N, decode-sized and multi-block routing, a bias.
+@pytest.mark.parametrize("T,E,topk,K,N,gk,gn", [(64, 8, 2, 256, 256, 64, 64), (300, 4, 2, 512, 520, 128, 1),
+                                                (130, 3, 1, 384, 260, 192, 7), (5, 8, 2, 640, 1000, 64, 128),
+                                                (700, 5, 2, 1024, 512, 128, 128), (16, 2, 2, 128, 4100, 64, 1)])
+def test_moe_blockscale(orc, T, E, topk, K, N, gk, gn):
+    require_gpu()
+    _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, T, E, topk, K, N, T + K + gn)
+    rng = np.random.default_rng(T + N)
+    G, C = (K + gk - 1) // gk, (N + gn - 1) // gn
+    xs = (rng.random((T, G)) * 0.02 + 0.005).astype(np.float32)
+    ws = (rng.random((E, G, C)) * 0.002 + 0.0005).astype(np.float32)
+    bias = (rng.standard_normal((E, N)) * 0.1).astype(np.float32) if T % 2 == 0 else None
+    Y = run_moe_bs(X, W, hist, offs, gather, ed, topk, xs, ws, gk, gn, bias)
+    ref = orc.moe_blockscale_ref(X, W, xs, ws, bias, gather, hist, offs, ed, topk, gk, gn)
+    check_rows(orc, Y, ref)
+
+
+def test_moe_blockscale_padding_and_malformed_entries(orc):
+    """-1 padding, an expert past E and words with bit 31 set are skipped; a
+    token past T reads zero."""
+    require_gpu()
+    T, E, topk, K, N = 200, 3, 2, 256, 256
+    _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, T, E, topk, K, N, 5)
+    rng = np.random.default_rng(6)
+    xs = (rng.random((T, 4)) * 0.01).astype(np.float32)
+    ws = (rng.random((E, 4, 4)) * 0.001).astype(np.float32)
+    bad = np.concatenate([ed, np.array([-1, 9, -0x7FFFFFFF], np.int32)])
+    g2 = gather.copy()
+    g2[3] = T * topk + 10
+    Y = run_moe_bs(X, W, hist, offs, g2, bad, topk, xs, ws, 64, 64)
+    ref = orc.moe_blockscale_ref(X, W, xs, ws, None, gather, hist, offs, ed, topk, 64, 64)
+    ref[3] = 0.0
+    check_rows(orc, Y, ref)
+
+
+def test_moe_blockscale_mixtral_group128(orc):
+    """Mixtral-8x7B gate/up (T=4096, E=8, top-2, K=4096, N=28672) with 1x128
+    activation groups and 128x128 weight blocks, every routed row against the
+    fp32 oracle with the same group scales."""
+    require_gpu()
+    T, E, topk, K, N = 4096, 8, 2, 4096, 28672
+    hist, offs, gather, ed = mixtral_routing(orc, T, E, topk, 77)
+    X, xs = orc.quant_rowwise(orc.randn_bf16((T, K), seed=78), 128, "fp8")   # xs [T, K/128]
+    W, _ = device_weights_fp8(E, N, K, seed=79)
+    rng = np.random.default_rng(80)
+    ws = (rng.random((E, K // 128, N // 128)) * 2e-4 + 1e-4).astype(np.float32)
+    Y = run_moe_bs(X, W, hist, offs, gather, ed, topk, xs, ws, 128, 128)
+    ref = orc.moe_ref_f32(X, W, xs, ws, gather, hist, offs, ed, topk, group_k=128, group_n=128)
+    assert not np.isnan(ref).any()
+    assert_gemm_close(Y, ref, "moe blockscale mixtral g128")
 
 
 def test_moe_hipkittens_modules(orc):
     """moe_op_gemm_a8w8_tk.moe_a8w8 and moe_op_gemm_a8w8_blockscale_tk with the
-    reference argument orders give the C-ABI bytes; [E, K, N] weights (the
-    reference test's layout, stride_wk != 1) are rejected with a clear error."""
+    reference argument orders give the C-ABI bytes, with K-contiguous [E, N, K]
+    weights and with the reference test's N-contiguous [E, K, N] ones
+    (stride_wk = N, stride_wn = 1, tests/test_moe.py:723-729)."""
     require_gpu()
     import hipkittens as hk
 
     T, E, topk, K, N = 96, 4, 2, 256, 256
     _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 21)
     Xd, Wd = dev_u8(X).view(torch.float8_e4m3fn), dev_u8(W).view(torch.float8_e4m3fn)
+    Wkn = Wd.transpose(1, 2).contiguous()  # [E, K, N]
     hd, od, gd, edd = dev_i32(hist), dev_i32(offs), dev_i32(gather), dev_i32(ed)
     xsd, wsd = dev_f32(np.array([0.02], np.float32)), dev_f32(ws[:, 0].copy())
     bias = dev_f32(np.random.default_rng(1).standard_normal((E, N)).astype(np.float32))
     ref = hkq.moe_a8w8(Xd, Wd, hd, od, edd, topk, gather=gd, x_scale=xsd, w_scale=wsd, bias=bias)
-    Y = torch.zeros((T * topk, N), dtype=torch.bfloat16, device="cuda")
     grid_m, grid_n = len(ed), (N + 127) // 128
-    hk.moe.a8w8.moe_a8w8(Xd, Wd, Y, xsd, wsd, bias, gd, hd, od, edd, N, K, grid_m, grid_n, topk,
-                         N, 1, K, 1, N * K, 1, K, False, 0.0)
-    torch.cuda.synchronize()
-    assert torch.equal(Y, ref)
-    with pytest.raises(ValueError, match="K-contiguous"):
-        hk.moe.a8w8.moe_a8w8(Xd, Wd, Y, xsd, wsd, bias, gd, hd, od, edd, N, K, grid_m, grid_n, topk,
-                             N, 1, K, 1, N * K, N, 1, False, 0.0)
+    for Wx, swk, swn in ((Wd, 1, K), (Wkn, N, 1)):
+        Y = torch.zeros((T * topk, N), dtype=torch.bfloat16, device="cuda")
+        hk.moe.a8w8.moe_a8w8(Xd, Wx, Y, xsd, wsd, bias, gd, hd, od, edd, N, K, grid_m, grid_n, topk,
+                             N, 1, K, 1, N * K, swk, swn, False, 0.0)
+        torch.cuda.synchronize()
+        assert torch.equal(Y, ref)
     # blockscale module, group_k == K: per-token x per-channel scales (strided [T,1] / [E,1,N])
     xs_t = dev_f32(xs.reshape(T, 1))
     ws_c = dev_f32(ws.reshape(E, 1, N))
     ref2 = hkq.moe_a8w8(Xd, Wd, hd, od, edd, topk, gather=gd, x_scale=dev_f32(xs.reshape(-1)), w_scale=dev_f32(ws))
-    Y2 = torch.zeros((T * topk, N), dtype=torch.bfloat16, device="cuda")
-    hk.moe.a8w8_blockscale.moe_a8w8_blockscale(Xd, Wd, Y2, xs_t, ws_c, None, gd, hd, od, edd, N, K, K, 1,
-                                                grid_m, grid_n, topk, N, 1, K, 1, N * K, 1, K, 1, 1, N, N, 1)
+    for Wx, swk, swn in ((Wd, 1, K), (Wkn, N, 1)):
+        Y2 = torch.zeros((T * topk, N), dtype=torch.bfloat16, device="cuda")
+        hk.moe.a8w8_blockscale.moe_a8w8_blockscale(Xd, Wx, Y2, xs_t, ws_c, None, gd, hd, od, edd, N, K, K, 1,
+                                                    grid_m, grid_n, topk, N, 1, K, 1, N * K, swk, swn, 1, 1, N, N, 1)
+        torch.cuda.synchronize()
+        assert torch.equal(Y2, ref2)
+
+
+def test_moe_blockscale_reference_call(orc):
+    """The reference's own call (tests/test_moe.py:771-815): 64 tokens, 8
+    experts, top-2, K = N = 256, group_k = group_n = 64, W [E, K, N]
+    (N-contiguous), X_scale [T, K/64], W_scale [E, K/64, N/64], grid_n over
+    64-column tiles, through moe_op_gemm_a8w8_blockscale_tk with its argument
+    list unchanged (E4M3FN codes in place of the int8 values), against the
+    oracle."""
+    require_gpu()
+    import hipkittens as hk
+
+    num_tokens, num_experts, top_k, K_dim, N_dim, group_k, group_n = 64, 8, 2, 256, 256, 64, 64
+    _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, num_tokens, num_experts, top_k, K_dim, N_dim, 42)
+    g = torch.Generator().manual_seed(42)
+    X_scale = torch.rand(num_tokens, K_dim // group_k, generator=g) * 0.01
+    W_scale = torch.rand(num_experts, K_dim // group_k, N_dim // group_n, generator=g) * 0.01
+    Wkn = np.ascontiguousarray(W.transpose(0, 2, 1))  # [E, K, N]
+    grid_m, grid_n = len(ed), (N_dim + 63) // 64
+    Y = torch.zeros(num_tokens * top_k, N_dim, dtype=torch.bfloat16, device="cuda")
+    keep = (dev_u8(X).view(torch.float8_e4m3fn), dev_u8(Wkn).view(torch.float8_e4m3fn), X_scale.cuda(),
+            W_scale.cuda(), dev_i32(gather), dev_i32(hist), dev_i32(offs), dev_i32(ed))
+    Xd, Wd, xsd, wsd, gd, hd, od, edd = keep
+    hk.moe.a8w8_blockscale.moe_a8w8_blockscale(
+        Xd, Wd, Y, xsd, wsd, None, gd, hd, od, edd,
+        N_dim, K_dim, group_k, group_n, grid_m, grid_n, top_k,
+        N_dim, 1,
+        K_dim, 1,
+        K_dim * N_dim, N_dim, 1,
+        K_dim // group_k, 1,
+        (K_dim // group_k) * (N_dim // group_n), N_dim // group_n, 1)
     torch.cuda.synchronize()
-    assert torch.equal(Y2, ref2)
-    with pytest.raises(ValueError, match="group_k"):
-        hk.moe.a8w8_blockscale.moe_a8w8_blockscale(Xd, Wd, Y2, xs_t, ws_c, None, gd, hd, od, edd, N, K, 128, 1,
-                                                    grid_m, grid_n, topk, N, 1, K, 1, N * K, 1, K, 1, 1, N, N, 1)
+    ref = orc.moe_blockscale_ref(X, Wkn, X_scale.numpy(), W_scale.numpy(), None, gather, hist, offs, ed, top_k,
+                                 group_k, group_n, w_layout="ekn")
+    check_rows(orc, host_bf16_f32(Y), ref)

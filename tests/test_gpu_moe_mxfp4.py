@@ -31,11 +31,12 @@ def problem(orc, T, E, K, N, seed):
 
 
 # (1, ...) and (16, ...) have at most 32 valid gate ids and a small tiled grid:
-# the decode (streaming) kernel, with K-steps uneven over its 4 waves;
+# the decode (streaming) kernel, with K-steps uneven over its 4 waves and 16
+# columns per workgroup, or 64 (N > 4096: (1, 8, 2, 512, 8192));
 # (5, 8, 2, 384, 4160) has few ids but a large tiled grid, so it stays tiled.
 @pytest.mark.parametrize("T,E,topk,K,N", [(64, 8, 2, 256, 256), (1024, 8, 2, 2048, 1024), (300, 4, 1, 384, 520),
                                           (77, 16, 4, 512, 64), (1, 8, 2, 256, 512), (5, 8, 2, 384, 4160),
-                                          (16, 8, 2, 640, 1000)])
+                                          (16, 8, 2, 640, 1000), (1, 8, 2, 512, 8192), (2, 8, 2, 384, 4400)])
 def test_moe_mxfp4(orc, T, E, topk, K, N):
     require_gpu()
     Aq, As, Bq, Bs = problem(orc, T, E, K, N, T + K)
@@ -115,10 +116,11 @@ def test_moe_mxfp4_decode_layouts(orc):
 
 
 def test_moe_mxfp4_module_reference_call(orc):
-    """tests/test_moe.py:902-936 of the reference: random E2M1 bytes and e8m0
-    scales in [120, 134), per-tensor and per-expert scales, routed weights. The
-    reference's [E, K/2, N] weights raise ValueError naming the transpose; the
-    transposed call matches the oracle."""
+    """tests/test_moe.py:902-936 of the reference, argument list unchanged:
+    random E2M1 bytes and e8m0 scales in [120, 134), B [E, K/2, N] and B_mx_scale
+    [E, K/32, N] (N-contiguous), per-tensor and per-expert scales, routed
+    weights; against the oracle on the same codes. The K-contiguous form of the
+    same weights gives the same bytes."""
     require_gpu()
     import hipkittens as hk
     num_tokens, num_experts, top_k, K, N, block_m, mx = 64, 8, 2, 256, 256, 128, 32
@@ -133,20 +135,74 @@ def test_moe_mxfp4_module_reference_call(orc):
     num_padded = len(s)
     w = torch.rand(num_padded, dtype=torch.float32, generator=g)
     C = torch.zeros(num_padded, N, dtype=torch.bfloat16, device="cuda")
-    args = (dev_u8(A.numpy()), dev_u8(B.numpy()), C, dev_u8(A_mx.numpy()), dev_u8(B_mx.numpy()), A_scale.cuda(),
-            B_scale.cuda(), w.cuda(), dev_i32(s), dev_i32(eids), N, K, num_tokens * top_k, top_k, True)
-    with pytest.raises(ValueError, match="transpose"):
-        hk.moe.mxfp4.moe_mxfp4(*args, K // 2, 1, (K // 2) * N, N, 1, N, 1, K // mx, 1, (K // mx) * N, N, 1,
-                               num_padded // block_m, (N + 127) // 128)
-    Bt = B.transpose(1, 2).contiguous()
-    Bmt = B_mx.transpose(1, 2).contiguous()
-    args = args[:1] + (dev_u8(Bt.numpy()),) + args[2:4] + (dev_u8(Bmt.numpy()),) + args[5:]
-    hk.moe.mxfp4.moe_mxfp4(*args, K // 2, 1, (K // 2) * N, 1, K // 2, N, 1, K // mx, 1, (K // mx) * N, 1, K // mx,
+    keep = (dev_u8(A.numpy()), dev_u8(B.numpy()), dev_u8(A_mx.numpy()), dev_u8(B_mx.numpy()), A_scale.cuda(),
+            B_scale.cuda(), w.cuda(), dev_i32(s), dev_i32(eids))
+    Ad, Bd, Amd, Bmd, asd, bsd, wd, sd, ed = keep
+    hk.moe.mxfp4.moe_mxfp4(Ad, Bd, C, Amd, Bmd, asd, bsd, wd, sd, ed, N, K, num_tokens * top_k, top_k, True,
+                           K // 2, 1, (K // 2) * N, N, 1, N, 1, K // mx, 1, (K // mx) * N, N, 1,
                            num_padded // block_m, (N + 127) // 128)
     torch.cuda.synchronize()
+    Bt = B.transpose(1, 2).contiguous()
+    Bmt = B_mx.transpose(1, 2).contiguous()
     ref = orc.moe_mxfp4_ref(A.numpy(), A_mx.numpy(), Bt.numpy(), Bmt.numpy(), 0.01, B_scale.numpy(), w.numpy(), s,
                             eids, N, num_tokens * top_k, top_k, True, num_padded)
     got = C.float().cpu().numpy()
     rows = ~np.isnan(ref).any(axis=1)
     assert_gemm_close(got[rows], ref[rows], "reference call")
     assert np.all(got[~rows] == 0)
+    C2 = torch.zeros_like(C)
+    Btd, Bmtd = dev_u8(Bt.numpy()), dev_u8(Bmt.numpy())
+    hk.moe.mxfp4.moe_mxfp4(Ad, Btd, C2, Amd, Bmtd, asd, bsd, wd, sd, ed, N, K, num_tokens * top_k, top_k, True,
+                           K // 2, 1, (K // 2) * N, 1, K // 2, N, 1, K // mx, 1, (K // mx) * N, 1, K // mx,
+                           num_padded // block_m, (N + 127) // 128)
+    torch.cuda.synchronize()
+    assert torch.equal(C, C2)
+
+
+def test_moe_pack_kmajor(orc):
+    """The prepack entry point on ragged shapes and padded strides: an exact
+    byte transpose of every expert plane, bytes outside the destination rows
+    untouched."""
+    require_gpu()
+    rng = np.random.default_rng(3)
+    for E, R, N, pad_r, pad_n in ((3, 100, 70, 0, 0), (2, 256, 512, 16, 32), (1, 64, 17, 5, 3)):
+        src = rng.integers(0, 256, (E, R, N + pad_r), dtype=np.uint8)
+        dst = torch.full((E, N, R + pad_n), 0xAB, dtype=torch.uint8, device="cuda")
+        sd = dev_u8(src)
+        hkq.call("hkq_moe_pack_kmajor", sd.data_ptr(), dst.data_ptr(), E, R, N, sd.stride(0), sd.stride(1),
+                 dst.stride(0), dst.stride(1), torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        got = dst.cpu().numpy()
+        assert np.array_equal(got[:, :, :R], src[:, :, :N].transpose(0, 2, 1))
+        assert np.all(got[:, :, R:] == 0xAB)
+
+
+@pytest.mark.parametrize("K,N", [(4096, 28672), (14336, 4096)])
+def test_moe_mxfp4_mixtral_full(orc, K, N):
+    """Mixtral-8x7B sizes (T=4096, E=8, top-2; gate/up K=4096, N=28672; down
+    K=14336, N=4096) on align_block_size routing from seeded softmax top-2:
+    weights ~N(0, 0.02) drawn on the device and MX-quantized by the GPU
+    quantizer (bit-exact with the oracle's, tests/test_gpu_quant.py), every
+    output row against the fp32 oracle (oracle.moe_mxfp4_ref_f32)."""
+    require_gpu()
+    T, E, topk = 4096, 8, 2
+    gl = torch.Generator(device="cpu").manual_seed(K)
+    logits = torch.randn(T, E, generator=gl)
+    ids = torch.topk(torch.softmax(logits, -1), topk, dim=-1).indices.numpy().astype(np.int32).ravel()
+    s, eids, _, _ = orc.align_block_size(ids, E, 128)
+    Aq, As = orc.mx_quant_fp4(orc.randn_bf16((T, K), seed=K + 1))
+    g = torch.Generator(device="cuda").manual_seed(K + 2)
+    wb = (torch.randn(E * N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    Bq_d, Bs_d = hkq.mx_quant(wb, True)
+    torch.cuda.synchronize()
+    del wb
+    Bq = Bq_d.cpu().numpy().reshape(E, N, K // 2)
+    Bs = Bs_d.cpu().numpy().reshape(E, N, K // 32)
+    rng = np.random.default_rng(K)
+    w = rng.random(T * topk).astype(np.float32)
+    C = hkq.moe_mxfp4(dev_u8(Aq), dev_u8(As), Bq_d.view(E, N, K // 2), Bs_d.view(E, N, K // 32), dev_i32(s),
+                      dev_i32(eids), T * topk, topk, topk_weights=dev_f32(w))
+    torch.cuda.synchronize()
+    ref = orc.moe_mxfp4_ref_f32(Aq, As, Bq, Bs, None, None, w, s, eids, N, T * topk, topk, True, T * topk)
+    assert not np.isnan(ref).any()
+    assert_gemm_close(C.float().cpu().numpy(), ref, f"moe mxfp4 mixtral K={K} N={N}")

@@ -85,3 +85,49 @@ def test_blockscale_mul_add_ref(orc):
                           orc.gemm_blockscale_ref(A, B, sa, sb, 128, 1))
     assert np.array_equal(orc.gemm_blockscale_mul_add_ref(A, B, sa, sb, zero, cb, 128, 1),
                           orc.bf16_bits_to_f32(cb).astype(np.float64))
+
+
+def _close_to_fp64(f32, f64, a_abs_b_abs):
+    """fp32-product reference within 2^-16 of the sum of |terms| of the fp64 one."""
+    assert f32.dtype == np.float32 and f32.shape == f64.shape
+    assert np.all(np.abs(f32.astype(np.float64) - f64) <= 2.0 ** -16 * a_abs_b_abs + 1e-30)
+
+
+def test_fp32_references_match_fp64(orc):
+    """The fp32 full-output references (used at BASELINE sizes) against the
+    fp64 ones on ragged shapes with per-row/column/group scales that differ
+    everywhere, so a transposed or mis-indexed scale would fail."""
+    M, N, K = 200, 260, 1024
+    xa = orc.randn_bf16((M, K), seed=11)
+    xw = orc.randn_bf16((N, K), seed=12, std=0.02)
+    A, sa = orc.quant_rowwise(xa, None, "fp8")
+    B, sb = orc.quant_rowwise(xw, None, "fp8")
+    a, b = orc.e4m3_decode(A).astype(np.float64), orc.e4m3_decode(B).astype(np.float64)
+    absum = (np.abs(a) @ np.abs(b).T) * np.abs(sa).reshape(-1, 1) * np.abs(sb).reshape(1, -1)
+    _close_to_fp64(orc.gemm_a8w8_ref_f32(A, B, sa, sb), orc.gemm_a8w8_ref(A, B, sa, sb), absum)
+
+    A1, sa1 = orc.quant_rowwise(xa, 128, "fp8")              # [M, K/128]
+    for gn in (128, 1):
+        Np = (N + 127) // 128 * 128
+        xw2 = orc.randn_bf16((Np, K), seed=13, std=0.02)
+        if gn == 128:
+            B1, sbt = orc.quant_block_2d(xw2)
+            sb1 = np.ascontiguousarray(sbt.T)                   # [K/128, N/128]
+        else:
+            B1, sbr = orc.quant_rowwise(xw2, 128, "fp8")
+            sb1 = np.ascontiguousarray(sbr.T[:, :N])            # [K/128, N]
+        B1 = np.ascontiguousarray(B1[:N])
+        ref = orc.gemm_blockscale_ref(A1, B1, sa1, sb1, 128, gn)
+        a1, b1 = orc.e4m3_decode(A1).astype(np.float64), orc.e4m3_decode(B1).astype(np.float64)
+        absum = np.zeros((M, N))
+        for g in range(K // 128):
+            s = slice(128 * g, 128 * g + 128)
+            absum += (np.abs(a1[:, s]) @ np.abs(b1[:, s]).T) * np.abs(sa1[:, g:g + 1]) * \
+                np.abs(np.repeat(sb1[g], gn)[:N])[None, :]
+        _close_to_fp64(orc.gemm_blockscale_ref_f32(A1, B1, sa1, sb1, 128, gn), ref, absum)
+
+    Aq, As = orc.mx_quant_fp4(xa)
+    Bq, Bs = orc.mx_quant_fp4(xw)
+    da, db = orc.mx_fp4_dequant_f32(Aq, As).astype(np.float64), orc.mx_fp4_dequant_f32(Bq, Bs).astype(np.float64)
+    _close_to_fp64(orc.gemm_mxfp4_ref_f32(Aq, As, Bq, Bs), orc.gemm_mxfp4_ref(Aq, As, Bq, Bs),
+                   np.abs(da) @ np.abs(db).T)
