@@ -15,6 +15,7 @@
 //                        kernel.cpp:59-203, batched_gemm_bf16/kernel.cpp:53-187;
 //                        formulas tests/test_gemm.py:316-390).
 #include <algorithm>
+#include <mutex>
 
 #include "gemm_mainloop.h"
 #include "hkq_host.h"
@@ -700,6 +701,62 @@ int hkq_gemm_a8w8_ws(const void* A, const void* B, const float* sa, const float*
 int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M, int64_t N,
                   int64_t K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t stream) {
     return hkq_gemm_a8w8_ws(A, B, sa, sb, C, M, N, K, lda, ldb, ldc, nullptr, 0, stream);
+}
+
+}  // extern "C"
+
+// Split-K partial sums of hkq_gemm_a8w8_noalloc: a library-owned workspace
+// that each GPU holds from the library's load to the end of the process, so
+// that the entry point allocates nothing. Its size bounds every split plan on
+// 256 CUs (at most 1.5 * 256 tile splits of 128 x 128 fp32 sums: 25.2 MB).
+constexpr size_t HKQ_SCRATCH_BYTES = size_t(32) << 20;
+static __device__ __align__(256) uint8_t scratch[HKQ_SCRATCH_BYTES];
+
+// Device address of `scratch` on the current device, looked up once per device
+// with that device current (the host-side name is only a stand-in for it).
+static int scratch_address(void** out) {
+    constexpr int MAXDEV = 64;
+    static void* addr[MAXDEV] = {};
+    static std::mutex mu;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= MAXDEV) {
+        set_error("hkq_gemm_a8w8_noalloc: no usable current device (%s)", hipGetErrorString(e));
+        return e != hipSuccess ? (int)e : (int)hipErrorInvalidDevice;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_error("hkq_gemm_a8w8_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+            return e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+        }
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return 0;
+}
+
+extern "C" {
+
+size_t hkq_gemm_a8w8_noalloc_max_workspace(void) { return HKQ_SCRATCH_BYTES; }
+
+int hkq_gemm_a8w8_noalloc(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M,
+                          int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, hipStream_t stream) {
+    // the same argument checks and plan as hkq_gemm_a8w8_ws, whose launches run
+    // unchanged on the library's scratch workspace
+    const size_t need = hkq_gemm_a8w8_workspace(M, N, K);
+    if (need > HKQ_SCRATCH_BYTES) {
+        set_error("hkq_gemm_a8w8_noalloc: the split plan of %lldx%lldx%lld needs %zu workspace bytes, more than the "
+                  "%zu-byte library scratch; use hkq_gemm_a8w8_ws with a caller workspace",
+                  (long long)M, (long long)N, (long long)K, need, HKQ_SCRATCH_BYTES);
+        return (int)hipErrorInvalidValue;
+    }
+    void* ws = nullptr;
+    if (need > 0)
+        if (int e = scratch_address(&ws)) return e;
+    return hkq_gemm_a8w8_ws(A, B, sa, sb, C, M, N, K, lda, ldb, ldc, ws, need, stream);
 }
 
 size_t hkq_gemm_mxfp4_workspace(int64_t M, int64_t N, int64_t K) {

@@ -30,6 +30,8 @@ SIGNATURES = {
     "hkq_gemm_mxfp4": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "hkq_gemm_a8w8_workspace": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "hkq_gemm_a8w8_ws": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, ctypes.c_size_t, _P]),
+    "hkq_gemm_a8w8_noalloc_max_workspace": (ctypes.c_size_t, []),
+    "hkq_gemm_a8w8_noalloc": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "hkq_gemm_mxfp4_workspace": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "hkq_gemm_mxfp4_ws": (_I, [_P, _P, _P, _P, _P] + [_I64] * 8 + [_P, ctypes.c_size_t, _P]),
     "hkq_gemm_blockscale": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),

@@ -132,6 +132,19 @@ int hkq_gemm_a8w8_ws(const void* A, const void* B, const float* sa, const float*
                      int64_t K, int64_t lda, int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes,
                      hkq_stream_t stream);
 
+/* hkq_gemm_a8w8_ws without a caller workspace and without allocating: the
+ * split-K partials go to a library-owned device array of
+ * hkq_gemm_a8w8_noalloc_max_workspace() bytes (32 MiB) that each GPU the
+ * library runs on holds until the process ends. Shapes whose plan needs more
+ * are rejected with hipErrorInvalidValue (none on a 256-CU MI355X). Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (several
+ * streams or host threads) race and must be serialized by the caller. No
+ * counterpart in the reference; for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+size_t hkq_gemm_a8w8_noalloc_max_workspace(void);
+int hkq_gemm_a8w8_noalloc(const void* A, const void* B, const float* sa, const float* sb, void* C, int64_t M,
+                          int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, hkq_stream_t stream);
+
 /* MXFP4 A4W4: C = bf16(sum_k e2m1(A) 2^(As-127) e2m1(B) 2^(Bs-127)).
  * A u8 [M, lda >= K/2], As u8 [M, ldsa >= K/32], B u8 [N, ldb], Bs u8 [N, ldsb].
  * K % 128 == 0, N % 4 == 0, ldc % 4 == 0. Replaces gemm_afp4wfp4_tk.dispatch (kernels/gemm-basic/gemm_afp4wfp4/kernel.cpp:147-159),
