@@ -17,7 +17,9 @@
 #include <algorithm>
 #include <mutex>
 
-#include "gemm_mainloop.h"
+#include <cstdlib>
+
+#include "gemm_stream.h"
 #include "hkq_host.h"
 
 namespace hkq {
@@ -212,6 +214,178 @@ __global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_g
         tile_coords(p.n_whole + t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
         dense_block<MODE, DENSE_TM / 2, KTB>(p, tm, tn, half, smem);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent streaming kernel (128-byte K-tiles, K-tiles per tile a multiple
+// of 8, one 2-D GEMM without bias): workgroup b of G computes whole tiles
+// b, b + G, ... < n_whole as one K-tile stream (gemm_stream.h), then, when the
+// last round is split, the M half (b >> 3) & 1 of tile n_whole + 8*(b >> 4) +
+// (b & 7) as a stream of one. Epilogues store C from registers: each lane
+// holds 4 consecutive columns of one row per register group, written as one
+// 8-byte store (the lanes of a wave cover 32 rows x 16 bytes per store; the
+// stores of the wave's 4 groups fill whole 64-byte pieces of each row, which
+// the L2 merges). A8W8 row/column scales of tile k are prefetched into LDS
+// slot k & 1 when the tile starts.
+constexpr int STREAM_SCL = 2 * DENSE_BM * 4;  // one scale slot: 256 row + 256 column scales
+
+template <int MODE>
+constexpr int stream_lds() {
+    using Whole = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM, DENSE_TN, 128>;
+    return 2 * Whole::STAGE + Whole::SB_BYTES + (MODE == MODE_A8W8 ? 2 * STREAM_SCL : 0);
+}
+
+// Tile k of the stream: tile id first + k * stride in tile_coords order,
+// rows [tm*256 + half*BM, +BM) of it.
+template <int BM>
+struct DenseSeq {
+    const DenseParams* p;
+    int tiles, KT;
+    uint32_t lsa, lsb;
+    int first, stride, half;
+    __device__ void coords(int k, int& m0, int& n0) const {
+        int tm, tn;
+        tile_coords(first + k * stride, p->tiles_m, p->tiles_n, p->group_m, tm, tn);
+        m0 = tm * DENSE_BM + half * BM;
+        n0 = tn * DENSE_BN;
+    }
+    __device__ StreamSrc src(int k) const {
+        int m0, n0;
+        coords(k, m0, n0);
+        const int rows_a = min(p->M - m0, BM), rows_b = min(p->N - n0, DENSE_BN);
+        StreamSrc s;
+        s.a = p->A + (int64_t)m0 * p->lda;
+        s.b = p->B + (int64_t)n0 * p->ldb;
+        s.a_bytes = (uint32_t)min((int64_t)rows_a * p->lda, (int64_t)0x7FFFFFFF);
+        s.b_bytes = (uint32_t)min((int64_t)rows_b * p->ldb, (int64_t)0x7FFFFFFF);
+        s.as = static_cast<const uint8_t*>(p->sa) + (int64_t)m0 * p->lsa;
+        s.bs = static_cast<const uint8_t*>(p->sb) + (int64_t)n0 * p->lsb;
+        s.as_bytes = (uint32_t)min((int64_t)rows_a * p->lsa, (int64_t)0x7FFFFFFF);
+        s.bs_bytes = (uint32_t)min((int64_t)rows_b * p->lsb, (int64_t)0x7FFFFFFF);
+        return s;
+    }
+};
+
+template <int MODE, int TM, int BM>
+struct DirectEpi {
+    static constexpr int TN = DENSE_TN;
+    const DenseSeq<BM>* seq;
+    const DenseParams* p;
+    HKQ_LDS uint8_t* scl;  // 2 slots of STREAM_SCL bytes
+    int lane, wave;
+    __device__ void begin(int k) {
+        if constexpr (MODE == MODE_A8W8) {
+            int m0, n0;
+            seq->coords(k, m0, n0);
+            const int rows_a = min(p->M - m0, BM), rows_b = min(p->N - n0, DENSE_BN);
+            HKQ_LDS uint8_t* slot = scl + (k & 1) * STREAM_SCL;
+            const uint32_t off = (uint32_t)(wave * 64 + lane) * 4u;
+            lds_load4(static_cast<const float*>(p->sa) + m0, (uint32_t)rows_a * 4u, slot + wave * 256, off);
+            lds_load4(static_cast<const float*>(p->sb) + n0, (uint32_t)rows_b * 4u, slot + DENSE_BM * 4 + wave * 256, off);
+        }
+    }
+    // Stores: per (n-tile i, m-tile j) the lane's 16 sums are 4 groups of 4
+    // consecutive columns; v_permlane32_swap exchanges half of them between
+    // lanes l and l + 32 so that each lane holds 8 consecutive columns of its
+    // row, written as one 16-byte buffer store (two per (i, j), 32 per wave;
+    // a store covers 32 rows x 32 bytes). Lanes whose row or columns lie
+    // outside C get an offset past the buffer, so every wave issues the same
+    // stores whatever the tile's edge. N % 4 == 0 leaves one partial case: 8
+    // columns of which the last 4 lie past N (the store would run into the
+    // next row); in a wave whose columns end there, such lanes write their
+    // first 4 columns with an extra 8-byte store instead.
+    __device__ void end(int k, v16f (&acc)[TN][TM]) {
+        int m0, n0;
+        seq->coords(k, m0, n0);
+        const int wm = wave / DENSE_WAVES_N, wn = wave % DENSE_WAVES_N;
+        const int khalf = lane >> 5, r = lane & 31;
+        const HKQ_LDS float* sl = reinterpret_cast<const HKQ_LDS float*>(scl + (k & 1) * STREAM_SCL);
+        const int mw0 = m0 + wm * TM * 32, nw0 = n0 + wn * TN * 32;
+        uint16_t* base = p->C + (int64_t)mw0 * p->ldc + nw0;
+        const auto rc = make_rsrc(base, 0x7FFFFFFFu);
+        const int rows = p->M - mw0, cols = p->N - nw0;  // of the wave's sub-tile inside C
+        const bool ragged = cols < TN * 32 && (cols & 7) != 0;
+        // The lane's offsets are rebuilt from an opaque value each tile: left
+        // visible, the compiler hoists every (row, column) offset out of the
+        // tile loop as an invariant and spills them.
+        uint32_t roff[TM];
+        float rs[TM];
+        const int kc = 8 * khalf;
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+            const int m = j * 32 + r;
+            roff[j] = m < rows ? (uint32_t)((m * p->ldc + kc) * 2) : OOB;
+            asm volatile("" : "+v"(roff[j]));
+            rs[j] = MODE == MODE_A8W8 ? sl[wm * TM * 32 + m] : 1.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < TN; ++i) {
+            v4f cs[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                cs[g] = MODE == MODE_A8W8 ? *reinterpret_cast<const HKQ_LDS v4f*>(sl + DENSE_BM + wn * TN * 32 + i * 32 + 8 * g + 4 * khalf)
+                                          : v4f{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                // Explicit reads out of the accumulator registers, in store
+                // order: the compiler's own copies tend to be hoisted to the
+                // start of the epilogue, all 256 of them live at once.
+                float v[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[i][j][e]));
+                uint32_t w[4][2];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float a = rs[j];
+                    w[g][0] = pk_bf16(v[4 * g + 0] * a * cs[g][0], v[4 * g + 1] * a * cs[g][1]);
+                    w[g][1] = pk_bf16(v[4 * g + 2] * a * cs[g][2], v[4 * g + 3] * a * cs[g][3]);
+                }
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    // lanes < 32 end with columns 16q + 0..7, lanes >= 32 with 16q + 8..15
+                    const auto s0 = __builtin_amdgcn_permlane32_swap(w[2 * q][0], w[2 * q + 1][0], false, false);
+                    const auto s1 = __builtin_amdgcn_permlane32_swap(w[2 * q][1], w[2 * q + 1][1], false, false);
+                    const int c = i * 32 + 16 * q;  // the lane's 8 columns start at c + kc
+                    const int left = cols - c;      // columns of C from c on
+                    const uint32_t off = kc + 8 <= left ? roff[j] + (uint32_t)(c * 2) : OOB;
+                    __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]}, rc, off, 0, 0);
+                    if (ragged) {
+                        const uint32_t off4 = kc + 4 == left ? roff[j] + (uint32_t)(c * 2) : OOB;
+                        __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)s0[0], (int)s1[0]}, rc, off4, 0, 0);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+};
+
+template <int MODE, int TM>
+__device__ __forceinline__ void dense_stream(const DenseParams& p, int tiles, int first, int stride, int half,
+                                             HKQ_LDS uint8_t* smem) {
+    constexpr int WM = DENSE_WAVES_M, WN = DENSE_WAVES_N, TN = DENSE_TN;
+    using Cfg = DenseCfg<MODE, WM, WN, TM, TN, 128>;
+    constexpr int BM = Cfg::BM;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    DenseSeq<BM> seq{&p, tiles, p.kbytes / 128, (uint32_t)p.lsa, (uint32_t)p.lsb, first, stride, half};
+    DirectEpi<MODE, TM, BM> epi{&seq, &p, smem + stream_lds<MODE>() - (MODE == MODE_A8W8 ? 2 * STREAM_SCL : 0), lane,
+                                wave};
+    const auto a_off = dense_offs<Cfg::NW, 128, Cfg::LA>(wave, lane, p.lda);
+    const auto b_off = dense_offs<Cfg::NW, 128, Cfg::LB>(wave, lane, p.ldb);
+    v16f acc[TN][TM];
+    gemm_stream<MODE, WM, WN, TM, TN>(seq, a_off, b_off, smem, lane, wave, acc, epi);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_stream_kernel(const DenseParams p) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
+    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+    const int b = blockIdx.x, G = gridDim.x;
+    const int mine = b < p.n_whole ? (p.n_whole - 1 - b) / G + 1 : 0;
+    if (mine > 0) dense_stream<MODE, DENSE_TM>(p, mine, b, G, 0, smem);
+    const int t = 8 * (b >> 4) + (b & 7);
+    if (t < p.n_split) dense_stream<MODE, DENSE_TM / 2>(p, 1, p.n_whole + t, 0, (b >> 3) & 1, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -576,6 +750,26 @@ static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
     const int64_t split = (!batched && last > 0 && 2 * last <= ncu && p.M > DENSE_BM / 2) ? last : 0;
     p.n_whole = (int)(tiles - split);
     p.n_split = (int)split;
+    if constexpr (KTB == 128 && MODE != MODE_MXFP4) {
+        // the persistent streaming kernel: one workgroup per CU, whole tiles as
+        // a K-tile stream (needs K-tiles per tile % 8 == 0; one 2-D GEMM without
+        // bias, C's rows 16-byte aligned); HKQ_DENSE_STREAM=0 selects the
+        // one-tile-per-workgroup kernel
+        static const bool stream_on = [] {
+            const char* e = std::getenv("HKQ_DENSE_STREAM");
+            return !(e && e[0] == '0');
+        }();
+        if (stream_on && ncu > 0 && !batched && p.bias == nullptr && (p.kbytes / 128) % 8 == 0 && p.ldc % 8 == 0) {
+            constexpr int SLDS = stream_lds<MODE>();
+            static_assert(SLDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
+            auto skern = dense_stream_kernel<MODE>;
+            static bool sattr = false;
+            if (int e = set_lds(skern, SLDS, sattr)) return e;
+            const int64_t g = std::min<int64_t>(ncu, std::max<int64_t>(p.n_whole, 2 * ((split + 7) / 8 * 8)));
+            skern<<<dim3((unsigned)g), 64 * DENSE_WAVES_M * DENSE_WAVES_N, SLDS, stream>>>(p);
+            return hkq_launch_status();
+        }
+    }
     const int64_t nblk = p.n_whole + 2 * ((split + 7) / 8 * 8);
     kern<<<dim3((unsigned)nblk, (unsigned)std::max(1, p.batch)), 64 * DENSE_WAVES_M * DENSE_WAVES_N, LDS, stream>>>(p);
     return hkq_launch_status();

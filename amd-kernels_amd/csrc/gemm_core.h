@@ -74,6 +74,16 @@ __device__ __forceinline__ void lds_load16(const void* base, uint32_t bytes, HKQ
                  : "s"(m0), "v"(off), "s"(buffer_desc(base, bytes))
                  : "memory", "m0");
 }
+// lds_load16 whose buffer descriptor is made wave-uniform explicitly: for
+// sources the compiler cannot prove uniform (a source switched inside a loop),
+// which would otherwise land in VGPRs and fail the instruction's SGPR operand.
+__device__ __forceinline__ void lds_load16_u(const void* base, uint32_t bytes, HKQ_LDS void* dst, uint32_t off) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint32_t n = __builtin_amdgcn_readfirstlane(bytes);
+    lds_load16(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo), n, dst, off);
+}
 __device__ __forceinline__ void lds_load4(const void* base, uint32_t bytes, HKQ_LDS void* dst, uint32_t off) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"

@@ -39,6 +39,13 @@ struct DenseCfg {
     static constexpr int GA = SK ? BM / 64 : 1, GB = SK ? BN / 64 : 1;
     static constexpr int LSA = SK ? (GA + NW - 1) / NW : 0, LSB = SK ? (GB + NW - 1) / NW : 0;
     static constexpr int STAGE = (BM + BN) * KTB + SCA + SCB;
+    // Ring layout of NS stages: the A tiles of all stages, then the B tiles,
+    // then (64-byte FP4 K-tiles) their scales: every fragment read of one
+    // operand then lies within a 64 KB immediate offset of one base register.
+    static constexpr int A_ST = BM * KTB, B_ST = BN * KTB, S_ST = SCA + SCB;
+    static constexpr int a_stage(int ns, int s) { return s * A_ST; }
+    static constexpr int b_stage(int ns, int s) { return ns * A_ST + s * B_ST; }
+    static constexpr int s_stage(int ns, int s) { return ns * (A_ST + B_ST) + s * S_ST; }
     static constexpr int NLD = LA + LB + LSA + LSB + (SBLK ? 1 : 0);  // LDS-direct loads per wave per K-tile
     static constexpr int PARTS = 2;                           // ds_read_b128 per fragment per K-step
     static constexpr int NRD = 2 * PARTS * (TM > TN ? TM : TN);  // fragment read slots per K-step
@@ -184,7 +191,6 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     auto load_piece = [&](int kt, int stage, int idx) {
         const int kb = kt * KTB;
         const bool live = kt < KTN;
-        HKQ_LDS uint8_t* st = smem + stage * STAGE;
         if constexpr (Cfg::SBLK) {
             if (idx == LA + LB) {
                 load_scale_unit(kt + Cfg::SB_KT - 1);
@@ -192,21 +198,25 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
             }
         }
         if (idx < LA) {
-            issue_rows16(src.a + kb, live ? src.a_bytes - kb : 0, a_off, idx, st + (idx * NW + wave) * 1024);
+            issue_rows16(src.a + kb, live ? src.a_bytes - kb : 0, a_off, idx,
+                         smem + Cfg::a_stage(NS, stage) + (idx * NW + wave) * 1024);
         } else if (idx < LA + LB) {
             const int i = idx - LA;
-            issue_rows16(src.b + kb, live ? src.b_bytes - kb : 0, b_off, i, st + BM * KTB + (i * NW + wave) * 1024);
+            issue_rows16(src.b + kb, live ? src.b_bytes - kb : 0, b_off, i,
+                         smem + Cfg::b_stage(NS, stage) + (i * NW + wave) * 1024);
         } else if (idx < LA + LB + LSA) {
             const int g = ((idx - LA - LB) * NW + wave) % GA;
             const int kb4 = kt * 4;
             const uint32_t off =
                 src.sa_gathered ? src.sa_row[(idx - LA - LB) & 3] : (uint32_t)((g * 64 + lane) * src.lsa);
-            lds_load4(src.as + kb4, live ? (uint32_t)(src.as_bytes - kb4) : 0u, st + (BM + BN) * KTB + g * 256, off);
+            lds_load4(src.as + kb4, live ? (uint32_t)(src.as_bytes - kb4) : 0u, smem + Cfg::s_stage(NS, stage) + g * 256,
+                      off);
         } else {
             const int g = ((idx - LA - LB - LSA) * NW + wave) % GB;
             const int kb4 = kt * 4;
             const uint32_t off = (uint32_t)((g * 64 + lane) * src.lsb);
-            lds_load4(src.bs + kb4, live ? (uint32_t)(src.bs_bytes - kb4) : 0u, st + (BM + BN) * KTB + SCA + g * 256, off);
+            lds_load4(src.bs + kb4, live ? (uint32_t)(src.bs_bytes - kb4) : 0u,
+                      smem + Cfg::s_stage(NS, stage) + SCA + g * 256, off);
         }
     };
 
@@ -214,16 +224,22 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
 
     // LDS addresses of the fragment reads. The lane reads rows
     // (wave's first row) + t*32 + lane%32; rows 32 apart share the chunk
-    // swizzle, so the address is a per-lane part that depends only on the
-    // K-step and part (frag_lo), a wave-uniform part (stage, operand, wave
-    // rows) and the constant t*32*KTB, which the reads carry as their offset.
-    int frag_lo[SUB][PARTS];
+    // swizzle. Per (K-step, part) one base address per operand (its region,
+    // the wave's rows and the lane's row and chunk); stage and row tile t are
+    // immediate offsets below 64 KB. The empty asm keeps the compiler from
+    // folding a region offset back into the immediates, which it would then
+    // have to split into one register per row tile.
+    uint32_t a_base[SUB][PARTS], b_base[SUB][PARTS];
 #pragma unroll
     for (int ks = 0; ks < SUB; ++ks)
 #pragma unroll
-        for (int part = 0; part < PARTS; ++part)
-            frag_lo[ks][part] = KT::swz(lane & 31, khalf * HCH + 2 * ks + part);
-    const int a_wave_off = wm * TM * 32 * KTB, b_wave_off = BM * KTB + wn * TN * 32 * KTB;
+        for (int part = 0; part < PARTS; ++part) {
+            const uint32_t lo = (uint32_t)KT::swz(lane & 31, khalf * HCH + 2 * ks + part);
+            a_base[ks][part] = (uint32_t)(uintptr_t)smem + (uint32_t)(Cfg::a_stage(NS, 0) + wm * TM * 32 * KTB) + lo;
+            b_base[ks][part] = (uint32_t)(uintptr_t)smem + (uint32_t)(Cfg::b_stage(NS, 0) + wn * TN * 32 * KTB) + lo;
+            asm volatile("" : "+v"(a_base[ks][part]));
+            asm volatile("" : "+v"(b_base[ks][part]));
+        }
 
     struct Frags {
         v4i a[TM][PARTS], b[TN][PARTS];
@@ -234,8 +250,9 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     auto read_piece = [&](int stage, int ks, Frags& f, int idx) {
         const int t = idx / (2 * PARTS), isb = (idx / PARTS) & 1, part = idx % PARTS;
         if ((isb ? TN : TM) <= t) return;
-        const HKQ_LDS uint8_t* base = smem + stage * STAGE + (isb ? b_wave_off : a_wave_off) + frag_lo[ks][part];
-        const v4i v = lds_read16(base + t * 32 * KTB);
+        const uint32_t base = isb ? b_base[ks][part] + (uint32_t)(Cfg::b_stage(NS, stage) - Cfg::b_stage(NS, 0))
+                                  : a_base[ks][part] + (uint32_t)Cfg::a_stage(NS, stage);
+        const v4i v = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base + (uint32_t)(t * 32 * KTB))));
         if (isb) f.b[t][part] = v;
         else f.a[t][part] = v;
     };
@@ -264,7 +281,7 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
                 const int o = ((kt % Cfg::SB_KT) * 8) ^ sc_x;
                 w = *reinterpret_cast<const HKQ_LDS int*>(slot + wave_row * 32 + sc_lo + o + t * 1024);
             } else {
-                const HKQ_LDS uint8_t* sca = smem + stage * STAGE + (BM + BN) * KTB + (isa ? 0 : SCA);
+                const HKQ_LDS uint8_t* sca = smem + Cfg::s_stage(NS, stage) + (isa ? 0 : SCA);
                 const int wave_row = isa ? wm * TM * 32 : wn * TN * 32;
                 w = *reinterpret_cast<const HKQ_LDS uint16_t*>(sca + wave_row * 4 + sk_lo + t * 128);
             }

@@ -1,0 +1,288 @@
+// gemm_stream.h -- the pipelined K loop of gemm_mainloop.h run over a stream of
+// output tiles by one persistent workgroup: the K-tiles of consecutive tiles
+// form one sequence through the LDS ring, so the loads of tile t+1's first
+// K-tiles are issued during tile t's last ones and the ring never drains.
+// Between two tiles the epilogue runs from registers only (the ring already
+// holds the next tile's first K-tiles), and the next tile's first K-step
+// starts its accumulators from zero (a literal-zero MFMA accumulator input),
+// so no accumulator is cleared.
+//
+// Restrictions (the caller checks them): 128-byte K-tiles in a 2-stage ring,
+// and a K-tile count per tile that is a multiple of 8, so that tiles start at
+// stage 0 with the fragment parity 0 and (MXFP4) the scale blocks of 4 K-tiles
+// never straddle two tiles and alternate their ring slot across tiles.
+#pragma once
+#include <type_traits>
+
+#include "gemm_mainloop.h"
+
+namespace hkq {
+
+// Where one tile's K-tiles come from (the fields of LoopSrc a dense tile needs,
+// with 32-bit extents: two of these stay in SGPRs across the stream).
+struct StreamSrc {
+    const uint8_t *a, *b;    // the tile's first A / B row
+    const uint8_t *as, *bs;  // MXFP4: its first e8m0 scale rows
+    uint32_t a_bytes, b_bytes, as_bytes, bs_bytes;  // loads at or past these read zero
+};
+
+// Seq: { int tiles; int KT; uint32_t lsa, lsb; __device__ StreamSrc src(int t) const; }  (t < tiles)
+// Epi: { __device__ void begin(int t); __device__ void end(int t, v16f (&acc)[TN][TM]); }
+//   begin(t) runs before tile t's first K-tile is computed (e.g. to prefetch
+//   the tile's epilogue scales; loads it issues are waited for by the loop's
+//   next barrier), end(t, acc) after tile t's last MFMA has drained; it must
+//   not touch the LDS ring. On return every wave is past a vmcnt(0) barrier.
+template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, typename AOff, typename BOff, typename Seq, typename Epi>
+__device__ __forceinline__ void gemm_stream(const Seq& seq, const AOff& a_off, const BOff& b_off, HKQ_LDS uint8_t* smem,
+                                            int lane, int wave, v16f (&acc)[TN][TM], Epi& epi) {
+    constexpr int KTB = 128, NS = 2;
+    using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>;
+    using KT = KTile<KTB>;
+    constexpr int NW = Cfg::NW, BM = Cfg::BM, SUB = Cfg::SUB;
+    constexpr int LA = Cfg::LA, LB = Cfg::LB, STAGE = Cfg::STAGE;
+    constexpr int NLD = Cfg::NLD, PARTS = Cfg::PARTS, NRD = Cfg::NRD, NSC = Cfg::NSC;
+    constexpr int NMF = Cfg::NMF;
+    constexpr bool FP4 = Cfg::FP4;
+    constexpr int HCH = KTB / 32;
+    static_assert(SUB == 2 && !Cfg::SK, "128-byte K-tiles");
+    static_assert((NS - 1) * NLD + 3 <= 63, "vmcnt budget");
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int KTN = seq.KT;
+
+    // Loads run NS K-tiles (data) and NS + SB_KT - 1 scale units (MXFP4) ahead
+    // of the compute, so near the end of a tile they read the next tile: `ld`
+    // is the source the data loads read (K-tile kl of it, `ld_live` false past
+    // the last tile), `ls` the one the scale units read. Each switches to the
+    // next tile at the top of a K-tile body, before its MFMAs (a branch there
+    // leaves the body's MFMA/load interleave in one basic block).
+    StreamSrc ld = seq.src(0), ls = ld;
+    bool ld_live = true, ls_live = true;
+
+    HKQ_LDS uint8_t* sblk = smem + NS * STAGE;
+    // LDS destination of a load: the wave's base plus a constant, rebuilt from
+    // an opaque copy at each load so that the compiler keeps one register
+    // instead of hoisting every (stage, piece) destination out of the loop.
+    const uint32_t lds_wave = (uint32_t)(uintptr_t)smem + (uint32_t)wave * 1024u;
+    auto wave_dst = [&](uint32_t c) {
+        uint32_t d = lds_wave;
+        asm volatile("" : "+s"(d));
+        return reinterpret_cast<HKQ_LDS uint8_t*>(d + c);
+    };
+    // scale unit u of the tile `ls` (see gemm_mainloop)
+    auto load_scale_unit = [&](int u) {
+        const int blk = u / Cfg::SB_KT;
+        const int g = ((u % Cfg::SB_KT) * NW + wave) % Cfg::SB_GROUPS;
+        const bool live = ls_live && blk * Cfg::SB_KT < KTN;
+        const int r = g * 32 + (lane >> 1);
+        const bool isa = g * 32 < BM;
+        const uint8_t* base = (isa ? ls.as : ls.bs) + blk * 32;
+        const uint32_t ext = isa ? ls.as_bytes : ls.bs_bytes, kb = (uint32_t)blk * 32u;
+        const uint32_t half = (uint32_t)((lane & 1) ^ ((lane >> 4) & 1));
+        const uint32_t a_row = (uint32_t)r * seq.lsa;
+        const uint32_t b_row = (uint32_t)(r - BM) * seq.lsb;
+        const uint32_t off = (isa ? a_row : b_row) + half * 16u;
+        lds_load16_u(base, live && ext > kb ? ext - kb : 0u, sblk + (blk & 1) * Cfg::SB_SLOT + g * 1024, off);
+    };
+
+    // load instruction idx of K-tile kl of `ld` into `stage`; MXFP4: scale
+    // unit kl + SB_KT - 1 of `ls`, counted in `ls`'s own K-tiles (kl + SB_KT - 1
+    // - KTN once `ls` has switched ahead of `ld`)
+    auto load_piece = [&](int kl, int ul, int stage, int idx) {
+        if constexpr (Cfg::SBLK) {
+            if (idx == LA + LB) {
+                load_scale_unit(ul);
+                return;
+            }
+        }
+        const uint32_t kb = (uint32_t)(kl * KTB);
+        if (idx < LA) {
+            lds_load16_u(ld.a + kb, ld_live && ld.a_bytes > kb ? ld.a_bytes - kb : 0u,
+                         wave_dst(Cfg::a_stage(NS, stage) + idx * NW * 1024), a_off.v[idx]);
+        } else {
+            const int i = idx - LA;
+            lds_load16_u(ld.b + kb, ld_live && ld.b_bytes > kb ? ld.b_bytes - kb : 0u,
+                         wave_dst(Cfg::b_stage(NS, stage) + i * NW * 1024), b_off.v[i]);
+        }
+    };
+
+    const int khalf = lane >> 5;
+    // Per (K-step, part) one base address per operand (its region, the wave's
+    // rows and the lane's row and chunk); stage and row tile are immediate
+    // offsets below 64 KB. The empty asm keeps the compiler from folding a
+    // region offset back into the immediates, which it would then have to
+    // split into one register per row tile.
+    uint32_t a_base[SUB][PARTS], b_base[SUB][PARTS];
+#pragma unroll
+    for (int ks = 0; ks < SUB; ++ks)
+#pragma unroll
+        for (int part = 0; part < PARTS; ++part) {
+            const uint32_t lo = (uint32_t)KT::swz(lane & 31, khalf * HCH + 2 * ks + part);
+            a_base[ks][part] = (uint32_t)(uintptr_t)smem + (uint32_t)(Cfg::a_stage(NS, 0) + wm * TM * 32 * KTB) + lo;
+            b_base[ks][part] = (uint32_t)(uintptr_t)smem + (uint32_t)(Cfg::b_stage(NS, 0) + wn * TN * 32 * KTB) + lo;
+            asm volatile("" : "+v"(a_base[ks][part]));
+            asm volatile("" : "+v"(b_base[ks][part]));
+        }
+
+    // A lane's operand of one 64-byte K-step: two 16-byte parts (FP8: the two
+    // halves of one MFMA operand; FP4 and BF16: one operand each).
+    struct Frags {
+        v4i a[TM][PARTS], b[TN][PARTS];
+    };
+    auto read_piece = [&](int stage, int ks, Frags& f, int idx) {
+        const int t = idx / (2 * PARTS), isb = (idx / PARTS) & 1, part = idx % PARTS;
+        if ((isb ? TN : TM) <= t) return;
+        const uint32_t base = isb ? b_base[ks][part] + (uint32_t)(Cfg::b_stage(NS, stage) - Cfg::b_stage(NS, 0))
+                                  : a_base[ks][part] + (uint32_t)Cfg::a_stage(NS, stage);
+        const v4i v = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base + (uint32_t)(t * 32 * KTB))));
+        if (isb) f.b[t][part] = v;
+        else f.a[t][part] = v;
+    };
+    struct Scales {
+        int a[TM], b[TN];
+    };
+    const int sc_lo = (lane & 31) * 32 + khalf * 4, sc_x = (((lane & 31) >> 3) & 1) << 4;
+    auto read_scale = [&](int kt, Scales& s, int idx) {
+        if constexpr (FP4) {
+            const bool isa = idx < TM;
+            const int t = isa ? idx : idx - TM;
+            const HKQ_LDS uint8_t* slot = sblk + ((kt / Cfg::SB_KT) & 1) * Cfg::SB_SLOT;
+            const int wave_row = isa ? wm * TM * 32 : BM + wn * TN * 32;
+            const int o = ((kt % Cfg::SB_KT) * 8) ^ sc_x;
+            const int w = *reinterpret_cast<const HKQ_LDS int*>(slot + wave_row * 32 + sc_lo + o + t * 1024);
+            if (isa) s.a[t] = w;
+            else s.b[t] = w;
+        }
+    };
+
+    // MFMA slot idx of K-step ks; ZERO: the accumulator input is zero (the
+    // first K-step of a tile)
+    auto mfma_one = [&](const Frags& f, int ks, const Scales& s, int idx, auto zero) {
+        constexpr bool ZERO = decltype(zero)::value;
+        const int i = idx / TM, j = idx % TM;
+        if constexpr (MODE == MODE_BF16) {
+            acc[i][j] = mfma_bf16(f.b[i][0], f.a[j][0], ZERO ? v16f{} : acc[i][j]);
+            acc[i][j] = mfma_bf16(f.b[i][1], f.a[j][1], acc[i][j]);
+        } else if constexpr (FP4) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const v8i b = v8i{f.b[i][q][0], f.b[i][q][1], f.b[i][q][2], f.b[i][q][3], 0, 0, 0, 0};
+                const v8i a = v8i{f.a[j][q][0], f.a[j][q][1], f.a[j][q][2], f.a[j][q][3], 0, 0, 0, 0};
+                const v16f c = (ZERO && q == 0) ? v16f{} : acc[i][j];
+                switch ((2 * ks + q) & 3) {
+                    case 0: acc[i][j] = mfma_sel<true, 0, 0>(b, a, c, s.b[i], s.a[j]); break;
+                    case 1: acc[i][j] = mfma_sel<true, 1, 1>(b, a, c, s.b[i], s.a[j]); break;
+                    case 2: acc[i][j] = mfma_sel<true, 2, 2>(b, a, c, s.b[i], s.a[j]); break;
+                    default: acc[i][j] = mfma_sel<true, 3, 3>(b, a, c, s.b[i], s.a[j]); break;
+                }
+            }
+        } else {
+            const v8i b = v8i{f.b[i][0][0], f.b[i][0][1], f.b[i][0][2], f.b[i][0][3], f.b[i][1][0], f.b[i][1][1], f.b[i][1][2], f.b[i][1][3]};
+            const v8i a = v8i{f.a[j][0][0], f.a[j][0][1], f.a[j][0][2], f.a[j][0][3], f.a[j][1][0], f.a[j][1][1], f.a[j][1][2], f.a[j][1][3]};
+            acc[i][j] = mfma_sel<false, 0, 0>(b, a, ZERO ? v16f{} : acc[i][j], 127, 127);
+        }
+    };
+
+    Frags F[2];
+    Scales S[2];
+    epi.begin(0);
+    if constexpr (Cfg::SBLK) {
+#pragma unroll
+        for (int u = 0; u + 1 < Cfg::SB_KT; ++u) load_scale_unit(u);
+    }
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) load_piece(t, t + Cfg::SB_KT - 1, t, i);
+    tile_barrier<(NS - 1) * NLD>();
+#pragma unroll
+    for (int i = 0; i < NRD; ++i) read_piece(0, 0, F[0], i);
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) read_scale(0, S[0], i);
+
+    int cur = 0;  // the tile being computed
+    // One K-tile (see gemm_mainloop); FIRST: the tile's first K-tile, whose
+    // first step starts the accumulators from zero; LAST: the tile's last
+    // K-tile, which leaves the next tile's first fragments to be read after
+    // the epilogue (keeping them live through it would exceed the registers).
+    auto ktile = [&](int kt, int stage, auto parity, auto first, auto last) {
+        constexpr int P = decltype(parity)::value;
+        constexpr bool FIRST = decltype(first)::value;
+        constexpr bool LAST = decltype(last)::value;
+        const int next_stage = stage ^ 1;
+        const int kl = kt + NS < KTN ? kt + NS : kt + NS - KTN;
+        const int ul = kt + NS + Cfg::SB_KT - 1 < KTN ? kt + NS + Cfg::SB_KT - 1 : kt + NS + Cfg::SB_KT - 1 - KTN;
+#pragma unroll
+        for (int c = 0; c < NMF; ++c) {
+            mfma_one(F[0], 0, S[P], c, std::integral_constant<bool, FIRST>{});
+#pragma unroll
+            for (int i = c * NRD / NMF; i < (c + 1) * NRD / NMF; ++i) read_piece(stage, 1, F[1], i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        tile_barrier<(NS - 2) * NLD>();  // K-tile kt+1 resident; this stage retired
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < NMF; ++c) {
+            mfma_one(F[1], 1, S[P], c, std::false_type{});
+#pragma unroll
+            for (int i = c * NLD / NMF; i < (c + 1) * NLD / NMF; ++i) load_piece(kl, ul, stage, i);
+            if constexpr (!LAST) {
+#pragma unroll
+                for (int i = c * NRD / NMF; i < (c + 1) * NRD / NMF; ++i) read_piece(next_stage, 0, F[0], i);
+#pragma unroll
+                for (int i = c * NSC / NMF; i < (c + 1) * NSC / NMF; ++i) read_scale(kt + 1, S[P ^ 1], i);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    for (int t = 0; t < seq.tiles; ++t) {
+        cur = t;
+        if (t > 0) epi.begin(t);
+        ktile(0, 0, P0{}, std::true_type{}, std::false_type{});
+        ktile(1, 1, P1{}, std::false_type{}, std::false_type{});
+        // The sources switch between K-tile bodies (a branch inside one would
+        // split its MFMA/load interleave): the scale units of the next tile
+        // start with K-tile KTN - 5 (MXFP4), its data with K-tile KTN - 2.
+        constexpr int PEEL = Cfg::SBLK ? 6 : 2;
+        for (int kt = 2; kt + PEEL < KTN; kt += 2) {
+            ktile(kt, 0, P0{}, std::false_type{}, std::false_type{});
+            ktile(kt + 1, 1, P1{}, std::false_type{}, std::false_type{});
+        }
+        if constexpr (Cfg::SBLK) {
+            ktile(KTN - 6, 0, P0{}, std::false_type{}, std::false_type{});
+            ls_live = t + 1 < seq.tiles;
+            ls = seq.src(min(t + 1, seq.tiles - 1));
+            ktile(KTN - 5, 1, P1{}, std::false_type{}, std::false_type{});
+            ktile(KTN - 4, 0, P0{}, std::false_type{}, std::false_type{});
+            ktile(KTN - 3, 1, P1{}, std::false_type{}, std::false_type{});
+        }
+        ld_live = t + 1 < seq.tiles;
+        ld = seq.src(min(t + 1, seq.tiles - 1));
+        ktile(KTN - 2, 0, P0{}, std::false_type{}, std::false_type{});
+        ktile(KTN - 1, 1, P1{}, std::false_type{}, std::true_type{});
+        mfma_drain();
+        // Pin the finished accumulators here: without it the compiler sinks
+        // the last K-tile's MFMAs past their scheduling barriers into the
+        // epilogue (and into its copy on the loop exit), where their operands
+        // and the epilogue's values together exceed the registers.
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) asm volatile("" ::"a"(acc[i][j]));
+        epi.end(t, acc);
+        // The next tile's K-tile 0 (stage 0) is resident: the last K-tile's
+        // barrier waited for it. Read unconditionally (after the last tile the
+        // values go unused): a condition here would let the compiler assume the
+        // previous fragments stay live through the epilogue.
+#pragma unroll
+        for (int i = 0; i < NRD; ++i) read_piece(0, 0, F[0], i);
+#pragma unroll
+        for (int i = 0; i < NSC; ++i) read_scale(0, S[0], i);
+    }
+    tile_barrier<0>();  // no load in flight, every wave past its reads
+}
+
+}  // namespace hkq

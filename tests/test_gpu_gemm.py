@@ -303,3 +303,38 @@ def test_gemm_mxfp4_split_and_skinny(orc, M, N, K):
     ref = orc.gemm_mxfp4_ref_f32(Aq, As, Bq, Bs)
     assert_gemm_close(host_bf16_f32(C1), ref, f"mxfp4 split {M}x{N}x{K}")
     assert_gemm_close(host_bf16_f32(C0), ref, f"mxfp4 unsplit {M}x{N}x{K}")
+
+
+# The persistent streaming kernel (256 x 256 tiles with K a multiple of 1024
+# bytes, C's rows 16-byte aligned): several tiles per workgroup, the last round
+# as M halves, ragged M and N at the grid edge (N % 8 == 4: the last 16-byte
+# store of a row straddles N), the minimum of 8 K-tiles per tile, and a round
+# count that leaves some workgroups one tile short; every output element
+# against the oracle. pad > 0 gives C a row pitch of N + pad (a multiple of 8,
+# so the streaming kernel takes it) whose extra columns must stay untouched;
+# pad == 0 with N % 8 == 4 takes the one-tile-per-workgroup kernel.
+@pytest.mark.parametrize("M,N,K,pad", [(4000, 14300, 4096, 4), (4000, 14300, 4096, 0), (4608, 14336, 1024, 0),
+                                       (3000, 8196, 2048, 12), (8192, 4100, 1024, 4)])
+def test_gemm_a8w8_stream_tiles(orc, M, N, K, pad):
+    require_gpu()
+    A, B, sa, sb = a8w8_inputs(orc, M, N, K, seed=M + N + K + 1)
+    sentinel = 7.0
+    Cp = torch.full((M, N + pad), sentinel, dtype=torch.bfloat16, device="cuda")
+    C = hkq.gemm_a8w8(dev_u8(A), dev_u8(B), dev_f32(sa), dev_f32(sb), Cp[:, :N])
+    torch.cuda.synchronize()
+    if pad:
+        assert bool((Cp[:, N:] == sentinel).all()), "stores past N reached the row padding"
+    assert_gemm_close(host_bf16_f32(C), orc.gemm_a8w8_ref_f32(A, B, sa, sb), f"a8w8 stream {M}x{N}x{K} pad {pad}")
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 512), (8200, 4096, 1024)])
+def test_gemm_bf16_stream_tiles(orc, M, N, K):
+    require_gpu()
+    A = orc.randn_bf16((M, K), seed=M)
+    B = orc.randn_bf16((N, K), seed=N + 1)
+    from gpu_util import dev_bf16
+    C = hkq.gemm_bf16(dev_bf16(A), dev_bf16(B))
+    torch.cuda.synchronize()
+    a = torch.from_numpy(orc.bf16_bits_to_f32(A))
+    b = torch.from_numpy(orc.bf16_bits_to_f32(B))
+    assert_gemm_close(host_bf16_f32(C), (a @ b.T).numpy(), f"bf16 stream {M}x{N}x{K}")
