@@ -43,6 +43,11 @@ HIP_FLAGS = [
 HIP_SOURCES = ["quant.hip", "gemm.hip", "gemm_blockscale.hip", "moe.hip", "moe_blockscale.hip", "routing.hip",
                "norm_quant.hip"]
 CPP_SOURCES = ["hkq_error.cpp"]
+# Per-source code generation options. The block-scale GEMM promotes every
+# K group on the VALU (acc += P * scale): its MFMAs must write the partial P
+# to arch VGPRs, which the compiler's default register-class choice does not
+# do (it writes AGPRs and then copies every element out).
+SRC_FLAGS = {"gemm_blockscale.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 # pybind11 module name -> binding source (module names are the reference's)
 MODULES = {
@@ -88,11 +93,12 @@ def _obj(src):
 def compile_hip(src, isa=False):
     path = os.path.join(CSRC, src)
     out = _obj(src)
-    cmd = [HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", path, "-o", out]
+    flags = [*HIP_FLAGS, *SRC_FLAGS.get(src, [])]
+    cmd = [HIPCC, *flags, "-Rpass-analysis=kernel-resource-usage", "-c", path, "-o", out]
     _run(cmd, log=os.path.join(BUILD, src + ".resource.txt"))
     if isa:
         s = os.path.join(BUILD, src + ".s")
-        _run([HIPCC, *HIP_FLAGS, "--cuda-device-only", "-S", path, "-o", s])
+        _run([HIPCC, *flags, "--cuda-device-only", "-S", path, "-o", s])
     return out
 
 

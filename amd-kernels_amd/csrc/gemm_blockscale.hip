@@ -9,11 +9,14 @@
 // fp32 scales cannot ride in the MFMA's e8m0 scale operands, so every K group
 // is "promoted" on the VALU: per 32x32 sub-tile two chained MFMAs (the group's
 // two 64-deep K-steps) produce a fresh partial P, then acc += P * sa * sb.
-// K-tiles are 128 bytes wide (one scale group), held in a 2-stage LDS ring;
-// the group scales live in their own 3-slot LDS rings (a tile's scales are read
-// while its stage is being refilled). Fragments of the next K-tile are read
-// into the registers of the current one as soon as those are consumed.
-#include "gemm_core.h"
+// The tiled kernel keeps the accumulators in arch VGPRs (waves of 64 x 128,
+// 128 fp32 per lane), so a promotion is one v_fma per element with no
+// accumulator-register traffic; the MFMAs write P straight to VGPRs and read
+// their operands from either register file. K-tiles are 128 bytes wide (one
+// scale group) in a 3-stage LDS ring, the group scales in a 4-slot ring, and
+// each K-tile's fragments are read into a second register set while the
+// previous set feeds the MFMAs.
+#include "gemm_mainloop.h"
 #include "hkq_host.h"
 
 namespace hkq {
@@ -64,77 +67,133 @@ struct MulAddElem {
     }
 };
 
-constexpr int BS_KT = 128;  // K-tile bytes per row = one 128-wide scale group
-
-__device__ __forceinline__ int lds_swz128(int r, int c) { return r * BS_KT + ((c ^ ((r >> 1) & 7)) << 4); }
+// Tiled kernel: 256 x 256 tiles, 8 waves of 64 x 128 (TM = 2 m-tiles, TN = 4
+// n-tiles of 32), two per SIMD. A wave's VALU promotions run while the other
+// wave of its SIMD issues MFMAs (measured on MI355X: one wave alternating 16
+// MFMA pairs with their promotions takes the sum of both times, two waves
+// overlap them). LDS: a 2-stage ring of A and B K-tiles (stage: A 32 KB, then
+// B as two 16 KB column halves, so every fragment offset fits the ds_read
+// immediate), then 2 scale slots of sa (256 floats) and sb (GN 1: the tile's
+// 256 columns; GN 128: its two column blocks).
+constexpr int BS_WM = 4, BS_WN = 2, BS_TM = 2, BS_TN = 4, BS_NW = BS_WM * BS_WN;
+constexpr int BS_BM = BS_WM * BS_TM * 32, BS_BN = BS_WN * BS_TN * 32;
+constexpr int BS_KT = 128, BS_NS = 2;
+constexpr int BS_LA = BS_BM * BS_KT / 1024 / BS_NW, BS_LB = BS_BN * BS_KT / 1024 / BS_NW;  // 4, 4 loads per wave
+constexpr int BS_NLD = BS_LA + BS_LB + 2;  // + one sa and one sb load per wave and K-tile
+constexpr int BS_STAGE = (BS_BM + BS_BN) * BS_KT;                                       // 64 KB
+constexpr int BS_BOFF = BS_BM * BS_KT, BS_BHALF = BS_BN / 2 * BS_KT;                     // 32 KB, 16 KB
+constexpr int BS_SC = BS_NS * BS_STAGE;
+constexpr int BS_SLOT = 2048;  // sa at 0, sb at 1024
+constexpr int BS_RING = BS_SC + 2 * BS_SLOT;
+constexpr int BS_EPI = BS_NW * BS_TM * 32 * (BS_TN * 32 * 2 + 16);
+constexpr int BS_LDS = BS_RING > BS_EPI ? BS_RING : BS_EPI;
+static_assert(BS_LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
 
 template <bool GN1>
-__global__ __launch_bounds__(256, 1) void blockscale_gemm_kernel(const BlockScaleParams p) {
-    constexpr int WAVES_M = 2, WAVES_N = 2, NW = 4, TM = 4, TN = 4;
-    constexpr int BM = WAVES_M * TM * 32, BN = WAVES_N * TN * 32;
-    constexpr int LA = BM * BS_KT / 1024 / NW, LB = BN * BS_KT / 1024 / NW;  // 16-byte loads per wave
-    constexpr int STAGE = (BM + BN) * BS_KT;
-    constexpr int SA_RING = 2 * STAGE, SB_RING = SA_RING + 3 * 1024;  // 3 slots of 256 floats each
-
+__global__ __launch_bounds__(64 * BS_NW, 1) void blockscale_gemm_kernel(const BlockScaleParams p) {
+    using KT = KTile<BS_KT>;
+    constexpr int TM = BS_TM, TN = BS_TN, NW = BS_NW;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
-
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int wm = wave / BS_WN, wn = wave % BS_WN;
     const int khalf = lane >> 5;
 
     int tm, tn;
     tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int rows_a = min(p.M - m0, BM), rows_b = min(p.N - n0, BN);
-    const int KT = p.K / BS_KT;
+    const int m0 = tm * BS_BM, n0 = tn * BS_BN;
+    const int rows_a = min(p.M - m0, BS_BM), rows_b = min(p.N - n0, BS_BN);
+    const int KTN = p.K / BS_KT;
 
-    // A/B loads: instruction i fills rows (i*NW + wave)*8 + lane/8 at physical
-    // chunk lane%8; with this swizzle the logical chunk depends on the lane and
-    // the wave's parity only.
-    const uint32_t chunk_off = (uint32_t)(((lane & 7) ^ (((wave & 1) * 4 + (lane >> 4)) & 7)) << 4);
-    uint32_t a_off[LA], b_off[LB];
+    // LDS-direct loads: load i of a wave fills rows (i*NW + wave)*8 .. +7 of
+    // its operand tile (B rows 128 and up: the second half)
+    uint32_t a_off[BS_LA], b_off[BS_LB];
 #pragma unroll
-    for (int i = 0; i < LA; ++i) a_off[i] = (uint32_t)(((i * NW + wave) * 8 + (lane >> 3)) * p.lda) + chunk_off;
+    for (int i = 0; i < BS_LA; ++i) a_off[i] = dense_row_off<NW, BS_KT>(i, wave, lane, p.lda);
 #pragma unroll
-    for (int i = 0; i < LB; ++i) b_off[i] = (uint32_t)(((i * NW + wave) * 8 + (lane >> 3)) * p.ldb) + chunk_off;
-    const uint8_t* a_base = p.A + (int64_t)m0 * p.lda;
-    const uint8_t* b_base = p.B + (int64_t)n0 * p.ldb;
+    for (int i = 0; i < BS_LB; ++i) b_off[i] = dense_row_off<NW, BS_KT>(i, wave, lane, p.ldb);
+    const uint8_t* a_src = p.A + (int64_t)m0 * p.lda;
+    const uint8_t* b_src = p.B + (int64_t)n0 * p.ldb;
     const int64_t a_bytes = min((int64_t)rows_a * p.lda, (int64_t)0x7FFFFFFF);
     const int64_t b_bytes = min((int64_t)rows_b * p.ldb, (int64_t)0x7FFFFFFF);
-    // scale loads: sa rows m0 + wave*64 + lane (one float per row per group);
-    // sb GN1: columns n0 + wave*64 + lane of row g; GN128: columns n0/128 + {0,1}
-    const float* sa_base = p.sa + (int64_t)m0 * p.lsa;
+    // scales: sa rows (wave & 3) * 64 + lane; sb GN 1: columns n0 + (wave &
+    // 3)*64 + lane, GN 128: column blocks n0/128 + {0, 1}. Waves 4-7 repeat the
+    // loads of 0-3 so that every wave issues the same loads.
+    const float* sa_src = p.sa + (int64_t)m0 * p.lsa;
     const int64_t sa_bytes = min((int64_t)rows_a * p.lsa * 4, (int64_t)0x7FFFFFFF);
-    const uint32_t sa_off = (uint32_t)((wave * 64 + lane) * p.lsa * 4);
+    const uint32_t sa_off = (uint32_t)(((wave & 3) * 64 + lane) * p.lsa * 4);
     const int sb_col0 = GN1 ? n0 : n0 / 128;
     const int sb_cols = GN1 ? rows_b : min((p.N + 127) / 128 - n0 / 128, 2);
-    const uint32_t sb_off = GN1 ? (uint32_t)((wave * 64 + lane) * 4) : (wave == 0 && lane < 2 ? (uint32_t)(lane * 4) : OOB);
+    const uint32_t sb_off = GN1 ? (uint32_t)(((wave & 3) * 64 + lane) * 4) : (lane < 2 ? (uint32_t)(lane * 4) : OOB);
+    const uint32_t lds_wave = (uint32_t)(uintptr_t)smem + (uint32_t)wave * 1024u;
 
-    auto issue = [&](int kt) {
-        const bool live = kt < KT;
-        const int kb = kt * BS_KT;
-        HKQ_LDS uint8_t* st = smem + (kt & 1) * STAGE;
-#pragma unroll
-        for (int i = 0; i < LA; ++i)
-            lds_load16(a_base + kb, live ? (uint32_t)(a_bytes - kb) : 0u, st + (i * NW + wave) * 1024, a_off[i]);
-#pragma unroll
-        for (int i = 0; i < LB; ++i)
-            lds_load16(b_base + kb, live ? (uint32_t)(b_bytes - kb) : 0u, st + BM * BS_KT + (i * NW + wave) * 1024, b_off[i]);
-        const int slot = kt % 3;
-        lds_load4(sa_base + kt, live ? (uint32_t)(sa_bytes - kt * 4) : 0u, smem + SA_RING + slot * 1024 + wave * 256, sa_off);
-        lds_load4(p.sb + (int64_t)kt * p.lsb + sb_col0, live ? (uint32_t)(sb_cols * 4) : 0u,
-                  smem + SB_RING + slot * 1024 + wave * 256, sb_off);
+    // load q (0 .. BS_NLD-1) of K-tile kt: A, B, then the sa and sb scales
+    auto issue_one = [&](int kt, int q) {
+        const bool live = kt < KTN;
+        const uint32_t kb = (uint32_t)(kt * BS_KT);
+        const int st = kt & 1;
+        if (q < BS_LA) {
+            lds_load16(a_src + kb, live ? (uint32_t)(a_bytes - kb) : 0u,
+                       reinterpret_cast<HKQ_LDS uint8_t*>(lds_wave + st * BS_STAGE + q * NW * 1024), a_off[q]);
+        } else if (q < BS_LA + BS_LB) {
+            const int i = q - BS_LA;
+            lds_load16(b_src + kb, live ? (uint32_t)(b_bytes - kb) : 0u,
+                       reinterpret_cast<HKQ_LDS uint8_t*>(lds_wave + st * BS_STAGE + BS_BOFF + i * NW * 1024), b_off[i]);
+        } else {
+            HKQ_LDS uint8_t* slot = smem + BS_SC + st * BS_SLOT;
+            if (q == BS_LA + BS_LB)
+                lds_load4(sa_src + kt, live ? (uint32_t)(sa_bytes - kt * 4) : 0u, slot + (wave & 3) * 256, sa_off);
+            else
+                lds_load4(p.sb + (int64_t)kt * p.lsb + sb_col0, live ? (uint32_t)(sb_cols * 4) : 0u,
+                          slot + 1024 + (GN1 ? (wave & 3) * 256 : 0), sb_off);
+        }
     };
 
-    const int arow = wm * TM * 32 + (lane & 31);
-    const int brow = wn * TN * 32 + (lane & 31);
-    // fragment of row r, K-step ks (0/1): logical chunks ks*4 + 2*khalf + {0,1}
-    auto frag = [&](const HKQ_LDS uint8_t* tile, int r, int ks) {
-        const v4i lo = lds_read16(tile + lds_swz128(r, ks * 4 + khalf * 2));
-        const v4i hi = lds_read16(tile + lds_swz128(r, ks * 4 + khalf * 2 + 1));
-        return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    // Fragment reads: lane row lane%32 of m-tile / n-tile t, logical chunks
+    // 4*ks + 2*khalf + {0, 1} of K-step ks. Rows 32 apart share the swizzle, so
+    // per (K-step, part) one base per operand and t*4 KB as the immediate.
+    uint32_t a_base[2][2], b_base[2][2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int c = 4 * ks + 2 * khalf + h;
+            a_base[ks][h] = (uint32_t)(uintptr_t)smem + (uint32_t)KT::swz(wm * TM * 32 + (lane & 31), c);
+            b_base[ks][h] = (uint32_t)(uintptr_t)smem + (uint32_t)(BS_BOFF + wn * TN * 32 * BS_KT) +
+                            (uint32_t)KT::swz(lane & 31, c);
+        }
+    // the bases of stage st, rebuilt from opaque copies each K-tile: left
+    // visible, the compiler hoists every piece address out of the loop
+    struct Bases {
+        uint32_t a[2][2], b[2][2];
+    };
+    auto bases = [&](int st) {
+        Bases r;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                r.a[ks][h] = a_base[ks][h] + (uint32_t)(st * BS_STAGE);
+                r.b[ks][h] = b_base[ks][h] + (uint32_t)(st * BS_STAGE);
+                asm volatile("" : "+v"(r.a[ks][h]));
+                asm volatile("" : "+v"(r.b[ks][h]));
+            }
+        return r;
+    };
+    // a tile's operand for both K-steps: [K-step] of 8 dwords
+    struct Op {
+        v8i k[2];
+    };
+    auto read_op = [&](const uint32_t (&base)[2][2], int t) {
+        Op o;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const v4i lo = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base[ks][0] + (uint32_t)(t * 32 * BS_KT))));
+            const v4i hi = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base[ks][1] + (uint32_t)(t * 32 * BS_KT))));
+            o.k[ks] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        return o;
     };
 
     v16f acc[TN][TM];
@@ -143,87 +202,56 @@ __global__ __launch_bounds__(256, 1) void blockscale_gemm_kernel(const BlockScal
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = v16f{};
 
-    v8i fa[TM][2], fb[TN][2];
-    issue(0);
-    issue(1);
-    tile_barrier<0>();
-    {
-        const HKQ_LDS uint8_t* At = smem;
 #pragma unroll
-        for (int j = 0; j < TM; ++j)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) fa[j][ks] = frag(At, arow + j * 32, ks);
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) fb[i][ks] = frag(At + BM * BS_KT, brow + i * 32, ks);
-    }
-
-    for (int kt = 0; kt < KT; ++kt) {
-        // everything issued so far has landed (K-tile kt+1 resident) and every wave
-        // has read K-tile kt's fragments: its stage takes K-tile kt+2
+    for (int q = 0; q < BS_NLD; ++q) issue_one(0, q);
+    for (int kt = 0; kt < KTN; ++kt) {
+        // K-tile kt resident and every wave past its reads of stage (kt-1) & 1,
+        // which takes K-tile kt+1 (its loads spread over the n-tiles below: a
+        // burst at this point stalls the waves on the load queue)
         tile_barrier<0>();
-        __builtin_amdgcn_sched_barrier(0);
-        issue(kt + 2);
-        const HKQ_LDS uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE;
-        const int slot = kt % 3;
-        const HKQ_LDS float* sas = reinterpret_cast<const HKQ_LDS float*>(smem + SA_RING + slot * 1024);
-        const HKQ_LDS float* sbs = reinterpret_cast<const HKQ_LDS float*>(smem + SB_RING + slot * 1024);
-        float sa_j[TM];
+        const int st = kt & 1;
+        const HKQ_LDS float* sl = reinterpret_cast<const HKQ_LDS float*>(smem + BS_SC + st * BS_SLOT);
+        float saj[TM];
 #pragma unroll
-        for (int j = 0; j < TM; ++j) sa_j[j] = sas[arow + j * 32];
-        float sbw = 0.f;
-        v4f sbn[4];
-        if constexpr (!GN1) sbw = sbs[wn];
-        auto load_sbn = [&](int i) {
+        for (int j = 0; j < TM; ++j) saj[j] = sl[wm * TM * 32 + j * 32 + (lane & 31)];
+        const float sbw = GN1 ? 0.f : sl[256 + wn];
+        const Bases rb = bases(st);
+        Op fa[TM];
+#pragma unroll
+        for (int j = 0; j < TM; ++j) fa[j] = read_op(rb.a, j);
+        Op fb = read_op(rb.b, 0);
+#pragma unroll
+        for (int i = 0; i < TN; ++i) {
+            constexpr int PER = (BS_NLD + TN - 1) / TN;
+#pragma unroll
+            for (int q = i * PER; q < (i + 1) * PER && q < BS_NLD; ++q) issue_one(kt + 1, q);
+            // n-tile i+1's operand and column scales, read under this n-tile's MFMAs
+            Op fb_next;
+            if (i + 1 < TN) fb_next = read_op(rb.b, i + 1);
+            v4f sbn[4];
             if constexpr (GN1) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
-                    sbn[g] = *reinterpret_cast<const HKQ_LDS v4f*>(sbs + wn * TN * 32 + i * 32 + 8 * g + 4 * khalf);
+                    sbn[g] = *reinterpret_cast<const HKQ_LDS v4f*>(sl + 256 + wn * TN * 32 + i * 32 + 8 * g + 4 * khalf);
             }
-        };
-        load_sbn(0);
-        __builtin_amdgcn_sched_barrier(0);
-        // Sub-tile s = i*TM + j: its two chained MFMAs make the group partial P,
-        // which is promoted (acc += P * scales) only after the MFMAs of sub-tile
-        // s+1 are issued, so the VALU promotion of one sub-tile runs while the
-        // matrix pipe works on the next.
-        v16f P[2];
-        auto promote = [&](int s2, const v16f& Ps) {
-            const int i = s2 / TM, j = s2 % TM;
-            if constexpr (GN1) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] += Ps[r] * sa_j[j] * sbn[r / 4][r & 3];
-            } else {
-                const float sc = sa_j[j] * sbw;
+            for (int j = 0; j < TM; ++j) {
+                // the group partial P of sub-tile (i, j), then acc += P * sa * sb
+                const v16f p0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb.k[0], fa[j].k[0], v16f{}, 0, 0, 0,
+                                                                              127, 0, 127);
+                const v16f P = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb.k[1], fa[j].k[1], p0, 0, 0, 0, 127,
+                                                                             0, 127);
+                const float sc = saj[j] * sbw;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] += Ps[r] * sc;
+                for (int r = 0; r < 16; ++r) {
+                    const float f = GN1 ? saj[j] * sbn[r >> 2][r & 3] : sc;
+                    acc[i][j][r] = __builtin_fmaf(P[r], f, acc[i][j][r]);
+                }
             }
-        };
-#pragma unroll
-        for (int s2 = 0; s2 < TN * TM; ++s2) {
-            const int i = s2 / TM, j = s2 % TM;
-            v16f Pn = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i][0], fa[j][0], v16f{}, 0, 0, 0, 127, 0, 127);
-            P[s2 & 1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i][1], fa[j][1], Pn, 0, 0, 0, 127, 0, 127);
-            // registers freed by this sub-tile's MFMAs take the next K-tile's fragments
-            if (j == TM - 1) {
-                fb[i][0] = frag(nxt + BM * BS_KT, brow + i * 32, 0);
-                fb[i][1] = frag(nxt + BM * BS_KT, brow + i * 32, 1);
-            }
-            if (i == TN - 1) {
-                fa[j][0] = frag(nxt, arow + j * 32, 0);
-                fa[j][1] = frag(nxt, arow + j * 32, 1);
-            }
-            if (s2 > 0) promote(s2 - 1, P[(s2 - 1) & 1]);
-            // the column scales of n-tile i+1 replace those of n-tile i once
-            // sub-tile (i, TM-1) is promoted
-            if (j == 0 && i > 0) load_sbn(i);
-            __builtin_amdgcn_sched_barrier(0);
+            if (i + 1 < TN) fb = fb_next;
         }
-        promote(TN * TM - 1, P[(TN * TM - 1) & 1]);
     }
-    mfma_drain();
-    tile_barrier<0>();
+    tile_barrier<0>();  // no load in flight, every wave past its reads: the LDS takes the epilogue
 
     const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
     auto one = [](int) { return 1.0f; };
@@ -418,11 +446,7 @@ static int launch_blockscale_narrow(const BlockScaleParams& p, hipStream_t strea
 
 template <bool GN1>
 static int launch_blockscale(BlockScaleParams& p, hipStream_t stream) {
-    constexpr int BM = 256, BN = 256;
-    constexpr int LDS_RING = 2 * (BM + BN) * BS_KT + 6 * 1024;
-    constexpr int LDS_EPI = 4 * 128 * (128 * 2 + 16);
-    constexpr int LDS = LDS_RING > LDS_EPI ? LDS_RING : LDS_EPI;
-    static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
+    constexpr int BM = BS_BM, BN = BS_BN, LDS = BS_LDS;
     auto kern = blockscale_gemm_kernel<GN1>;
     static bool attr_set = false;
     if (!attr_set) {
@@ -439,7 +463,7 @@ static int launch_blockscale(BlockScaleParams& p, hipStream_t stream) {
     p.c16 = (p.ldc % 8 == 0) && (reinterpret_cast<uintptr_t>(p.C) % 16 == 0);
     const int64_t nblk = (int64_t)p.tiles_m * p.tiles_n;
     if (nblk == 0) return 0;
-    kern<<<dim3((unsigned)nblk), 256, LDS, stream>>>(p);
+    kern<<<dim3((unsigned)nblk), 64 * BS_NW, LDS, stream>>>(p);
     return hkq_launch_status();
 }
 
