@@ -269,6 +269,10 @@ struct DenseSeq {
 template <int MODE, int TM, int BM>
 struct DirectEpi {
     static constexpr int TN = DENSE_TN;
+    // vector-memory instructions a wave issues in end() (at least: ragged
+    // tiles add 8-byte stores) plus the next begin(); the stream's first
+    // barrier after an epilogue leaves that many in flight
+    static constexpr int VM_ISSUED = TN * TM * 2 + (MODE == MODE_A8W8 ? 2 : 0);
     const DenseSeq<BM>* seq;
     const DenseParams* p;
     HKQ_LDS uint8_t* scl;  // 2 slots of STREAM_SCL bytes
@@ -759,7 +763,12 @@ static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
             const char* e = std::getenv("HKQ_DENSE_STREAM");
             return !(e && e[0] == '0');
         }();
-        if (stream_on && ncu > 0 && !batched && p.bias == nullptr && (p.kbytes / 128) % 8 == 0 && p.ldc % 8 == 0) {
+        // Past 4 rounds of tiles the one-tile-per-workgroup kernel's dynamic
+        // dispatch balances better than the fixed per-CU tile lists (measured
+        // on MI355X: 8192x14336x4096, 7 rounds, 347 vs 362 us; at 4 rounds and
+        // below the stream wins by 1-7%).
+        if (stream_on && ncu > 0 && !batched && p.bias == nullptr && (p.kbytes / 128) % 8 == 0 && p.ldc % 8 == 0 &&
+            tiles <= 4 * (int64_t)ncu) {
             constexpr int SLDS = stream_lds<MODE>();
             static_assert(SLDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
             auto skern = dense_stream_kernel<MODE>;

@@ -204,10 +204,14 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, const AOff& a_off, c
     // first step starts the accumulators from zero; LAST: the tile's last
     // K-tile, which leaves the next tile's first fragments to be read after
     // the epilogue (keeping them live through it would exceed the registers).
-    auto ktile = [&](int kt, int stage, auto parity, auto first, auto last) {
+    // VM: vector-memory operations younger than K-tile kt+1's loads when the
+    // body waits for them (the C stores and scale loads of an epilogue that ran
+    // after those loads were issued may stay in flight)
+    auto ktile_vm = [&](int kt, int stage, auto parity, auto first, auto last, auto vm) {
         constexpr int P = decltype(parity)::value;
         constexpr bool FIRST = decltype(first)::value;
         constexpr bool LAST = decltype(last)::value;
+        constexpr int VM = decltype(vm)::value;
         const int next_stage = stage ^ 1;
         const int kl = kt + NS < KTN ? kt + NS : kt + NS - KTN;
         const int ul = kt + NS + Cfg::SB_KT - 1 < KTN ? kt + NS + Cfg::SB_KT - 1 : kt + NS + Cfg::SB_KT - 1 - KTN;
@@ -219,7 +223,7 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, const AOff& a_off, c
             __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        tile_barrier<(NS - 2) * NLD>();  // K-tile kt+1 resident; this stage retired
+        tile_barrier<VM>();  // K-tile kt+1 resident; this stage retired
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int c = 0; c < NMF; ++c) {
@@ -235,13 +239,23 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, const AOff& a_off, c
             __builtin_amdgcn_sched_barrier(0);
         }
     };
+    auto ktile = [&](int kt, int stage, auto parity, auto first, auto last) {
+        ktile_vm(kt, stage, parity, first, last, std::integral_constant<int, (NS - 2) * NLD>{});
+    };
 
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
     for (int t = 0; t < seq.tiles; ++t) {
         cur = t;
-        if (t > 0) epi.begin(t);
-        ktile(0, 0, P0{}, std::true_type{}, std::false_type{});
+        if (t > 0) {
+            epi.begin(t);
+            // K-tile 1's loads went out before the previous tile's epilogue:
+            // its C stores (and this tile's scale loads) need not be waited for
+            ktile_vm(0, 0, P0{}, std::true_type{}, std::false_type{},
+                     std::integral_constant<int, (NS - 2) * NLD + Epi::VM_ISSUED>{});
+        } else {
+            ktile(0, 0, P0{}, std::true_type{}, std::false_type{});
+        }
         ktile(1, 1, P1{}, std::false_type{}, std::false_type{});
         // The sources switch between K-tile bodies (a branch inside one would
         // split its MFMA/load interleave): the scale units of the next tile
