@@ -42,6 +42,14 @@ moe_ref / ogs_routing  tests/test_moe.py:97-128,733-753 restated; invariants
                        agreement with per-expert dense GEMMs.
 moe_mxfp4_ref          per-expert dense gemm_mxfp4_ref on the gathered rows
                        (tests/test_oracle_moe.py); routed-weight and -1 block cases.
+moe_blockscale_ref     per-expert dense gemm_blockscale_ref on the gathered rows
+                       with each group's scales (group_k 64 / 128, group_n 1 /
+                       64 / 128), and for [E, K, N] weights the same result
+                       (tests/test_oracle_moe.py).
+*_ref_f32              fp32 restatements used at BASELINE sizes (gemm_a8w8,
+                       gemm_blockscale, gemm_mxfp4, moe, moe_mxfp4): against
+                       the fp64 references within 2^-16 of the sum of |terms|
+                       (tests/test_oracle_gemm_ext.py, tests/test_oracle_moe.py).
 rmsnorm_quant          fp64 numpy RMSNorm (the test_parity.py formula of
                        fused_fp8_quant) then the pinned group / MX quantizers:
                        codes equal except where y sits within an ulp of a
