@@ -322,44 +322,58 @@ struct DirectEpi {
             asm volatile("" : "+v"(roff[j]));
             rs[j] = MODE == MODE_A8W8 ? sl[wm * TM * 32 + m] : 1.0f;
         }
+        // n-tiles in pairs: the four 16-byte stores of a row's 128-byte line
+        // (columns 64a .. 64a+63) go out back to back, so L2 merges them into
+        // whole lines before they are written back
+        static_assert(TN % 2 == 0, "n-tiles in pairs");
 #pragma unroll
-        for (int i = 0; i < TN; ++i) {
-            v4f cs[4];
+        for (int ip = 0; ip < TN; ip += 2) {
+            v4f cs[2][4];
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
-                cs[g] = MODE == MODE_A8W8 ? *reinterpret_cast<const HKQ_LDS v4f*>(sl + DENSE_BM + wn * TN * 32 + i * 32 + 8 * g + 4 * khalf)
-                                          : v4f{1.f, 1.f, 1.f, 1.f};
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    cs[ii][g] = MODE == MODE_A8W8
+                                    ? *reinterpret_cast<const HKQ_LDS v4f*>(sl + DENSE_BM + wn * TN * 32 + (ip + ii) * 32 +
+                                                                            8 * g + 4 * khalf)
+                                    : v4f{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
-                // Explicit reads out of the accumulator registers, in store
-                // order: the compiler's own copies tend to be hoisted to the
-                // start of the epilogue, all 256 of them live at once.
-                float v[16];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[i][j][e]));
-                uint32_t w[4][2];
+                for (int ii = 0; ii < 2; ++ii) {
+                    const int i = ip + ii;
+                    // Explicit reads out of the accumulator registers, in store
+                    // order: the compiler's own copies tend to be hoisted to the
+                    // start of the epilogue, all 256 of them live at once.
+                    float v[16];
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float a = rs[j];
-                    w[g][0] = pk_bf16(v[4 * g + 0] * a * cs[g][0], v[4 * g + 1] * a * cs[g][1]);
-                    w[g][1] = pk_bf16(v[4 * g + 2] * a * cs[g][2], v[4 * g + 3] * a * cs[g][3]);
-                }
+                    for (int e = 0; e < 16; ++e)
+                        asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[i][j][e]));
+                    uint32_t w[4][2];
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    // lanes < 32 end with columns 16q + 0..7, lanes >= 32 with 16q + 8..15
-                    const auto s0 = __builtin_amdgcn_permlane32_swap(w[2 * q][0], w[2 * q + 1][0], false, false);
-                    const auto s1 = __builtin_amdgcn_permlane32_swap(w[2 * q][1], w[2 * q + 1][1], false, false);
-                    const int c = i * 32 + 16 * q;  // the lane's 8 columns start at c + kc
-                    const int left = cols - c;      // columns of C from c on
-                    const uint32_t off = kc + 8 <= left ? roff[j] + (uint32_t)(c * 2) : OOB;
-                    __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]}, rc, off, 0, 0);
-                    if (ragged) {
-                        const uint32_t off4 = kc + 4 == left ? roff[j] + (uint32_t)(c * 2) : OOB;
-                        __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)s0[0], (int)s1[0]}, rc, off4, 0, 0);
+                    for (int g = 0; g < 4; ++g) {
+                        const float a = rs[j];
+                        w[g][0] = pk_bf16(v[4 * g + 0] * a * cs[ii][g][0], v[4 * g + 1] * a * cs[ii][g][1]);
+                        w[g][1] = pk_bf16(v[4 * g + 2] * a * cs[ii][g][2], v[4 * g + 3] * a * cs[ii][g][3]);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        // lanes < 32 end with columns 16q + 0..7, lanes >= 32 with 16q + 8..15
+                        const auto s0 = __builtin_amdgcn_permlane32_swap(w[2 * q][0], w[2 * q + 1][0], false, false);
+                        const auto s1 = __builtin_amdgcn_permlane32_swap(w[2 * q][1], w[2 * q + 1][1], false, false);
+                        const int c = i * 32 + 16 * q;  // the lane's 8 columns start at c + kc
+                        const int left = cols - c;      // columns of C from c on
+                        const uint32_t off = kc + 8 <= left ? roff[j] + (uint32_t)(c * 2) : OOB;
+                        __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]}, rc,
+                                                               off, 0, 0);
+                        if (ragged) {
+                            const uint32_t off4 = kc + 4 == left ? roff[j] + (uint32_t)(c * 2) : OOB;
+                            __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)s0[0], (int)s1[0]}, rc, off4, 0, 0);
+                        }
                     }
                 }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
     }
 };

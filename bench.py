@@ -287,7 +287,34 @@ def main():
                 ms_d = time_launches(fn, steps, warmup, preheat=0.05)
                 moe_res.append({"proj": f"decode {name}", "T": td, "active_experts": act, "N": nn, "K": kk,
                                 "us": round(ms_d * 1e3, 2), "GB/s": round(act * nn * kk / (ms_d * 1e-3) / 1e9, 1)})
-        del w1, w2
+        # block-scale MoE on the same weights: 1x128 activation scales and
+        # 128x128 weight-block scales (group_k = group_n = 128)
+        g = torch.Generator(device="cuda").manual_seed(50)
+        xs_g = torch.rand((T, hidden // 128), generator=g, device="cuda") + 0.5
+        s2_g = torch.rand((T * topk, ffn // 128), generator=g, device="cuda") + 0.5
+        for name, nn, kk, xx, xsc, wq, gat, tk, yy in (
+                ("blockscale gate_up", 2 * ffn, hidden, qx, xs_g, w1, gather, topk, Y1),
+                ("blockscale down", hidden, ffn, q2, s2_g, w2, None, 1, Y2)):
+            wsc = torch.rand((E, kk // 128, nn // 128), generator=g, device="cuda") + 0.5
+            fn = (lambda xx=xx, xsc=xsc, wq=wq, gat=gat, tk=tk, yy=yy, wsc=wsc:
+                  hkq.moe_a8w8_blockscale(xx, wq, hist, offs, expt_data, tk, xsc, wsc, 128, 128, gather=gat, Y=yy))
+            fn()
+            torch.cuda.synchronize()
+            log(f"moe {name} N={nn} K={kk}")
+            ms_b = time_launches(fn, steps, warmup)
+            moe_res.append({"proj": name, "N": nn, "K": kk, "group_k": 128, "group_n": 128, "ms": round(ms_b, 5),
+                            "tflops": round(2.0 * T * topk * nn * kk / (ms_b * 1e-3) / 1e12, 2)})
+        # K-major prepack of the reference's N-contiguous [E, K, N] gate/up weights
+        w1_kn = w1.view(torch.uint8).transpose(1, 2).contiguous()
+        w1_nk = torch.empty((E, 2 * ffn, hidden), dtype=torch.uint8, device="cuda")
+        pack = hkq.bind("hkq_moe_pack_kmajor", w1_kn.data_ptr(), w1_nk.data_ptr(), E, hidden, 2 * ffn,
+                        w1_kn.stride(0), w1_kn.stride(1), w1_nk.stride(0), w1_nk.stride(1),
+                        torch.cuda.current_stream().cuda_stream)
+        log("moe pack_kmajor [E, K, N] -> [E, N, K]")
+        ms_p = time_launches(pack, steps, warmup)
+        moe_res.append({"proj": "pack_kmajor", "E": E, "K": hidden, "N": 2 * ffn, "us": round(ms_p * 1e3, 2),
+                        "GB/s": round(2 * w1_kn.numel() / (ms_p * 1e-3) / 1e9, 1)})
+        del w1, w2, w1_kn, w1_nk
 
         # MXFP4 experts over the block-sorted routing of the same top-2 choice
         # (moe_align_block_size, 128-row blocks)
