@@ -119,6 +119,9 @@ def main():
                     default=None,
                     help="run one kernel only (for profiling); prints no JSON line. 'copy' is a plain "
                          "1 GiB device copy used to calibrate the HBM byte counters")
+    ap.add_argument("--shape", default=None,
+                    help="with --only a8w8 / mxfp4 / blockscale: profile this M,N,K instead of the "
+                         "benchmark's shape(s) (the block-scale decode rows are skipped)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
@@ -140,7 +143,13 @@ def main():
         return
 
     # ---- A8W8 headline ----
-    M, N, K = HEADLINE["M"], HEADLINE["N"], HEADLINE["K"]
+    shape = None
+    if args.shape:
+        if args.only not in ("a8w8", "mxfp4", "blockscale"):
+            print("--shape needs --only a8w8, mxfp4 or blockscale", file=sys.stderr)
+            sys.exit(2)
+        shape = tuple(int(v) for v in args.shape.split(","))
+    M, N, K = shape if shape and args.only == "a8w8" else (HEADLINE["M"], HEADLINE["N"], HEADLINE["K"])
     x = seeded_bf16((M, K), 1.0, 1)
     w = seeded_bf16((N, K), 0.02, 2)
     qa, sa = hkq.per_token_quant(x)
@@ -156,7 +165,7 @@ def main():
 
     # ---- MXFP4 ----
     if args.only in (None, "mxfp4"):
-        m4, n4, k4 = MXFP4["M"], MXFP4["N"], MXFP4["K"]
+        m4, n4, k4 = shape if shape else (MXFP4["M"], MXFP4["N"], MXFP4["K"])
         xa = seeded_bf16((m4, k4), 1.0, 3)
         xw = seeded_bf16((n4, k4), 0.02, 4)
         Aq, As = hkq.mx_quant(xa, True)
@@ -182,7 +191,7 @@ def main():
     # ---- block-scale FP8 GEMM at the DeepSeek-V3 shapes (1x128 act / 128x128 weight scales) ----
     bs_res = []
     if args.only in (None, "blockscale"):
-        for (bm, bn, bk) in BLOCKSCALE:
+        for (bm, bn, bk) in ([shape] if shape else BLOCKSCALE):
             xa = seeded_bf16((bm, bk), 1.0, 6)
             xw = seeded_bf16((bn, bk), 0.02, 7)
             qa_b, sa_b = hkq.group_quant(xa, 128)
@@ -196,7 +205,7 @@ def main():
             bs_res.append({"M": bm, "N": bn, "K": bk, "ms": round(ms_b, 5),
                            "tflops": round(2.0 * bm * bn * bk / (ms_b * 1e-3) / 1e12, 2)})
             # decode-size rows on the same weights (the narrow path): HBM-bound, GB/s of weights + activations
-            for dm in (1, 16):
+            for dm in (() if shape else (1, 16)):
                 qa_d, sa_d = qa_b[:dm].contiguous(), sa_b[:dm].contiguous()
                 Cd = torch.empty((dm, bn), dtype=torch.bfloat16, device="cuda")
                 launch = hkq.bind("hkq_gemm_blockscale", qa_d.data_ptr(), qw_b.data_ptr(), sa_d.data_ptr(),
