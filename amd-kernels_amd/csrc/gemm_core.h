@@ -241,7 +241,12 @@ __device__ __forceinline__ void store_tile_bf16(v16f (&acc)[TN][TM], HKQ_LDS uin
     constexpr int PASSES = TM * 32 / ROWS_PER_PASS;
     constexpr int BATCH = PASSES < 8 ? PASSES : 8;  // LDS reads in flight before their stores
     static_assert(PASSES % BATCH == 0, "whole batches");
-    const int rl = lane / SEGS, seg = lane % SEGS;
+    // derived from an opaque copy of the lane: otherwise the compiler computes
+    // rl / seg in the kernel's prologue and keeps them live (or spilled)
+    // through the main loop
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int rl = ln / SEGS, seg = ln % SEGS;
     if (c16 && mw + TM * 32 <= M && nw + TN * 32 <= N) {
         // the wave's sub-tile lies inside C: no per-piece checks
         uint16_t* dst = C + (int64_t)(mw + rl) * ldc + nw + seg * 8;
