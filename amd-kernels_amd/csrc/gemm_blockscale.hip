@@ -9,14 +9,9 @@
 // fp32 scales cannot ride in the MFMA's e8m0 scale operands, so every K group
 // is "promoted" on the VALU: per 32x32 sub-tile two chained MFMAs (the group's
 // two 64-deep K-steps) produce a fresh partial P, then acc += P * sa * sb.
-// The tiled kernel keeps the accumulators in arch VGPRs (waves of 64 x 128,
-// 128 fp32 per lane), so a promotion is one v_fma per element with no
-// accumulator-register traffic; the MFMAs write P straight to VGPRs and read
-// their operands from either register file. K-tiles are 128 bytes wide (one
-// scale group) in a 3-stage LDS ring, the group scales in a 4-slot ring, and
-// each K-tile's fragments are read into a second register set while the
-// previous set feeds the MFMAs.
-#include "gemm_mainloop.h"
+// M > 192 runs the 8-wave K loop of blockscale_core.h over 256 x 256 tiles;
+// narrow M streams the weights through registers (blockscale_narrow_kernel).
+#include "blockscale_core.h"
 #include "hkq_host.h"
 
 namespace hkq {
@@ -67,47 +62,25 @@ struct MulAddElem {
     }
 };
 
-// Tiled kernel: 256 x 256 tiles, 8 waves of 64 x 128 (TM = 2 m-tiles, TN = 4
-// n-tiles of 32), two per SIMD. A wave's VALU promotions run while the other
-// wave of its SIMD issues MFMAs (measured on MI355X: one wave alternating 16
-// MFMA pairs with their promotions takes the sum of both times, two waves
-// overlap them). LDS: a 2-stage ring of A and B K-tiles (stage: A 32 KB, then
-// B as two 16 KB column halves, so every fragment offset fits the ds_read
-// immediate), then 2 scale slots of sa (256 floats) and sb (GN 1: the tile's
-// 256 columns; GN 128: its two column blocks).
-constexpr int BS_WM = 4, BS_WN = 2, BS_TM = 2, BS_TN = 4, BS_NW = BS_WM * BS_WN;
-constexpr int BS_BM = BS_WM * BS_TM * 32, BS_BN = BS_WN * BS_TN * 32;
-constexpr int BS_KT = 128, BS_NS = 2;
-constexpr int BS_LA = BS_BM * BS_KT / 1024 / BS_NW, BS_LB = BS_BN * BS_KT / 1024 / BS_NW;  // 4, 4 loads per wave
-constexpr int BS_NLD = BS_LA + BS_LB + 2;  // + one sa and one sb load per wave and K-tile
-constexpr int BS_STAGE = (BS_BM + BS_BN) * BS_KT;                                       // 64 KB
-constexpr int BS_BOFF = BS_BM * BS_KT, BS_BHALF = BS_BN / 2 * BS_KT;                     // 32 KB, 16 KB
-constexpr int BS_SC = BS_NS * BS_STAGE;
-constexpr int BS_SLOT = 2048;  // sa at 0, sb at 1024
-constexpr int BS_RING = BS_SC + 2 * BS_SLOT;
-constexpr int BS_EPI = BS_NW * BS_TM * 32 * (BS_TN * 32 * 2 + 16);
-constexpr int BS_LDS = BS_RING > BS_EPI ? BS_RING : BS_EPI;
-static_assert(BS_LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
-
+// Tiled kernel: the 8-wave K loop of blockscale_core.h over 256 x 256 tiles.
+// Scale slot: sa of the tile's 256 rows; sb GN 1: its 256 columns, GN 128: its
+// two column blocks.
 template <bool GN1>
 __global__ __launch_bounds__(64 * BS_NW, 1) void blockscale_gemm_kernel(const BlockScaleParams p) {
-    using KT = KTile<BS_KT>;
     constexpr int TM = BS_TM, TN = BS_TN, NW = BS_NW;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / BS_WN, wn = wave % BS_WN;
-    const int khalf = lane >> 5;
 
     int tm, tn;
     tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
     const int m0 = tm * BS_BM, n0 = tn * BS_BN;
     const int rows_a = min(p.M - m0, BS_BM), rows_b = min(p.N - n0, BS_BN);
-    const int KTN = p.K / BS_KT;
 
     // LDS-direct loads: load i of a wave fills rows (i*NW + wave)*8 .. +7 of
-    // its operand tile (B rows 128 and up: the second half)
+    // its operand tile
     uint32_t a_off[BS_LA], b_off[BS_LB];
 #pragma unroll
     for (int i = 0; i < BS_LA; ++i) a_off[i] = dense_row_off<NW, BS_KT>(i, wave, lane, p.lda);
@@ -126,20 +99,20 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void blockscale_gemm_kernel(const Bl
     const int sb_col0 = GN1 ? n0 : n0 / 128;
     const int sb_cols = GN1 ? rows_b : min((p.N + 127) / 128 - n0 / 128, 2);
     const uint32_t sb_off = GN1 ? (uint32_t)(((wave & 3) * 64 + lane) * 4) : (lane < 2 ? (uint32_t)(lane * 4) : OOB);
-    const uint32_t lds_wave = (uint32_t)(uintptr_t)smem + (uint32_t)wave * 1024u;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)smem;
+    const int KTN = p.K / BS_KT;
 
     // load q (0 .. BS_NLD-1) of K-tile kt: A, B, then the sa and sb scales
-    auto issue_one = [&](int kt, int q) {
+    auto issue = [&](int kt, int q) {
         const bool live = kt < KTN;
         const uint32_t kb = (uint32_t)(kt * BS_KT);
         const int st = kt & 1;
-        if (q < BS_LA) {
-            lds_load16(a_src + kb, live ? (uint32_t)(a_bytes - kb) : 0u,
-                       reinterpret_cast<HKQ_LDS uint8_t*>(lds_wave + st * BS_STAGE + q * NW * 1024), a_off[q]);
-        } else if (q < BS_LA + BS_LB) {
-            const int i = q - BS_LA;
-            lds_load16(b_src + kb, live ? (uint32_t)(b_bytes - kb) : 0u,
-                       reinterpret_cast<HKQ_LDS uint8_t*>(lds_wave + st * BS_STAGE + BS_BOFF + i * NW * 1024), b_off[i]);
+        if (q < BS_LA + BS_LB) {
+            HKQ_LDS uint8_t* dst = reinterpret_cast<HKQ_LDS uint8_t*>((uintptr_t)(lds_base + bs_load_dst(st, q, wave)));
+            if (q < BS_LA)
+                lds_load16(a_src + kb, live ? (uint32_t)(a_bytes - kb) : 0u, dst, a_off[q]);
+            else
+                lds_load16(b_src + kb, live ? (uint32_t)(b_bytes - kb) : 0u, dst, b_off[q - BS_LA]);
         } else {
             HKQ_LDS uint8_t* slot = smem + BS_SC + st * BS_SLOT;
             if (q == BS_LA + BS_LB)
@@ -150,108 +123,8 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void blockscale_gemm_kernel(const Bl
         }
     };
 
-    // Fragment reads: lane row lane%32 of m-tile / n-tile t, logical chunks
-    // 4*ks + 2*khalf + {0, 1} of K-step ks. Rows 32 apart share the swizzle, so
-    // per (K-step, part) one base per operand and t*4 KB as the immediate.
-    uint32_t a_base[2][2], b_base[2][2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int c = 4 * ks + 2 * khalf + h;
-            a_base[ks][h] = (uint32_t)(uintptr_t)smem + (uint32_t)KT::swz(wm * TM * 32 + (lane & 31), c);
-            b_base[ks][h] = (uint32_t)(uintptr_t)smem + (uint32_t)(BS_BOFF + wn * TN * 32 * BS_KT) +
-                            (uint32_t)KT::swz(lane & 31, c);
-        }
-    // the bases of stage st, rebuilt from opaque copies each K-tile: left
-    // visible, the compiler hoists every piece address out of the loop
-    struct Bases {
-        uint32_t a[2][2], b[2][2];
-    };
-    auto bases = [&](int st) {
-        Bases r;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                r.a[ks][h] = a_base[ks][h] + (uint32_t)(st * BS_STAGE);
-                r.b[ks][h] = b_base[ks][h] + (uint32_t)(st * BS_STAGE);
-                asm volatile("" : "+v"(r.a[ks][h]));
-                asm volatile("" : "+v"(r.b[ks][h]));
-            }
-        return r;
-    };
-    // a tile's operand for both K-steps: [K-step] of 8 dwords
-    struct Op {
-        v8i k[2];
-    };
-    auto read_op = [&](const uint32_t (&base)[2][2], int t) {
-        Op o;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const v4i lo = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base[ks][0] + (uint32_t)(t * 32 * BS_KT))));
-            const v4i hi = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base[ks][1] + (uint32_t)(t * 32 * BS_KT))));
-            o.k[ks] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-        return o;
-    };
-
     v16f acc[TN][TM];
-#pragma unroll
-    for (int i = 0; i < TN; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j) acc[i][j] = v16f{};
-
-#pragma unroll
-    for (int q = 0; q < BS_NLD; ++q) issue_one(0, q);
-    for (int kt = 0; kt < KTN; ++kt) {
-        // K-tile kt resident and every wave past its reads of stage (kt-1) & 1,
-        // which takes K-tile kt+1 (its loads spread over the n-tiles below: a
-        // burst at this point stalls the waves on the load queue)
-        tile_barrier<0>();
-        const int st = kt & 1;
-        const HKQ_LDS float* sl = reinterpret_cast<const HKQ_LDS float*>(smem + BS_SC + st * BS_SLOT);
-        float saj[TM];
-#pragma unroll
-        for (int j = 0; j < TM; ++j) saj[j] = sl[wm * TM * 32 + j * 32 + (lane & 31)];
-        const float sbw = GN1 ? 0.f : sl[256 + wn];
-        const Bases rb = bases(st);
-        Op fa[TM];
-#pragma unroll
-        for (int j = 0; j < TM; ++j) fa[j] = read_op(rb.a, j);
-        Op fb = read_op(rb.b, 0);
-#pragma unroll
-        for (int i = 0; i < TN; ++i) {
-            constexpr int PER = (BS_NLD + TN - 1) / TN;
-#pragma unroll
-            for (int q = i * PER; q < (i + 1) * PER && q < BS_NLD; ++q) issue_one(kt + 1, q);
-            // n-tile i+1's operand and column scales, read under this n-tile's MFMAs
-            Op fb_next;
-            if (i + 1 < TN) fb_next = read_op(rb.b, i + 1);
-            v4f sbn[4];
-            if constexpr (GN1) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    sbn[g] = *reinterpret_cast<const HKQ_LDS v4f*>(sl + 256 + wn * TN * 32 + i * 32 + 8 * g + 4 * khalf);
-            }
-#pragma unroll
-            for (int j = 0; j < TM; ++j) {
-                // the group partial P of sub-tile (i, j), then acc += P * sa * sb
-                const v16f p0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb.k[0], fa[j].k[0], v16f{}, 0, 0, 0,
-                                                                              127, 0, 127);
-                const v16f P = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb.k[1], fa[j].k[1], p0, 0, 0, 0, 127,
-                                                                             0, 127);
-                const float sc = saj[j] * sbw;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float f = GN1 ? saj[j] * sbn[r >> 2][r & 3] : sc;
-                    acc[i][j][r] = __builtin_fmaf(P[r], f, acc[i][j][r]);
-                }
-            }
-            if (i + 1 < TN) fb = fb_next;
-        }
-    }
-    tile_barrier<0>();  // no load in flight, every wave past its reads: the LDS takes the epilogue
+    bs8_kloop<GN1 ? BS_SB_COL : BS_SB_WAVE>(smem, wave, lane, KTN, issue, acc);
 
     const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
     auto one = [](int) { return 1.0f; };

@@ -13,22 +13,29 @@
 // group_k is a multiple of 64 (the reference's kernel is exact only then: it
 // indexes the group once per 64-deep tile); group_n >= 1.
 //
-// fp32 group scales cannot ride in the MFMA's e8m0 operands, so every 64-deep
-// K-step is promoted on the VALU: one MFMA makes the step's partial P of a
-// 32x32 sub-tile, then acc += P * xs * ws. A workgroup computes one routing
-// block (128 rows, gathered through the routing index) by 256 columns with 4
-// waves of 64 x 128; K-tiles are 64 bytes (one K-step, hence one scale group)
-// in a 3-stage LDS ring fed by buffer_load ... lds, each stage carrying the
-// step's 128 row scales and 256 column scales next to the operand rows. The
-// ring (76.5 KB) lets two workgroups share a CU, so one's VALU promotion runs
-// beside the other's MFMAs.
+// fp32 group scales cannot ride in the MFMA's e8m0 operands, so every K-tile
+// of one scale group is promoted on the VALU: acc += P * xs * ws, P the
+// tile's partial of a 32x32 sub-tile. Two kernels:
+//  - group_k = 128 * 2^j and K % 128 == 0: the 8-wave K loop of
+//    blockscale_core.h (128-wide K-tiles, two MFMAs per partial) over
+//    256 x 256 tiles that take two routing blocks of an expert at once;
+//  - any other group_k (a multiple of 64): a workgroup computes one routing
+//    block (128 rows) by 256 columns with 4 waves of 64 x 128; K-tiles are 64
+//    bytes (one K-step, hence one scale group) in a 3-stage LDS ring, each
+//    stage carrying the step's 128 row scales and 256 column scales next to
+//    the operand rows. The ring (76.5 KB) lets two workgroups share a CU, so
+//    one's VALU promotion runs beside the other's MFMAs.
+// Both gather the A rows per lane through the routing index (rows of other
+// tokens never enter LDS) and fill LDS with buffer_load ... lds.
 //
 // hkq_moe_pack_kmajor transposes [E, R, N] byte planes (N contiguous: the
 // reference's MoE weights [E, K, N], MXFP4 weights [E, K/2, N] and e8m0 weight
 // scales [E, K/32, N], tests/test_moe.py:723-729, 808-815, 909-925) into the
 // K-contiguous [E, N, R] rows the MoE kernels stream into LDS.
-#include "gemm_mainloop.h"
+#include "blockscale_core.h"
 #include "hkq_host.h"
+
+#include <cstdlib>
 
 namespace hkq {
 
@@ -284,6 +291,129 @@ __global__ __launch_bounds__(64 * MBS_NW, 2) void moe_blockscale_kernel(const Mo
                                 NoBias{});
 }
 
+// ---------------------------------------------------------------------------
+// group_k a multiple of 128 (and K too): the 8-wave K loop of
+// blockscale_core.h, 128-wide K-tiles of one scale group each, over tiles of
+// 256 rows x 256 columns. A tile takes a pair of routing blocks of one expert
+// when the pair sits in consecutive ExptData words (e | b << 16 with b even,
+// then e | (b+1) << 16): the first word's workgroup computes both, the second
+// returns. Any other word computes its own 128 rows (the tile's other half
+// reads zero). Every listed block is computed once per word, as the
+// reference's grid does.
+// ---------------------------------------------------------------------------
+template <int SBM>
+__global__ __launch_bounds__(64 * BS_NW, 1) void moe_blockscale8_kernel(const MoeBsParams p) {
+    constexpr int TM = BS_TM, TN = BS_TN, NW = BS_NW;
+    using KT = KTile<BS_KT>;
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
+    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / BS_WN, wn = wave % BS_WN;
+    const int khalf = lane >> 5;
+
+    const int pm = blockIdx.x / p.tiles_n, tn = blockIdx.x % p.tiles_n;
+    const int ed = p.expt_data[pm];
+    const int e = ed & 0xFFFF, b = ed >> 16;
+    if (ed < 0 || e >= p.E) return;  // uniform: -1 or a malformed entry
+    if ((b & 1) && pm > 0 && p.expt_data[pm - 1] == ed - 0x10000) return;  // the pair's first word computes it
+    const bool pair = !(b & 1) && pm + 1 < p.grid_m && p.expt_data[pm + 1] == ed + 0x10000;
+    const int m_e = p.hist[e], start = p.offs[e];
+    const int row0 = b * 128;
+    const int rows = min(m_e - row0, pair ? BS_BM : 128);
+    if (rows <= 0 || start < 0) return;
+    const int n0 = tn * BS_BN;
+    const int rows_b = min(p.N - n0, BS_BN);
+
+    auto token_of = [&](int r) {
+        const int s = start + row0 + r;
+        if (r >= rows || s >= p.g_len) return -1;
+        const int t = p.gather ? p.gather[s] / p.topk : s;
+        return (t >= 0 && t < p.T) ? t : -1;
+    };
+
+    // operand rows: A gathered per lane (rows of other tokens never enter LDS),
+    // B the expert's rows n0 .. n0 + 255; load i of a wave fills rows
+    // (i*NW + wave)*8 .. +7 of its operand tile
+    uint32_t a_off[BS_LA], b_off[BS_LB];
+#pragma unroll
+    for (int i = 0; i < BS_LA; ++i) {
+        const int r = (i * NW + wave) * KT::ROWS_PER_LOAD + lane / KT::CHUNKS;
+        const int t = token_of(r);
+        a_off[i] = t < 0 ? OOB : (uint32_t)t * (uint32_t)p.sxm + (uint32_t)(KT::load_chunk(lane, r) << 4);
+        asm volatile("" : "+v"(a_off[i]));  // kept as the 32-bit offset, not re-derived in the loop
+    }
+#pragma unroll
+    for (int i = 0; i < BS_LB; ++i) b_off[i] = dense_row_off<NW, BS_KT>(i, wave, lane, p.swn);
+    const uint8_t* wb = p.W + (int64_t)e * p.swe + (int64_t)n0 * p.swn;
+    const int64_t a_bytes = min((int64_t)p.T * p.sxm, (int64_t)0x7FFFFFFF);
+    const int64_t b_bytes = min((int64_t)rows_b * p.swn, (int64_t)0x7FFFFFFF);
+    // scales: row (wave & 3) * 64 + lane, column n0 + (wave & 3) * 64 + lane
+    // (waves 4-7 repeat the loads of 0-3, so that every wave issues the same
+    // loads); the group moves the base
+    const int t_sa = token_of((wave & 3) * 64 + lane);
+    uint32_t sa_off = t_sa < 0 ? OOB : (uint32_t)t_sa * (uint32_t)p.xsm * 4u;
+    const int nc = n0 + (wave & 3) * 64 + lane;
+    uint32_t sb_off = nc < p.N ? (uint32_t)(nc / p.gn) * (uint32_t)p.wsn * 4u : OOB;
+    asm volatile("" : "+v"(sa_off));
+    asm volatile("" : "+v"(sb_off));
+    const float* wsb = p.ws + (int64_t)e * p.wse;
+    const int64_t xs_bytes = min(p.xs_elems * 4, (int64_t)0x7FFFFFFF);
+    const int64_t ws_bytes = min(max(p.ws_elems - (int64_t)e * p.wse, (int64_t)0) * 4, (int64_t)0x7FFFFFFF);
+    // K-tile kt lies in scale group kt >> kpg_log2 (group_k / 128 is a power
+    // of 2: a division here is VALU work that costs the K loop its registers)
+    const int kpg_log2 = 31 - __builtin_clz(p.gk / BS_KT);
+    const uint32_t lds_base = (uint32_t)(uintptr_t)smem;
+    const int KTN = p.K / BS_KT;
+
+    // load q (0 .. BS_NLD-1) of K-tile kt: A, B, then the row and column scales
+    auto issue = [&](int kt, int q) {
+        const bool live = kt < KTN;
+        const int64_t kb = (int64_t)kt * BS_KT;
+        const int st = kt & 1;
+        if (q < BS_LA + BS_LB) {
+            HKQ_LDS uint8_t* dst = reinterpret_cast<HKQ_LDS uint8_t*>((uintptr_t)(lds_base + bs_load_dst(st, q, wave)));
+            if (q < BS_LA)
+                lds_load16(p.X + kb, live && a_bytes > kb ? (uint32_t)(a_bytes - kb) : 0u, dst, a_off[q]);
+            else
+                lds_load16(wb + kb, live && b_bytes > kb ? (uint32_t)(b_bytes - kb) : 0u, dst, b_off[q - BS_LA]);
+        } else {
+            HKQ_LDS uint8_t* slot = smem + BS_SC + st * BS_SLOT;
+            const int g = live ? kt >> kpg_log2 : 0;
+            if (q == BS_LA + BS_LB) {
+                const int64_t gb = (int64_t)g * p.xsk * 4;
+                lds_load4(p.xs + (int64_t)g * p.xsk, live && xs_bytes > gb ? (uint32_t)(xs_bytes - gb) : 0u,
+                          slot + (wave & 3) * 256, sa_off);
+            } else {
+                const int64_t gb = (int64_t)g * p.wsk * 4;
+                lds_load4(wsb + (int64_t)g * p.wsk, live && ws_bytes > gb ? (uint32_t)(ws_bytes - gb) : 0u,
+                          slot + 1024 + (wave & 3) * 256, sb_off);
+            }
+        }
+    };
+
+    v16f acc[TN][TM];
+    bs8_kloop<SBM>(smem, wave, lane, KTN, issue, acc);
+
+    const int s0 = start + row0;
+    const int nw = n0 + wn * TN * 32;
+    const int out_rows = min(rows, p.y_rows - s0);
+    auto one = [](int) { return 1.0f; };
+    auto ones = [](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); };
+    uint16_t* Y = p.Y + (int64_t)s0 * p.sym;
+    if (p.bias)
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, Y, p.sym, out_rows, p.N, wm * TM * 32, nw, p.c16 != 0, one, ones,
+                                [&](int i, int g) {
+                                    const int n = nw + i * 32 + 8 * g + 4 * khalf;
+                                    if (n >= p.N) return make_float4(0.f, 0.f, 0.f, 0.f);
+                                    const float* bp = p.bias + (int64_t)e * p.bias_e + n;
+                                    return make_float4(bp[0], bp[1], bp[2], bp[3]);
+                                });
+    else
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, Y, p.sym, out_rows, p.N, wm * TM * 32, nw, p.c16 != 0, one, ones,
+                                NoBias{});
+}
+
 }  // namespace hkq
 
 using namespace hkq;
@@ -366,6 +496,32 @@ extern "C" int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, co
     p.bias_e = bias_stride_e;
     p.xs_elems = xs_elems; p.ws_elems = ws_elems;
     p.c16 = (stride_ym % 8 == 0) && (reinterpret_cast<uintptr_t>(Y) % 16 == 0);
+    // group_k = 128 * 2^j (and K % 128 == 0): the 8-wave kernel, 128-wide
+    // K-tiles of one scale group each; HKQ_MOE_BLOCKSCALE8=0 selects the
+    // 64-wide kernel for every group_k
+    static const bool bs8_on = [] {
+        const char* v = std::getenv("HKQ_MOE_BLOCKSCALE8");
+        return !(v && v[0] == '0');
+    }();
+    const int64_t kpg = group_k / BS_KT;  // K-tiles per scale group
+    if (bs8_on && K % BS_KT == 0 && group_k % BS_KT == 0 && (kpg & (kpg - 1)) == 0) {
+        p.tiles_n = (int)((N + BS_BN - 1) / BS_BN);
+        const int64_t nblk = grid_m * p.tiles_n;
+        if (nblk == 0) return 0;
+        const bool ntile = group_n % 32 == 0;
+        auto kern = ntile ? moe_blockscale8_kernel<BS_SB_NTILE> : moe_blockscale8_kernel<BS_SB_COL>;
+        static bool attr8_set[2] = {false, false};
+        if (!attr8_set[ntile]) {
+            hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, BS_LDS);
+            if (err != hipSuccess) {
+                set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", BS_LDS, hipGetErrorString(err));
+                return (int)err;
+            }
+            attr8_set[ntile] = true;
+        }
+        kern<<<dim3((unsigned)nblk), 64 * BS_NW, BS_LDS, stream>>>(p);
+        return hkq_launch_status();
+    }
     p.tiles_n = (int)((N + MBS_BN - 1) / MBS_BN);
     const int64_t nblk = grid_m * p.tiles_n;
     if (nblk == 0) return 0;

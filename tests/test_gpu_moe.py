@@ -219,10 +219,16 @@ def run_moe_bs(X, W, hist, offs, gather, ed, topk, xs, ws, gk, gn, bias=None, y_
 
 # group_k 64 / 128 / 192 (one, two, three K-tiles per group), group_n 1 (per
 # column), 7 (groups across sub-tiles), 64 and 128 (one scale per sub-tile),
-# ragged N, decode-sized and multi-block routing, a bias.
+# ragged N, decode-sized and multi-block routing, a bias. group_k = 128 * 2^j
+# with K % 128 == 0 takes the 8-wave kernel (128-wide K-tiles, routing blocks
+# in pairs): (300, ..., 128, 1), (700, ..., 128, 128), (600, ..., 256, 7),
+# (900, ..., 128, 64), (500, ..., 512, 1); group_k 384 (3 K-tiles) and 192
+# take the 64-wide kernel.
 @pytest.mark.parametrize("T,E,topk,K,N,gk,gn", [(64, 8, 2, 256, 256, 64, 64), (300, 4, 2, 512, 520, 128, 1),
                                                 (130, 3, 1, 384, 260, 192, 7), (5, 8, 2, 640, 1000, 64, 128),
-                                                (700, 5, 2, 1024, 512, 128, 128), (16, 2, 2, 128, 4100, 64, 1)])
+                                                (700, 5, 2, 1024, 512, 128, 128), (16, 2, 2, 128, 4100, 64, 1),
+                                                (600, 3, 2, 512, 1000, 256, 7), (900, 4, 2, 768, 264, 128, 64),
+                                                (500, 2, 2, 1024, 512, 512, 1), (200, 2, 2, 768, 256, 384, 128)])
 def test_moe_blockscale(orc, T, E, topk, K, N, gk, gn):
     require_gpu()
     _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, T, E, topk, K, N, T + K + gn)
@@ -251,6 +257,38 @@ def test_moe_blockscale_padding_and_malformed_entries(orc):
     Y = run_moe_bs(X, W, hist, offs, g2, bad, topk, xs, ws, 64, 64)
     ref = orc.moe_blockscale_ref(X, W, xs, ws, None, gather, hist, offs, ed, topk, 64, 64)
     ref[3] = 0.0
+    check_rows(orc, Y, ref)
+
+
+@pytest.mark.parametrize("gk,gn", [(128, 128), (256, 1)])
+def test_moe_blockscale_block_pairs(orc, gk, gn):
+    """The 8-wave kernel computes two routing blocks of an expert per workgroup
+    when their ExptData words are adjacent (b even, then b + 1). Words
+    shuffled, a pair split by a -1, a duplicated word and dropped words: every
+    listed block is computed, the blocks of dropped words stay untouched."""
+    require_gpu()
+    T, E, topk, K, N = 700, 2, 2, 512, 384
+    _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, T, E, topk, K, N, 31)
+    rng = np.random.default_rng(32)
+    G, C = K // gk, (N + gn - 1) // gn
+    xs = (rng.random((T, G)) * 0.02 + 0.005).astype(np.float32)
+    ws = (rng.random((E, G, C)) * 0.002 + 0.0005).astype(np.float32)
+    live = [int(w) for w in ed if w >= 0]
+    assert len(live) >= 10  # several blocks per expert
+    # drop expert 0's block 3 (block 2 then runs alone) and expert 1's block 0
+    # (its block 1 has no partner), duplicate one word, split a pair with -1,
+    # and put the rest in a shuffled order
+    kept = [w for w in live if w not in (0 | (3 << 16), 1 | (0 << 16))]
+    order = list(rng.permutation(len(kept)))
+    words = [kept[i] for i in order] + [0 | (4 << 16), -1, 0 | (5 << 16), kept[0]]
+    # and one adjacent pair in place: expert 1, blocks 2 and 3
+    words = [1 | (2 << 16), 1 | (3 << 16)] + words
+    bad = np.array(words, np.int32)
+    Y = run_moe_bs(X, W, hist, offs, gather, bad, topk, xs, ws, gk, gn)
+    ref = orc.moe_blockscale_ref(X, W, xs, ws, None, gather, hist, offs, bad, topk, gk, gn)
+    dropped = orc.moe_blockscale_ref(X, W, xs, ws, None, gather, hist, offs,
+                                     np.array([0 | (3 << 16), 1], np.int32), topk, gk, gn)
+    assert (~np.isnan(dropped).any(axis=1)).sum() > 0  # the dropped blocks hold routed rows
     check_rows(orc, Y, ref)
 
 
