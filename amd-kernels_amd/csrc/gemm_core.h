@@ -74,6 +74,16 @@ __device__ __forceinline__ void lds_load16(const void* base, uint32_t bytes, HKQ
                  : "s"(m0), "v"(off), "s"(buffer_desc(base, bytes))
                  : "memory", "m0");
 }
+// lds_load16 with a prepared buffer descriptor (one per operand tile, built
+// once outside the K loop; the K position then rides in the lane offset, so a
+// load costs one VALU add instead of a descriptor's worth of scalar work).
+__device__ __forceinline__ void lds_load16_d(const v4i& desc, HKQ_LDS void* dst, uint32_t off) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(off), "s"(desc)
+                 : "memory", "m0");
+}
 // lds_load16 whose buffer descriptor is made wave-uniform explicitly: for
 // sources the compiler cannot prove uniform (a source switched inside a loop),
 // which would otherwise land in VGPRs and fail the instruction's SGPR operand.

@@ -105,14 +105,6 @@ __device__ __forceinline__ TableOff<N> dense_offs(int wave, int lane, int64_t ld
     return o;
 }
 
-// Issue load i of a K-tile: `base` / `bytes` already start at the K-tile (bytes
-// <= 0: read zero).
-template <int N>
-__device__ __forceinline__ void issue_rows16(const uint8_t* base, int64_t bytes, const TableOff<N>& o, int i,
-                                             HKQ_LDS uint8_t* dst) {
-    lds_load16(base, bytes > 0 ? (uint32_t)(bytes < 0x7FFFFFFF ? bytes : 0x7FFFFFFF) : 0u, dst, o.v[i]);
-}
-
 // Pipeline (per wave; one barrier per K-tile, NS ring stages):
 //   K-tile kt lives in stage kt % NS. Its SUB K-steps run their MFMAs with
 //   double-buffered fragments: the LDS reads of the next step are issued between
@@ -146,6 +138,7 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     constexpr int GA = Cfg::GA, GB = Cfg::GB;
     constexpr int NLD = Cfg::NLD, PARTS = Cfg::PARTS, NRD = Cfg::NRD, NSC = Cfg::NSC;
     constexpr int NMF = Cfg::NMF, HALF = Cfg::HALF;
+    constexpr int RDS = NMF > 1 ? NMF / 2 : 1;  // MFMA slots that carry phase A's fragment reads
     constexpr bool FP4 = Cfg::FP4;
     constexpr int HCH = KTB / 32;  // logical chunks per lane half
     static_assert(NS >= 2 && (NS - 1) * NLD + 3 <= 63, "ring depth and vmcnt budget");
@@ -180,14 +173,21 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
         lds_load16(base, live && bytes > 0 ? (uint32_t)bytes : 0u, sblk + (blk & 1) * Cfg::SB_SLOT + g * 1024, off);
     };
 
+    // Operand buffers: the whole tile's rows, K positions in the lane offsets.
+    // Rows that read zero have offsets at or past 2^31 (OOB), past every
+    // extent; the loads of K-tiles kt >= KTN (the ring's look-ahead past the
+    // end) read rows' later bytes or zero, into stages the loop never reads.
+    const v4i desc_a = buffer_desc(src.a, (uint32_t)(src.a_bytes < 0x7FFFFFFF ? (src.a_bytes > 0 ? src.a_bytes : 0) : 0x7FFFFFFF));
+    const v4i desc_b = buffer_desc(src.b, (uint32_t)(src.b_bytes < 0x7FFFFFFF ? (src.b_bytes > 0 ? src.b_bytes : 0) : 0x7FFFFFFF));
+
     // Load instruction idx of K-tile kt into `stage`: A rows, B rows, then (FP4)
     // scales: KTB 64: group g covers rows g*64 + lane; KTB 128: one scale unit,
     // kt + SB_KT - 1 (with the 2-stage ring the loads issued in K-tile j are
     // those of K-tile j + 2, so K-tile j fetches unit j + SB_KT + 1: block b + 1
     // arrives during K-tiles 4b-1 .. 4b+2, after block b-1, which used the same
     // slot, was last read in K-tile 4b-2, and before K-tile 4b+3 reads it).
-    // For kt >= KTN the buffers are empty, so the loads read zero (the loop needs
-    // no branches).
+    // For kt >= KTN the scale buffers are empty, so those loads read zero (the
+    // loop needs no branches).
     auto load_piece = [&](int kt, int stage, int idx) {
         const int kb = kt * KTB;
         const bool live = kt < KTN;
@@ -198,12 +198,10 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
             }
         }
         if (idx < LA) {
-            issue_rows16(src.a + kb, live ? src.a_bytes - kb : 0, a_off, idx,
-                         smem + Cfg::a_stage(NS, stage) + (idx * NW + wave) * 1024);
+            lds_load16_d(desc_a, smem + Cfg::a_stage(NS, stage) + (idx * NW + wave) * 1024, a_off.v[idx] + (uint32_t)kb);
         } else if (idx < LA + LB) {
             const int i = idx - LA;
-            issue_rows16(src.b + kb, live ? src.b_bytes - kb : 0, b_off, i,
-                         smem + Cfg::b_stage(NS, stage) + (i * NW + wave) * 1024);
+            lds_load16_d(desc_b, smem + Cfg::b_stage(NS, stage) + (i * NW + wave) * 1024, b_off.v[i] + (uint32_t)kb);
         } else if (idx < LA + LB + LSA) {
             const int g = ((idx - LA - LB) * NW + wave) % GA;
             const int kb4 = kt * 4;
@@ -345,14 +343,15 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
         constexpr int P = decltype(parity)::value;
         const int next_stage = stage + 1 == NS ? 0 : stage + 1;
         // phase A: steps 0 .. SUB-2, the fragment reads of the next step spread
-        // over the MFMAs
+        // over the first RDS MFMA slots, so that they have landed when the
+        // barrier below waits for every LDS read of the stage
 #pragma unroll
         for (int ks = 0; ks + 1 < SUB; ++ks) {
 #pragma unroll
             for (int c = 0; c < NMF; ++c) {
                 mfma_one(F[(P * SUB + ks) & 1], ks, S[P], c);
 #pragma unroll
-                for (int i = c * NRD / NMF; i < (c + 1) * NRD / NMF; ++i)
+                for (int i = c * NRD / RDS; i < (c + 1) * NRD / RDS && i < NRD; ++i)
                     read_piece(stage, ks + 1, F[(P * SUB + ks + 1) & 1], i);
                 __builtin_amdgcn_sched_barrier(0);
             }

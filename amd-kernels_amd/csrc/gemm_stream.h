@@ -215,11 +215,14 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, const AOff& a_off, c
         const int next_stage = stage ^ 1;
         const int kl = kt + NS < KTN ? kt + NS : kt + NS - KTN;
         const int ul = kt + NS + Cfg::SB_KT - 1 < KTN ? kt + NS + Cfg::SB_KT - 1 : kt + NS + Cfg::SB_KT - 1 - KTN;
+        // K-step 1's fragment reads go out over the first half of K-step 0's
+        // MFMAs: the barrier below waits for every LDS read of the stage
+        constexpr int RDS = NMF > 1 ? NMF / 2 : 1;
 #pragma unroll
         for (int c = 0; c < NMF; ++c) {
             mfma_one(F[0], 0, S[P], c, std::integral_constant<bool, FIRST>{});
 #pragma unroll
-            for (int i = c * NRD / NMF; i < (c + 1) * NRD / NMF; ++i) read_piece(stage, 1, F[1], i);
+            for (int i = c * NRD / RDS; i < (c + 1) * NRD / RDS && i < NRD; ++i) read_piece(stage, 1, F[1], i);
             __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_sched_barrier(0);
