@@ -147,30 +147,38 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int KTN = src.KT;
 
-    // Scale unit u (SBLK): group slot u % SB_KT of block u / SB_KT; this wave
-    // loads group (slot * NW + wave) % SB_GROUPS of the block's [A; B] rows.
+    // Scale unit u (SBLK): group slot k = u % SB_KT of block u / SB_KT; this
+    // wave loads group (k * NW + wave) % SB_GROUPS of the block's [A; B] rows.
+    // Per slot the group, its operand and the lane's row offset are fixed;
+    // the block moves the offset by 32 bytes. Units of blocks past the last
+    // one (the look-ahead past the end) land in a slot no remaining K-tile
+    // reads.
     HKQ_LDS uint8_t* sblk = smem + NS * STAGE;
-    auto load_scale_unit = [&](int u) {
-        const int blk = u / Cfg::SB_KT;
-        const int g = ((u % Cfg::SB_KT) * NW + wave) % Cfg::SB_GROUPS;
-        const bool live = blk * Cfg::SB_KT < KTN;
+    constexpr int SBK = Cfg::SBLK ? Cfg::SB_KT : 1;
+    int su_g[SBK];
+    bool su_a[SBK];
+    uint32_t su_off[SBK];
+#pragma unroll
+    for (int k = 0; k < SBK; ++k) {
+        const int g = (k * NW + wave) % Cfg::SB_GROUPS;
         const int r = g * 32 + (lane >> 1);
-        const bool isa = g * 32 < BM;
-        const uint8_t* base = (isa ? src.as : src.bs) + blk * 32;
-        const int64_t bytes = (isa ? src.as_bytes : src.bs_bytes) - blk * 32;
+        su_g[k] = g;
+        su_a[k] = g * 32 < BM;
         // row slot s = lane / 2 of the group; its two 16-byte halves are stored
         // swapped when bit 3 of s is set (see read_scale)
         const uint32_t half = (uint32_t)((lane & 1) ^ ((lane >> 4) & 1));
-        // both row offsets are formed and one is selected: a branch here would
-        // split the loop body into blocks, and the compiler then sinks the
-        // MFMAs of the earlier blocks past the loads they should overlap
-        const int k = u % Cfg::SB_KT;
-        const uint32_t ga = k == 0 ? src.sa_row[0] : k == 1 ? src.sa_row[1] : k == 2 ? src.sa_row[2] : src.sa_row[3];
-        const uint32_t a_row = src.sa_gathered ? ga : (uint32_t)(r * src.lsa);
+        const uint32_t a_row = src.sa_gathered ? src.sa_row[k & 3] : (uint32_t)(r * src.lsa);
         const uint32_t b_row = (uint32_t)((r - BM) * src.lsb);
-        const uint32_t row_off = isa ? a_row : b_row;
-        const uint32_t off = row_off + half * 16u;
-        lds_load16(base, live && bytes > 0 ? (uint32_t)bytes : 0u, sblk + (blk & 1) * Cfg::SB_SLOT + g * 1024, off);
+        su_off[k] = (su_a[k] ? a_row : b_row) + half * 16u;
+        asm volatile("" : "+v"(su_off[k]));
+    }
+    const v4i desc_as = buffer_desc(src.as, (uint32_t)(src.as_bytes < 0x7FFFFFFF ? (src.as_bytes > 0 ? src.as_bytes : 0) : 0x7FFFFFFF));
+    const v4i desc_bs = buffer_desc(src.bs, (uint32_t)(src.bs_bytes < 0x7FFFFFFF ? (src.bs_bytes > 0 ? src.bs_bytes : 0) : 0x7FFFFFFF));
+    auto load_scale_unit = [&](int u, auto kslot) {
+        constexpr int k = decltype(kslot)::value;
+        const int blk = u / Cfg::SB_KT;
+        lds_load16_d(su_a[k] ? desc_as : desc_bs, sblk + (blk & 1) * Cfg::SB_SLOT + su_g[k] * 1024,
+                     su_off[k] + (uint32_t)(blk * 32));
     };
 
     // Operand buffers: the whole tile's rows, K positions in the lane offsets.
@@ -188,12 +196,13 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     // slot, was last read in K-tile 4b-2, and before K-tile 4b+3 reads it).
     // For kt >= KTN the scale buffers are empty, so those loads read zero (the
     // loop needs no branches).
-    auto load_piece = [&](int kt, int stage, int idx) {
+    // kslot: (kt + SB_KT - 1) % SB_KT, the slot of the scale unit (SBLK)
+    auto load_piece = [&](int kt, int stage, int idx, auto kslot) {
         const int kb = kt * KTB;
         const bool live = kt < KTN;
         if constexpr (Cfg::SBLK) {
             if (idx == LA + LB) {
-                load_scale_unit(kt + Cfg::SB_KT - 1);
+                load_scale_unit(kt + Cfg::SB_KT - 1, kslot);
                 return;
             }
         }
@@ -324,23 +333,36 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     Scales S[2];
     // prologue: (SBLK) units 0 .. SB_KT-2 of scale block 0, then K-tiles 0 .. NS-1
     // (whose loads carry units SB_KT-1, SB_KT: the rest of block 0, the start of 1)
+    using Q0 = std::integral_constant<int, 0>;
+    using Q1 = std::integral_constant<int, 1>;
+    using Q2 = std::integral_constant<int, 2>;
+    using Q3 = std::integral_constant<int, 3>;
     if constexpr (Cfg::SBLK) {
+        static_assert(Cfg::SB_KT == 4 && NS == 2, "scale slots of the prologue");
+        load_scale_unit(0, Q0{});
+        load_scale_unit(1, Q1{});
+        load_scale_unit(2, Q2{});
 #pragma unroll
-        for (int u = 0; u + 1 < Cfg::SB_KT; ++u) load_scale_unit(u);
+        for (int i = 0; i < NLD; ++i) load_piece(0, 0, i, Q3{});
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) load_piece(1, 1, i, Q0{});
+    } else {
+#pragma unroll
+        for (int t = 0; t < NS; ++t)
+#pragma unroll
+            for (int i = 0; i < NLD; ++i) load_piece(t, t, i, Q0{});
     }
-#pragma unroll
-    for (int t = 0; t < NS; ++t)
-#pragma unroll
-        for (int i = 0; i < NLD; ++i) load_piece(t, t, i);
     tile_barrier<(NS - 1) * NLD>();  // K-tile 0 (and everything issued before it) resident
 #pragma unroll
     for (int i = 0; i < NRD; ++i) read_piece(0, 0, F[0], i);
 #pragma unroll
     for (int i = 0; i < NSC; ++i) read_scale(0, 0, S[0], i);
 
-    // One K-tile; P is the tile's parity (fragment and scale buffers alternate).
-    auto ktile = [&](int kt, int stage, auto parity) {
+    // One K-tile; P is the tile's parity (fragment and scale buffers alternate),
+    // Q (SBLK) kt % 4: its loads carry scale unit kt + NS + 3, slot (Q + 1) % 4.
+    auto ktile = [&](int kt, int stage, auto parity, auto qslot) {
         constexpr int P = decltype(parity)::value;
+        using KS = std::integral_constant<int, (decltype(qslot)::value + NS + Cfg::SB_KT - 1) % 4>;
         const int next_stage = stage + 1 == NS ? 0 : stage + 1;
         // phase A: steps 0 .. SUB-2, the fragment reads of the next step spread
         // over the first RDS MFMA slots, so that they have landed when the
@@ -374,7 +396,7 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
         for (int c = 0; c < POST; ++c) {
             mfma_one(cur, LAST, S[P], PRE + c);
 #pragma unroll
-            for (int i = c * NLD / POST; i < (c + 1) * NLD / POST; ++i) load_piece(kt + NS, stage, i);
+            for (int i = c * NLD / POST; i < (c + 1) * NLD / POST; ++i) load_piece(kt + NS, stage, i, KS{});
 #pragma unroll
             for (int i = c * NRD / POST; i < (c + 1) * NRD / POST; ++i) read_piece(next_stage, 0, nxt, i);
 #pragma unroll
@@ -383,15 +405,28 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
         }
     };
 
-    int stage = 0;
     int kt = 0;
-    for (; kt + 1 < KTN; kt += 2) {
-        ktile(kt, stage, std::integral_constant<int, 0>{});
-        stage = stage + 1 == NS ? 0 : stage + 1;
-        ktile(kt + 1, stage, std::integral_constant<int, 1>{});
-        stage = stage + 1 == NS ? 0 : stage + 1;
+    if constexpr (Cfg::SBLK) {
+        // four K-tiles per iteration: the scale slot of each is a constant
+        for (; kt + 3 < KTN; kt += 4) {
+            ktile(kt, 0, Q0{}, Q0{});
+            ktile(kt + 1, 1, Q1{}, Q1{});
+            ktile(kt + 2, 0, Q0{}, Q2{});
+            ktile(kt + 3, 1, Q1{}, Q3{});
+        }
+        if (kt < KTN) ktile(kt, 0, Q0{}, Q0{});
+        if (kt + 1 < KTN) ktile(kt + 1, 1, Q1{}, Q1{});
+        if (kt + 2 < KTN) ktile(kt + 2, 0, Q0{}, Q2{});
+    } else {
+        int stage = 0;
+        for (; kt + 1 < KTN; kt += 2) {
+            ktile(kt, stage, Q0{}, Q0{});
+            stage = stage + 1 == NS ? 0 : stage + 1;
+            ktile(kt + 1, stage, Q1{}, Q0{});
+            stage = stage + 1 == NS ? 0 : stage + 1;
+        }
+        if (kt < KTN) ktile(kt, stage, Q0{}, Q0{});
     }
-    if (kt < KTN) ktile(kt, stage, std::integral_constant<int, 0>{});
     mfma_drain();
     tile_barrier<0>();  // every wave is done with the stages and no load is in flight
 }
