@@ -269,6 +269,23 @@ def test_gemm_blockscale(orc, M, N, K, group_n):
     assert_gemm_close(C, orc.gemm_blockscale_ref(A, B, sa, sb, 128, group_n), f"blockscale {M}x{N}x{K} gn{group_n}")
 
 
+# The tiled kernel with C rows 16-byte aligned: C with a row pitch of N + pad
+# (a multiple of 8) whose extra columns must stay untouched, N % 8 == 4 (the
+# last 16-byte piece of a row straddles N) and ragged M.
+@pytest.mark.parametrize("M,N,K,pad,group_n", [(600, 772, 2048, 4, 128), (333, 516, 384, 12, 1),
+                                               (520, 1028, 256, 4, 1)])
+def test_gemm_blockscale_padded_rows(orc, M, N, K, pad, group_n):
+    require_gpu()
+    A, B, sa, sb = blockscale_inputs(orc, M, N, K, M + N + K + 7, group_n)
+    sentinel = 7.0
+    Cp = torch.full((M, N + pad), sentinel, dtype=torch.bfloat16, device="cuda")
+    C = hkq.gemm_blockscale(dev_u8(A), dev_u8(B), dev_f32(sa), dev_f32(sb), Cp[:, :N], group_n=group_n)
+    torch.cuda.synchronize()
+    assert bool((Cp[:, N:] == sentinel).all()), "stores past N reached the row padding"
+    assert_gemm_close(host_bf16_f32(C), orc.gemm_blockscale_ref(A, B, sa, sb, 128, group_n),
+                      f"blockscale padded {M}x{N}x{K} gn{group_n}")
+
+
 def test_gemm_blockscale_uniform_scales_reduce_to_a8w8(orc):
     """Scales constant over K groups: the block-scale GEMM equals the A8W8 GEMM
     with the same per-row / per-column factors."""

@@ -222,13 +222,15 @@ def run_moe_bs(X, W, hist, offs, gather, ed, topk, xs, ws, gk, gn, bias=None, y_
 # ragged N, decode-sized and multi-block routing, a bias. group_k = 128 * 2^j
 # with K % 128 == 0 takes the 8-wave kernel (128-wide K-tiles, routing blocks
 # in pairs): (300, ..., 128, 1), (700, ..., 128, 128), (600, ..., 256, 7),
-# (900, ..., 128, 64), (500, ..., 512, 1); group_k 384 (3 K-tiles) and 192
-# take the 64-wide kernel.
+# (900, ..., 128, 64), (500, ..., 512, 1), and group_k past K (100, ..., 128,
+# 256, 256, 128); group_k 384 (3 K-tiles), 192, and 128 with K % 128 == 64
+# (300, ..., 320, 264, 128, 64) take the 64-wide kernel.
 @pytest.mark.parametrize("T,E,topk,K,N,gk,gn", [(64, 8, 2, 256, 256, 64, 64), (300, 4, 2, 512, 520, 128, 1),
                                                 (130, 3, 1, 384, 260, 192, 7), (5, 8, 2, 640, 1000, 64, 128),
                                                 (700, 5, 2, 1024, 512, 128, 128), (16, 2, 2, 128, 4100, 64, 1),
                                                 (600, 3, 2, 512, 1000, 256, 7), (900, 4, 2, 768, 264, 128, 64),
-                                                (500, 2, 2, 1024, 512, 512, 1), (200, 2, 2, 768, 256, 384, 128)])
+                                                (500, 2, 2, 1024, 512, 512, 1), (200, 2, 2, 768, 256, 384, 128),
+                                                (300, 4, 2, 320, 264, 128, 64), (100, 3, 2, 128, 256, 256, 128)])
 def test_moe_blockscale(orc, T, E, topk, K, N, gk, gn):
     require_gpu()
     _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, T, E, topk, K, N, T + K + gn)
@@ -290,6 +292,28 @@ def test_moe_blockscale_block_pairs(orc, gk, gn):
                                      np.array([0 | (3 << 16), 1], np.int32), topk, gk, gn)
     assert (~np.isnan(dropped).any(axis=1)).sum() > 0  # the dropped blocks hold routed rows
     check_rows(orc, Y, ref)
+
+
+def test_moe_blockscale_padded_rows(orc):
+    """The 8-wave kernel with Y rows of pitch N + 4 (16-byte aligned rows, N %
+    8 == 4: the last 16-byte piece of a row straddles N): the padding stays
+    untouched, unrouted rows stay zero, routed rows match the oracle."""
+    require_gpu()
+    T, E, topk, K, N, gk, gn = 400, 3, 2, 512, 772, 128, 128
+    _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, T, E, topk, K, N, 61)
+    rng = np.random.default_rng(62)
+    G, C = K // gk, (N + gn - 1) // gn
+    xs = (rng.random((T, G)) * 0.02 + 0.005).astype(np.float32)
+    ws = (rng.random((E, G, C)) * 0.002 + 0.0005).astype(np.float32)
+    sentinel = 7.0
+    Yp = torch.zeros((T * topk, N + 4), dtype=torch.bfloat16, device="cuda")
+    Yp[:, N:] = sentinel
+    hkq.moe_a8w8_blockscale(dev_u8(X), dev_u8(W), dev_i32(hist), dev_i32(offs), dev_i32(ed), topk, dev_f32(xs),
+                            dev_f32(ws), gk, gn, gather=dev_i32(gather), Y=Yp[:, :N])
+    torch.cuda.synchronize()
+    assert bool((Yp[:, N:] == sentinel).all()), "stores past N reached the row padding"
+    ref = orc.moe_blockscale_ref(X, W, xs, ws, None, gather, hist, offs, ed, topk, gk, gn)
+    check_rows(orc, host_bf16_f32(Yp[:, :N].contiguous()), ref)
 
 
 def test_moe_blockscale_mixtral_group128(orc):
