@@ -102,7 +102,7 @@ constexpr int dense_lds() { return dense_ring_lds<MODE, KTB>() + (MODE == MODE_A
 // K loop of one (WM*TM*32) x (WN*TN*32) block of C at (m0, n0) over K-tiles
 // [kt0, kt1): the operand sources start kt0 K-tiles into the rows, so the
 // loop (and its scale-block schedule) counts K-tiles from 0.
-template <int MODE, int WM, int WN, int TM, int TN, int KTB>
+template <int MODE, int WM, int WN, int TM, int TN, int KTB, int NS = dense_ns<KTB>()>
 __device__ __forceinline__ void dense_kloop(const DenseParams& p, int m0, int n0, int kt0, int kt1, HKQ_LDS uint8_t* smem,
                                             v16f (&acc)[TN][TM]) {
     using Cfg = DenseCfg<MODE, WM, WN, TM, TN, KTB>;
@@ -128,7 +128,7 @@ __device__ __forceinline__ void dense_kloop(const DenseParams& p, int m0, int n0
     src.KT = kt1 - kt0;
     const auto a_off = dense_offs<NW, KTB, Cfg::LA>(wave, lane, p.lda);
     const auto b_off = dense_offs<NW, KTB, Cfg::LB>(wave, lane, p.ldb);
-    gemm_mainloop<MODE, WM, WN, TM, TN, KTB, dense_ns<KTB>()>(src, a_off, b_off, smem, lane, wave, acc);
+    gemm_mainloop<MODE, WM, WN, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
 }
 
 // One (TM*64) x 256 block of C: rows [m0, m0 + TM*64) of tile (tm, tn) of the
@@ -442,7 +442,7 @@ __device__ __forceinline__ void dense_epilogue_global(const DenseParams& p, v16f
                                 NoBias{});
 }
 
-template <int MODE, int WM, int WN, int TM, int TN, int KTB, int MINB>
+template <int MODE, int WM, int WN, int TM, int TN, int KTB, int MINB, int NS>
 __global__ __launch_bounds__(64 * WM * WN, MINB) void dense_tile_kernel(const DenseParams pb) {
     using Cfg = DenseCfg<MODE, WM, WN, TM, TN, KTB>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::NW;
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void dense_tile_kernel(const De
     const int kt0 = split * p.kt_split, kt1 = min(KT, kt0 + p.kt_split);
 
     v16f acc[TN][TM];
-    dense_kloop<MODE, WM, WN, TM, TN, KTB>(p, m0, n0, kt0, kt1, smem, acc);
+    dense_kloop<MODE, WM, WN, TM, TN, KTB, NS>(p, m0, n0, kt0, kt1, smem, acc);
 
     if (p.splits > 1) {
         v4f* slot = reinterpret_cast<v4f*>(p.ws) + ((int64_t)(split * tiles + tile) * NW + wave) * NQ * 64;
@@ -726,12 +726,12 @@ static DensePlan dense_plan(int mode, int64_t M, int64_t N, int64_t kbytes, bool
     return pl;
 }
 
-template <int MODE, int WM, int WN, int TM, int TN, int KTB, int MINB>
+template <int MODE, int WM, int WN, int TM, int TN, int KTB, int MINB, int NS = dense_ns<KTB>()>
 static int launch_dense_tiles(DenseParams& p, const DensePlan& pl, hipStream_t stream) {
     using Cfg = DenseCfg<MODE, WM, WN, TM, TN, KTB>;
-    constexpr int LDS = Cfg::lds_bytes(dense_ns<KTB>());
+    constexpr int LDS = Cfg::lds_bytes(NS);
     static_assert(LDS * MINB <= 160 * 1024, "LDS budget of a CDNA4 CU");
-    auto kern = dense_tile_kernel<MODE, WM, WN, TM, TN, KTB, MINB>;
+    auto kern = dense_tile_kernel<MODE, WM, WN, TM, TN, KTB, MINB, NS>;
     static bool attr_set = false;
     if (int e = set_lds(kern, LDS, attr_set)) return e;
     p.tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
@@ -863,9 +863,25 @@ static int launch_dense_ktb(DenseParams& p, void* ws, size_t ws_bytes, hipStream
             if (pl.skinny_tm == 1) return launch_dense_tiles<MODE, 1, SKINNY_WAVES_N, 1, SKINNY_TN, KTB, 1>(p, pl, stream);
             return launch_dense_tiles<MODE, 1, SKINNY_WAVES_N, 2, SKINNY_TN, KTB, 1>(p, pl, stream);
         }
-        if (pl.geo == GEO_128) return launch_dense_tiles<MODE, 2, 2, 2, 2, KTB, 2>(p, pl, stream);
+        // Grids of at most one workgroup per CU run one workgroup each with a
+        // 3-stage ring (two K-tiles of loads in flight) rather than two per CU
+        // with 2-stage rings (measured on MI355X: 128 x 128 tiles at
+        // 1024x4096x4096 25.8 -> 21.2 us, 1024x4096x14336 75.1 -> 58.1,
+        // 512x4096x4096 21.4 -> 15.8; 128 x 64 tiles at 128x4096x4096 12.7 ->
+        // 11.3, 128x6144x4096 13.3 -> 11.4; at 1.5 rounds, 1024x6144x4096,
+        // two per CU win: 29.6 vs 36.5). MXFP4's scale blocks assume 2 stages.
+        const int ncu = cu_count() > 0 ? cu_count() : 256;
+        const bool one_round = MODE != MODE_MXFP4 && pl.tiles * pl.splits * std::max(1, p.batch) <= ncu;
+        if (pl.geo == GEO_128) {
+            if constexpr (MODE != MODE_MXFP4)
+                if (one_round) return launch_dense_tiles<MODE, 2, 2, 2, 2, KTB, 1, 3>(p, pl, stream);
+            return launch_dense_tiles<MODE, 2, 2, 2, 2, KTB, 2>(p, pl, stream);
+        }
         if constexpr (MODE == MODE_A8W8)
-            if (pl.geo == GEO_128x64) return launch_dense_tiles<MODE, 4, 1, 1, 2, KTB, 2>(p, pl, stream);
+            if (pl.geo == GEO_128x64) {
+                if (one_round) return launch_dense_tiles<MODE, 4, 1, 1, 2, KTB, 1, 3>(p, pl, stream);
+                return launch_dense_tiles<MODE, 4, 1, 1, 2, KTB, 2>(p, pl, stream);
+            }
     }
     return launch_dense_whole<MODE, KTB>(p, stream);
 }
