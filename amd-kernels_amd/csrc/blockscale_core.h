@@ -38,6 +38,7 @@ static_assert(BS_LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
 // How the K loop reads the column scales of its slot (floats from 256):
 //   BS_SB_COL:   one per column, tile column c at 256 + c
 //   BS_SB_WAVE:  one per 128-column half of the tile, half h at 256 + h
+//                (the wave's columns lie in one half)
 //   BS_SB_NTILE: one per 32-column n-tile, read at 256 + (its first column)
 enum : int { BS_SB_COL = 0, BS_SB_WAVE = 1, BS_SB_NTILE = 2 };
 
@@ -54,12 +55,15 @@ __device__ __forceinline__ uint32_t bs_load_dst(int st, int q, int wave) {
 // BS_NLD-1: A rows, B rows, row scales, column scales) of K-tile kt into
 // stage kt & 1 and scale slot kt & 1 (loads of kt >= KTN read zero). On
 // return every load has landed and every wave is past its LDS reads.
-template <int SBM, class Issue>
-__device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int wave, int lane, int KTN, Issue& issue,
-                                          v16f (&acc)[BS_TN][BS_TM]) {
+// The wave computes tile rows wm*64 .. +63 and TN n-tiles from tile column cn
+// (TN may differ between the waves of a workgroup: every wave issues the same
+// loads and barriers).
+template <int SBM, int TN, class Issue>
+__device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int lane, int wm, int cn, int KTN, Issue& issue,
+                                          v16f (&acc)[TN][BS_TM]) {
     using KT = KTile<BS_KT>;
-    constexpr int TM = BS_TM, TN = BS_TN;
-    const int wm = wave / BS_WN, wn = wave % BS_WN;
+    constexpr int TM = BS_TM;
+    static_assert(TN >= 1 && TN <= BS_TN, "n-tiles per wave");
     const int khalf = lane >> 5;
 
     // Fragment reads: lane row lane%32 of m-tile / n-tile t, logical chunks
@@ -72,8 +76,7 @@ __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int wave, int l
         for (int h = 0; h < 2; ++h) {
             const int c = 4 * ks + 2 * khalf + h;
             a_base[ks][h] = (uint32_t)(uintptr_t)smem + (uint32_t)KT::swz(wm * TM * 32 + (lane & 31), c);
-            b_base[ks][h] = (uint32_t)(uintptr_t)smem + (uint32_t)(BS_BOFF + wn * TN * 32 * BS_KT) +
-                            (uint32_t)KT::swz(lane & 31, c);
+            b_base[ks][h] = (uint32_t)(uintptr_t)smem + (uint32_t)(BS_BOFF + cn * BS_KT) + (uint32_t)KT::swz(lane & 31, c);
         }
     // the bases of stage st, rebuilt from opaque copies each K-tile: left
     // visible, the compiler hoists every piece address out of the loop
@@ -128,7 +131,7 @@ __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int wave, int l
         float sbt[TN];
 #pragma unroll
         for (int i = 0; i < TN; ++i)
-            sbt[i] = SBM == BS_SB_WAVE ? sl[256 + wn] : SBM == BS_SB_NTILE ? sl[256 + wn * TN * 32 + i * 32] : 0.f;
+            sbt[i] = SBM == BS_SB_WAVE ? sl[256 + cn / 128] : SBM == BS_SB_NTILE ? sl[256 + cn + i * 32] : 0.f;
         const Bases rb = bases(st);
         Op fa[TM];
 #pragma unroll
@@ -146,7 +149,7 @@ __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int wave, int l
             if constexpr (SBM == BS_SB_COL) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
-                    sbn[g] = *reinterpret_cast<const HKQ_LDS v4f*>(sl + 256 + wn * TN * 32 + i * 32 + 8 * g + 4 * khalf);
+                    sbn[g] = *reinterpret_cast<const HKQ_LDS v4f*>(sl + 256 + cn + i * 32 + 8 * g + 4 * khalf);
             }
 #pragma unroll
             for (int j = 0; j < TM; ++j) {

@@ -11,6 +11,8 @@
 // two 64-deep K-steps) produce a fresh partial P, then acc += P * sa * sb.
 // M > 192 runs the 8-wave K loop of blockscale_core.h over 256 x 256 tiles;
 // narrow M streams the weights through registers (blockscale_narrow_kernel).
+#include <cstdlib>
+
 #include "blockscale_core.h"
 #include "hkq_host.h"
 
@@ -62,22 +64,30 @@ struct MulAddElem {
     }
 };
 
-// Tiled kernel: the 8-wave K loop of blockscale_core.h over 256 x 256 tiles.
-// Scale slot: sa of the tile's 256 rows; sb GN 1: its 256 columns, GN 128: its
-// two column blocks.
-template <bool GN1>
+// Tiled kernel: the 8-wave K loop of blockscale_core.h over 256 x BN tiles.
+// BN 256: waves of 64 x 128 (two per SIMD). BN 224, for grids that the
+// 256-wide tiles would leave a CU short (2048 x 7168: 224 tiles of 256 x 256,
+// 256 of 256 x 224): waves 0-3 take n-tiles 0-3 and waves 4-7 n-tiles 4-6 of
+// their 64 rows, so that each SIMD holds one wave of each kind (the hardware
+// places wave w on SIMD w % 4) and does 7/8 of a 256-wide tile's work; the B
+// rows past 224 read zero. Scale slot: sa of the tile's 256 rows; sb GN 1 or
+// BN 224: one value per tile column (GN 128: its block's), GN 128 with BN
+// 256: the tile's two column blocks.
+template <bool GN1, int BN>
 __global__ __launch_bounds__(64 * BS_NW, 1) void blockscale_gemm_kernel(const BlockScaleParams p) {
+    static_assert(BN == BS_BN || BN == BS_BN - 32, "tile widths of 256 or 224 columns");
+    constexpr bool W224 = BN != BS_BN;
     constexpr int TM = BS_TM, TN = BS_TN, NW = BS_NW;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave / BS_WN, wn = wave % BS_WN;
+    const int wm = W224 ? wave & 3 : wave / BS_WN, wn = W224 ? wave >> 2 : wave % BS_WN;
 
     int tm, tn;
     tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-    const int m0 = tm * BS_BM, n0 = tn * BS_BN;
-    const int rows_a = min(p.M - m0, BS_BM), rows_b = min(p.N - n0, BS_BN);
+    const int m0 = tm * BS_BM, n0 = tn * BN;
+    const int rows_a = min(p.M - m0, BS_BM), rows_b = min(p.N - n0, BN);
 
     // LDS-direct loads: load i of a wave fills rows (i*NW + wave)*8 .. +7 of
     // its operand tile
@@ -90,15 +100,18 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void blockscale_gemm_kernel(const Bl
     const uint8_t* b_src = p.B + (int64_t)n0 * p.ldb;
     const int64_t a_bytes = min((int64_t)rows_a * p.lda, (int64_t)0x7FFFFFFF);
     const int64_t b_bytes = min((int64_t)rows_b * p.ldb, (int64_t)0x7FFFFFFF);
-    // scales: sa rows (wave & 3) * 64 + lane; sb GN 1: columns n0 + (wave &
-    // 3)*64 + lane, GN 128: column blocks n0/128 + {0, 1}. Waves 4-7 repeat the
-    // loads of 0-3 so that every wave issues the same loads.
+    // scales: sa rows (wave & 3) * 64 + lane; sb per column: tile column c =
+    // (wave & 3)*64 + lane from sb's row of the K-tile (GN 128: its block's
+    // value), per block (GN 128, BN 256): blocks n0/128 + {0, 1}. Waves 4-7
+    // repeat the loads of 0-3 so that every wave issues the same loads.
     const float* sa_src = p.sa + (int64_t)m0 * p.lsa;
     const int64_t sa_bytes = min((int64_t)rows_a * p.lsa * 4, (int64_t)0x7FFFFFFF);
     const uint32_t sa_off = (uint32_t)(((wave & 3) * 64 + lane) * p.lsa * 4);
-    const int sb_col0 = GN1 ? n0 : n0 / 128;
-    const int sb_cols = GN1 ? rows_b : min((p.N + 127) / 128 - n0 / 128, 2);
-    const uint32_t sb_off = GN1 ? (uint32_t)(((wave & 3) * 64 + lane) * 4) : (lane < 2 ? (uint32_t)(lane * 4) : OOB);
+    constexpr bool PER_COL = GN1 || W224;
+    const int sb_row = GN1 ? p.N : (p.N + 127) / 128;  // values per sb row
+    const int sc = (wave & 3) * 64 + lane;
+    const uint32_t sb_off = PER_COL ? (sc < rows_b ? (uint32_t)((GN1 ? n0 + sc : (n0 + sc) / 128) * 4) : OOB)
+                                    : (lane < 2 ? (uint32_t)((n0 / 128 + lane) * 4) : OOB);
     const uint32_t lds_base = (uint32_t)(uintptr_t)smem;
     const int KTN = p.K / BS_KT;
 
@@ -118,15 +131,23 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void blockscale_gemm_kernel(const Bl
             if (q == BS_LA + BS_LB)
                 lds_load4(sa_src + kt, live ? (uint32_t)(sa_bytes - kt * 4) : 0u, slot + (wave & 3) * 256, sa_off);
             else
-                lds_load4(p.sb + (int64_t)kt * p.lsb + sb_col0, live ? (uint32_t)(sb_cols * 4) : 0u,
-                          slot + 1024 + (GN1 ? (wave & 3) * 256 : 0), sb_off);
+                lds_load4(p.sb + (int64_t)kt * p.lsb, live ? (uint32_t)(sb_row * 4) : 0u,
+                          slot + 1024 + (PER_COL ? (wave & 3) * 256 : 0), sb_off);
         }
     };
 
     v16f acc[TN][TM];
-    bs8_kloop<GN1 ? BS_SB_COL : BS_SB_WAVE>(smem, wave, lane, KTN, issue, acc);
+    constexpr int SBM = GN1 ? BS_SB_COL : W224 ? BS_SB_NTILE : BS_SB_WAVE;
+    if (W224 && wn == 1) {
+        bs8_kloop<SBM, TN - 1>(smem, lane, wm, TN * 32, KTN, issue, reinterpret_cast<v16f(&)[TN - 1][TM]>(acc));
+#pragma unroll
+        for (int j = 0; j < TM; ++j) acc[TN - 1][j] = v16f{};
+    } else
+        bs8_kloop<SBM, TN>(smem, lane, wm, wn * TN * 32, KTN, issue, acc);
 
+    // BN 224: the last n-tile of waves 4-7 lies past the tile (never stored)
     const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
+    const int n_end = W224 ? min(p.N, n0 + BN) : p.N;
     auto one = [](int) { return 1.0f; };
     auto ones = [](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); };
     if (p.ca) {
@@ -136,13 +157,13 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void blockscale_gemm_kernel(const Bl
         e.ldca = p.ldca;
         e.ldcb = p.ldcb;
         e.M = p.M;
-        e.N = p.N;
+        e.N = n_end;
         e.mw = mw;
         e.nw = nw;
         e.lane = lane;
-        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, NoBias{}, e);
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, n_end, mw, nw, p.c16 != 0, one, ones, NoBias{}, e);
     } else {
-        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, one, ones, NoBias{});
+        store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, n_end, mw, nw, p.c16 != 0, one, ones, NoBias{});
     }
 }
 
@@ -317,10 +338,10 @@ static int launch_blockscale_narrow(const BlockScaleParams& p, hipStream_t strea
     return launch_blockscale_narrow_mt<GN1, 4>(p, stream);
 }
 
-template <bool GN1>
-static int launch_blockscale(BlockScaleParams& p, hipStream_t stream) {
-    constexpr int BM = BS_BM, BN = BS_BN, LDS = BS_LDS;
-    auto kern = blockscale_gemm_kernel<GN1>;
+template <bool GN1, int BN>
+static int launch_blockscale_bn(BlockScaleParams& p, hipStream_t stream) {
+    constexpr int BM = BS_BM, LDS = BS_LDS;
+    auto kern = blockscale_gemm_kernel<GN1, BN>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
@@ -338,6 +359,21 @@ static int launch_blockscale(BlockScaleParams& p, hipStream_t stream) {
     if (nblk == 0) return 0;
     kern<<<dim3((unsigned)nblk), 64 * BS_NW, LDS, stream>>>(p);
     return hkq_launch_status();
+}
+
+// 224-column tiles when they take fewer SIMD-steps: rounds of tiles over the
+// CUs times the n-tiles a SIMD computes per tile (8 for 256 columns, 7 for
+// 224). HKQ_BLOCKSCALE_W224=0 (read at each call) keeps the 256-column tiles.
+template <bool GN1>
+static int launch_blockscale(BlockScaleParams& p, hipStream_t stream) {
+    const char* w224_env = std::getenv("HKQ_BLOCKSCALE_W224");
+    const bool w224_on = !(w224_env && w224_env[0] == '0');
+    const int64_t ncu = cu_count() > 0 ? cu_count() : 256;
+    const int64_t tm = (p.M + BS_BM - 1) / BS_BM;
+    const int64_t r256 = (tm * ((p.N + BS_BN - 1) / BS_BN) + ncu - 1) / ncu;
+    const int64_t r224 = (tm * ((p.N + BS_BN - 33) / (BS_BN - 32)) + ncu - 1) / ncu;
+    if (w224_on && 7 * r224 < 8 * r256) return launch_blockscale_bn<GN1, BS_BN - 32>(p, stream);
+    return launch_blockscale_bn<GN1, BS_BN>(p, stream);
 }
 
 }  // namespace hkq

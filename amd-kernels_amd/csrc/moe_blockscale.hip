@@ -393,7 +393,7 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void moe_blockscale8_kernel(const Mo
     };
 
     v16f acc[TN][TM];
-    bs8_kloop<SBM>(smem, wave, lane, KTN, issue, acc);
+    bs8_kloop<SBM, BS_TN>(smem, lane, wm, wn * BS_TN * 32, KTN, issue, acc);
 
     const int s0 = start + row0;
     const int nw = n0 + wn * TN * 32;

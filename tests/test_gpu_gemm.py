@@ -286,6 +286,24 @@ def test_gemm_blockscale_padded_rows(orc, M, N, K, pad, group_n):
                       f"blockscale padded {M}x{N}x{K} gn{group_n}")
 
 
+# Tile widths: grids that 256-column tiles leave a CU short run 256 x 224
+# tiles (waves 4-7 with three n-tiles); HKQ_BLOCKSCALE_W224=0 forces 256-column
+# tiles. Both compute every element with the same K steps and promotions, so
+# their outputs agree bit for bit. Shapes: ragged N (1000 = 4*224 + 104: the
+# last tile's waves 4-7 lie wholly past N), a 128-block boundary inside a
+# 224-column tile (GN 128), per-column scales, and the 2048 x 7168 BASELINE grid.
+@pytest.mark.parametrize("M,N,K,group_n", [(256, 1000, 512, 1), (600, 772, 2048, 128), (333, 516, 384, 1),
+                                           (520, 1792, 640, 128), (2048, 7168, 2048, 128)])
+def test_gemm_blockscale_tile_widths(orc, monkeypatch, M, N, K, group_n):
+    require_gpu()
+    A, B, sa, sb = blockscale_inputs(orc, M, N, K, M + N + K + 11, group_n)
+    C224 = run_blockscale(A, B, sa, sb, group_n)
+    monkeypatch.setenv("HKQ_BLOCKSCALE_W224", "0")
+    C256 = run_blockscale(A, B, sa, sb, group_n)
+    assert np.array_equal(C224, C256), f"tile widths disagree {M}x{N}x{K} gn{group_n}"
+    assert_gemm_close(C224, orc.gemm_blockscale_ref_f32(A, B, sa, sb, 128, group_n), f"blockscale {M}x{N}x{K}")
+
+
 def test_gemm_blockscale_uniform_scales_reduce_to_a8w8(orc):
     """Scales constant over K groups: the block-scale GEMM equals the A8W8 GEMM
     with the same per-row / per-column factors."""
