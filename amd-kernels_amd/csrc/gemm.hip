@@ -780,12 +780,10 @@ static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
             const char* e = std::getenv("HKQ_DENSE_STREAM");
             return !(e && e[0] == '0');
         }();
-        // Past 4 rounds of tiles the one-tile-per-workgroup kernel's dynamic
-        // dispatch balances better than the fixed per-CU tile lists (measured
-        // on MI355X: 8192x14336x4096, 7 rounds, 347 vs 362 us; at 4 rounds and
-        // below the stream wins by 1-7%).
-        if (stream_on && ncu > 0 && !batched && p.bias == nullptr && (p.kbytes / 128) % 8 == 0 && p.ldc % 8 == 0 &&
-            tiles <= 4 * (int64_t)ncu) {
+        // Measured on MI355X against the one-tile-per-workgroup kernel: 1-3%
+        // faster at 1.75-3.5 rounds of tiles, 1-2% at 7 and 14 rounds
+        // (4096x28672, 8192x14336 and 8192x28672, K = 4096).
+        if (stream_on && ncu > 0 && !batched && p.bias == nullptr && (p.kbytes / 128) % 8 == 0 && p.ldc % 8 == 0) {
             constexpr int SLDS = stream_lds<MODE>();
             static_assert(SLDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
             auto skern = dense_stream_kernel<MODE>;
