@@ -149,4 +149,15 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// n / d with C's truncation toward zero, for |n| < 2^31 and 1 <= d < 2^16,
+// from r = 1.0 / d rounded to double (3 VALU instructions instead of an
+// integer division's ~20): |n * r - n / d| <= 2^31 * 2^-52 = 2^-21, and a
+// quotient that is not an integer lies at least 1/d > 2^-16 from the
+// integers, so moving 2^-20 away from zero before truncating gives the exact
+// quotient in both cases.
+__device__ __forceinline__ int div_recip(int n, double r) {
+    const double x = (double)n * r;
+    return (int)(n >= 0 ? x + 0x1p-20 : x - 0x1p-20);
+}
+
 }  // namespace hkq

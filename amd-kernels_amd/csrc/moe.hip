@@ -36,9 +36,11 @@ struct MoeParams {
     const int32_t* offs;
     const int32_t* expt_data;
     int T, E, N, K, topk, grid_m, y_rows, g_len;
+    double rtopk;  // 1.0 / topk (div_recip)
     int64_t sxm, swe, swn, sym;
     int64_t xs_tok, ws_e, ws_n, ws_gn, bias_e;
     int tiles_n, group_m, c16;
+    int xcd_cols;  // pair_walk's column order
     // per-channel scales / bias readable as float4 (16-byte aligned rows of
     // contiguous channels, one scale per channel)
     int ws_vec, bias_vec;
@@ -52,8 +54,10 @@ constexpr int MOE_BM = 128;  // rows per OGS routing block
 constexpr int MOE_WM = 2, MOE_WN = 2, MOE_TN = 4, MOE_BN = MOE_WN * MOE_TN * 32;
 
 // Rows [row0, row0 + TM*64) of expert e (sorted rows start + row0 + r) times
-// columns [n0, n0 + 256).
-template <int TM, int KTB, int NS>
+// columns [n0, n0 + 256). LEAN: no bias, and the column scales absent or one
+// per channel readable as float4 (ws_vec); the epilogue then carries no code
+// for the other layouts.
+template <int TM, int KTB, int NS, bool LEAN>
 __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, int n0, HKQ_LDS uint8_t* smem) {
     constexpr int TN = MOE_TN;
     using Cfg = DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, TM, TN, KTB>;
@@ -72,7 +76,7 @@ __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, i
     auto token_of = [&](int r) {
         const int s = start + row0 + r;
         if (r >= rows || s >= p.g_len) return -1;
-        const int t = p.gather ? p.gather[s] / p.topk : s;
+        const int t = p.gather ? div_recip(p.gather[s], p.rtopk) : s;
         return (t >= 0 && t < p.T) ? t : -1;
     };
 
@@ -114,7 +118,7 @@ __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, i
         if (!p.ws) return make_float4(1.f, 1.f, 1.f, 1.f);
         if (n >= p.N) return make_float4(0.f, 0.f, 0.f, 0.f);
         const float* w = p.ws + (int64_t)e * p.ws_e;
-        if (p.ws_vec) return *reinterpret_cast<const float4*>(w + n);
+        if (LEAN || p.ws_vec) return *reinterpret_cast<const float4*>(w + n);
         float v[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) v[c] = w[(int64_t)((n + c) / p.ws_gn) * p.ws_n];
@@ -122,7 +126,7 @@ __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, i
     };
     auto row_scale = [&](int j) { return rs[j]; };
     uint16_t* Y = p.Y + (int64_t)s0 * p.sym;
-    if (p.bias)
+    if (!LEAN && p.bias)
         store_tile_bf16<TM, TN>(acc, smem, wave, lane, Y, p.sym, out_rows, p.N, wm * TM * 32, nw, p.c16 != 0, row_scale,
                                 col_scale4, [&](int i, int g) {
                                     const int n = nw + i * 32 + 8 * g + 4 * khalf;
@@ -142,12 +146,27 @@ __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, i
 // differ, and giving each XCD its own range of experts (as tile_coords does for
 // the dense GEMMs) left XCDs idle: the A8W8 gate/up and down projections ran
 // 9% and 31% slower that way, the MXFP4 ones 16% and 33%.
-__device__ __forceinline__ void pair_walk(int bid, int pairs, int tiles_n, int group, int& q, int& tn) {
+// xcd_cols: within a group the columns go in blocks of 8, one column of the
+// block per consecutive id and the group's pairs one after the other, so that
+// (dispatch placing id u on XCD u % 8, and group * tiles_n % 8 == 0) each XCD
+// holds every pair of the group on the same columns: the pairs share each
+// weight tile and each pair's activation rows in that XCD's L2. Otherwise the
+// group's pairs alternate id by id (a weight tile's pairs on neighbouring XCDs).
+__device__ __forceinline__ void pair_walk(int bid, int pairs, int tiles_n, int group, int xcd_cols, int& q, int& tn) {
     const int per = group * tiles_n;
     const int grp = bid / per, first = grp * group;
     const int gsize = min(pairs - first, group), in_g = bid - grp * per;
-    q = first + in_g % gsize;
-    tn = in_g / gsize;
+    if (!xcd_cols) {
+        q = first + in_g % gsize;
+        tn = in_g / gsize;
+        return;
+    }
+    const int nfull = tiles_n >> 3, blk = 8 * gsize;
+    const int cb = min(in_g / blk, nfull);  // column block; the last one may be narrower
+    const int rem = in_g - cb * blk;
+    const int w = cb < nfull ? 8 : tiles_n - 8 * nfull;
+    q = first + rem / w;
+    tn = 8 * cb + rem % w;
 }
 
 // Work unit of workgroup bid: tile t (pair q, column tn) in pair_walk order,
@@ -157,8 +176,8 @@ __device__ __forceinline__ void pair_walk(int bid, int pairs, int tiles_n, int g
 // last, so these are the last live tiles and the empty ones after them):
 //   units [0, s0): tile u; then block (u - s0) & 1 of tile s0 + (u - s0) / 2.
 // Returns false for the spare units past the last tile.
-__device__ __forceinline__ bool pair_unit(int bid, int pairs, int tiles_n, int group, int split, int& q, int& tn,
-                                          int& half) {
+__device__ __forceinline__ bool pair_unit(int bid, int pairs, int tiles_n, int group, int xcd_cols, int split, int& q,
+                                          int& tn, int& half) {
     const int total = pairs * tiles_n;
     const int s0 = total - split;
     int t;
@@ -170,9 +189,16 @@ __device__ __forceinline__ bool pair_unit(int bid, int pairs, int tiles_n, int g
         half = (bid - s0) & 1;
         if (t >= total) return false;
     }
-    pair_walk(t, pairs, tiles_n, group, q, tn);
+    pair_walk(t, pairs, tiles_n, group, xcd_cols, q, tn);
     return true;
 }
+
+// pair_walk's column order (host side): XCD-aligned columns for wide
+// projections (measured on MI355X, Mixtral A8W8 gate/up, N = 28672: 0.981 ->
+// 0.963 ms, L2 hit rate 44% -> 55%; with 8 x 1024 rows per expert 0.858 ->
+// 0.825 ms, 35% -> 62%), the alternating order for narrow ones (down, N =
+// 4096: 0.540 vs 0.552 ms).
+static int moe_xcd_cols(int tiles_n) { return tiles_n >= 32 ? 1 : 0; }
 
 // Tiles of the last round that pair_unit cuts in two (host side).
 static int64_t moe_tail_split(int64_t tiles) {
@@ -184,12 +210,12 @@ static int64_t moe_tail_split(int64_t tiles) {
 // Workgroup: routing entries (2q, 2q + 1) x column tile tn. Two consecutive
 // blocks of one expert form one 256-row tile; otherwise each valid entry is a
 // 128-row tile, one after the other.
-template <int KTB, int NS>
+template <int KTB, int NS, bool LEAN>
 __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const MoeParams p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
     int q, tn;
-    pair_walk(blockIdx.x, (p.grid_m + 1) / 2, p.tiles_n, p.group_m, q, tn);
+    pair_walk(blockIdx.x, (p.grid_m + 1) / 2, p.tiles_n, p.group_m, p.xcd_cols, q, tn);
     const int n0 = tn * MOE_BN;
     const int pm0 = 2 * q, pm1 = 2 * q + 1;
     const int ed0 = p.expt_data[pm0], ed1 = pm1 < p.grid_m ? p.expt_data[pm1] : -1;
@@ -199,13 +225,13 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const
     const bool v0 = ed0 >= 0 && e0 < p.E, v1 = ed1 >= 0 && e1 < p.E;
     const int b0 = ed0 >> 16, b1 = ed1 >> 16;
     if (v0 && v1 && e0 == e1 && b1 == b0 + 1) {
-        moe_block<4, KTB, NS>(p, e0, b0 * MOE_BM, n0, smem);
+        moe_block<4, KTB, NS, LEAN>(p, e0, b0 * MOE_BM, n0, smem);
         return;
     }
-    if (v0) moe_block<2, KTB, NS>(p, e0, b0 * MOE_BM, n0, smem);
+    if (v0) moe_block<2, KTB, NS, LEAN>(p, e0, b0 * MOE_BM, n0, smem);
     if (v1) {
         __syncthreads();  // every wave is done with the first block's epilogue staging
-        moe_block<2, KTB, NS>(p, e1, b1 * MOE_BM, n0, smem);
+        moe_block<2, KTB, NS, LEAN>(p, e1, b1 * MOE_BM, n0, smem);
     }
 }
 
@@ -242,7 +268,7 @@ __global__ __launch_bounds__(64 * MOE_NARROW_WAVES) void moe_narrow_kernel(const
         const int rr = t * 16 + r, sr = start + b * MOE_BM + rr;
         int tk = -1;
         if (rr < rows && sr < p.g_len) {
-            tk = p.gather ? p.gather[sr] / p.topk : sr;
+            tk = p.gather ? div_recip(p.gather[sr], p.rtopk) : sr;
             if (tk < 0 || tk >= p.T) tk = -1;
         }
         srow[t] = sr;
@@ -374,18 +400,20 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
     using Half = DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 2, MOE_TN, KTB>;
     constexpr int LDS = Whole::lds_bytes(NS) > Half::lds_bytes(NS) ? Whole::lds_bytes(NS) : Half::lds_bytes(NS);
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
-    auto kern = moe_gemm_kernel<KTB, NS>;
-    static bool attr_set = false;
-    if (!attr_set) {
+    const bool lean = !p.bias && (!p.ws || p.ws_vec);
+    auto kern = lean ? moe_gemm_kernel<KTB, NS, true> : moe_gemm_kernel<KTB, NS, false>;
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[lean]) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
         if (e != hipSuccess) {
             set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", LDS, hipGetErrorString(e));
             return (int)e;
         }
-        attr_set = true;
+        attr_set[lean] = true;
     }
     p.tiles_n = (p.N + MOE_BN - 1) / MOE_BN;
     if (p.group_m <= 0) p.group_m = 2;
+    p.xcd_cols = moe_xcd_cols(p.tiles_n);
     const int64_t nblk = (int64_t)((p.grid_m + 1) / 2) * p.tiles_n;
     if (nblk == 0) return 0;
     kern<<<dim3((unsigned)nblk), 64 * MOE_WM * MOE_WN, LDS, stream>>>(p);
@@ -415,7 +443,9 @@ struct MoeFp4Params {
     const int32_t* sorted;  // [grid_m * 128]
     const int32_t* expert;  // [grid_m]
     int tokens, E, N, K, topk, num_valid, grid_m, tiles_n, group_m, c16;
-    int split;  // tiles of the last round cut into their two blocks (pair_unit)
+    double rtopk;  // 1.0 / topk (div_recip)
+    int split;     // tiles of the last round cut into their two blocks (pair_unit)
+    int xcd_cols;  // pair_walk's column order
     int64_t sam, sas, sbe, sbn, sbse, sbsn, scm;
 };
 
@@ -441,7 +471,7 @@ __device__ __forceinline__ void moe_fp4_block(const MoeFp4Params& p, int pm, int
     // A row of tile row r, or -1 (padding, or a row past the activations)
     auto arow_of = [&](int r) {
         const int id = gate_of(r);
-        const int t = id < 0 ? -1 : id / p.topk;
+        const int t = id < 0 ? -1 : div_recip(id, p.rtopk);
         return t < p.tokens ? t : -1;
     };
 
@@ -523,7 +553,7 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_mxfp4_kernel(cons
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
     int q, tn, half;
-    if (!pair_unit(blockIdx.x, (p.grid_m + 1) / 2, p.tiles_n, p.group_m, p.split, q, tn, half)) return;
+    if (!pair_unit(blockIdx.x, (p.grid_m + 1) / 2, p.tiles_n, p.group_m, p.xcd_cols, p.split, q, tn, half)) return;
     const int n0 = tn * MOE_BN;
     const int pm0 = 2 * q, pm1 = 2 * q + 1;
     const int e0 = p.expert[pm0], e1 = pm1 < p.grid_m ? p.expert[pm1] : -2;
@@ -599,7 +629,7 @@ __global__ __launch_bounds__(64 * MOE_NARROW_WAVES) void moe_fp4_narrow_kernel(c
         const int id0 = ids[g * 16 + r];
         const int id = (id0 >= 0 && id0 < p.num_valid) ? id0 : -1;
         if (__builtin_amdgcn_ballot_w64(id >= 0) == 0) continue;  // uniform: no valid entry in the group
-        const int tk = id < 0 ? -1 : id / p.topk;
+        const int tk = id < 0 ? -1 : div_recip(id, p.rtopk);
         const bool live = tk >= 0 && tk < p.tokens;
         // Offsets stay below 2^32: valid ones are below 2^31, an invalid row's
         // is OOB itself, and the K part is below 2^31.
@@ -692,6 +722,7 @@ static int launch_moe_fp4(MoeFp4Params& p, hipStream_t stream) {
     }
     p.tiles_n = (p.N + MOE_BN - 1) / MOE_BN;
     if (p.group_m <= 0) p.group_m = 1;
+    p.xcd_cols = moe_xcd_cols(p.tiles_n);
     const int64_t tiles = (int64_t)((p.grid_m + 1) / 2) * p.tiles_n;
     if (tiles == 0) return 0;
     p.split = (int)moe_tail_split(tiles);
@@ -711,8 +742,8 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
                             int64_t K, int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we,
                             int64_t stride_wn, int64_t stride_ym, int64_t y_rows, int64_t gather_len,
                             hipStream_t stream) {
-    HKQ_CHECK_ARG(T >= 0 && E > 0 && E <= 0xFFFF && N >= 0 && K > 0 && grid_m >= 0 && topk > 0,
-                  "T, grid_m >= 0; 0 < E <= 65535; K, topk > 0");
+    HKQ_CHECK_ARG(T >= 0 && E > 0 && E <= 0xFFFF && N >= 0 && K > 0 && grid_m >= 0 && topk > 0 && topk <= 0xFFFF,
+                  "T, grid_m >= 0; 0 < E <= 65535; K > 0; 0 < topk <= 65535");
     HKQ_CHECK_ARG(T < (1 << 30) && N < (1 << 30) && K < (1 << 30) && grid_m < (1 << 30), "dimensions must be < 2^30");
     HKQ_CHECK_ARG(K % 64 == 0, "K must be a multiple of 64");
     HKQ_CHECK_ARG(N % 4 == 0, "N must be a multiple of 4");
@@ -739,7 +770,7 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     p.hist = hist;
     p.offs = offs;
     p.expt_data = expt_data;
-    p.T = (int)T; p.E = (int)E; p.N = (int)N; p.K = (int)K; p.topk = (int)topk; p.grid_m = (int)grid_m;
+    p.T = (int)T; p.E = (int)E; p.N = (int)N; p.K = (int)K; p.topk = (int)topk; p.rtopk = 1.0 / (double)topk; p.grid_m = (int)grid_m;
     p.y_rows = (int)y_rows;
     p.g_len = gather ? (int)gather_len : (int)y_rows;
     p.sxm = stride_xm; p.swe = stride_we; p.swn = stride_wn; p.sym = stride_ym;
@@ -769,9 +800,9 @@ extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* 
                              int64_t stride_be, int64_t stride_bn, int64_t stride_cm, int64_t stride_amxm,
                              int64_t stride_bmxe, int64_t stride_bmxn, int64_t num_tokens, int64_t num_experts,
                              int64_t grid_m, hipStream_t stream) {
-    HKQ_CHECK_ARG(N >= 0 && K > 0 && num_valid_tokens >= 0 && top_k > 0 && num_tokens >= 0 && num_experts > 0 &&
-                      grid_m >= 0,
-                  "N, num_valid_tokens, num_tokens, grid_m >= 0; K, top_k, num_experts > 0");
+    HKQ_CHECK_ARG(N >= 0 && K > 0 && num_valid_tokens >= 0 && top_k > 0 && top_k <= 0xFFFF && num_tokens >= 0 &&
+                      num_experts > 0 && grid_m >= 0,
+                  "N, num_valid_tokens, num_tokens, grid_m >= 0; K, num_experts > 0; 0 < top_k <= 65535");
     HKQ_CHECK_ARG(N < (1 << 30) && K < (1 << 30) && grid_m < (1 << 22) && num_tokens < (1 << 30) &&
                       num_valid_tokens < (1 << 30),
                   "dimensions out of range");
@@ -807,7 +838,7 @@ extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* 
     p.topk_w = mul_routed_weight ? topk_weights : nullptr;
     p.sorted = sorted_token_ids;
     p.expert = expert_ids;
-    p.tokens = (int)num_tokens; p.E = (int)num_experts; p.N = (int)N; p.K = (int)K; p.topk = (int)top_k;
+    p.tokens = (int)num_tokens; p.E = (int)num_experts; p.N = (int)N; p.K = (int)K; p.topk = (int)top_k; p.rtopk = 1.0 / (double)top_k;
     p.num_valid = (int)num_valid_tokens; p.grid_m = (int)grid_m;
     p.sam = stride_am; p.sas = stride_amxm; p.sbe = stride_be; p.sbn = stride_bn; p.sbse = stride_bmxe;
     p.sbsn = stride_bmxn; p.scm = stride_cm;

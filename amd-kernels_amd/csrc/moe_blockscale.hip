@@ -110,6 +110,7 @@ struct MoeBsParams {
     const int32_t* offs;
     const int32_t* expt_data;
     int T, E, N, K, topk, grid_m, y_rows, g_len, gk, gn, tiles_n, c16;
+    double rtopk;  // 1.0 / topk (div_recip)
     int64_t sxm, swe, swn, sym, xsm, xsk, wse, wsk, wsn, bias_e;
     int64_t xs_elems, ws_elems;  // reads of the scale tensors stay below these extents
 };
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(64 * MBS_NW, 2) void moe_blockscale_kernel(const Mo
     auto token_of = [&](int r) {
         const int s = start + row0 + r;
         if (r >= rows || s >= p.g_len) return -1;
-        const int t = p.gather ? p.gather[s] / p.topk : s;
+        const int t = p.gather ? div_recip(p.gather[s], p.rtopk) : s;
         return (t >= 0 && t < p.T) ? t : -1;
     };
 
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void moe_blockscale8_kernel(const Mo
     auto token_of = [&](int r) {
         const int s = start + row0 + r;
         if (r >= rows || s >= p.g_len) return -1;
-        const int t = p.gather ? p.gather[s] / p.topk : s;
+        const int t = p.gather ? div_recip(p.gather[s], p.rtopk) : s;
         return (t >= 0 && t < p.T) ? t : -1;
     };
 
@@ -447,8 +448,8 @@ extern "C" int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, co
                                        int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we,
                                        int64_t stride_wn, int64_t stride_ym, int64_t y_rows, int64_t gather_len,
                                        hkq_stream_t stream) {
-    HKQ_CHECK_ARG(T >= 0 && E > 0 && E <= 0xFFFF && N >= 0 && K > 0 && grid_m >= 0 && topk > 0,
-                  "T, grid_m >= 0; 0 < E <= 65535; K, topk > 0");
+    HKQ_CHECK_ARG(T >= 0 && E > 0 && E <= 0xFFFF && N >= 0 && K > 0 && grid_m >= 0 && topk > 0 && topk <= 0xFFFF,
+                  "T, grid_m >= 0; 0 < E <= 65535; K > 0; 0 < topk <= 65535");
     HKQ_CHECK_ARG(T < (1 << 30) && N < (1 << 30) && K < (1 << 30) && grid_m < (1 << 30), "dimensions must be < 2^30");
     HKQ_CHECK_ARG(K % 64 == 0, "K must be a multiple of 64");
     HKQ_CHECK_ARG(N % 4 == 0, "N must be a multiple of 4");
@@ -487,7 +488,7 @@ extern "C" int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, co
     p.hist = hist;
     p.offs = offs;
     p.expt_data = expt_data;
-    p.T = (int)T; p.E = (int)E; p.N = (int)N; p.K = (int)K; p.topk = (int)topk; p.grid_m = (int)grid_m;
+    p.T = (int)T; p.E = (int)E; p.N = (int)N; p.K = (int)K; p.topk = (int)topk; p.rtopk = 1.0 / (double)topk; p.grid_m = (int)grid_m;
     p.y_rows = (int)y_rows;
     p.g_len = gather ? (int)gather_len : (int)y_rows;
     p.gk = (int)group_k; p.gn = (int)group_n;

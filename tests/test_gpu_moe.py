@@ -68,11 +68,13 @@ def test_moe_reference_setup(orc):
 # At most 32 routed rows (or 64 with N <= 4096): the decode (streaming)
 # kernel, with 16 or 64 columns per workgroup (N > 4096), one, two or four
 # 16-row groups, ragged N and K-steps uneven over the 4 waves; (24, 2, 2, 384,
-# 4104) has 48 rows and a wide N, so it takes the tiled kernel.
+# 4104) has 48 rows and a wide N, so it takes the tiled kernel. N >= 8192 (32
+# or more column tiles) walks the columns in XCD-aligned blocks of 8: 8320 has
+# 33 column tiles (a last block of one), 700 x 3 with topk 2 odd pair groups.
 @pytest.mark.parametrize("T,E,topk,K,N", [(300, 4, 2, 512, 520), (1, 8, 2, 256, 512), (1000, 8, 2, 1024, 1024),
                                           (257, 3, 1, 384, 260), (77, 4, 2, 320, 256), (5, 8, 2, 512, 4100),
                                           (16, 8, 2, 384, 1000), (16, 4, 2, 640, 4200), (30, 8, 2, 256, 520),
-                                          (24, 2, 2, 384, 4104)])
+                                          (24, 2, 2, 384, 4104), (300, 4, 2, 256, 8320), (700, 3, 2, 384, 9216)])
 def test_moe_per_token_per_channel(orc, T, E, topk, K, N):
     require_gpu()
     _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, T + N)
