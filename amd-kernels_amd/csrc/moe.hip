@@ -19,6 +19,8 @@
 // never enter LDS). Metadata is bounds-checked: entries naming an expert >= E,
 // rows past the gather index or tokens past T read zero or are skipped instead
 // of faulting.
+#include <algorithm>
+
 #include "gemm_mainloop.h"
 #include "hkq_host.h"
 
@@ -54,9 +56,9 @@ constexpr int MOE_BM = 128;  // rows per OGS routing block
 constexpr int MOE_WM = 2, MOE_WN = 2, MOE_TN = 4, MOE_BN = MOE_WN * MOE_TN * 32;
 
 // Rows [row0, row0 + TM*64) of expert e (sorted rows start + row0 + r) times
-// columns [n0, n0 + 256). LEAN: no bias, and the column scales absent or one
-// per channel readable as float4 (ws_vec); the epilogue then carries no code
-// for the other layouts.
+// columns [n0, n0 + 256). LEAN: no bias, and the column scales absent, one
+// per expert or one per channel readable as float4 (ws_vec); the epilogue
+// then carries no code for the other layouts.
 template <int TM, int KTB, int NS, bool LEAN>
 __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, int n0, HKQ_LDS uint8_t* smem) {
     constexpr int TN = MOE_TN;
@@ -118,10 +120,16 @@ __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, i
         if (!p.ws) return make_float4(1.f, 1.f, 1.f, 1.f);
         if (n >= p.N) return make_float4(0.f, 0.f, 0.f, 0.f);
         const float* w = p.ws + (int64_t)e * p.ws_e;
+        if (p.ws_n == 0) {  // one scale per expert
+            const float v = w[0];
+            return make_float4(v, v, v, v);
+        }
         if (LEAN || p.ws_vec) return *reinterpret_cast<const float4*>(w + n);
+        // column groups (ws_gn >= 2, clamped to N by the host: 32-bit quotients)
+        const int gn = (int)p.ws_gn;
         float v[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] = w[(int64_t)((n + c) / p.ws_gn) * p.ws_n];
+        for (int c = 0; c < 4; ++c) v[c] = w[(int64_t)((n + c) / gn) * p.ws_n];
         return make_float4(v[0], v[1], v[2], v[3]);
     };
     auto row_scale = [&](int j) { return rs[j]; };
@@ -349,8 +357,9 @@ __global__ __launch_bounds__(64 * MOE_NARROW_WAVES) void moe_narrow_kernel(const
             if (p.ws_vec) {
                 cs = *reinterpret_cast<const float4*>(wsc + n);
             } else {
-                cs = make_float4(wsc[(int64_t)(n / p.ws_gn) * p.ws_n], wsc[(int64_t)((n + 1) / p.ws_gn) * p.ws_n],
-                                 wsc[(int64_t)((n + 2) / p.ws_gn) * p.ws_n], wsc[(int64_t)((n + 3) / p.ws_gn) * p.ws_n]);
+                const int gn = (int)p.ws_gn;
+                cs = make_float4(wsc[(int64_t)(n / gn) * p.ws_n], wsc[(int64_t)((n + 1) / gn) * p.ws_n],
+                                 wsc[(int64_t)((n + 2) / gn) * p.ws_n], wsc[(int64_t)((n + 3) / gn) * p.ws_n]);
             }
         }
         if (p.bias) {
@@ -400,7 +409,7 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
     using Half = DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 2, MOE_TN, KTB>;
     constexpr int LDS = Whole::lds_bytes(NS) > Half::lds_bytes(NS) ? Whole::lds_bytes(NS) : Half::lds_bytes(NS);
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
-    const bool lean = !p.bias && (!p.ws || p.ws_vec);
+    const bool lean = !p.bias && (!p.ws || p.ws_vec || p.ws_n == 0);
     auto kern = lean ? moe_gemm_kernel<KTB, NS, true> : moe_gemm_kernel<KTB, NS, false>;
     static bool attr_set[2] = {false, false};
     if (!attr_set[lean]) {
@@ -774,7 +783,8 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     p.y_rows = (int)y_rows;
     p.g_len = gather ? (int)gather_len : (int)y_rows;
     p.sxm = stride_xm; p.swe = stride_we; p.swn = stride_wn; p.sym = stride_ym;
-    p.xs_tok = xs_stride_tok; p.ws_e = ws_stride_e; p.ws_n = ws_stride_n; p.ws_gn = ws_group_n; p.bias_e = bias_stride_e;
+    p.xs_tok = xs_stride_tok; p.ws_e = ws_stride_e; p.ws_n = ws_stride_n; p.bias_e = bias_stride_e;
+    p.ws_gn = std::min<int64_t>(ws_group_n, std::max<int64_t>(N, 1));  // same quotients for n < N, 32-bit
     p.ws_vec = w_scale && ws_stride_n == 1 && ws_group_n == 1 && ws_stride_e % 4 == 0 &&
                reinterpret_cast<uintptr_t>(w_scale) % 16 == 0;
     p.bias_vec = bias && bias_stride_e % 4 == 0 && reinterpret_cast<uintptr_t>(bias) % 16 == 0;

@@ -118,6 +118,21 @@ def test_moe_entry_order_and_pairing(orc):
         check_rows(orc, Y, ref)
 
 
+@pytest.mark.parametrize("bias", [False, True])
+def test_moe_per_expert_weight_scale_tiled(orc, bias):
+    """One weight scale per expert on the tiled kernel, without a bias (the
+    lean epilogue's per-expert branch) and with one (the general epilogue)."""
+    require_gpu()
+    T, E, topk, K, N = 600, 4, 2, 512, 1040
+    _, hist, offs, gather, ed, X, xs, W, _ = make_problem(orc, T, E, topk, K, N, 23)
+    rng = np.random.default_rng(24)
+    ws = (rng.random(E) * 0.01 + 0.001).astype(np.float32)
+    b = (rng.standard_normal((E, N)) * 0.1).astype(np.float32) if bias else None
+    Y = run_moe(X, W, hist, offs, gather, ed, topk, xs, ws, b)
+    ref = orc.moe_ref(X, W, xs, ws, b, gather, hist, offs, ed, topk, 128, "enk")
+    check_rows(orc, Y, ref)
+
+
 def test_moe_decode_reference_setup(orc):
     """The reference test's scale and bias layout (per-tensor activation scale,
     per-expert weight scale, bias) at a decode size (8 tokens, top-2)."""
