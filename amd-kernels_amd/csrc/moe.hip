@@ -217,7 +217,8 @@ static int64_t moe_tail_split(int64_t tiles) {
 
 // Workgroup: routing entries (2q, 2q + 1) x column tile tn. Two consecutive
 // blocks of one expert form one 256-row tile; otherwise each valid entry is a
-// 128-row tile, one after the other.
+// 128-row tile (64 rows when it holds at most 64 of its expert's rows), one
+// after the other.
 template <int KTB, int NS, bool LEAN>
 __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const MoeParams p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
@@ -236,10 +237,18 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const
         moe_block<4, KTB, NS, LEAN>(p, e0, b0 * MOE_BM, n0, smem);
         return;
     }
-    if (v0) moe_block<2, KTB, NS, LEAN>(p, e0, b0 * MOE_BM, n0, smem);
+    // a block holding at most 64 of its expert's rows (an expert's last block)
+    // runs as a 64-row tile
+    auto block = [&](int e, int b) {
+        if (p.hist[e] - b * MOE_BM <= MOE_BM / 2)
+            moe_block<1, KTB, NS, LEAN>(p, e, b * MOE_BM, n0, smem);
+        else
+            moe_block<2, KTB, NS, LEAN>(p, e, b * MOE_BM, n0, smem);
+    };
+    if (v0) block(e0, b0);
     if (v1) {
         __syncthreads();  // every wave is done with the first block's epilogue staging
-        moe_block<2, KTB, NS, LEAN>(p, e1, b1 * MOE_BM, n0, smem);
+        block(e1, b1);
     }
 }
 
