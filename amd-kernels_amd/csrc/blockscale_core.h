@@ -57,14 +57,31 @@ __device__ __forceinline__ uint32_t bs_load_dst(int st, int q, int wave) {
 // return every load has landed and every wave is past its LDS reads.
 // The wave computes tile rows wm*64 .. +63 and TN n-tiles from tile column cn
 // (TN may differ between the waves of a workgroup: every wave issues the same
-// loads and barriers).
-template <int SBM, int TN, class Issue>
+// loads and barriers). COMPUTE false: a wave whose rows all lie outside the
+// tile only issues its share of the loads and takes the barriers (acc stays
+// zero), leaving its SIMD's MFMA and VALU pipes to the other wave.
+template <int SBM, int TN, bool COMPUTE = true, class Issue>
 __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int lane, int wm, int cn, int KTN, Issue& issue,
                                           v16f (&acc)[TN][BS_TM]) {
     using KT = KTile<BS_KT>;
     constexpr int TM = BS_TM;
     static_assert(TN >= 1 && TN <= BS_TN, "n-tiles per wave");
     const int khalf = lane >> 5;
+    if constexpr (!COMPUTE) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) acc[i][j] = v16f{};
+#pragma unroll
+        for (int q = 0; q < BS_NLD; ++q) issue(0, q);
+        for (int kt = 0; kt < KTN; ++kt) {
+            tile_barrier<0>();
+#pragma unroll
+            for (int q = 0; q < BS_NLD; ++q) issue(kt + 1, q);
+        }
+        tile_barrier<0>();
+        return;
+    }
 
     // Fragment reads: lane row lane%32 of m-tile / n-tile t, logical chunks
     // 4*ks + 2*khalf + {0, 1} of K-step ks. Rows 32 apart share the swizzle, so

@@ -393,8 +393,13 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void moe_blockscale8_kernel(const Mo
         }
     };
 
+    // waves whose 64 rows lie past the tile's (every wave with wm >= 2 in a
+    // lone block) only load: one computing wave per SIMD instead of two
     v16f acc[TN][TM];
-    bs8_kloop<SBM, BS_TN>(smem, lane, wm, wn * BS_TN * 32, KTN, issue, acc);
+    if (wm * TM * 32 < rows)
+        bs8_kloop<SBM, BS_TN, true>(smem, lane, wm, wn * BS_TN * 32, KTN, issue, acc);
+    else
+        bs8_kloop<SBM, BS_TN, false>(smem, lane, wm, wn * BS_TN * 32, KTN, issue, acc);
 
     const int s0 = start + row0;
     const int nw = n0 + wn * TN * 32;
