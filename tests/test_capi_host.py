@@ -115,3 +115,14 @@ def test_moe_a8w8_rejects_x_past_2gib():
     args = [p, p, p, None, 0, None, 0, 0, 1, None, 0, None, p, p, p,
             T, 8, 4096, K, 16, 2, K, 4096 * K, K, 4096, T * 2, 0, None]
     _expect_invalid("hkq_moe_a8w8", *args, match="2\\^31")
+
+
+def test_moe_a8w8_rejects_topk_past_65535():
+    """The MoE kernels divide gather indices by top_k through a reciprocal
+    multiply that is exact for top_k < 2^16; larger values are rejected before
+    any launch."""
+    p = 0x1000  # never dereferenced: validation fails first
+    K = 256
+    args = [p, p, p, None, 0, None, 0, 0, 1, None, 0, None, p, p, p,
+            16, 8, 256, K, 16, 1 << 16, K, 256 * K, K, 256, 16, 0, None]
+    _expect_invalid("hkq_moe_a8w8", *args, match="topk")
