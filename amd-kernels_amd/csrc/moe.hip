@@ -565,7 +565,8 @@ __device__ __forceinline__ void moe_fp4_zero_block(const MoeFp4Params& p, int pm
 
 // Workgroup: routing blocks (2q, 2q + 1) x column tile tn; two blocks of one
 // expert form one 256-row tile, otherwise each block is its own 128-row tile
-// (or, with expert -1, zeros). Tile order: pair_walk, one pair at a time.
+// (64 rows when its upper half is padding; with expert -1, zeros). Tile
+// order: pair_walk, one pair at a time.
 template <int KTB, int NS>
 __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_mxfp4_kernel(const MoeFp4Params p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
@@ -591,7 +592,13 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_mxfp4_kernel(cons
             moe_fp4_zero_block(p, pm, n0);
         } else if (e >= 0 && e < p.E) {
             __syncthreads();  // every wave is done with an earlier block's epilogue staging
-            moe_fp4_block<2, KTB, NS>(p, pm, e, n0, smem);
+            // entries 64..127 all padding (an expert's last block): a 64-row
+            // tile (every wave reads the same 64 entries: a uniform choice)
+            const int id = p.sorted[(int64_t)pm * MOE_BM + MOE_BM / 2 + (threadIdx.x & 63)];
+            if (__ballot(id >= 0 && id < p.num_valid) == 0)
+                moe_fp4_block<1, KTB, NS>(p, pm, e, n0, smem);
+            else
+                moe_fp4_block<2, KTB, NS>(p, pm, e, n0, smem);
         }
     }
 }
