@@ -184,6 +184,26 @@ def test_moe_malformed_metadata_does_not_fault(orc):
     check_rows(orc, Y, ref)
 
 
+def test_moe_gather_division_bounds(orc):
+    """Gather values are divided by top_k through a reciprocal multiply: values
+    at the top of the int32 range give tokens past T (rows read zero), and
+    2T - 1 with top_k 2 gives the last token exactly."""
+    require_gpu()
+    T, E, topk, K, N = 128, 2, 2, 128, 256
+    _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 12)
+    g2 = gather.copy()
+    g2[3] = 0x7FFFFFFF  # token 2^30 - 1, past T
+    g2[4] = 0x7FFFFFFE
+    g2[6] = 2 * T - 1  # token T - 1
+    g2[7] = 2 * T      # token T, past T
+    Y = run_moe(X, W, hist, offs, g2, ed, topk, xs, ws)
+    g_ref = g2.copy()
+    g_ref[[3, 4, 7]] = 0  # any valid value: those rows are zeroed below
+    ref = orc.moe_ref(X, W, xs, ws, None, g_ref, hist, offs, ed, topk, 128, "enk")
+    ref[[3, 4, 7]] = 0.0
+    check_rows(orc, Y, ref)
+
+
 def mixtral_routing(orc, T, E, topk, seed):
     g = torch.Generator(device="cpu").manual_seed(seed)
     logits = torch.randn(T, E, generator=g)
