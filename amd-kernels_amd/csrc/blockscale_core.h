@@ -117,14 +117,15 @@ __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int lane, int w
     struct Op {
         v8i k[2];
     };
+    auto read_step = [&](const uint32_t (&base)[2][2], int t, int ks) {
+        const v4i lo = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base[ks][0] + (uint32_t)(t * 32 * BS_KT))));
+        const v4i hi = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base[ks][1] + (uint32_t)(t * 32 * BS_KT))));
+        return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
     auto read_op = [&](const uint32_t (&base)[2][2], int t) {
         Op o;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const v4i lo = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base[ks][0] + (uint32_t)(t * 32 * BS_KT))));
-            const v4i hi = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base[ks][1] + (uint32_t)(t * 32 * BS_KT))));
-            o.k[ks] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
+        for (int ks = 0; ks < 2; ++ks) o.k[ks] = read_step(base, t, ks);
         return o;
     };
 
@@ -150,10 +151,16 @@ __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int lane, int w
         for (int i = 0; i < TN; ++i)
             sbt[i] = SBM == BS_SB_WAVE ? sl[256 + cn / 128] : SBM == BS_SB_NTILE ? sl[256 + cn + i * 32] : 0.f;
         const Bases rb = bases(st);
-        Op fa[TM];
+        // the first MFMA's operands (K-step 0 of n-tile 0 and m-tile 0) are
+        // read first: the LDS counter is in order, so the MFMAs can start
+        // while the other fragments are still in flight
+        Op fa[TM], fb;
+        fb.k[0] = read_step(rb.b, 0, 0);
+        fa[0].k[0] = read_step(rb.a, 0, 0);
+        fb.k[1] = read_step(rb.b, 0, 1);
+        fa[0].k[1] = read_step(rb.a, 0, 1);
 #pragma unroll
-        for (int j = 0; j < TM; ++j) fa[j] = read_op(rb.a, j);
-        Op fb = read_op(rb.b, 0);
+        for (int j = 1; j < TM; ++j) fa[j] = read_op(rb.a, j);
 #pragma unroll
         for (int i = 0; i < TN; ++i) {
             constexpr int PER = (BS_NLD + TN - 1) / TN;
