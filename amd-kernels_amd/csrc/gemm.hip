@@ -236,6 +236,7 @@ constexpr int stream_lds() {
 // rows [tm*256 + half*BM, +BM) of it.
 template <int BM>
 struct DenseSeq {
+    static constexpr bool GATHER = false;
     const DenseParams* p;
     int tiles, KT;
     uint32_t lsa, lsb;
@@ -386,7 +387,7 @@ __device__ __forceinline__ void dense_stream(const DenseParams& p, int tiles, in
     DenseSeq<BM> seq{&p, tiles, p.kbytes / 128, (uint32_t)p.lsa, (uint32_t)p.lsb, first, stride, half};
     DirectEpi<MODE, TM, BM> epi{&seq, &p, smem + stream_lds<MODE>() - (MODE == MODE_A8W8 ? 2 * STREAM_SCL : 0), lane,
                                 wave};
-    const auto a_off = dense_offs<Cfg::NW, 128, Cfg::LA>(wave, lane, p.lda);
+    auto a_off = dense_offs<Cfg::NW, 128, Cfg::LA>(wave, lane, p.lda);
     const auto b_off = dense_offs<Cfg::NW, 128, Cfg::LB>(wave, lane, p.ldb);
     v16f acc[TN][TM];
     gemm_stream<MODE, WM, WN, TM, TN>(seq, a_off, b_off, smem, lane, wave, acc, epi);

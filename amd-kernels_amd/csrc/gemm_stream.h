@@ -26,14 +26,18 @@ struct StreamSrc {
     uint32_t a_bytes, b_bytes, as_bytes, bs_bytes;  // loads at or past these read zero
 };
 
-// Seq: { int tiles; int KT; uint32_t lsa, lsb; __device__ StreamSrc src(int t) const; }  (t < tiles)
+// Seq: { int tiles; int KT; uint32_t lsa, lsb; __device__ StreamSrc src(int t) const;  (t < tiles)
+//        static constexpr bool GATHER;   // true: the A rows differ per tile and
+//        __device__ void a_rows(int t, AOff& a_off) const;  // sets tile t's load offsets;
+//        called where the loads switch to tile t (two K-tiles before the end of
+//        tile t - 1), after at least one vmcnt(0) barrier of tile t - 1 }
 // Epi: { __device__ void begin(int t); __device__ void end(int t, v16f (&acc)[TN][TM]); }
 //   begin(t) runs before tile t's first K-tile is computed (e.g. to prefetch
 //   the tile's epilogue scales; loads it issues are waited for by the loop's
 //   next barrier), end(t, acc) after tile t's last MFMA has drained; it must
 //   not touch the LDS ring. On return every wave is past a vmcnt(0) barrier.
 template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, typename AOff, typename BOff, typename Seq, typename Epi>
-__device__ __forceinline__ void gemm_stream(const Seq& seq, const AOff& a_off, const BOff& b_off, HKQ_LDS uint8_t* smem,
+__device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const BOff& b_off, HKQ_LDS uint8_t* smem,
                                             int lane, int wave, v16f (&acc)[TN][TM], Epi& epi) {
     constexpr int KTB = 128, NS = 2;
     using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>;
@@ -278,6 +282,7 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, const AOff& a_off, c
         }
         ld_live = t + 1 < seq.tiles;
         ld = seq.src(min(t + 1, seq.tiles - 1));
+        if constexpr (Seq::GATHER) seq.a_rows(min(t + 1, seq.tiles - 1), a_off);
         ktile(KTN - 2, 0, P0{}, std::false_type{}, std::false_type{});
         ktile(KTN - 1, 1, P1{}, std::false_type{}, std::true_type{});
         mfma_drain();

@@ -20,8 +20,9 @@
 // rows past the gather index or tokens past T read zero or are skipped instead
 // of faulting.
 #include <algorithm>
+#include <cstdlib>
 
-#include "gemm_mainloop.h"
+#include "gemm_stream.h"
 #include "hkq_host.h"
 
 namespace hkq {
@@ -412,6 +413,309 @@ static int launch_moe_narrow(const MoeParams& p, int64_t routed_rows, hipStream_
     return hkq_launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// Persistent A8W8 MoE kernel over the dense GEMMs' K-tile stream
+// (gemm_stream.h), one workgroup per CU. The units whose two routing entries
+// are consecutive blocks of one expert (256-row tiles) form one stream: the
+// next tile's first K-tiles load during the current tile's last ones, its
+// gather entries reach LDS while the current tile computes (the tiled kernel
+// waits for them in each tile's prologue), and the epilogue stores C from
+// registers. The other units (pairs straddling two experts, lone blocks) run
+// afterwards as in the tiled kernel.
+// LEAN scale layouts only (no bias; column scales absent, per expert or per
+// channel), 128-byte K-tiles, K % 1024 == 0.
+constexpr int MS_MAXU = 64;  // units per workgroup (one per lane of wave 0; the host checks)
+using MoeWhole = DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 4, MOE_TN, 128>;
+constexpr int MS_SCL = 2 * MoeWhole::STAGE;   // 2 slots: 256 row scales, then 256 column scales
+constexpr int MS_SLOT = 2 * 256 * 4;
+constexpr int MS_TOK = MS_SCL + 2 * MS_SLOT;  // 2 slots of 256 gather entries
+constexpr int MS_WL = MS_TOK + 2 * 1024;      // stream units: e, row0, n0, start, rows (8 ints each)
+constexpr int MS_RL = MS_WL + MS_MAXU * 32;   // other units: ed0, ed1, n0 (4 ints each)
+constexpr int MS_CNT = MS_RL + MS_MAXU * 16;  // unit counts
+constexpr int MS_MAXP = 512;                  // routing-entry pairs (the host checks)
+constexpr int MS_WP = MS_CNT + 64;            // whole pairs: e, row0, start, rows (4 ints each)
+constexpr int MS_RP = MS_WP + MS_MAXP * 16;   // other pairs: ed0, ed1 (2 ints each)
+constexpr int MS_LDS = MS_RP + MS_MAXP * 8;
+static_assert(MS_LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
+static_assert(DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 2, MOE_TN, 128>::lds_bytes(2) <= MS_WL,
+              "the tiled blocks after the stream leave the unit lists alone");
+
+struct MoeStreamSeq {
+    static constexpr bool GATHER = true;
+    const MoeParams* p;
+    int tiles, KT;
+    uint32_t lsa, lsb;
+    const HKQ_LDS int* wl;
+    HKQ_LDS int* tok;
+    int lane, wave;
+    struct Unit {
+        int e, row0, n0, start, rows;
+    };
+    __device__ Unit unit(int k) const {
+        const HKQ_LDS int* u = wl + 8 * k;
+        return Unit{__builtin_amdgcn_readfirstlane(u[0]), __builtin_amdgcn_readfirstlane(u[1]),
+                    __builtin_amdgcn_readfirstlane(u[2]), __builtin_amdgcn_readfirstlane(u[3]),
+                    __builtin_amdgcn_readfirstlane(u[4])};
+    }
+    __device__ StreamSrc src(int k) const {
+        const Unit u = unit(k);
+        StreamSrc s;
+        s.a = p->X;
+        s.a_bytes = (uint32_t)min((int64_t)p->T * p->sxm, (int64_t)0x7FFFFFFF);
+        s.b = p->W + (int64_t)u.e * p->swe + (int64_t)u.n0 * p->swn;
+        s.b_bytes = (uint32_t)min((int64_t)min(p->N - u.n0, MOE_BN) * p->swn, (int64_t)0x7FFFFFFF);
+        s.as = s.bs = nullptr;
+        s.as_bytes = s.bs_bytes = 0;
+        return s;
+    }
+    // token of row r of tile k (-1: past the expert's rows, the gather index or T)
+    __device__ int token(int k, const Unit& u, int r) const {
+        const int s = u.start + u.row0 + r;
+        if (r >= u.rows || s >= p->g_len) return -1;
+        const int t = p->gather ? div_recip(tok[(k & 1) * 256 + r], p->rtopk) : s;
+        return (t >= 0 && t < p->T) ? t : -1;
+    }
+    // gather entries of tile k's 256 rows into token slot k & 1: one 4-byte
+    // LDS-direct load per lane and wave (zeros past the gather index, past the
+    // last tile or without a gather, so that every wave issues the load)
+    __device__ void load_tokens(int k) const {
+        int s0 = 0;
+        bool live = k < tiles && p->gather != nullptr;
+        if (live) {
+            const Unit u = unit(k);
+            s0 = u.start + u.row0;
+            live = s0 < p->g_len;
+        }
+        const uint32_t bytes = live ? (uint32_t)min(p->g_len - s0, 256) * 4u : 0u;
+        lds_load4(live ? p->gather + s0 : p->gather, bytes,
+                  reinterpret_cast<HKQ_LDS uint8_t*>(tok + (k & 1) * 256 + wave * 64), (uint32_t)(wave * 64 + lane) * 4u);
+    }
+    template <class AOff>
+    __device__ void a_rows(int k, AOff& a) const {
+        using KT = MoeWhole::KT;
+        const Unit u = unit(k);
+#pragma unroll
+        for (int i = 0; i < MoeWhole::LA; ++i) {
+            const int r = (i * MoeWhole::NW + wave) * MoeWhole::RPL + lane / KT::CHUNKS;
+            const int t = token(k, u, r);
+            a.v[i] = t < 0 ? OOB : (uint32_t)(t * p->sxm) + (uint32_t)(KT::load_chunk(lane, r) << 4);
+        }
+    }
+};
+
+// Epilogue of a stream tile: the A8W8 stream's register epilogue (one 16-byte
+// store per lane and (n-tile, m-tile, 16 columns), lanes outside C sent past
+// the buffer) into the tile's sorted rows, with the row scales (gathered per
+// token) and the column scales fetched into LDS when the tile begins.
+struct MoeStreamEpi {
+    static constexpr int TM = 4, TN = MOE_TN;
+    // per wave: the epilogue's C stores, then begin()'s row-scale, column-scale
+    // and gather-entry loads
+    static constexpr int VM_ISSUED = TN * TM * 2 + 3;
+    const MoeStreamSeq* seq;
+    const MoeParams* p;
+    HKQ_LDS uint8_t* scl;
+    int lane, wave;
+    __device__ void begin(int k) {
+        const MoeStreamSeq::Unit u = seq->unit(k);
+        HKQ_LDS uint8_t* slot = scl + (k & 1) * MS_SLOT;
+        const int t = seq->token(k, u, wave * 64 + lane);
+        const uint32_t xs_bytes =
+            p->xs ? (uint32_t)min(((int64_t)(p->T - 1) * p->xs_tok + 1) * 4, (int64_t)0x7FFFFFFF) : 0u;
+        lds_load4(p->xs, xs_bytes, slot + wave * 256, t < 0 ? OOB : (uint32_t)t * (uint32_t)p->xs_tok * 4u);
+        const int n = u.n0 + wave * 64 + lane;
+        const float* w = p->ws ? p->ws + (int64_t)u.e * p->ws_e : nullptr;
+        const uint32_t ws_bytes = p->ws ? (p->ws_n == 0 ? 4u : (uint32_t)p->N * 4u) : 0u;
+        lds_load4(w, ws_bytes, slot + 1024 + wave * 256, n < p->N ? (p->ws_n == 0 ? 0u : (uint32_t)n * 4u) : OOB);
+        seq->load_tokens(k + 1);
+    }
+    __device__ void end(int k, v16f (&acc)[TN][TM]) {
+        const MoeStreamSeq::Unit u = seq->unit(k);
+        const int wm = wave / MOE_WN, wn = wave % MOE_WN;
+        const int khalf = lane >> 5, r = lane & 31;
+        const HKQ_LDS float* sl = reinterpret_cast<const HKQ_LDS float*>(scl + (k & 1) * MS_SLOT);
+        const int s0 = u.start + u.row0;
+        const int mw0 = wm * TM * 32, nw0 = u.n0 + wn * TN * 32;
+        uint16_t* base = p->Y + (int64_t)(s0 + mw0) * p->sym + nw0;
+        const auto rc = make_rsrc(base, 0x7FFFFFFFu);
+        const int rows = min(u.rows, p->y_rows - s0) - mw0, cols = p->N - nw0;
+        const bool ragged = cols < TN * 32 && (cols & 7) != 0;
+        uint32_t roff[TM];
+        float rs[TM];
+        const int kc = 8 * khalf;
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+            const int m = j * 32 + r;
+            roff[j] = m < rows ? (uint32_t)((m * p->sym + kc) * 2) : OOB;
+            asm volatile("" : "+v"(roff[j]));
+            rs[j] = p->xs ? sl[mw0 + m] : 1.0f;
+        }
+        static_assert(TN % 2 == 0, "n-tiles in pairs");
+#pragma unroll
+        for (int ip = 0; ip < TN; ip += 2) {
+            v4f cs[2][4];
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    cs[ii][g] = p->ws ? *reinterpret_cast<const HKQ_LDS v4f*>(sl + 256 + wn * TN * 32 + (ip + ii) * 32 +
+                                                                             8 * g + 4 * khalf)
+                                      : v4f{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii) {
+                    const int i = ip + ii;
+                    float v[16];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[i][j][e]));
+                    uint32_t w[4][2];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const float a = rs[j];
+                        w[g][0] = pk_bf16(v[4 * g + 0] * a * cs[ii][g][0], v[4 * g + 1] * a * cs[ii][g][1]);
+                        w[g][1] = pk_bf16(v[4 * g + 2] * a * cs[ii][g][2], v[4 * g + 3] * a * cs[ii][g][3]);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const auto s0v = __builtin_amdgcn_permlane32_swap(w[2 * q][0], w[2 * q + 1][0], false, false);
+                        const auto s1v = __builtin_amdgcn_permlane32_swap(w[2 * q][1], w[2 * q + 1][1], false, false);
+                        const int c = i * 32 + 16 * q;
+                        const int left = cols - c;
+                        const uint32_t off = kc + 8 <= left ? roff[j] + (uint32_t)(c * 2) : OOB;
+                        __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)s0v[0], (int)s1v[0], (int)s0v[1], (int)s1v[1]},
+                                                               rc, off, 0, 0);
+                        if (ragged) {
+                            const uint32_t off4 = kc + 4 == left ? roff[j] + (uint32_t)(c * 2) : OOB;
+                            __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)s0v[0], (int)s1v[0]}, rc, off4, 0, 0);
+                        }
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+};
+
+__global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(const MoeParams p) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
+    HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int b = blockIdx.x, G = gridDim.x;
+    const int pairs = (p.grid_m + 1) / 2;
+    HKQ_LDS int* wl = reinterpret_cast<HKQ_LDS int*>(smem + MS_WL);
+    HKQ_LDS int* rl = reinterpret_cast<HKQ_LDS int*>(smem + MS_RL);
+    HKQ_LDS int* cnt = reinterpret_cast<HKQ_LDS int*>(smem + MS_CNT);
+    // Work units in two global lists, each in pair_walk order over its own
+    // pairs: the whole pairs' tiles (the stream) and the other pairs' tiles.
+    // Workgroup b takes stream units b, b + G, ... and other units G-1-b,
+    // 2G-1-b, ...: a workgroup with one more stream tile than others gets the
+    // fewer of the (cheaper) other units. Wave 0 classifies the pairs 64 at a
+    // time, then lane k builds entry k of each of the workgroup's lists.
+    HKQ_LDS int* wp = reinterpret_cast<HKQ_LDS int*>(smem + MS_WP);
+    HKQ_LDS int* rp = reinterpret_cast<HKQ_LDS int*>(smem + MS_RP);
+    if (wave == 0) {
+        const uint64_t below = (1ull << lane) - 1ull;
+        int nwp = 0, nrp = 0;
+        for (int q0 = 0; q0 < pairs; q0 += 64) {
+            const int q = q0 + lane;
+            bool whole = false, rest = false;
+            int e0 = 0, row0 = 0, start = 0, rows = 0, ed0 = -1, ed1 = -1;
+            if (q < pairs) {
+                const int pm0 = 2 * q, pm1 = 2 * q + 1;
+                ed0 = p.expt_data[pm0];
+                ed1 = pm1 < p.grid_m ? p.expt_data[pm1] : -1;
+                const int x0 = ed0 & 0xFFFF, x1 = ed1 & 0xFFFF;
+                const bool v0 = ed0 >= 0 && x0 < p.E, v1 = ed1 >= 0 && x1 < p.E;
+                if (!v0) ed0 = -1;
+                if (!v1) ed1 = -1;
+                const int b0 = ed0 >> 16, b1 = ed1 >> 16;
+                if (v0 && v1 && x0 == x1 && b1 == b0 + 1) {
+                    e0 = x0;
+                    row0 = b0 * MOE_BM;
+                    start = p.offs[x0];
+                    rows = min(p.hist[x0] - row0, 2 * MOE_BM);
+                    whole = rows > 0 && start >= 0;  // else the pair has nothing to compute
+                } else {
+                    rest = v0 || v1;
+                }
+            }
+            const uint64_t bw = __ballot(whole), br = __ballot(rest);
+            if (whole) {
+                HKQ_LDS int* d = wp + 4 * (nwp + __popcll(bw & below));
+                d[0] = e0;
+                d[1] = row0;
+                d[2] = start;
+                d[3] = rows;
+            }
+            if (rest) {
+                HKQ_LDS int* d = rp + 2 * (nrp + __popcll(br & below));
+                d[0] = ed0;
+                d[1] = ed1;
+            }
+            nwp += __popcll(bw);
+            nrp += __popcll(br);
+        }
+        const int k = lane;
+        const int w = b + k * G, r = (G - 1 - b) + k * G;
+        const bool wl_live = w < nwp * p.tiles_n, rl_live = r < nrp * p.tiles_n;
+        if (wl_live) {
+            int qi, tn;
+            pair_walk(w, nwp, p.tiles_n, p.group_m, p.xcd_cols, qi, tn);
+            const HKQ_LDS int* src = wp + 4 * qi;
+            HKQ_LDS int* d = wl + 8 * k;
+            d[0] = src[0];
+            d[1] = src[1];
+            d[2] = tn * MOE_BN;
+            d[3] = src[2];
+            d[4] = src[3];
+        }
+        if (rl_live) {
+            int qi, tn;
+            pair_walk(r, nrp, p.tiles_n, p.group_m, p.xcd_cols, qi, tn);
+            HKQ_LDS int* d = rl + 4 * k;
+            d[0] = rp[2 * qi];
+            d[1] = rp[2 * qi + 1];
+            d[2] = tn * MOE_BN;
+        }
+        const uint64_t cw = __ballot(wl_live), cr = __ballot(rl_live);
+        if (lane == 0) {
+            cnt[0] = __popcll(cw);
+            cnt[1] = __popcll(cr);
+        }
+    }
+    __syncthreads();
+    const int n_whole = __builtin_amdgcn_readfirstlane(cnt[0]), n_rest = __builtin_amdgcn_readfirstlane(cnt[1]);
+
+    if (n_whole > 0) {
+        MoeStreamSeq seq{&p, n_whole, p.K / 128, 0u, 0u, wl, reinterpret_cast<HKQ_LDS int*>(smem + MS_TOK), lane, wave};
+        seq.load_tokens(0);
+        tile_barrier<0>();  // tile 0's gather entries visible to every wave
+        TableOff<MoeWhole::LA> a_off;
+        seq.a_rows(0, a_off);
+        const auto b_off = dense_offs<MoeWhole::NW, 128, MoeWhole::LB>(wave, lane, p.swn);
+        MoeStreamEpi epi{&seq, &p, smem + MS_SCL, lane, wave};
+        v16f acc[MOE_TN][4];
+        gemm_stream<MODE_A8W8, MOE_WM, MOE_WN, 4, MOE_TN>(seq, a_off, b_off, smem, lane, wave, acc, epi);
+    }
+    for (int i = 0; i < n_rest; ++i) {
+        const int ed0 = __builtin_amdgcn_readfirstlane(rl[4 * i]), ed1 = __builtin_amdgcn_readfirstlane(rl[4 * i + 1]);
+        const int n0 = __builtin_amdgcn_readfirstlane(rl[4 * i + 2]);
+        auto block = [&](int ed) {
+            const int e = ed & 0xFFFF, bk = ed >> 16;
+            __syncthreads();  // every wave is done with the LDS of what ran before
+            if (p.hist[e] - bk * MOE_BM <= MOE_BM / 2)
+                moe_block<1, 128, 2, true>(p, e, bk * MOE_BM, n0, smem);
+            else
+                moe_block<2, 128, 2, true>(p, e, bk * MOE_BM, n0, smem);
+        };
+        if (ed0 >= 0) block(ed0);
+        if (ed1 >= 0) block(ed1);
+    }
+}
+
 template <int KTB, int NS>
 static int launch_moe(MoeParams& p, hipStream_t stream) {
     using Whole = DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 4, MOE_TN, KTB>;
@@ -434,6 +738,33 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
     p.xcd_cols = moe_xcd_cols(p.tiles_n);
     const int64_t nblk = (int64_t)((p.grid_m + 1) / 2) * p.tiles_n;
     if (nblk == 0) return 0;
+    if constexpr (KTB == 128) {
+        // the persistent stream (HKQ_MOE_STREAM=0 keeps the tiled kernel): at
+        // least four units per CU (measured on MI355X, Mixtral A8W8: gate/up,
+        // 15.75 units per CU, 0.946 -> 0.918 ms; down, 2.25 per CU, 0.501 ->
+        // 0.518 ms), at most MS_MAXU units per CU and MS_MAXP pairs, 16-byte
+        // aligned Y rows, and 32-bit offsets for the gathered row scales
+        const char* se = std::getenv("HKQ_MOE_STREAM");
+        const int64_t ncu = cu_count();
+        if (!(se && se[0] == '0') && lean && ncu > 0 && (p.K / 128) % 8 == 0 && nblk >= 4 * ncu &&
+            (nblk + ncu - 1) / ncu <= MS_MAXU && (p.grid_m + 1) / 2 <= MS_MAXP && p.sym % 8 == 0 &&
+            reinterpret_cast<uintptr_t>(p.Y) % 16 == 0 &&
+            (int64_t)p.T * p.xs_tok * 4 < (1ll << 31) && 256 * p.sym * 2 < (1ll << 31)) {
+            static bool sattr = false;
+            if (!sattr) {
+                hipError_t e = hipFuncSetAttribute((const void*)moe_stream_kernel,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, MS_LDS);
+                if (e != hipSuccess) {
+                    set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", MS_LDS,
+                              hipGetErrorString(e));
+                    return (int)e;
+                }
+                sattr = true;
+            }
+            moe_stream_kernel<<<dim3((unsigned)ncu), 64 * MOE_WM * MOE_WN, MS_LDS, stream>>>(p);
+            return hkq_launch_status();
+        }
+    }
     kern<<<dim3((unsigned)nblk), 64 * MOE_WM * MOE_WN, LDS, stream>>>(p);
     return hkq_launch_status();
 }

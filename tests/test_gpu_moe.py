@@ -103,6 +103,43 @@ def test_moe_skewed_routing_and_padding(orc):
     check_rows(orc, Y, ref)
 
 
+# The persistent stream (at least four work units per CU, K a multiple of
+# 1024): stream tiles over whole block pairs, the straddling pairs and lone
+# blocks after them; the same products and epilogue as the tiled kernel, so the
+# outputs agree bit for bit (HKQ_MOE_STREAM=0 selects the tiled kernel). Uneven
+# routing with per-token, per-tensor and absent scales, one per expert or per
+# channel. Without scales the sums of raw code products exceed what the FP8
+# MFMA accumulates exactly, so that case is checked against the tiled kernel
+# only (the scaled cases also against the oracle).
+@pytest.mark.parametrize("xs_kind,ws_kind", [("token", "channel"), ("tensor", "expert"), ("none", "none")])
+def test_moe_stream_matches_tiled(orc, monkeypatch, xs_kind, ws_kind):
+    require_gpu()
+    T, E, topk, K, N = 2304, 5, 2, 1024, 16384
+
+    def uneven(rng, T, E, topk):
+        p = np.array([0.35, 0.25, 0.2, 0.12, 0.08])
+        out = np.zeros((T, topk), np.int64)
+        for t in range(T):
+            out[t] = rng.choice(E, size=topk, replace=False, p=p)
+        return out
+
+    _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 31, uneven)
+    assert len(ed) // 2 * (N // 256) >= 1024  # four units per CU: the stream runs
+    if xs_kind == "tensor":
+        xs = np.array([0.02], np.float32)
+    if ws_kind == "expert":
+        ws = (np.random.default_rng(32).random(E) * 0.01 + 0.001).astype(np.float32)
+    xs_a = None if xs_kind == "none" else xs
+    ws_a = None if ws_kind == "none" else ws
+    Y = run_moe(X, W, hist, offs, gather, ed, topk, xs_a, ws_a)
+    monkeypatch.setenv("HKQ_MOE_STREAM", "0")
+    Y0 = run_moe(X, W, hist, offs, gather, ed, topk, xs_a, ws_a)
+    assert np.array_equal(Y, Y0), "stream and tiled kernels disagree"
+    if xs_a is not None and ws_a is not None:
+        ref = orc.moe_ref(X, W, xs_a, ws_a, None, gather, hist, offs, ed, topk, 128, "enk")
+        check_rows(orc, Y, ref)
+
+
 def test_moe_entry_order_and_pairing(orc):
     """ExptData in another order than the producers write it: consecutive
     entries that are blocks b, b+1 of one expert run as one 256-row tile, any
