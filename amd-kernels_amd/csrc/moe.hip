@@ -239,10 +239,15 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const
         return;
     }
     // a block holding at most 64 of its expert's rows (an expert's last block)
-    // runs as a 64-row tile
+    // runs as a 64-row tile, with 128-byte K-tiles on a 3-stage ring (its
+    // little MFMA work hides less of the load latency)
+    constexpr int NS1 = KTB == 128 && NS == 2 ? 3 : NS;
+    static_assert(DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 1, MOE_TN, KTB>::lds_bytes(NS1) <=
+                      DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 4, MOE_TN, KTB>::lds_bytes(NS),
+                  "the 64-row ring fits the launch's LDS");
     auto block = [&](int e, int b) {
         if (p.hist[e] - b * MOE_BM <= MOE_BM / 2)
-            moe_block<1, KTB, NS, LEAN>(p, e, b * MOE_BM, n0, smem);
+            moe_block<1, KTB, NS1, LEAN>(p, e, b * MOE_BM, n0, smem);
         else
             moe_block<2, KTB, NS, LEAN>(p, e, b * MOE_BM, n0, smem);
     };
@@ -420,8 +425,9 @@ static int launch_moe_narrow(const MoeParams& p, int64_t routed_rows, hipStream_
 // next tile's first K-tiles load during the current tile's last ones, its
 // gather entries reach LDS while the current tile computes (the tiled kernel
 // waits for them in each tile's prologue), and the epilogue stores C from
-// registers. The other units (pairs straddling two experts, lone blocks) run
-// afterwards as in the tiled kernel.
+// registers. The lone blocks run before or after the stream with the tiled
+// kernel's block code (64-row blocks on a 3-stage ring: a 64 x 256 tile has
+// little MFMA work to hide its loads behind).
 // LEAN scale layouts only (no bias; column scales absent, per expert or per
 // channel), 128-byte K-tiles, K % 1024 == 0.
 constexpr int MS_MAXU = 64;  // units per workgroup (one per lane of wave 0; the host checks)
@@ -432,12 +438,13 @@ constexpr int MS_TOK = MS_SCL + 2 * MS_SLOT;  // 2 slots of 256 gather entries
 constexpr int MS_WL = MS_TOK + 2 * 1024;      // stream units: e, row0, n0, start, rows (8 ints each)
 constexpr int MS_RL = MS_WL + MS_MAXU * 32;   // other units: ed0, ed1, n0 (4 ints each)
 constexpr int MS_CNT = MS_RL + MS_MAXU * 16;  // unit counts
-constexpr int MS_MAXP = 512;                  // routing-entry pairs (the host checks)
+constexpr int MS_MAXE = 1024;                 // routing entries (the host checks)
 constexpr int MS_WP = MS_CNT + 64;            // whole pairs: e, row0, start, rows (4 ints each)
-constexpr int MS_RP = MS_WP + MS_MAXP * 16;   // other pairs: ed0, ed1 (2 ints each)
-constexpr int MS_LDS = MS_RP + MS_MAXP * 8;
+constexpr int MS_RP = MS_WP + MS_MAXE / 2 * 16;  // lone blocks: the entry (1 int each)
+constexpr int MS_LDS = MS_RP + MS_MAXE * 4;
 static_assert(MS_LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
-static_assert(DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 2, MOE_TN, 128>::lds_bytes(2) <= MS_WL,
+static_assert(DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 2, MOE_TN, 128>::lds_bytes(2) <= MS_WL &&
+                  DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 1, MOE_TN, 128>::lds_bytes(3) <= MS_WL,
               "the tiled blocks after the stream leave the unit lists alone");
 
 struct MoeStreamSeq {
@@ -604,45 +611,46 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int b = blockIdx.x, G = gridDim.x;
-    const int pairs = (p.grid_m + 1) / 2;
     HKQ_LDS int* wl = reinterpret_cast<HKQ_LDS int*>(smem + MS_WL);
     HKQ_LDS int* rl = reinterpret_cast<HKQ_LDS int*>(smem + MS_RL);
     HKQ_LDS int* cnt = reinterpret_cast<HKQ_LDS int*>(smem + MS_CNT);
     // Work units in two global lists, each in pair_walk order over its own
-    // pairs: the whole pairs' tiles (the stream) and the other pairs' tiles.
-    // Workgroup b takes stream units b, b + G, ... and other units G-1-b,
-    // 2G-1-b, ...: a workgroup with one more stream tile than others gets the
-    // fewer of the (cheaper) other units. Wave 0 classifies the pairs 64 at a
-    // time, then lane k builds entry k of each of the workgroup's lists.
+    // entries: the whole pairs' tiles (the stream) and the lone blocks' tiles.
+    // A whole pair is an entry (e, b) with b even followed by the entry
+    // (e, b + 1), so that with the producers' layout every expert's blocks pair
+    // up among themselves and only an odd count's last block (the expert's
+    // fewest rows) is lone; any other valid entry is a lone block. Workgroup b
+    // takes stream units b, b + G, ... and lone units G-1-b, 2G-1-b, ...: a
+    // workgroup with one more stream tile than others gets the fewer of the
+    // (cheaper) lone units. Wave 0 classifies the entries 64 at a time, then
+    // lane k builds entry k of each of the workgroup's lists.
     HKQ_LDS int* wp = reinterpret_cast<HKQ_LDS int*>(smem + MS_WP);
     HKQ_LDS int* rp = reinterpret_cast<HKQ_LDS int*>(smem + MS_RP);
     if (wave == 0) {
         const uint64_t below = (1ull << lane) - 1ull;
+        auto entry = [&](int m) {  // -1 past the list or for an invalid entry
+            const int ed = m >= 0 && m < p.grid_m ? p.expt_data[m] : -1;
+            return ed >= 0 && (ed & 0xFFFF) < p.E ? ed : -1;
+        };
+        auto leads = [](int ed, int next) {  // (e, b even) followed by (e, b + 1)
+            return ed >= 0 && ((ed >> 16) & 1) == 0 && next == ed + (1 << 16);
+        };
         int nwp = 0, nrp = 0;
-        for (int q0 = 0; q0 < pairs; q0 += 64) {
-            const int q = q0 + lane;
-            bool whole = false, rest = false;
-            int e0 = 0, row0 = 0, start = 0, rows = 0, ed0 = -1, ed1 = -1;
-            if (q < pairs) {
-                const int pm0 = 2 * q, pm1 = 2 * q + 1;
-                ed0 = p.expt_data[pm0];
-                ed1 = pm1 < p.grid_m ? p.expt_data[pm1] : -1;
-                const int x0 = ed0 & 0xFFFF, x1 = ed1 & 0xFFFF;
-                const bool v0 = ed0 >= 0 && x0 < p.E, v1 = ed1 >= 0 && x1 < p.E;
-                if (!v0) ed0 = -1;
-                if (!v1) ed1 = -1;
-                const int b0 = ed0 >> 16, b1 = ed1 >> 16;
-                if (v0 && v1 && x0 == x1 && b1 == b0 + 1) {
-                    e0 = x0;
-                    row0 = b0 * MOE_BM;
-                    start = p.offs[x0];
-                    rows = min(p.hist[x0] - row0, 2 * MOE_BM);
-                    whole = rows > 0 && start >= 0;  // else the pair has nothing to compute
-                } else {
-                    rest = v0 || v1;
-                }
+        for (int m0 = 0; m0 < p.grid_m; m0 += 64) {
+            const int m = m0 + lane;
+            const int ed = entry(m), next = entry(m + 1), prev = entry(m - 1);
+            const bool lead = leads(ed, next);
+            const bool lone = ed >= 0 && !lead && !leads(prev, ed);
+            bool whole = false;
+            int e0 = 0, row0 = 0, start = 0, rows = 0;
+            if (lead) {
+                e0 = ed & 0xFFFF;
+                row0 = (ed >> 16) * MOE_BM;
+                start = p.offs[e0];
+                rows = min(p.hist[e0] - row0, 2 * MOE_BM);
+                whole = rows > 0 && start >= 0;  // else the pair has nothing to compute
             }
-            const uint64_t bw = __ballot(whole), br = __ballot(rest);
+            const uint64_t bw = __ballot(whole), br = __ballot(lone);
             if (whole) {
                 HKQ_LDS int* d = wp + 4 * (nwp + __popcll(bw & below));
                 d[0] = e0;
@@ -650,11 +658,7 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
                 d[2] = start;
                 d[3] = rows;
             }
-            if (rest) {
-                HKQ_LDS int* d = rp + 2 * (nrp + __popcll(br & below));
-                d[0] = ed0;
-                d[1] = ed1;
-            }
+            if (lone) rp[nrp + __popcll(br & below)] = ed;
             nwp += __popcll(bw);
             nrp += __popcll(br);
         }
@@ -676,8 +680,8 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
             int qi, tn;
             pair_walk(r, nrp, p.tiles_n, p.group_m, p.xcd_cols, qi, tn);
             HKQ_LDS int* d = rl + 4 * k;
-            d[0] = rp[2 * qi];
-            d[1] = rp[2 * qi + 1];
+            d[0] = rp[qi];
+            d[1] = -1;
             d[2] = tn * MOE_BN;
         }
         const uint64_t cw = __ballot(wl_live), cr = __ballot(rl_live);
@@ -689,7 +693,25 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
     __syncthreads();
     const int n_whole = __builtin_amdgcn_readfirstlane(cnt[0]), n_rest = __builtin_amdgcn_readfirstlane(cnt[1]);
 
+    auto lone = [&]() {
+        for (int i = 0; i < n_rest; ++i) {
+            const int ed = __builtin_amdgcn_readfirstlane(rl[4 * i]), n0 = __builtin_amdgcn_readfirstlane(rl[4 * i + 2]);
+            const int e = ed & 0xFFFF, bk = ed >> 16;
+            __syncthreads();  // every wave is done with the LDS of what ran before
+            if (p.hist[e] - bk * MOE_BM <= MOE_BM / 2)
+                moe_block<1, 128, 3, true>(p, e, bk * MOE_BM, n0, smem);
+            else
+                moe_block<2, 128, 2, true>(p, e, bk * MOE_BM, n0, smem);
+        }
+    };
+    // Odd workgroups run their lone units before the stream, even ones after
+    // it: a lone block reads its expert's weight columns with few rows to
+    // hide them (mostly from HBM: the whole pairs of its expert ran long
+    // before or after), so half of them at each end halves the HBM demand.
+    const bool first = b & 1;
+    if (first) lone();
     if (n_whole > 0) {
+        __syncthreads();  // every wave is done with the LDS of what ran before
         MoeStreamSeq seq{&p, n_whole, p.K / 128, 0u, 0u, wl, reinterpret_cast<HKQ_LDS int*>(smem + MS_TOK), lane, wave};
         seq.load_tokens(0);
         tile_barrier<0>();  // tile 0's gather entries visible to every wave
@@ -700,20 +722,7 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
         v16f acc[MOE_TN][4];
         gemm_stream<MODE_A8W8, MOE_WM, MOE_WN, 4, MOE_TN>(seq, a_off, b_off, smem, lane, wave, acc, epi);
     }
-    for (int i = 0; i < n_rest; ++i) {
-        const int ed0 = __builtin_amdgcn_readfirstlane(rl[4 * i]), ed1 = __builtin_amdgcn_readfirstlane(rl[4 * i + 1]);
-        const int n0 = __builtin_amdgcn_readfirstlane(rl[4 * i + 2]);
-        auto block = [&](int ed) {
-            const int e = ed & 0xFFFF, bk = ed >> 16;
-            __syncthreads();  // every wave is done with the LDS of what ran before
-            if (p.hist[e] - bk * MOE_BM <= MOE_BM / 2)
-                moe_block<1, 128, 2, true>(p, e, bk * MOE_BM, n0, smem);
-            else
-                moe_block<2, 128, 2, true>(p, e, bk * MOE_BM, n0, smem);
-        };
-        if (ed0 >= 0) block(ed0);
-        if (ed1 >= 0) block(ed1);
-    }
+    if (!first) lone();
 }
 
 template <int KTB, int NS>
@@ -741,13 +750,13 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
     if constexpr (KTB == 128) {
         // the persistent stream (HKQ_MOE_STREAM=0 keeps the tiled kernel): at
         // least four units per CU (measured on MI355X, Mixtral A8W8: gate/up,
-        // 15.75 units per CU, 0.946 -> 0.918 ms; down, 2.25 per CU, 0.501 ->
-        // 0.518 ms), at most MS_MAXU units per CU and MS_MAXP pairs, 16-byte
+        // 15.75 units per CU, 0.946 -> 0.891 ms; down, 2.25 per CU, 0.501 ->
+        // 0.518 ms), at most MS_MAXU units per CU and MS_MAXE entries, 16-byte
         // aligned Y rows, and 32-bit offsets for the gathered row scales
         const char* se = std::getenv("HKQ_MOE_STREAM");
         const int64_t ncu = cu_count();
         if (!(se && se[0] == '0') && lean && ncu > 0 && (p.K / 128) % 8 == 0 && nblk >= 4 * ncu &&
-            (nblk + ncu - 1) / ncu <= MS_MAXU && (p.grid_m + 1) / 2 <= MS_MAXP && p.sym % 8 == 0 &&
+            ((int64_t)p.grid_m * p.tiles_n + ncu - 1) / ncu <= MS_MAXU && p.grid_m <= MS_MAXE && p.sym % 8 == 0 &&
             reinterpret_cast<uintptr_t>(p.Y) % 16 == 0 &&
             (int64_t)p.T * p.xs_tok * 4 < (1ll << 31) && 256 * p.sym * 2 < (1ll << 31)) {
             static bool sattr = false;

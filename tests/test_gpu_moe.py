@@ -104,15 +104,20 @@ def test_moe_skewed_routing_and_padding(orc):
 
 
 # The persistent stream (at least four work units per CU, K a multiple of
-# 1024): stream tiles over whole block pairs, the straddling pairs and lone
-# blocks after them; the same products and epilogue as the tiled kernel, so the
-# outputs agree bit for bit (HKQ_MOE_STREAM=0 selects the tiled kernel). Uneven
-# routing with per-token, per-tensor and absent scales, one per expert or per
-# channel. Without scales the sums of raw code products exceed what the FP8
-# MFMA accumulates exactly, so that case is checked against the tiled kernel
-# only (the scaled cases also against the oracle).
-@pytest.mark.parametrize("xs_kind,ws_kind", [("token", "channel"), ("tensor", "expert"), ("none", "none")])
-def test_moe_stream_matches_tiled(orc, monkeypatch, xs_kind, ws_kind):
+# 1024): stream tiles over whole block pairs (entries (e, b even), (e, b + 1)),
+# the lone blocks before or after them; the same products and epilogue as the tiled
+# kernel, which pairs entries by position, so the outputs agree bit for bit
+# (HKQ_MOE_STREAM=0 selects the tiled kernel). Uneven routing (odd block
+# counts) with per-token, per-tensor and absent scales, one per expert or per
+# channel; the entries in the producers' order, rotated by one (a pair across
+# the list's wrap) and reversed (no pair: every block lone). Without scales the
+# sums of raw code products exceed what the FP8 MFMA accumulates exactly, so
+# that case is checked against the tiled kernel only (the scaled cases also
+# against the oracle).
+@pytest.mark.parametrize("xs_kind,ws_kind,order", [("token", "channel", "sorted"), ("tensor", "expert", "sorted"),
+                                                   ("none", "none", "sorted"), ("token", "channel", "rotated"),
+                                                   ("token", "expert", "reversed")])
+def test_moe_stream_matches_tiled(orc, monkeypatch, xs_kind, ws_kind, order):
     require_gpu()
     T, E, topk, K, N = 2304, 5, 2, 1024, 16384
 
@@ -125,6 +130,11 @@ def test_moe_stream_matches_tiled(orc, monkeypatch, xs_kind, ws_kind):
 
     _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 31, uneven)
     assert len(ed) // 2 * (N // 256) >= 1024  # four units per CU: the stream runs
+    assert any(np.bincount(ed[ed >= 0] & 0xFFFF) % 2 == 1)  # an expert with an odd block count
+    if order == "rotated":
+        ed = np.roll(ed, 1)
+    elif order == "reversed":
+        ed = ed[::-1].copy()
     if xs_kind == "tensor":
         xs = np.array([0.02], np.float32)
     if ws_kind == "expert":
