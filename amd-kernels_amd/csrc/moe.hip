@@ -749,13 +749,13 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
     if (nblk == 0) return 0;
     if constexpr (KTB == 128) {
         // the persistent stream (HKQ_MOE_STREAM=0 keeps the tiled kernel): at
-        // least four units per CU (measured on MI355X, Mixtral A8W8: gate/up,
-        // 15.75 units per CU, 0.946 -> 0.891 ms; down, 2.25 per CU, 0.501 ->
-        // 0.518 ms), at most MS_MAXU units per CU and MS_MAXE entries, 16-byte
+        // least two units per CU (measured on MI355X, Mixtral A8W8: gate/up,
+        // 15.75 units per CU, 0.946 -> 0.878 ms; down, 2.25 per CU, 0.491 ->
+        // 0.475 ms), at most MS_MAXU units per CU and MS_MAXE entries, 16-byte
         // aligned Y rows, and 32-bit offsets for the gathered row scales
         const char* se = std::getenv("HKQ_MOE_STREAM");
         const int64_t ncu = cu_count();
-        if (!(se && se[0] == '0') && lean && ncu > 0 && (p.K / 128) % 8 == 0 && nblk >= 4 * ncu &&
+        if (!(se && se[0] == '0') && lean && ncu > 0 && (p.K / 128) % 8 == 0 && nblk >= 2 * ncu &&
             ((int64_t)p.grid_m * p.tiles_n + ncu - 1) / ncu <= MS_MAXU && p.grid_m <= MS_MAXE && p.sym % 8 == 0 &&
             reinterpret_cast<uintptr_t>(p.Y) % 16 == 0 &&
             (int64_t)p.T * p.xs_tok * 4 < (1ll << 31) && 256 * p.sym * 2 < (1ll << 31)) {
