@@ -436,7 +436,7 @@ constexpr int MS_SCL = 2 * MoeWhole::STAGE;   // 2 slots: 256 row scales, then 2
 constexpr int MS_SLOT = 2 * 256 * 4;
 constexpr int MS_TOK = MS_SCL + 2 * MS_SLOT;  // 2 slots of 256 gather entries
 constexpr int MS_WL = MS_TOK + 2 * 1024;      // stream units: e, row0, n0, start, rows (8 ints each)
-constexpr int MS_RL = MS_WL + MS_MAXU * 32;   // other units: ed0, ed1, n0 (4 ints each)
+constexpr int MS_RL = MS_WL + MS_MAXU * 32;   // lone units: entry, n0 (4 ints each)
 constexpr int MS_CNT = MS_RL + MS_MAXU * 16;  // unit counts
 constexpr int MS_MAXE = 1024;                 // routing entries (the host checks)
 constexpr int MS_WP = MS_CNT + 64;            // whole pairs: e, row0, start, rows (4 ints each)
@@ -681,8 +681,7 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
             pair_walk(r, nrp, p.tiles_n, p.group_m, p.xcd_cols, qi, tn);
             HKQ_LDS int* d = rl + 4 * k;
             d[0] = rp[qi];
-            d[1] = -1;
-            d[2] = tn * MOE_BN;
+            d[1] = tn * MOE_BN;
         }
         const uint64_t cw = __ballot(wl_live), cr = __ballot(rl_live);
         if (lane == 0) {
@@ -695,7 +694,7 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
 
     auto lone = [&]() {
         for (int i = 0; i < n_rest; ++i) {
-            const int ed = __builtin_amdgcn_readfirstlane(rl[4 * i]), n0 = __builtin_amdgcn_readfirstlane(rl[4 * i + 2]);
+            const int ed = __builtin_amdgcn_readfirstlane(rl[4 * i]), n0 = __builtin_amdgcn_readfirstlane(rl[4 * i + 1]);
             const int e = ed & 0xFFFF, bk = ed >> 16;
             __syncthreads();  // every wave is done with the LDS of what ran before
             if (p.hist[e] - bk * MOE_BM <= MOE_BM / 2)
