@@ -770,11 +770,11 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
                 }
                 sattr = true;
             }
-            // one pair per walk group where the columns are too few for the
-            // XCD-aligned walk (Mixtral down, 16 column tiles: 0.477 -> 0.464
-            // ms; gate/up, 112 column tiles, keeps 2: 1 took 0.918 ms against
-            // 0.899)
-            if (group_default && !p.xcd_cols) p.group_m = 1;
+            // walk groups of four pairs with the XCD-aligned walk (Mixtral
+            // gate/up, 112 column tiles: 0.920 -> 0.912 ms against two; one
+            // took 0.918 against 0.899), one pair where the columns are too
+            // few for it (down, 16 column tiles: 0.477 -> 0.464 ms against two)
+            if (group_default) p.group_m = p.xcd_cols ? 4 : 1;
             moe_stream_kernel<<<dim3((unsigned)ncu), 64 * MOE_WM * MOE_WN, MS_LDS, stream>>>(p);
             return hkq_launch_status();
         }
