@@ -132,12 +132,14 @@ __device__ __forceinline__ void dense_kloop(const DenseParams& p, int m0, int n0
 }
 
 // One (TM*64) x 256 block of C: rows [m0, m0 + TM*64) of tile (tm, tn) of the
-// 256 x 256 tile grid, starting `half` * 128 rows into the tile.
-template <int MODE, int TM, int KTB>
+// 256 x 256 tile grid, starting `half` * 128 rows into the tile, on an NS-stage
+// K-tile ring (the tile's row and column scales follow the ring).
+template <int MODE, int TM, int KTB, int NS = dense_ns<KTB>()>
 __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn, int half, HKQ_LDS uint8_t* smem) {
     constexpr int WAVES_M = DENSE_WAVES_M, WAVES_N = DENSE_WAVES_N, TN = DENSE_TN;
     using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN;
+    constexpr int RING = NS == dense_ns<KTB>() ? dense_ring_lds<MODE, KTB>() : Cfg::lds_bytes(NS);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -152,7 +154,7 @@ __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn
     // (rows past M / columns past N read zero); each wave loads 64 of each.
     // These loads are older than the K-tile loads, so the loop's vmcnt waits
     // cover them, and its final vmcnt(0) barrier makes them visible.
-    HKQ_LDS uint8_t* scl = smem + dense_ring_lds<MODE, KTB>();
+    HKQ_LDS uint8_t* scl = smem + RING;
     if constexpr (MODE == MODE_A8W8) {
         const float* sa = static_cast<const float*>(p.sa) + m0;
         const float* sb = static_cast<const float*>(p.sb) + n0;
@@ -161,7 +163,7 @@ __device__ __forceinline__ void dense_block(const DenseParams& p, int tm, int tn
     }
 
     v16f acc[TN][TM];
-    dense_kloop<MODE, WAVES_M, WAVES_N, TM, TN, KTB>(p, m0, n0, 0, p.kbytes / KTB, smem, acc);
+    dense_kloop<MODE, WAVES_M, WAVES_N, TM, TN, KTB, NS>(p, m0, n0, 0, p.kbytes / KTB, smem, acc);
 
     // Epilogue (scales of A8W8 applied in registers; MXFP4 has none left)
     const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
@@ -221,15 +223,34 @@ __global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_g
 // of 8, one 2-D GEMM without bias): workgroup b of G computes whole tiles
 // b, b + G, ... < n_whole as one K-tile stream (gemm_stream.h) and, when the
 // last round is split, the M half (b >> 3) & 1 of tile n_whole + 8*(b >> 4) +
-// (b & 7) as a stream of one (before or after the whole tiles). Epilogues
-// store C from registers (DirectEpi). A8W8 row/column scales of tile k are
-// prefetched into LDS slot k & 1 when the tile starts.
-constexpr int STREAM_SCL = 2 * DENSE_BM * 4;  // one scale slot: 256 row + 256 column scales
+// (b & 7) (before or after the whole tiles). Epilogues store C from registers
+// through a per-wave LDS staging area (DirectEpi). A8W8 row/column scales of
+// tile k are prefetched into LDS slot k & 1 when the tile starts.
+//
+// A half tile (128 x 256) runs on the one-tile K loop with a 3-stage ring:
+// per K-tile it moves 48 KB through the LDS for half of a whole tile's MFMAs,
+// and its K loop is bound by that traffic; the deeper ring gives the loads
+// two K-tiles of lead (measured on MI355X, with the staged epilogue below:
+// 4096 x 14336 x 4096 308.8K -> 293.7K cycles per workgroup, 179.4 -> 173.8 us).
+constexpr int STREAM_SCL = 2 * DENSE_BM * 4;       // one scale slot: 256 row + 256 column scales
+constexpr int STREAM_STG_PITCH = 144;              // staged row: 64 bf16 columns + 16 bytes
+constexpr int STREAM_STG = 32 * STREAM_STG_PITCH;  // one wave's staging area: 32 rows
+constexpr int HALF_NS = 3;                         // ring stages of a half tile
 
 template <int MODE>
-constexpr int stream_lds() {
+constexpr int stream_ring_lds() {
     using Whole = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM, DENSE_TN, 128>;
-    return 2 * Whole::STAGE + Whole::SB_BYTES + (MODE == MODE_A8W8 ? 2 * STREAM_SCL : 0);
+    return 2 * Whole::STAGE + Whole::SB_BYTES;
+}
+// The staging areas follow the ring and (A8W8) the two scale slots.
+template <int MODE>
+constexpr int stream_stg_off() { return stream_ring_lds<MODE>() + (MODE == MODE_A8W8 ? 2 * STREAM_SCL : 0); }
+template <int MODE>
+constexpr int stream_lds() {
+    using Half = DenseCfg<MODE, DENSE_WAVES_M, DENSE_WAVES_N, DENSE_TM / 2, DENSE_TN, 128>;
+    constexpr int whole = stream_stg_off<MODE>() + DENSE_WAVES_M * DENSE_WAVES_N * STREAM_STG;
+    constexpr int half = Half::lds_bytes(HALF_NS) + (MODE == MODE_A8W8 ? 2 * DENSE_BM * 4 : 0);
+    return whole > half ? whole : half;
 }
 
 // Tile k of the stream: tile id first + k * stride in tile_coords order,
@@ -274,6 +295,7 @@ struct DirectEpi {
     const DenseSeq<BM>* seq;
     const DenseParams* p;
     HKQ_LDS uint8_t* scl;  // 2 slots of STREAM_SCL bytes
+    HKQ_LDS uint8_t* stg;  // this wave's STREAM_STG bytes of staging
     int lane, wave;
     __device__ void begin(int k) {
         if constexpr (MODE == MODE_A8W8) {
@@ -286,16 +308,21 @@ struct DirectEpi {
             lds_load4(static_cast<const float*>(p->sb) + n0, (uint32_t)rows_b * 4u, slot + DENSE_BM * 4 + wave * 256, off);
         }
     }
-    // Stores: per (n-tile i, m-tile j) the lane's 16 sums are 4 groups of 4
-    // consecutive columns; v_permlane32_swap exchanges half of them between
-    // lanes l and l + 32 so that each lane holds 8 consecutive columns of its
-    // row, written as one 16-byte buffer store (two per (i, j), 32 per wave;
-    // a store covers 32 rows x 32 bytes). Lanes whose row or columns lie
-    // outside C get an offset past the buffer, so every wave issues the same
-    // stores whatever the tile's edge. N % 4 == 0 leaves one partial case: 8
-    // columns of which the last 4 lie past N (the store would run into the
-    // next row); in a wave whose columns end there, such lanes write their
-    // first 4 columns with an extra 8-byte store instead.
+    // Stores: per (n-tile pair ip, m-tile j) the wave's 32 rows x 64 columns
+    // (2 n-tiles: one 128-byte line per row) are scaled, converted and written
+    // to the wave's staging area (row pitch STREAM_STG_PITCH; each lane writes
+    // its 4 consecutive columns of a register group as 8 bytes), then read
+    // back so that lane l holds 16 bytes of row l / 8 at column 8 * (l % 8),
+    // and written with four 16-byte buffer stores, each covering 8 whole
+    // 128-byte lines of C (32 per wave and tile). Stores of 32-byte pieces
+    // straight from the accumulator layout (32 partial lines per instruction)
+    // held the epilogue up for longer: all CUs store their tiles at about the
+    // same time and those partial lines cost the memory path more requests.
+    // Lanes whose row or columns lie outside C get an offset past the buffer,
+    // so every wave issues the same stores whatever the tile's edge. N % 4 == 0
+    // leaves one partial case: 8 columns of which the last 4 lie past N (the
+    // store would run into the next row); in a wave whose columns end there,
+    // such lanes write their first 4 columns with an extra 8-byte store.
     __device__ void end(int k, v16f (&acc)[TN][TM]) {
         int m0, n0;
         seq->coords(k, m0, n0);
@@ -307,22 +334,18 @@ struct DirectEpi {
         const auto rc = make_rsrc(base, 0x7FFFFFFFu);
         const int rows = p->M - mw0, cols = p->N - nw0;  // of the wave's sub-tile inside C
         const bool ragged = cols < TN * 32 && (cols & 7) != 0;
-        // The lane's offsets are rebuilt from an opaque value each tile: left
-        // visible, the compiler hoists every (row, column) offset out of the
-        // tile loop as an invariant and spills them.
-        uint32_t roff[TM];
         float rs[TM];
-        const int kc = 8 * khalf;
 #pragma unroll
-        for (int j = 0; j < TM; ++j) {
-            const int m = j * 32 + r;
-            roff[j] = m < rows ? (uint32_t)((m * p->ldc + kc) * 2) : OOB;
-            asm volatile("" : "+v"(roff[j]));
-            rs[j] = MODE == MODE_A8W8 ? sl[wm * TM * 32 + m] : 1.0f;
-        }
-        // n-tiles in pairs: the four 16-byte stores of a row's 128-byte line
-        // (columns 64a .. 64a+63) go out back to back, so L2 merges them into
-        // whole lines before they are written back
+        for (int j = 0; j < TM; ++j) rs[j] = MODE == MODE_A8W8 ? sl[wm * TM * 32 + j * 32 + r] : 1.0f;
+        // The lane's offsets come from an opaque copy of the lane each tile:
+        // left visible, the compiler hoists them out of the tile loop as
+        // invariants and spills them.
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int sr = ln >> 3, sc = (ln & 7) * 8;  // the store lane's row in an 8-row group, first column
+        const uint32_t so = (uint32_t)((sr * p->ldc + sc) * 2);
+        const uint32_t wr_lo = (uint32_t)(r * STREAM_STG_PITCH + 8 * khalf);
+        const uint32_t rd_lo = (uint32_t)(sr * STREAM_STG_PITCH + (ln & 7) * 16);
         static_assert(TN % 2 == 0, "n-tiles in pairs");
 #pragma unroll
         for (int ip = 0; ip < TN; ip += 2) {
@@ -339,36 +362,35 @@ struct DirectEpi {
             for (int j = 0; j < TM; ++j) {
 #pragma unroll
                 for (int ii = 0; ii < 2; ++ii) {
-                    const int i = ip + ii;
                     // Explicit reads out of the accumulator registers, in store
                     // order: the compiler's own copies tend to be hoisted to the
                     // start of the epilogue, all 256 of them live at once.
                     float v[16];
 #pragma unroll
                     for (int e = 0; e < 16; ++e)
-                        asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[i][j][e]));
-                    uint32_t w[4][2];
+                        asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[ip + ii][j][e]));
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const float a = rs[j];
-                        w[g][0] = pk_bf16(v[4 * g + 0] * a * cs[ii][g][0], v[4 * g + 1] * a * cs[ii][g][1]);
-                        w[g][1] = pk_bf16(v[4 * g + 2] * a * cs[ii][g][2], v[4 * g + 3] * a * cs[ii][g][3]);
+                        const uint32_t lo = pk_bf16(v[4 * g + 0] * a * cs[ii][g][0], v[4 * g + 1] * a * cs[ii][g][1]);
+                        const uint32_t hi = pk_bf16(v[4 * g + 2] * a * cs[ii][g][2], v[4 * g + 3] * a * cs[ii][g][3]);
+                        *reinterpret_cast<HKQ_LDS v2i*>(stg + wr_lo + (ii * 32 + 8 * g) * 2) = v2i{(int)lo, (int)hi};
                     }
+                }
+                // LDS operations of a wave complete in order: the reads see the
+                // writes above, and the next group's writes follow these reads
+                v4i dv[4];
 #pragma unroll
-                    for (int q = 0; q < 2; ++q) {
-                        // lanes < 32 end with columns 16q + 0..7, lanes >= 32 with 16q + 8..15
-                        const auto s0 = __builtin_amdgcn_permlane32_swap(w[2 * q][0], w[2 * q + 1][0], false, false);
-                        const auto s1 = __builtin_amdgcn_permlane32_swap(w[2 * q][1], w[2 * q + 1][1], false, false);
-                        const int c = i * 32 + 16 * q;  // the lane's 8 columns start at c + kc
-                        const int left = cols - c;      // columns of C from c on
-                        const uint32_t off = kc + 8 <= left ? roff[j] + (uint32_t)(c * 2) : OOB;
-                        __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]}, rc,
-                                                               off, 0, 0);
-                        if (ragged) {
-                            const uint32_t off4 = kc + 4 == left ? roff[j] + (uint32_t)(c * 2) : OOB;
-                            __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)s0[0], (int)s1[0]}, rc, off4, 0, 0);
-                        }
-                    }
+                for (int pp = 0; pp < 4; ++pp)
+                    dv[pp] = *reinterpret_cast<const HKQ_LDS v4i*>(stg + rd_lo + pp * 8 * STREAM_STG_PITCH);
+#pragma unroll
+                for (int pp = 0; pp < 4; ++pp) {
+                    const int m = j * 32 + pp * 8 + sr, c = ip * 32 + sc;
+                    const uint32_t at = so + (uint32_t)(((j * 32 + pp * 8) * p->ldc + ip * 32) * 2);
+                    __builtin_amdgcn_raw_buffer_store_b128(dv[pp], rc, m < rows && c + 8 <= cols ? at : OOB, 0, 0);
+                    if (ragged)
+                        __builtin_amdgcn_raw_buffer_store_b64(v2i{dv[pp][0], dv[pp][1]}, rc,
+                                                              m < rows && c + 4 == cols ? at : OOB, 0, 0);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -385,8 +407,8 @@ __device__ __forceinline__ void dense_stream(const DenseParams& p, int tiles, in
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     DenseSeq<BM> seq{&p, tiles, p.kbytes / 128, (uint32_t)p.lsa, (uint32_t)p.lsb, first, stride, half};
-    DirectEpi<MODE, TM, BM> epi{&seq, &p, smem + stream_lds<MODE>() - (MODE == MODE_A8W8 ? 2 * STREAM_SCL : 0), lane,
-                                wave};
+    DirectEpi<MODE, TM, BM> epi{&seq, &p, smem + stream_ring_lds<MODE>(),
+                                smem + stream_stg_off<MODE>() + wave * STREAM_STG, lane, wave};
     auto a_off = dense_offs<Cfg::NW, 128, Cfg::LA>(wave, lane, p.lda);
     const auto b_off = dense_offs<Cfg::NW, 128, Cfg::LB>(wave, lane, p.ldb);
     v16f acc[TN][TM];
@@ -405,9 +427,17 @@ __global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_s
     // bursts of C stores come in two waves (measured on MI355X: 4096 x 14336
     // x 4096, 190.3 -> 186.9 us)
     const bool half_first = (b >> 4) & 1;
-    if (half_first && t < p.n_split) dense_stream<MODE, DENSE_TM / 2>(p, 1, p.n_whole + t, 0, (b >> 3) & 1, smem);
+    const bool has_half = t < p.n_split;
+    int tm = 0, tn = 0;
+    if (has_half) tile_coords(p.n_whole + t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    if (half_first && has_half) {
+        dense_block<MODE, DENSE_TM / 2, 128, HALF_NS>(p, tm, tn, (b >> 3) & 1, smem);
+        // the stream's first loads overwrite the half tile's staging: every
+        // wave's LDS reads are done first (its C stores may still drain)
+        lds_barrier();
+    }
     if (mine > 0) dense_stream<MODE, DENSE_TM>(p, mine, b, G, 0, smem);
-    if (!half_first && t < p.n_split) dense_stream<MODE, DENSE_TM / 2>(p, 1, p.n_whole + t, 0, (b >> 3) & 1, smem);
+    if (!half_first && has_half) dense_block<MODE, DENSE_TM / 2, 128, HALF_NS>(p, tm, tn, (b >> 3) & 1, smem);
 }
 
 // ---------------------------------------------------------------------------

@@ -132,6 +132,13 @@ __device__ __forceinline__ void tile_barrier() {
     __syncthreads();
 }
 
+// Workgroup barrier after this wave's LDS operations are done; vector memory
+// operations (e.g. stores still draining) are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+    __syncthreads();
+}
+
 // Wait states after the last MFMA before its accumulators are read by VALU or
 // memory instructions when the reads sit in another basic block (the compiler
 // under-counts the 16-pass FP8 form across block boundaries).
