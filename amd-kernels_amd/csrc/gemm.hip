@@ -814,13 +814,17 @@ static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
         // Measured on MI355X against the one-tile-per-workgroup kernel: 1-3%
         // faster at 1.75-3.5 rounds of tiles, 1-2% at 7 and 14 rounds
         // (4096x28672, 8192x14336 and 8192x28672, K = 4096).
-        if (stream_on && ncu > 0 && !batched && p.bias == nullptr && (p.kbytes / 128) % 8 == 0 && p.ldc % 8 == 0) {
+        // Half tile t belongs to workgroup b with t = 8 * (b >> 4) + (b & 7), so
+        // the split needs 2 * roundup8(split) workgroups: grids that cannot hold
+        // them within one per CU take the one-tile kernel.
+        const int64_t g = std::min<int64_t>(ncu, std::max<int64_t>(p.n_whole, 2 * ((split + 7) / 8 * 8)));
+        if (stream_on && ncu > 0 && !batched && p.bias == nullptr && (p.kbytes / 128) % 8 == 0 && p.c16 &&
+            2 * ((split + 7) / 8 * 8) <= g) {
             constexpr int SLDS = stream_lds<MODE>();
             static_assert(SLDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
             auto skern = dense_stream_kernel<MODE>;
             static bool sattr = false;
             if (int e = set_lds(skern, SLDS, sattr)) return e;
-            const int64_t g = std::min<int64_t>(ncu, std::max<int64_t>(p.n_whole, 2 * ((split + 7) / 8 * 8)));
             skern<<<dim3((unsigned)g), 64 * DENSE_WAVES_M * DENSE_WAVES_N, SLDS, stream>>>(p);
             return hkq_launch_status();
         }

@@ -528,7 +528,7 @@ struct MoeStreamEpi {
         HKQ_LDS uint8_t* slot = scl + (k & 1) * MS_SLOT;
         const int t = seq->token(k, u, wave * 64 + lane);
         const uint32_t xs_bytes =
-            p->xs ? (uint32_t)min(((int64_t)(p->T - 1) * p->xs_tok + 1) * 4, (int64_t)0x7FFFFFFF) : 0u;
+            p->xs && p->T > 0 ? (uint32_t)min(((int64_t)(p->T - 1) * p->xs_tok + 1) * 4, (int64_t)0x7FFFFFFF) : 0u;
         lds_load4(p->xs, xs_bytes, slot + wave * 256, t < 0 ? OOB : (uint32_t)t * (uint32_t)p->xs_tok * 4u);
         const int n = u.n0 + wave * 64 + lane;
         const float* w = p->ws ? p->ws + (int64_t)u.e * p->ws_e : nullptr;
@@ -1124,6 +1124,7 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     HKQ_CHECK_ARG(stride_we >= 0 && stride_we % 16 == 0, "stride_we must be a non-negative multiple of 16");
     HKQ_CHECK_ARG(stride_ym >= N && stride_ym % 4 == 0, "stride_ym must be >= N and a multiple of 4");
     HKQ_CHECK_ARG(ws_group_n >= 1, "ws_group_n must be >= 1");
+    HKQ_CHECK_ARG(xs_stride_tok >= 0, "xs_stride_tok must be >= 0");
     HKQ_CHECK_ARG(y_rows >= 0 && gather_len >= 0, "y_rows and gather_len must be >= 0");
     HKQ_CHECK_ARG(hist && offs && expt_data, "routing metadata pointers must not be null");
     HKQ_CHECK_ALIGN(X, 16);

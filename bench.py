@@ -451,14 +451,15 @@ def main():
     sweep = []
     if args.only in (None, "sweep"):
         log("a8w8 sweep")
-        for (nn, kk) in SWEEP_NK:
-            wb = torch.randint(0, 0x70, (nn, kk), dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
-            wsb = torch.rand(nn, device="cuda") * 1e-3
+        # BASELINE's data: bf16 activations ~N(0,1) and weights ~N(0,0.02),
+        # quantized per token / per channel to E4M3FN by this library
+        for si, (nn, kk) in enumerate(SWEEP_NK):
+            wb, wsb = hkq.per_token_quant(seeded_bf16_dev((nn, kk), 0.02, 100 + si))
+            xall, xsall = hkq.per_token_quant(seeded_bf16_dev((max(SWEEP_M), kk), 1.0, 110 + si))
             for mm in SWEEP_M:
                 if (mm, nn, kk) == (M, N, K):
                     continue
-                xa = torch.randint(0, 0x70, (mm, kk), dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
-                xsa = torch.rand(mm, device="cuda")
+                xa, xsa = xall[:mm], xsall[:mm]
                 Cs = torch.empty((mm, nn), dtype=torch.bfloat16, device="cuda")
                 nws = hkq.lib().hkq_gemm_a8w8_workspace(mm, nn, kk)
                 wsp = torch.empty(max(nws, 16), dtype=torch.uint8, device="cuda")

@@ -150,6 +150,32 @@ def test_moe_stream_matches_tiled(orc, monkeypatch, xs_kind, ws_kind, order):
         check_rows(orc, Y, ref)
 
 
+# The stream kernel's ragged store branch: N % 8 == 4 (a row's last 8-column
+# piece holds 4 columns inside C) and Y rows padded past N, the padding checked
+# untouched. Still four units per CU, so the stream runs.
+def test_moe_stream_ragged_n_padded_y(orc, monkeypatch):
+    require_gpu()
+    T, E, topk, K, N, pad = 2304, 5, 2, 1024, 16388, 12
+    _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 41)
+    assert len(ed) // 2 * ((N + 255) // 256) >= 1024 and N % 8 == 4
+    sentinel = 0x7F7F  # a bf16 NaN pattern no kernel writes
+
+    def run():
+        Yp = torch.full((T * topk, N + pad), sentinel, dtype=torch.int16, device="cuda").view(torch.bfloat16)
+        Yp[:, :N] = 0
+        hkq.moe_a8w8(dev_u8(X), dev_u8(W), dev_i32(hist), dev_i32(offs), dev_i32(ed), topk, gather=dev_i32(gather),
+                     x_scale=dev_f32(xs), w_scale=dev_f32(ws), Y=Yp[:, :N])
+        torch.cuda.synchronize()
+        assert torch.all(Yp[:, N:].view(torch.int16) == sentinel), "padding of Y rows written"
+        return host_bf16_f32(Yp[:, :N])
+
+    Y = run()
+    monkeypatch.setenv("HKQ_MOE_STREAM", "0")
+    Y0 = run()
+    assert np.array_equal(Y, Y0), "stream and tiled kernels disagree"
+    check_rows(orc, Y, orc.moe_ref(X, W, xs, ws, None, gather, hist, offs, ed, topk, 128, "enk"))
+
+
 def test_moe_entry_order_and_pairing(orc):
     """ExptData in another order than the producers write it: consecutive
     entries that are blocks b, b+1 of one expert run as one 256-row tile, any
