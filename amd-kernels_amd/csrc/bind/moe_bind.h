@@ -12,9 +12,11 @@ struct MoeScales {
     int64_t ws_e = 0, ws_n = 0, ws_gn = 1;
 };
 
-// Tensors and strides of one MoE call after validation; W points at K-contiguous
-// rows (the reference's N-contiguous [E, K, N] weights are copied K-major into
-// `packed`, which must outlive the launch).
+// Tensors and strides of one MoE call after validation. W points at
+// K-contiguous rows (stride_wn), or (kn) at the reference's N-contiguous
+// [E, K, N] weights, read in place (stride_wk); N-contiguous weights with
+// K % 128 != 0, which the A8W8 kernels cannot read in place, are copied
+// K-major into `packed` (kept alive until the launch is queued).
 struct MoeArgs {
     const void* X = nullptr;
     const void* W = nullptr;
@@ -22,14 +24,15 @@ struct MoeArgs {
     const float* bias = nullptr;
     const int32_t *gather = nullptr, *hist = nullptr, *offs = nullptr, *ed = nullptr;
     int64_t T = 0, E = 0, glen = 0, y_rows = 0;
-    int64_t stride_xm = 0, stride_we = 0, stride_wn = 0, stride_ym = 0;
+    int64_t stride_xm = 0, stride_we = 0, stride_wn = 0, stride_wk = 0, stride_ym = 0;
+    bool kn = false;
     Workspace packed;
 };
 
 inline MoeArgs moe_prepare(py::object X, py::object W, py::object Y, py::object bias, py::object GatherIndx,
                            py::object ExptHist, py::object ExptOffs, py::object ExptData, int N, int K, int grid_m,
                            int stride_ym, int stride_yn, int stride_xm, int stride_xk, int stride_we, int stride_wk,
-                           int stride_wn) {
+                           int stride_wn, bool in_place_kn = false) {
     auto x = view(X, "X"), w = view(W, "W"), y = view(Y, "Y");
     if (x.dtype == kBF16 || x.dtype == kI8 || w.dtype == kBF16 || w.dtype == kI8)
         throw py::type_error("X and W must hold E4M3FN codes (torch.float8_e4m3fn or uint8)");
@@ -72,6 +75,14 @@ inline MoeArgs moe_prepare(py::object X, py::object W, py::object Y, py::object 
         a.W = (const void*)w.ptr;
         a.stride_we = stride_we;
         a.stride_wn = stride_wn;
+    } else if (K % 128 == 0 && in_place_kn) {
+        // the reference's [E, K, N] layout (tests/test_moe.py:723-729), read in place
+        expect(w.numel() >= (a.E - 1) * (int64_t)stride_we + (int64_t)(K - 1) * stride_wk + N,
+               "W is smaller than its strides say");
+        a.W = (const void*)w.ptr;
+        a.stride_we = stride_we;
+        a.stride_wk = stride_wk;
+        a.kn = true;
     } else {
         // the reference's [E, K, N] layout (tests/test_moe.py:723-729): rows of
         // K per output channel are what the kernels stream, so copy it K-major
@@ -90,10 +101,11 @@ inline void moe_call(py::object X, py::object W, py::object Y, const MoeScales& 
                      int K, int grid_m, int n_expts_act, int stride_ym, int stride_yn, int stride_xm, int stride_xk,
                      int stride_we, int stride_wk, int stride_wn) {
     MoeArgs a = moe_prepare(X, W, Y, bias, GatherIndx, ExptHist, ExptOffs, ExptData, N, K, grid_m, stride_ym,
-                            stride_yn, stride_xm, stride_xk, stride_we, stride_wk, stride_wn);
-    check(hkq_moe_a8w8(a.X, a.W, a.Y, sc.xs, sc.xs_tok, sc.ws, sc.ws_e, sc.ws_n, sc.ws_gn, a.bias, N, a.gather, a.hist,
-                       a.offs, a.ed, a.T, a.E, N, K, grid_m, n_expts_act, a.stride_xm, a.stride_we, a.stride_wn,
-                       a.stride_ym, a.y_rows, a.glen, current_stream()),
+                            stride_yn, stride_xm, stride_xk, stride_we, stride_wk, stride_wn, true);
+    auto fn = a.kn ? hkq_moe_a8w8_kn : hkq_moe_a8w8;
+    check(fn(a.X, a.W, a.Y, sc.xs, sc.xs_tok, sc.ws, sc.ws_e, sc.ws_n, sc.ws_gn, a.bias, N, a.gather, a.hist, a.offs,
+             a.ed, a.T, a.E, N, K, grid_m, n_expts_act, a.stride_xm, a.stride_we, a.kn ? a.stride_wk : a.stride_wn,
+             a.stride_ym, a.y_rows, a.glen, current_stream()),
           "moe");
 }
 

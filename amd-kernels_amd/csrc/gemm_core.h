@@ -104,6 +104,26 @@ __device__ __forceinline__ void lds_load4(const void* base, uint32_t bytes, HKQ_
 
 __device__ __forceinline__ v4i lds_read16(const HKQ_LDS uint8_t* p) { return *reinterpret_cast<const HKQ_LDS v4i*>(p); }
 
+// N-contiguous ("transposed") B tiles: the weights of a K-tile stored as they
+// lie in memory, 128 rows of K, each holding the tile's 256 output columns
+// (256 bytes). Logical 16-byte chunk c of row r lives at physical chunk
+// c ^ (2 * (r & 7)): the transposed reads below touch 8 consecutive rows at
+// two adjacent logical chunks per 32 lanes, which then fall on 16 distinct
+// chunk slots (all 64 banks).
+struct KTileT {
+    static constexpr int ROW = 256, ROWS = 128;
+    static constexpr int ROWS_PER_LOAD = 1024 / ROW;  // rows written by one wave-wide 16-byte LDS-direct load
+    __device__ static __forceinline__ int phys(int r, int c) { return c ^ (2 * (r & 7)); }
+};
+
+// ds_read_b64_tr_b8 (measured on gfx950): in each group of 16 lanes, lane j
+// receives byte (j & 7) of the 8-byte pieces addressed by lanes 2i + (j >> 3),
+// i = 0..7, as its bytes i. With lanes 2i and 2i + 1 addressing the two halves
+// of row i's 16 bytes, lane j receives column j of 8 consecutive rows.
+__device__ __forceinline__ v2i lds_read_tr8(const HKQ_LDS uint8_t* p) {
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<HKQ_LDS v2i*>(const_cast<HKQ_LDS uint8_t*>(p)));
+}
+
 template <bool FP4, int OPA, int OPB>
 __device__ __forceinline__ v16f mfma_sel(const v8i& a, const v8i& b, const v16f& c, int sa, int sb) {
     if (FP4) return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 4, 4, OPA, sa, OPB, sb);

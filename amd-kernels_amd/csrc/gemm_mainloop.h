@@ -79,6 +79,8 @@ struct LoopSrc {
     // scale row is at r * lsa.
     bool sa_gathered = false;
     uint32_t sa_row[4] = {0u, 0u, 0u, 0u};
+    // N-contiguous B (BT): bytes from one K-tile of B to the next (128 rows of K)
+    int64_t b_kstep = 0;
 };
 
 // Byte offset (row and logical chunk, excluding the K position) of LDS-direct
@@ -105,6 +107,45 @@ __device__ __forceinline__ TableOff<N> dense_offs(int wave, int lane, int64_t ld
     return o;
 }
 
+// Load offsets of an N-contiguous B tile (KTileT; row stride ld bytes): load i
+// of `wave` writes rows (i*NW + wave)*4 .. +3 of the K-tile; the lane carries
+// physical chunk lane % 16 of row (i*NW + wave)*4 + lane / 16, i.e. logical
+// chunk phys(r, lane % 16) (the swizzle is its own inverse).
+template <int NW, int N>
+__device__ __forceinline__ TableOff<N> dense_offs_t(int wave, int lane, int64_t ld) {
+    TableOff<N> o;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int r = (i * NW + wave) * KTileT::ROWS_PER_LOAD + lane / 16;
+        o.v[i] = (uint32_t)(r * ld) + (uint32_t)(KTileT::phys(r, lane % 16) << 4);
+    }
+    return o;
+}
+
+// LDS base addresses of the transposed B fragment reads (BT): per n-tile t
+// of the wave, the lane's row 64h + (j >> 1) (h = lane / 32, j = lane % 16)
+// and byte 8 (j & 1) of logical chunk (wave's first column)/16 + 2t + g
+// (g = (lane / 16) & 1). The K-step / part / read rows ride as immediates in
+// multiples of 8 rows, so the row's swizzle term is the lane constant
+// 2 (j >> 1).
+template <int TN>
+struct TBase {
+    uint32_t v[TN];
+};
+template <int TN>
+__device__ __forceinline__ TBase<TN> tr_bases(uint32_t b_region, int wave_col, int lane) {
+    TBase<TN> o;
+    const int j = lane & 15, g = (lane >> 4) & 1, h = lane >> 5;
+    const int row = 64 * h + (j >> 1);
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+        const int chunk = (wave_col >> 4) + 2 * t + g;
+        o.v[t] = b_region + (uint32_t)(row * KTileT::ROW + (KTileT::phys(row, chunk) << 4) + 8 * (j & 1));
+        asm volatile("" : "+v"(o.v[t]));
+    }
+    return o;
+}
+
 // Pipeline (per wave; one barrier per K-tile, NS ring stages):
 //   K-tile kt lives in stage kt % NS. Its SUB K-steps run their MFMAs with
 //   double-buffered fragments: the LDS reads of the next step are issued between
@@ -128,7 +169,8 @@ __device__ __forceinline__ TableOff<N> dense_offs(int wave, int lane, int64_t ld
 // each load instruction (TableOff; out of bounds for rows that must read zero).
 // On return acc holds the tile's fp32 sums and every wave is past a vmcnt(0)
 // barrier, so the caller may reuse the LDS.
-template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int KTB, int NS, typename AOff, typename BOff>
+template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, int KTB, int NS, bool BT = false, typename AOff,
+          typename BOff>
 __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_off, const BOff& b_off,
                                               HKQ_LDS uint8_t* smem, int lane, int wave, v16f (&acc)[TN][TM]) {
     using Cfg = DenseCfg<MODE, WAVES_M, WAVES_N, TM, TN, KTB>;
@@ -144,6 +186,8 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     static_assert(NS >= 2 && (NS - 1) * NLD + 3 <= 63, "ring depth and vmcnt budget");
     static_assert(!Cfg::SBLK || NS == 2, "the scale-block schedule assumes a 2-stage ring");
     static_assert(Cfg::SB_KT <= 4 && LSA <= 4, "gathered scale rows: at most 4 load slots per lane");
+    static_assert(!BT || (KTB == 128 && Cfg::BN == KTileT::ROW && MODE == MODE_A8W8),
+                  "N-contiguous B: FP8, 128-byte K-tiles of 256 columns");
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int KTN = src.KT;
 
@@ -210,7 +254,8 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
             lds_load16_d(desc_a, smem + Cfg::a_stage(NS, stage) + (idx * NW + wave) * 1024, a_off.v[idx] + (uint32_t)kb);
         } else if (idx < LA + LB) {
             const int i = idx - LA;
-            lds_load16_d(desc_b, smem + Cfg::b_stage(NS, stage) + (i * NW + wave) * 1024, b_off.v[i] + (uint32_t)kb);
+            const uint32_t kbb = BT ? (uint32_t)(kt * src.b_kstep) : (uint32_t)kb;
+            lds_load16_d(desc_b, smem + Cfg::b_stage(NS, stage) + (i * NW + wave) * 1024, b_off.v[i] + kbb);
         } else if (idx < LA + LB + LSA) {
             const int g = ((idx - LA - LB) * NW + wave) % GA;
             const int kb4 = kt * 4;
@@ -248,6 +293,9 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
             asm volatile("" : "+v"(b_base[ks][part]));
         }
 
+    const TBase<TN> bt = BT ? tr_bases<TN>((uint32_t)(uintptr_t)smem + (uint32_t)Cfg::b_stage(NS, 0), wn * TN * 32, lane)
+                            : TBase<TN>{};
+
     struct Frags {
         v4i a[TM][PARTS], b[TN][PARTS];
     };
@@ -257,6 +305,16 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     auto read_piece = [&](int stage, int ks, Frags& f, int idx) {
         const int t = idx / (2 * PARTS), isb = (idx / PARTS) & 1, part = idx % PARTS;
         if ((isb ? TN : TM) <= t) return;
+        if (BT && isb) {
+            // the lane's 16 bytes of K [64h + 32ks + 16part, +16) of its column:
+            // two transposed reads of 8 rows each
+            const uint32_t b = bt.v[t] + (uint32_t)(Cfg::b_stage(NS, stage) - Cfg::b_stage(NS, 0)) +
+                               (uint32_t)((32 * ks + 16 * part) * KTileT::ROW);
+            const v2i lo = lds_read_tr8(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)b));
+            const v2i hi = lds_read_tr8(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(b + 8 * KTileT::ROW)));
+            f.b[t][part] = v4i{lo[0], lo[1], hi[0], hi[1]};
+            return;
+        }
         const uint32_t base = isb ? b_base[ks][part] + (uint32_t)(Cfg::b_stage(NS, stage) - Cfg::b_stage(NS, 0))
                                   : a_base[ks][part] + (uint32_t)Cfg::a_stage(NS, stage);
         const v4i v = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base + (uint32_t)(t * 32 * KTB))));

@@ -36,7 +36,10 @@ struct StreamSrc {
 //   the tile's epilogue scales; loads it issues are waited for by the loop's
 //   next barrier), end(t, acc) after tile t's last MFMA has drained; it must
 //   not touch the LDS ring. On return every wave is past a vmcnt(0) barrier.
-template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, typename AOff, typename BOff, typename Seq, typename Epi>
+// BT: B tiles N-contiguous (KTileT layout, transposed fragment reads; the
+// sequence then provides b_kstep, the bytes from one K-tile of B to the next).
+template <int MODE, int WAVES_M, int WAVES_N, int TM, int TN, bool BT = false, typename AOff, typename BOff,
+          typename Seq, typename Epi>
 __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const BOff& b_off, HKQ_LDS uint8_t* smem,
                                             int lane, int wave, v16f (&acc)[TN][TM], Epi& epi) {
     constexpr int KTB = 128, NS = 2;
@@ -50,6 +53,7 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const B
     constexpr int HCH = KTB / 32;
     static_assert(SUB == 2 && !Cfg::SK, "128-byte K-tiles");
     static_assert((NS - 1) * NLD + 3 <= 63, "vmcnt budget");
+    static_assert(!BT || (Cfg::BN == KTileT::ROW && MODE == MODE_A8W8), "N-contiguous B: FP8 tiles of 256 columns");
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int KTN = seq.KT;
 
@@ -104,7 +108,9 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const B
                          wave_dst(Cfg::a_stage(NS, stage) + idx * NW * 1024), a_off.v[idx]);
         } else {
             const int i = idx - LA;
-            lds_load16_u(ld.b + kb, ld_live && ld.b_bytes > kb ? ld.b_bytes - kb : 0u,
+            uint32_t kbb = kb;
+            if constexpr (BT) kbb = (uint32_t)kl * seq.b_kstep;
+            lds_load16_u(ld.b + kbb, ld_live && ld.b_bytes > kbb ? ld.b_bytes - kbb : 0u,
                          wave_dst(Cfg::b_stage(NS, stage) + i * NW * 1024), b_off.v[i]);
         }
     };
@@ -129,12 +135,23 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const B
 
     // A lane's operand of one 64-byte K-step: two 16-byte parts (FP8: the two
     // halves of one MFMA operand; FP4 and BF16: one operand each).
+    const TBase<TN> bt = BT ? tr_bases<TN>((uint32_t)(uintptr_t)smem + (uint32_t)Cfg::b_stage(NS, 0), wn * TN * 32, lane)
+                            : TBase<TN>{};
     struct Frags {
         v4i a[TM][PARTS], b[TN][PARTS];
     };
     auto read_piece = [&](int stage, int ks, Frags& f, int idx) {
         const int t = idx / (2 * PARTS), isb = (idx / PARTS) & 1, part = idx % PARTS;
         if ((isb ? TN : TM) <= t) return;
+        if (BT && isb) {
+            // see gemm_mainloop: two transposed reads of 8 rows of K each
+            const uint32_t b = bt.v[t] + (uint32_t)(Cfg::b_stage(NS, stage) - Cfg::b_stage(NS, 0)) +
+                               (uint32_t)((32 * ks + 16 * part) * KTileT::ROW);
+            const v2i lo = lds_read_tr8(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)b));
+            const v2i hi = lds_read_tr8(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(b + 8 * KTileT::ROW)));
+            f.b[t][part] = v4i{lo[0], lo[1], hi[0], hi[1]};
+            return;
+        }
         const uint32_t base = isb ? b_base[ks][part] + (uint32_t)(Cfg::b_stage(NS, stage) - Cfg::b_stage(NS, 0))
                                   : a_base[ks][part] + (uint32_t)Cfg::a_stage(NS, stage);
         const v4i v = lds_read16(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)(base + (uint32_t)(t * 32 * KTB))));

@@ -29,7 +29,8 @@ namespace hkq {
 
 struct MoeParams {
     const uint8_t* X;        // [T, sxm] E4M3FN, K contiguous
-    const uint8_t* W;        // expert e at W + e*swe, row n at + n*swn, K contiguous
+    const uint8_t* W;        // expert e at W + e*swe; wt == 0: row n at + n*swn, K contiguous;
+                             // wt == 1 (N-contiguous [K, N]): row k at + k*swk, N contiguous
     uint16_t* Y;             // sorted row s at Y + s*sym
     const float* xs;         // nullptr: 1
     const float* ws;         // nullptr: 1
@@ -40,7 +41,8 @@ struct MoeParams {
     const int32_t* expt_data;
     int T, E, N, K, topk, grid_m, y_rows, g_len;
     double rtopk;  // 1.0 / topk (div_recip)
-    int64_t sxm, swe, swn, sym;
+    int64_t sxm, swe, swn, swk, sym;
+    int wt;
     int64_t xs_tok, ws_e, ws_n, ws_gn, bias_e;
     int tiles_n, group_m, c16;
     int xcd_cols;  // pair_walk's column order
@@ -60,7 +62,7 @@ constexpr int MOE_WM = 2, MOE_WN = 2, MOE_TN = 4, MOE_BN = MOE_WN * MOE_TN * 32;
 // columns [n0, n0 + 256). LEAN: no bias, and the column scales absent, one
 // per expert or one per channel readable as float4 (ws_vec); the epilogue
 // then carries no code for the other layouts.
-template <int TM, int KTB, int NS, bool LEAN>
+template <int TM, int KTB, int NS, bool LEAN, bool BT = false>
 __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, int n0, HKQ_LDS uint8_t* smem) {
     constexpr int TN = MOE_TN;
     using Cfg = DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, TM, TN, KTB>;
@@ -86,8 +88,17 @@ __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, i
     LoopSrc src;
     src.a = p.X;
     src.a_bytes = min((int64_t)p.T * p.sxm, (int64_t)0x7FFFFFFF);
-    src.b = p.W + (int64_t)e * p.swe + (int64_t)n0 * p.swn;
-    src.b_bytes = min((int64_t)rows_b * p.swn, (int64_t)0x7FFFFFFF);
+    if constexpr (BT) {
+        // N-contiguous weights: the tile's columns of every row of K (columns
+        // past N read the next row's bytes, which only reach output columns
+        // that are never stored; the last row's read zero)
+        src.b = p.W + (int64_t)e * p.swe + n0;
+        src.b_bytes = min((int64_t)(p.K - 1) * p.swk + rows_b, (int64_t)0x7FFFFFFF);
+        src.b_kstep = (int64_t)KTB * p.swk;
+    } else {
+        src.b = p.W + (int64_t)e * p.swe + (int64_t)n0 * p.swn;
+        src.b_bytes = min((int64_t)rows_b * p.swn, (int64_t)0x7FFFFFFF);
+    }
     src.as = src.bs = nullptr;
     src.as_bytes = src.bs_bytes = src.lsa = src.lsb = 0;
     src.KT = p.K / KTB;
@@ -98,7 +109,9 @@ __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, i
         const int t = token_of(r);
         a_off.v[i] = t < 0 ? OOB : (uint32_t)(t * p.sxm) + (uint32_t)(Cfg::KT::load_chunk(lane, r) << 4);
     }
-    const auto b_off = dense_offs<NW, KTB, LB>(wave, lane, p.swn);
+    TableOff<LB> b_off;
+    if constexpr (BT) b_off = dense_offs_t<NW, LB>(wave, lane, p.swk);
+    else b_off = dense_offs<NW, KTB, LB>(wave, lane, p.swn);
 
     // the epilogue's row scales, fetched before the K loop so that their
     // dependent loads (gather index, then scale) are not on the tile's tail
@@ -110,7 +123,7 @@ __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, i
     }
 
     v16f acc[TN][TM];
-    gemm_mainloop<MODE_A8W8, MOE_WM, MOE_WN, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
+    gemm_mainloop<MODE_A8W8, MOE_WM, MOE_WN, TM, TN, KTB, NS, BT>(src, a_off, b_off, smem, lane, wave, acc);
 
     const int s0 = start + row0;
     const int nw = n0 + wn * TN * 32;
@@ -220,7 +233,7 @@ static int64_t moe_tail_split(int64_t tiles) {
 // blocks of one expert form one 256-row tile; otherwise each valid entry is a
 // 128-row tile (64 rows when it holds at most 64 of its expert's rows), one
 // after the other.
-template <int KTB, int NS, bool LEAN>
+template <int KTB, int NS, bool LEAN, bool BT = false>
 __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const MoeParams p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
@@ -235,7 +248,7 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const
     const bool v0 = ed0 >= 0 && e0 < p.E, v1 = ed1 >= 0 && e1 < p.E;
     const int b0 = ed0 >> 16, b1 = ed1 >> 16;
     if (v0 && v1 && e0 == e1 && b1 == b0 + 1) {
-        moe_block<4, KTB, NS, LEAN>(p, e0, b0 * MOE_BM, n0, smem);
+        moe_block<4, KTB, NS, LEAN, BT>(p, e0, b0 * MOE_BM, n0, smem);
         return;
     }
     // a block holding at most 64 of its expert's rows (an expert's last block)
@@ -247,9 +260,9 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_gemm_kernel(const
                   "the 64-row ring fits the launch's LDS");
     auto block = [&](int e, int b) {
         if (p.hist[e] - b * MOE_BM <= MOE_BM / 2)
-            moe_block<1, KTB, NS1, LEAN>(p, e, b * MOE_BM, n0, smem);
+            moe_block<1, KTB, NS1, LEAN, BT>(p, e, b * MOE_BM, n0, smem);
         else
-            moe_block<2, KTB, NS, LEAN>(p, e, b * MOE_BM, n0, smem);
+            moe_block<2, KTB, NS, LEAN, BT>(p, e, b * MOE_BM, n0, smem);
     };
     if (v0) block(e0, b0);
     if (v1) {
@@ -452,6 +465,7 @@ struct MoeStreamSeq {
     const MoeParams* p;
     int tiles, KT;
     uint32_t lsa, lsb;
+    uint32_t b_kstep;  // N-contiguous weights: bytes from one K-tile to the next
     const HKQ_LDS int* wl;
     HKQ_LDS int* tok;
     int lane, wave;
@@ -469,8 +483,13 @@ struct MoeStreamSeq {
         StreamSrc s;
         s.a = p->X;
         s.a_bytes = (uint32_t)min((int64_t)p->T * p->sxm, (int64_t)0x7FFFFFFF);
-        s.b = p->W + (int64_t)u.e * p->swe + (int64_t)u.n0 * p->swn;
-        s.b_bytes = (uint32_t)min((int64_t)min(p->N - u.n0, MOE_BN) * p->swn, (int64_t)0x7FFFFFFF);
+        if (p->wt) {
+            s.b = p->W + (int64_t)u.e * p->swe + u.n0;
+            s.b_bytes = (uint32_t)min((int64_t)(p->K - 1) * p->swk + min(p->N - u.n0, MOE_BN), (int64_t)0x7FFFFFFF);
+        } else {
+            s.b = p->W + (int64_t)u.e * p->swe + (int64_t)u.n0 * p->swn;
+            s.b_bytes = (uint32_t)min((int64_t)min(p->N - u.n0, MOE_BN) * p->swn, (int64_t)0x7FFFFFFF);
+        }
         s.as = s.bs = nullptr;
         s.as_bytes = s.bs_bytes = 0;
         return s;
@@ -605,6 +624,7 @@ struct MoeStreamEpi {
     }
 };
 
+template <bool BT>
 __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(const MoeParams p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
@@ -698,9 +718,9 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
             const int e = ed & 0xFFFF, bk = ed >> 16;
             __syncthreads();  // every wave is done with the LDS of what ran before
             if (p.hist[e] - bk * MOE_BM <= MOE_BM / 2)
-                moe_block<1, 128, 3, true>(p, e, bk * MOE_BM, n0, smem);
+                moe_block<1, 128, 3, true, BT>(p, e, bk * MOE_BM, n0, smem);
             else
-                moe_block<2, 128, 2, true>(p, e, bk * MOE_BM, n0, smem);
+                moe_block<2, 128, 2, true, BT>(p, e, bk * MOE_BM, n0, smem);
         }
     };
     // Odd workgroups run their lone units before the stream, even ones after
@@ -711,15 +731,18 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
     if (first) lone();
     if (n_whole > 0) {
         __syncthreads();  // every wave is done with the LDS of what ran before
-        MoeStreamSeq seq{&p, n_whole, p.K / 128, 0u, 0u, wl, reinterpret_cast<HKQ_LDS int*>(smem + MS_TOK), lane, wave};
+        MoeStreamSeq seq{&p,   n_whole, p.K / 128, 0u, 0u, (uint32_t)(128 * p.swk), wl,
+                         reinterpret_cast<HKQ_LDS int*>(smem + MS_TOK), lane, wave};
         seq.load_tokens(0);
         tile_barrier<0>();  // tile 0's gather entries visible to every wave
         TableOff<MoeWhole::LA> a_off;
         seq.a_rows(0, a_off);
-        const auto b_off = dense_offs<MoeWhole::NW, 128, MoeWhole::LB>(wave, lane, p.swn);
+        TableOff<MoeWhole::LB> b_off;
+        if constexpr (BT) b_off = dense_offs_t<MoeWhole::NW, MoeWhole::LB>(wave, lane, p.swk);
+        else b_off = dense_offs<MoeWhole::NW, 128, MoeWhole::LB>(wave, lane, p.swn);
         MoeStreamEpi epi{&seq, &p, smem + MS_SCL, lane, wave};
         v16f acc[MOE_TN][4];
-        gemm_stream<MODE_A8W8, MOE_WM, MOE_WN, 4, MOE_TN>(seq, a_off, b_off, smem, lane, wave, acc, epi);
+        gemm_stream<MODE_A8W8, MOE_WM, MOE_WN, 4, MOE_TN, BT>(seq, a_off, b_off, smem, lane, wave, acc, epi);
     }
     if (!first) lone();
 }
@@ -731,15 +754,19 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
     constexpr int LDS = Whole::lds_bytes(NS) > Half::lds_bytes(NS) ? Whole::lds_bytes(NS) : Half::lds_bytes(NS);
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
     const bool lean = !p.bias && (!p.ws || p.ws_vec || p.ws_n == 0);
+    // N-contiguous weights (wt) need 128-byte K-tiles (the entry point checks)
     auto kern = lean ? moe_gemm_kernel<KTB, NS, true> : moe_gemm_kernel<KTB, NS, false>;
-    static bool attr_set[2] = {false, false};
-    if (!attr_set[lean]) {
+    if constexpr (KTB == 128)
+        if (p.wt) kern = lean ? moe_gemm_kernel<KTB, NS, true, true> : moe_gemm_kernel<KTB, NS, false, true>;
+    const int variant = (lean ? 1 : 0) + (p.wt ? 2 : 0);
+    static bool attr_set[4] = {false, false, false, false};
+    if (!attr_set[variant]) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
         if (e != hipSuccess) {
             set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", LDS, hipGetErrorString(e));
             return (int)e;
         }
-        attr_set[lean] = true;
+        attr_set[variant] = true;
     }
     p.tiles_n = (p.N + MOE_BN - 1) / MOE_BN;
     const bool group_default = p.group_m <= 0;
@@ -759,23 +786,24 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
             ((int64_t)p.grid_m * p.tiles_n + ncu - 1) / ncu <= MS_MAXU && p.grid_m <= MS_MAXE && p.sym % 8 == 0 &&
             reinterpret_cast<uintptr_t>(p.Y) % 16 == 0 &&
             (int64_t)p.T * p.xs_tok * 4 < (1ll << 31) && 256 * p.sym * 2 < (1ll << 31)) {
-            static bool sattr = false;
-            if (!sattr) {
-                hipError_t e = hipFuncSetAttribute((const void*)moe_stream_kernel,
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, MS_LDS);
+            auto skern = p.wt ? moe_stream_kernel<true> : moe_stream_kernel<false>;
+            static bool sattr[2] = {false, false};
+            if (!sattr[p.wt]) {
+                hipError_t e =
+                    hipFuncSetAttribute((const void*)skern, hipFuncAttributeMaxDynamicSharedMemorySize, MS_LDS);
                 if (e != hipSuccess) {
                     set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", MS_LDS,
                               hipGetErrorString(e));
                     return (int)e;
                 }
-                sattr = true;
+                sattr[p.wt] = true;
             }
             // walk groups of four pairs with the XCD-aligned walk (Mixtral
             // gate/up, 112 column tiles: 0.920 -> 0.912 ms against two; one
             // took 0.918 against 0.899), one pair where the columns are too
             // few for it (down, 16 column tiles: 0.477 -> 0.464 ms against two)
             if (group_default) p.group_m = p.xcd_cols ? 4 : 1;
-            moe_stream_kernel<<<dim3((unsigned)ncu), 64 * MOE_WM * MOE_WN, MS_LDS, stream>>>(p);
+            skern<<<dim3((unsigned)ncu), 64 * MOE_WM * MOE_WN, MS_LDS, stream>>>(p);
             return hkq_launch_status();
         }
     }
@@ -1105,13 +1133,14 @@ static int launch_moe_fp4(MoeFp4Params& p, hipStream_t stream) {
 
 using namespace hkq;
 
-extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* x_scale, int64_t xs_stride_tok,
-                            const float* w_scale, int64_t ws_stride_e, int64_t ws_stride_n, int64_t ws_group_n,
-                            const float* bias, int64_t bias_stride_e, const int32_t* gather, const int32_t* hist,
-                            const int32_t* offs, const int32_t* expt_data, int64_t T, int64_t E, int64_t N,
-                            int64_t K, int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we,
-                            int64_t stride_wn, int64_t stride_ym, int64_t y_rows, int64_t gather_len,
-                            hipStream_t stream) {
+// wt == 0: W[e] is [N, K] with row stride stride_w (K contiguous); wt == 1:
+// W[e] is [K, N] with row stride stride_w (N contiguous, the reference's layout).
+static int moe_a8w8_impl(const void* X, const void* W, void* Y, const float* x_scale, int64_t xs_stride_tok,
+                         const float* w_scale, int64_t ws_stride_e, int64_t ws_stride_n, int64_t ws_group_n,
+                         const float* bias, int64_t bias_stride_e, const int32_t* gather, const int32_t* hist,
+                         const int32_t* offs, const int32_t* expt_data, int64_t T, int64_t E, int64_t N, int64_t K,
+                         int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we, int64_t stride_w, int wt,
+                         int64_t stride_ym, int64_t y_rows, int64_t gather_len, hipStream_t stream) {
     HKQ_CHECK_ARG(T >= 0 && E > 0 && E <= 0xFFFF && N >= 0 && K > 0 && grid_m >= 0 && topk > 0 && topk <= 0xFFFF,
                   "T, grid_m >= 0; 0 < E <= 65535; K > 0; 0 < topk <= 65535");
     HKQ_CHECK_ARG(T < (1 << 30) && N < (1 << 30) && K < (1 << 30) && grid_m < (1 << 30), "dimensions must be < 2^30");
@@ -1120,7 +1149,13 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     HKQ_CHECK_ARG(stride_xm >= K && stride_xm % 16 == 0, "stride_xm must be >= K and a multiple of 16");
     // the kernels address gathered X rows with 32-bit buffer offsets
     HKQ_CHECK_ARG(T * stride_xm < (1ll << 31), "X must span less than 2^31 bytes (T * stride_xm)");
-    HKQ_CHECK_ARG(stride_wn >= K && stride_wn % 16 == 0, "stride_wn must be >= K and a multiple of 16 (W[e] is [N, K])");
+    if (wt) {
+        HKQ_CHECK_ARG(K % 128 == 0, "N-contiguous weights need K to be a multiple of 128");
+        HKQ_CHECK_ARG(stride_w >= N && stride_w % 16 == 0, "stride_wk must be >= N and a multiple of 16 (W[e] is [K, N])");
+        HKQ_CHECK_ARG(K * stride_w < (1ll << 31), "one expert's weights must span less than 2^31 bytes (K * stride_wk)");
+    } else {
+        HKQ_CHECK_ARG(stride_w >= K && stride_w % 16 == 0, "stride_wn must be >= K and a multiple of 16 (W[e] is [N, K])");
+    }
     HKQ_CHECK_ARG(stride_we >= 0 && stride_we % 16 == 0, "stride_we must be a non-negative multiple of 16");
     HKQ_CHECK_ARG(stride_ym >= N && stride_ym % 4 == 0, "stride_ym must be >= N and a multiple of 4");
     HKQ_CHECK_ARG(ws_group_n >= 1, "ws_group_n must be >= 1");
@@ -1144,7 +1179,10 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     p.T = (int)T; p.E = (int)E; p.N = (int)N; p.K = (int)K; p.topk = (int)topk; p.rtopk = 1.0 / (double)topk; p.grid_m = (int)grid_m;
     p.y_rows = (int)y_rows;
     p.g_len = gather ? (int)gather_len : (int)y_rows;
-    p.sxm = stride_xm; p.swe = stride_we; p.swn = stride_wn; p.sym = stride_ym;
+    p.sxm = stride_xm; p.swe = stride_we; p.sym = stride_ym;
+    p.wt = wt;
+    p.swn = wt ? 1 : stride_w;
+    p.swk = wt ? stride_w : 1;
     p.xs_tok = xs_stride_tok; p.ws_e = ws_stride_e; p.ws_n = ws_stride_n; p.bias_e = bias_stride_e;
     p.ws_gn = std::min<int64_t>(ws_group_n, std::max<int64_t>(N, 1));  // same quotients for n < N, 32-bit
     p.ws_vec = w_scale && ws_stride_n == 1 && ws_group_n == 1 && ws_stride_e % 4 == 0 &&
@@ -1158,11 +1196,35 @@ extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* 
     // a gather; every block then holds at most that many rows.
     const int64_t routed = gather ? T * topk : T;
     const bool decode = routed <= 32 || (routed <= MOE_NARROW_MAX_ROWS && N <= 4096);
-    if (decode && K % 128 == 0 && 64 * stride_wn < (1ll << 31))
+    if (decode && !wt && K % 128 == 0 && 64 * stride_w < (1ll << 31))
         return launch_moe_narrow(p, routed, stream);
     // 128-byte K-tiles (2-stage ring) when every row has whole ones: a partial
     // last K-tile would read the next row's bytes instead of zeros
     return K % 128 == 0 ? launch_moe<128, 2>(p, stream) : launch_moe<64, 4>(p, stream);
+}
+
+extern "C" int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* x_scale, int64_t xs_stride_tok,
+                            const float* w_scale, int64_t ws_stride_e, int64_t ws_stride_n, int64_t ws_group_n,
+                            const float* bias, int64_t bias_stride_e, const int32_t* gather, const int32_t* hist,
+                            const int32_t* offs, const int32_t* expt_data, int64_t T, int64_t E, int64_t N,
+                            int64_t K, int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we,
+                            int64_t stride_wn, int64_t stride_ym, int64_t y_rows, int64_t gather_len,
+                            hipStream_t stream) {
+    return moe_a8w8_impl(X, W, Y, x_scale, xs_stride_tok, w_scale, ws_stride_e, ws_stride_n, ws_group_n, bias,
+                         bias_stride_e, gather, hist, offs, expt_data, T, E, N, K, grid_m, topk, stride_xm, stride_we,
+                         stride_wn, 0, stride_ym, y_rows, gather_len, stream);
+}
+
+extern "C" int hkq_moe_a8w8_kn(const void* X, const void* W, void* Y, const float* x_scale, int64_t xs_stride_tok,
+                               const float* w_scale, int64_t ws_stride_e, int64_t ws_stride_n, int64_t ws_group_n,
+                               const float* bias, int64_t bias_stride_e, const int32_t* gather, const int32_t* hist,
+                               const int32_t* offs, const int32_t* expt_data, int64_t T, int64_t E, int64_t N,
+                               int64_t K, int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we,
+                               int64_t stride_wk, int64_t stride_ym, int64_t y_rows, int64_t gather_len,
+                               hipStream_t stream) {
+    return moe_a8w8_impl(X, W, Y, x_scale, xs_stride_tok, w_scale, ws_stride_e, ws_stride_n, ws_group_n, bias,
+                         bias_stride_e, gather, hist, offs, expt_data, T, E, N, K, grid_m, topk, stride_xm, stride_we,
+                         stride_wk, 1, stride_ym, y_rows, gather_len, stream);
 }
 
 extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* A_mx_scale, const void* B_mx_scale,

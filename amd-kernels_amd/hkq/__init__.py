@@ -42,6 +42,8 @@ SIGNATURES = {
     "hkq_batched_gemm_bf16": (_I, [_P] * 4 + [_I64] * 11 + [_P, ctypes.c_size_t, _P]),
     "hkq_moe_a8w8": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]
                      + [_I64] * 12 + [_P]),
+    "hkq_moe_a8w8_kn": (_I, [_P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]
+                        + [_I64] * 12 + [_P]),
     "hkq_moe_a8w8_blockscale": (_I, [_P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64,
                                      _P, _P, _P, _P] + [_I64] * 12 + [_P]),
     "hkq_moe_pack_kmajor": (_I, [_P, _P] + [_I64] * 7 + [_P]),
@@ -332,8 +334,9 @@ def gemm_bf16(A, B, C=None, bias=None, stream=None, split: bool = True):
 
 
 def moe_a8w8(X, W, hist, offs, expt_data, topk, gather=None, x_scale=None, w_scale=None, bias=None, Y=None,
-             y_rows=None, stream=None):
-    """OGS-routed A8W8 MoE GEMM. X [T, K] E4M3FN; W [E, N, K] E4M3FN (K contiguous);
+             y_rows=None, stream=None, w_kn=False):
+    """OGS-routed A8W8 MoE GEMM. X [T, K] E4M3FN; W [E, N, K] E4M3FN (K contiguous),
+    or with w_kn the reference's [E, K, N] (N contiguous, read in place);
     x_scale: None, [1] (per tensor) or [T] (per token); w_scale: None, [E] (per
     expert) or [E, N] (per channel); bias: None or fp32 [E, N]; int32 routing
     tensors as in the reference (gather [T*topk], hist [E], offs [E],
@@ -341,7 +344,7 @@ def moe_a8w8(X, W, hist, offs, expt_data, topk, gather=None, x_scale=None, w_sca
     import torch
 
     T, K = X.shape
-    E, N = W.shape[0], W.shape[1]
+    E, N = (W.shape[0], W.shape[2]) if w_kn else (W.shape[0], W.shape[1])
     rows = T * topk if y_rows is None else y_rows
     if Y is None:
         Y = torch.zeros((rows, N), dtype=torch.bfloat16, device=X.device)
@@ -351,7 +354,8 @@ def moe_a8w8(X, W, hist, offs, expt_data, topk, gather=None, x_scale=None, w_sca
     else:
         ws_e, ws_n = N, 1
     null = 0
-    call("hkq_moe_a8w8", _ptr(X), _ptr(W), _ptr(Y), _ptr(x_scale) if x_scale is not None else null, xs_tok,
+    call("hkq_moe_a8w8_kn" if w_kn else "hkq_moe_a8w8", _ptr(X), _ptr(W), _ptr(Y),
+         _ptr(x_scale) if x_scale is not None else null, xs_tok,
          _ptr(w_scale) if w_scale is not None else null, ws_e, ws_n, 1,
          _ptr(bias) if bias is not None else null, N, _ptr(gather) if gather is not None else null,
          _ptr(hist), _ptr(offs), _ptr(expt_data), T, E, N, K, expt_data.numel(), topk, X.stride(0), W.stride(0),

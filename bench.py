@@ -313,8 +313,21 @@ def main():
             ms_b = time_launches(fn, steps, warmup)
             moe_res.append({"proj": name, "N": nn, "K": kk, "group_k": 128, "group_n": 128, "ms": round(ms_b, 5),
                             "tflops": round(2.0 * T * topk * nn * kk / (ms_b * 1e-3) / 1e12, 2)})
-        # K-major prepack of the reference's N-contiguous [E, K, N] gate/up weights
+        # the reference's N-contiguous [E, K, N] weights: read in place by the
+        # kernels (hkq_moe_a8w8_kn), and the K-major prepack a caller may run once
         w1_kn = w1.view(torch.uint8).transpose(1, 2).contiguous()
+        w2_kn = w2.view(torch.uint8).transpose(1, 2).contiguous()
+        for name, nn, kk, fn in (
+                ("gate_up [E,K,N]", 2 * ffn, hidden, lambda: hkq.moe_a8w8(qx, w1_kn, hist, offs, expt_data, topk,
+                                                                          gather=gather, x_scale=sx, w_scale=ws1, Y=Y1,
+                                                                          w_kn=True)),
+                ("down [E,K,N]", hidden, ffn, lambda: hkq.moe_a8w8(q2, w2_kn, hist, offs, expt_data, 1, gather=None,
+                                                                    x_scale=s2, w_scale=ws2, Y=Y2, w_kn=True))):
+            log(f"moe {name} N={nn} K={kk}")
+            ms_m = time_launches(fn, steps, warmup)
+            moe_res.append({"proj": name, "N": nn, "K": kk, "ms": round(ms_m, 5),
+                            "tflops": round(2.0 * T * topk * nn * kk / (ms_m * 1e-3) / 1e12, 2)})
+        del w2_kn
         w1_nk = torch.empty((E, 2 * ffn, hidden), dtype=torch.uint8, device="cuda")
         pack = hkq.bind("hkq_moe_pack_kmajor", w1_kn.data_ptr(), w1_nk.data_ptr(), E, hidden, 2 * ffn,
                         w1_kn.stride(0), w1_kn.stride(1), w1_nk.stride(0), w1_nk.stride(1),

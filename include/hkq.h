@@ -227,8 +227,8 @@ int hkq_batched_gemm_bf16(const void* A, const void* B, const void* bias, void* 
  * token = gather[s] / topk (gather == NULL: token = s):
  *   Y[s, n] = bf16((sum_k X[token, k] * W[e, n, k]) * xs(token) * ws(e, n) + bias[e, n]).
  * X E4M3FN [T, stride_xm], K contiguous; W E4M3FN with expert stride stride_we and
- * row (n) stride stride_wn, K contiguous (the reference's [E, K, N] layout goes
- * through hkq_moe_pack_kmajor first); Y bf16 rows of stride_ym, y_rows of them.
+ * row (n) stride stride_wn, K contiguous (the reference's N-contiguous [E, K, N]
+ * layout: hkq_moe_a8w8_kn); Y bf16 rows of stride_ym, y_rows of them.
  * xs: NULL (1), x_scale[0] (xs_stride_tok 0) or x_scale[token * xs_stride_tok].
  * ws: NULL (1) or w_scale[e * ws_stride_e + (n / ws_group_n) * ws_stride_n]
  *   (per expert: ws_stride_n 0; per channel: ws_stride_e N, ws_stride_n 1, ws_group_n 1).
@@ -244,6 +244,22 @@ int hkq_moe_a8w8(const void* X, const void* W, void* Y, const float* x_scale, in
                  const int32_t* expt_data, int64_t T, int64_t E, int64_t N, int64_t K, int64_t grid_m, int64_t topk,
                  int64_t stride_xm, int64_t stride_we, int64_t stride_wn, int64_t stride_ym, int64_t y_rows,
                  int64_t gather_len, hkq_stream_t stream);
+
+/* hkq_moe_a8w8 on the reference's N-contiguous weights: W[e, k, n] at
+ * W + e * stride_we + k * stride_wk + n (stride_wk >= N, a multiple of 16;
+ * K % 128 == 0; K * stride_wk < 2^31). The kernels stage each K-tile of W as
+ * it lies (rows of K) and build the MFMA operand with transposed LDS reads, so
+ * no K-major copy is made; every output element is the one hkq_moe_a8w8 gives
+ * for the same weights in [E, N, K] (bit for bit). Decode-sized launches run the
+ * tiled kernel. Replaces moe_op_gemm_a8w8_tk.moe_a8w8 with stride_wn == 1, the
+ * reference's own call (kernels/moe-gemm/moe_op_gemm_a8w8/kernel.cpp:120, the
+ * weight read W[e*stride_we + k*stride_wk + n*stride_wn]; tests/test_moe.py:703-729). */
+int hkq_moe_a8w8_kn(const void* X, const void* W, void* Y, const float* x_scale, int64_t xs_stride_tok,
+                    const float* w_scale, int64_t ws_stride_e, int64_t ws_stride_n, int64_t ws_group_n,
+                    const float* bias, int64_t bias_stride_e, const int32_t* gather, const int32_t* hist,
+                    const int32_t* offs, const int32_t* expt_data, int64_t T, int64_t E, int64_t N, int64_t K,
+                    int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we, int64_t stride_wk,
+                    int64_t stride_ym, int64_t y_rows, int64_t gather_len, hkq_stream_t stream);
 
 /* The same grouped GEMM with per-K-group scales: for group g = k / group_k
  * (group_k a multiple of 64),

@@ -176,6 +176,47 @@ def test_moe_stream_ragged_n_padded_y(orc, monkeypatch):
     check_rows(orc, Y, orc.moe_ref(X, W, xs, ws, None, gather, hist, offs, ed, topk, 128, "enk"))
 
 
+# The reference's N-contiguous [E, K, N] weights read in place (hkq_moe_a8w8_kn:
+# K-tiles staged as rows of K, the MFMA operand built with transposed LDS
+# reads): the products and their order are those of the K-contiguous path, so
+# every output element is the same bits. Cases: the persistent stream (uneven
+# routing: lone blocks, 64-row tiles), the tiled kernel, decode-sized routing,
+# a bias and per-channel scales (the general epilogue), N that is not a
+# multiple of 256 or 16 (the last column chunk reads the next row's bytes into
+# columns that are never stored), and rows of K padded past N.
+@pytest.mark.parametrize("T,E,topk,K,N,pad,stream,bias", [(2304, 5, 2, 1024, 16384, 0, True, False),
+                                                          (2304, 5, 2, 1024, 16384, 0, False, False),
+                                                          (4, 8, 2, 1024, 512, 0, True, False),
+                                                          (300, 4, 2, 512, 1000, 24, True, True),
+                                                          (700, 3, 2, 2048, 4104, 8, True, False)])
+def test_moe_kn_matches_kmajor(orc, monkeypatch, T, E, topk, K, N, pad, stream, bias):
+    require_gpu()
+
+    def uneven(rng, T, E, topk):
+        p = np.linspace(2.0, 1.0, E)
+        p /= p.sum()
+        out = np.zeros((T, topk), np.int64)
+        for t in range(T):
+            out[t] = rng.choice(E, size=topk, replace=False, p=p)
+        return out
+
+    _, hist, offs, gather, ed, X, xs, W, ws = make_problem(orc, T, E, topk, K, N, 51, uneven)
+    Wkn = np.zeros((E, K, N + pad), np.uint8)
+    Wkn[:, :, :N] = W.transpose(0, 2, 1)
+    b = (np.random.default_rng(52).standard_normal((E, N)) * 0.1).astype(np.float32) if bias else None
+    if not stream:
+        monkeypatch.setenv("HKQ_MOE_STREAM", "0")
+    args = dict(gather=dev_i32(gather), x_scale=dev_f32(xs), w_scale=dev_f32(ws),
+                bias=dev_f32(b) if b is not None else None)
+    Xd, hd, od, edd = dev_u8(X), dev_i32(hist), dev_i32(offs), dev_i32(ed)
+    Y = hkq.moe_a8w8(Xd, dev_u8(W), hd, od, edd, topk, **args)
+    Wkn_d = dev_u8(Wkn)[:, :, :N]  # [E, K, N] view with row stride N + pad
+    Ykn = hkq.moe_a8w8(Xd, Wkn_d, hd, od, edd, topk, w_kn=True, **args)
+    torch.cuda.synchronize()
+    assert torch.equal(Y, Ykn), "N-contiguous weights give other bits than K-contiguous ones"
+    check_rows(orc, host_bf16_f32(Ykn), orc.moe_ref(X, W, xs, ws, b, gather, hist, offs, ed, topk, 128, "enk"))
+
+
 def test_moe_entry_order_and_pairing(orc):
     """ExptData in another order than the producers write it: consecutive
     entries that are blocks b, b+1 of one expert run as one 256-row tile, any
@@ -312,6 +353,33 @@ def test_moe_mixtral_full(orc, K, N):
     ref = orc.moe_ref_f32(X, W, xs, ws, gather, hist, offs, ed, topk)
     assert not np.isnan(ref).any()  # every (token, choice) routed
     assert_gemm_close(Y, ref, f"moe mixtral K={K} N={N}")
+
+
+@pytest.mark.parametrize("K,N", [(4096, 28672), (14336, 4096)])
+def test_moe_mixtral_reference_layout_module(orc, K, N):
+    """The reference's own call shape at Mixtral size: moe_op_gemm_a8w8_tk with
+    N-contiguous [E, K, N] weights (stride_wk = N, stride_wn = 1,
+    tests/test_moe.py:723-729), read in place by the kernels; every routed row
+    against the fp32 oracle."""
+    require_gpu()
+    import hipkittens as hk
+
+    T, E, topk = 4096, 8, 2
+    hist, offs, gather, ed = mixtral_routing(orc, T, E, topk, K)
+    X, xs = orc.quant_rowwise(orc.randn_bf16((T, K), seed=K + 11), None, "fp8")
+    xs = xs.reshape(-1)
+    W, ws = device_weights_fp8(E, N, K, seed=K + 12)
+    Wkn = dev_u8(W).transpose(1, 2).contiguous().view(torch.float8_e4m3fn)  # [E, K, N]
+    Y = torch.zeros((T * topk, N), dtype=torch.bfloat16, device="cuda")
+    grid_m, grid_n = len(ed), (N + 127) // 128
+    hk.moe.a8w8.moe_a8w8(dev_u8(X).view(torch.float8_e4m3fn), Wkn, Y, dev_f32(xs), dev_f32(ws), None,
+                         dev_i32(gather), dev_i32(hist), dev_i32(offs), dev_i32(ed), N, K, grid_m, grid_n, topk,
+                         N, 1, K, 1, K * N, N, 1, False, 0.0)
+    torch.cuda.synchronize()
+    del Wkn
+    ref = orc.moe_ref_f32(X, W, xs, ws, gather, hist, offs, ed, topk)
+    assert not np.isnan(ref).any()
+    assert_gemm_close(host_bf16_f32(Y), ref, f"moe mixtral [E, K, N] module K={K} N={N}")
 
 
 # ---------------------------------------------------------------------------
