@@ -3,7 +3,8 @@
 // names and order). X_scale: None, numel 1 (per tensor, the reference's) or T
 // (per token); W_scale: None, numel E (per expert, the reference's) or E*N (per
 // output channel). W may be K-contiguous ([E, N, K]) or the reference's
-// N-contiguous [E, K, N] (copied K-major first). apply_swiglu / swiglu_alpha
+// N-contiguous [E, K, N] (read in place when K % 128 == 0, else copied
+// K-major first). apply_swiglu / swiglu_alpha
 // are accepted and, as in the reference, do not change the output.
 #include "moe_bind.h"
 

@@ -5,7 +5,7 @@
 // any group_k that is a multiple of 64 and group_n >= 1. group_k == K
 // (per-token x per-channel-group scales) runs on the per-token MoE kernel,
 // smaller groups on the per-group promotion kernel. W may be K-contiguous
-// ([E, N, K]) or the reference's N-contiguous [E, K, N].
+// ([E, N, K]) or the reference's N-contiguous [E, K, N], read in place.
 #include "moe_bind.h"
 
 using namespace hkqbind;
@@ -45,17 +45,18 @@ void moe_a8w8_blockscale(py::object X, py::object W, py::object Y, py::object X_
     expect_dtype(xs, "X_scale", {kF32});
     expect_dtype(ws, "W_scale", {kF32});
     MoeArgs a = moe_prepare(X, W, Y, bias, GatherIndx, ExptHist, ExptOffs, ExptData, N, K, grid_m, stride_ym,
-                            stride_yn, stride_xm, stride_xk, stride_we, stride_wk, stride_wn);
+                            stride_yn, stride_xm, stride_xk, stride_we, stride_wk, stride_wn, 64);
     const int64_t G = (K + group_k - 1) / group_k, C = (N + group_n - 1) / group_n;
     expect(a.T == 0 || xs.numel() >= (a.T - 1) * (int64_t)stride_xsm + (G - 1) * (int64_t)stride_xsk + 1,
            "X_scale is smaller than its strides say");
     expect(ws.numel() >= (a.E - 1) * (int64_t)stride_wse + (G - 1) * (int64_t)stride_wsk +
                              (C - 1) * (int64_t)stride_wsn + 1,
            "W_scale is smaller than its strides say");
-    check(hkq_moe_a8w8_blockscale(a.X, a.W, a.Y, (const float*)xs.ptr, stride_xsm, stride_xsk, (const float*)ws.ptr,
-                                  stride_wse, stride_wsk, stride_wsn, group_k, group_n, a.bias, N, a.gather, a.hist,
-                                  a.offs, a.ed, a.T, a.E, N, K, grid_m, n_expts_act, a.stride_xm, a.stride_we,
-                                  a.stride_wn, a.stride_ym, a.y_rows, a.glen, current_stream()),
+    auto fn = a.kn ? hkq_moe_a8w8_blockscale_kn : hkq_moe_a8w8_blockscale;
+    check(fn(a.X, a.W, a.Y, (const float*)xs.ptr, stride_xsm, stride_xsk, (const float*)ws.ptr, stride_wse, stride_wsk,
+             stride_wsn, group_k, group_n, a.bias, N, a.gather, a.hist, a.offs, a.ed, a.T, a.E, N, K, grid_m,
+             n_expts_act, a.stride_xm, a.stride_we, a.kn ? a.stride_wk : a.stride_wn, a.stride_ym, a.y_rows, a.glen,
+             current_stream()),
           "moe_a8w8_blockscale");
 }
 

@@ -14,9 +14,9 @@ struct MoeScales {
 
 // Tensors and strides of one MoE call after validation. W points at
 // K-contiguous rows (stride_wn), or (kn) at the reference's N-contiguous
-// [E, K, N] weights, read in place (stride_wk); N-contiguous weights with
-// K % 128 != 0, which the A8W8 kernels cannot read in place, are copied
-// K-major into `packed` (kept alive until the launch is queued).
+// [E, K, N] weights, read in place (stride_wk) when K is a multiple of
+// kn_kmul (the kernels' K-tile; 0: never); other N-contiguous weights are
+// copied K-major into `packed` (kept alive until the launch is queued).
 struct MoeArgs {
     const void* X = nullptr;
     const void* W = nullptr;
@@ -32,7 +32,7 @@ struct MoeArgs {
 inline MoeArgs moe_prepare(py::object X, py::object W, py::object Y, py::object bias, py::object GatherIndx,
                            py::object ExptHist, py::object ExptOffs, py::object ExptData, int N, int K, int grid_m,
                            int stride_ym, int stride_yn, int stride_xm, int stride_xk, int stride_we, int stride_wk,
-                           int stride_wn, bool in_place_kn = false) {
+                           int stride_wn, int kn_kmul = 0) {
     auto x = view(X, "X"), w = view(W, "W"), y = view(Y, "Y");
     if (x.dtype == kBF16 || x.dtype == kI8 || w.dtype == kBF16 || w.dtype == kI8)
         throw py::type_error("X and W must hold E4M3FN codes (torch.float8_e4m3fn or uint8)");
@@ -75,7 +75,7 @@ inline MoeArgs moe_prepare(py::object X, py::object W, py::object Y, py::object 
         a.W = (const void*)w.ptr;
         a.stride_we = stride_we;
         a.stride_wn = stride_wn;
-    } else if (K % 128 == 0 && in_place_kn) {
+    } else if (kn_kmul > 0 && K % kn_kmul == 0) {
         // the reference's [E, K, N] layout (tests/test_moe.py:723-729), read in place
         expect(w.numel() >= (a.E - 1) * (int64_t)stride_we + (int64_t)(K - 1) * stride_wk + N,
                "W is smaller than its strides say");
@@ -101,7 +101,7 @@ inline void moe_call(py::object X, py::object W, py::object Y, const MoeScales& 
                      int K, int grid_m, int n_expts_act, int stride_ym, int stride_yn, int stride_xm, int stride_xk,
                      int stride_we, int stride_wk, int stride_wn) {
     MoeArgs a = moe_prepare(X, W, Y, bias, GatherIndx, ExptHist, ExptOffs, ExptData, N, K, grid_m, stride_ym,
-                            stride_yn, stride_xm, stride_xk, stride_we, stride_wk, stride_wn, true);
+                            stride_yn, stride_xm, stride_xk, stride_we, stride_wk, stride_wn, 128);
     auto fn = a.kn ? hkq_moe_a8w8_kn : hkq_moe_a8w8;
     check(fn(a.X, a.W, a.Y, sc.xs, sc.xs_tok, sc.ws, sc.ws_e, sc.ws_n, sc.ws_gn, a.bias, N, a.gather, a.hist, a.offs,
              a.ed, a.T, a.E, N, K, grid_m, n_expts_act, a.stride_xm, a.stride_we, a.kn ? a.stride_wk : a.stride_wn,

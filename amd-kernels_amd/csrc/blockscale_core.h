@@ -60,7 +60,9 @@ __device__ __forceinline__ uint32_t bs_load_dst(int st, int q, int wave) {
 // loads and barriers). COMPUTE false: a wave whose rows all lie outside the
 // tile only issues its share of the loads and takes the barriers (acc stays
 // zero), leaving its SIMD's MFMA and VALU pipes to the other wave.
-template <int SBM, int TN, bool COMPUTE = true, class Issue>
+// BT: the B K-tiles are N-contiguous (KTileT: 128 rows of K x 256 columns at
+// BS_BOFF of each stage), their operands built with transposed reads.
+template <int SBM, int TN, bool COMPUTE = true, bool BT = false, class Issue>
 __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int lane, int wm, int cn, int KTN, Issue& issue,
                                           v16f (&acc)[TN][BS_TM]) {
     using KT = KTile<BS_KT>;
@@ -95,10 +97,21 @@ __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int lane, int w
             a_base[ks][h] = (uint32_t)(uintptr_t)smem + (uint32_t)KT::swz(wm * TM * 32 + (lane & 31), c);
             b_base[ks][h] = (uint32_t)(uintptr_t)smem + (uint32_t)(BS_BOFF + cn * BS_KT) + (uint32_t)KT::swz(lane & 31, c);
         }
+    // BT: per n-tile the lane's row 32 * khalf + (j >> 1) (j = lane % 16) and
+    // byte 8 (j & 1) of logical chunk cn / 16 + 2t + g (g = (lane / 16) & 1);
+    // K-step, part and read rows are immediates in multiples of 8 rows
+    uint32_t bt_base[TN];
+    if constexpr (BT) {
+        const int j = lane & 15, g = (lane >> 4) & 1, row = 32 * khalf + (j >> 1);
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+            bt_base[t] = (uint32_t)(uintptr_t)smem + (uint32_t)BS_BOFF +
+                         (uint32_t)(row * KTileT::ROW + (KTileT::phys(row, cn / 16 + 2 * t + g) << 4) + 8 * (j & 1));
+    }
     // the bases of stage st, rebuilt from opaque copies each K-tile: left
     // visible, the compiler hoists every piece address out of the loop
     struct Bases {
-        uint32_t a[2][2], b[2][2];
+        uint32_t a[2][2], b[2][2], bt[TN];
     };
     auto bases = [&](int st) {
         Bases r;
@@ -107,10 +120,19 @@ __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int lane, int w
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 r.a[ks][h] = a_base[ks][h] + (uint32_t)(st * BS_STAGE);
-                r.b[ks][h] = b_base[ks][h] + (uint32_t)(st * BS_STAGE);
                 asm volatile("" : "+v"(r.a[ks][h]));
-                asm volatile("" : "+v"(r.b[ks][h]));
+                if constexpr (!BT) {
+                    r.b[ks][h] = b_base[ks][h] + (uint32_t)(st * BS_STAGE);
+                    asm volatile("" : "+v"(r.b[ks][h]));
+                }
             }
+        if constexpr (BT) {
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+                r.bt[t] = bt_base[t] + (uint32_t)(st * BS_STAGE);
+                asm volatile("" : "+v"(r.bt[t]));
+            }
+        }
         return r;
     };
     // a tile's operand for both K-steps: [K-step] of 8 dwords
@@ -126,6 +148,26 @@ __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int lane, int w
         Op o;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) o.k[ks] = read_step(base, t, ks);
+        return o;
+    };
+    // BT: K-step ks of n-tile t from the transposed tile, rows 64ks + 32khalf
+    // + 8q (q = 0..3) of the lane's column
+    auto read_step_t = [&](const Bases& rb, int t, int ks) {
+        v2i q[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            q[r] = lds_read_tr8(reinterpret_cast<const HKQ_LDS uint8_t*>(
+                (uintptr_t)(rb.bt[t] + (uint32_t)((64 * ks + 8 * r) * KTileT::ROW))));
+        return v8i{q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
+    };
+    auto read_b_step = [&](const Bases& rb, int t, int ks) {
+        if constexpr (BT) return read_step_t(rb, t, ks);
+        else return read_step(rb.b, t, ks);
+    };
+    auto read_b_op = [&](const Bases& rb, int t) {
+        Op o;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) o.k[ks] = read_b_step(rb, t, ks);
         return o;
     };
 
@@ -155,9 +197,9 @@ __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int lane, int w
         // read first: the LDS counter is in order, so the MFMAs can start
         // while the other fragments are still in flight
         Op fa[TM], fb;
-        fb.k[0] = read_step(rb.b, 0, 0);
+        fb.k[0] = read_b_step(rb, 0, 0);
         fa[0].k[0] = read_step(rb.a, 0, 0);
-        fb.k[1] = read_step(rb.b, 0, 1);
+        fb.k[1] = read_b_step(rb, 0, 1);
         fa[0].k[1] = read_step(rb.a, 0, 1);
 #pragma unroll
         for (int j = 1; j < TM; ++j) fa[j] = read_op(rb.a, j);
@@ -168,7 +210,7 @@ __device__ __forceinline__ void bs8_kloop(HKQ_LDS uint8_t* smem, int lane, int w
             for (int q = i * PER; q < (i + 1) * PER && q < BS_NLD; ++q) issue(kt + 1, q);
             // n-tile i+1's operand and column scales, read under this n-tile's MFMAs
             Op fb_next;
-            if (i + 1 < TN) fb_next = read_op(rb.b, i + 1);
+            if (i + 1 < TN) fb_next = read_b_op(rb, i + 1);
             v4f sbn[4];
             if constexpr (SBM == BS_SB_COL) {
 #pragma unroll

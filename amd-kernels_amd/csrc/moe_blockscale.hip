@@ -100,7 +100,8 @@ __global__ __launch_bounds__(256) void pack_kmajor_kernel(const uint8_t* __restr
 // ---------------------------------------------------------------------------
 struct MoeBsParams {
     const uint8_t* X;       // [T, sxm] E4M3FN, K contiguous
-    const uint8_t* W;       // expert e at W + e*swe, row n at + n*swn, K contiguous
+    const uint8_t* W;       // expert e at W + e*swe; wt == 0: row n at + n*swn, K contiguous;
+                            // wt == 1 (N-contiguous [K, N]): row k at + k*swk
     uint16_t* Y;            // sorted row s at Y + s*sym
     const float* xs;        // X_scale (t, g) at t*xsm + g*xsk
     const float* ws;        // W_scale (e, g, c) at e*wse + g*wsk + c*wsn, c = n / gn
@@ -113,7 +114,38 @@ struct MoeBsParams {
     double rtopk;  // 1.0 / topk (div_recip)
     int64_t sxm, swe, swn, sym, xsm, xsk, wse, wsk, wsn, bias_e;
     int64_t xs_elems, ws_elems;  // reads of the scale tensors stay below these extents
+    int64_t swk;
+    int wt;
 };
+
+// The expert's weight source of a tile at column n0: base, extent (bytes from
+// the base; N-contiguous columns past N read the next row's bytes, which only
+// reach output columns that are never stored) and the bytes from one K-tile of
+// KTB values to the next.
+struct MoeBsB {
+    const uint8_t* base;
+    int64_t bytes, kstep;
+};
+template <bool BT, int KTB>
+__device__ __forceinline__ MoeBsB moe_bs_b(const MoeBsParams& p, int e, int n0, int rows_b) {
+    if constexpr (BT)
+        return MoeBsB{p.W + (int64_t)e * p.swe + n0, min((int64_t)(p.K - 1) * p.swk + rows_b, (int64_t)0x7FFFFFFF),
+                      (int64_t)KTB * p.swk};
+    else
+        return MoeBsB{p.W + (int64_t)e * p.swe + (int64_t)n0 * p.swn, min((int64_t)rows_b * p.swn, (int64_t)0x7FFFFFFF),
+                      (int64_t)KTB};
+}
+// Load offset of a wave's B load i (NW waves, KTB-byte K-tiles): K-major rows
+// of KTB bytes, or (BT) 4 rows of K x 256 columns per load in KTileT order.
+template <bool BT, int NW, int KTB>
+__device__ __forceinline__ uint32_t moe_bs_b_off(const MoeBsParams& p, int i, int wave, int lane) {
+    if constexpr (BT) {
+        const int r = (i * NW + wave) * KTileT::ROWS_PER_LOAD + lane / 16;
+        return (uint32_t)(r * p.swk) + (uint32_t)(KTileT::phys(r, lane % 16) << 4);
+    } else {
+        return dense_row_off<NW, KTB>(i, wave, lane, p.swn);
+    }
+}
 
 constexpr int MBS_WM = 2, MBS_WN = 2, MBS_TM = 2, MBS_TN = 4, MBS_NW = 4;
 constexpr int MBS_BM = MBS_WM * MBS_TM * 32, MBS_BN = MBS_WN * MBS_TN * 32;  // 128 x 256
@@ -128,7 +160,7 @@ static_assert(2 * MBS_LDS <= 160 * 1024, "two workgroups per CU");
 
 // GNW: group_n is a multiple of 32, so the 32 columns of a sub-tile share one
 // weight scale; otherwise every column has its own.
-template <bool GNW>
+template <bool GNW, bool BT = false>
 __global__ __launch_bounds__(64 * MBS_NW, 2) void moe_blockscale_kernel(const MoeBsParams p) {
     using KT = KTile<MBS_KTB>;
     constexpr int TM = MBS_TM, TN = MBS_TN, NW = MBS_NW;
@@ -167,10 +199,11 @@ __global__ __launch_bounds__(64 * MBS_NW, 2) void moe_blockscale_kernel(const Mo
         a_off[i] = t < 0 ? OOB : (uint32_t)(t * p.sxm) + (uint32_t)(KT::load_chunk(lane, r) << 4);
     }
 #pragma unroll
-    for (int i = 0; i < MBS_LB; ++i) b_off[i] = dense_row_off<NW, MBS_KTB>(i, wave, lane, p.swn);
-    const uint8_t* wb = p.W + (int64_t)e * p.swe + (int64_t)n0 * p.swn;
+    for (int i = 0; i < MBS_LB; ++i) b_off[i] = moe_bs_b_off<BT, NW, MBS_KTB>(p, i, wave, lane);
+    const MoeBsB bsrc = moe_bs_b<BT, MBS_KTB>(p, e, n0, rows_b);
+    const uint8_t* wb = bsrc.base;
     const int64_t a_bytes = min((int64_t)p.T * p.sxm, (int64_t)0x7FFFFFFF);
-    const int64_t b_bytes = min((int64_t)rows_b * p.swn, (int64_t)0x7FFFFFFF);
+    const int64_t b_bytes = bsrc.bytes;
     // scales: row r = (wave & 1) * 64 + lane (waves 2, 3 load the same rows as
     // 0, 1, so that every wave issues the same number of loads), column
     // n0 + wave * 64 + lane; the group part is added per K-tile
@@ -192,9 +225,10 @@ __global__ __launch_bounds__(64 * MBS_NW, 2) void moe_blockscale_kernel(const Mo
         for (int i = 0; i < MBS_LA; ++i)
             lds_load16(p.X + kb, live && a_bytes > kb ? (uint32_t)(a_bytes - kb) : 0u, st + (i * NW + wave) * 1024,
                        a_off[i]);
+        const int64_t kbb = (int64_t)kt * bsrc.kstep;
 #pragma unroll
         for (int i = 0; i < MBS_LB; ++i)
-            lds_load16(wb + kb, live && b_bytes > kb ? (uint32_t)(b_bytes - kb) : 0u,
+            lds_load16(wb + kbb, live && b_bytes > kbb ? (uint32_t)(b_bytes - kbb) : 0u,
                        st + MBS_BM * MBS_KTB + (i * NW + wave) * 1024, b_off[i]);
         lds_load4(p.xs, live ? xs_bytes : 0u, st + MBS_SA + (wave & 1) * 256, sa_off + (uint32_t)(g * p.xsk * 4));
         lds_load4(wsb, live ? ws_bytes : 0u, st + MBS_SB + wave * 256, sb_off + (uint32_t)(g * p.wsk * 4));
@@ -212,6 +246,17 @@ __global__ __launch_bounds__(64 * MBS_NW, 2) void moe_blockscale_kernel(const Mo
         const v4i hi = lds_read16(tile + KT::swz(r, 2 * khalf + 1));
         return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
+    // BT: n-tile i's operand from the transposed K-tile (64 rows of K x 256
+    // columns): rows 32 * khalf + 8q + (j >> 1) of the lane's column, q = 0..3
+    const int tj = lane & 15, tg = (lane >> 4) & 1, trow = 32 * khalf + (tj >> 1);
+    auto frag_t = [&](const HKQ_LDS uint8_t* tile, int i) {
+        const HKQ_LDS uint8_t* b =
+            tile + trow * KTileT::ROW + (KTileT::phys(trow, (wn * TN * 32 + i * 32) / 16 + tg) << 4) + 8 * (tj & 1);
+        v2i q[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) q[r] = lds_read_tr8(b + 8 * r * KTileT::ROW);
+        return v8i{q[0][0], q[0][1], q[1][0], q[1][1], q[2][0], q[2][1], q[3][0], q[3][1]};
+    };
 
     issue(0);
     issue(1);
@@ -225,7 +270,10 @@ __global__ __launch_bounds__(64 * MBS_NW, 2) void moe_blockscale_kernel(const Mo
 #pragma unroll
         for (int j = 0; j < TM; ++j) fa[j] = frag(st, arow + j * 32);
 #pragma unroll
-        for (int i = 0; i < TN; ++i) fb[i] = frag(st + MBS_BM * MBS_KTB, brow + i * 32);
+        for (int i = 0; i < TN; ++i) {
+            if constexpr (BT) fb[i] = frag_t(st + MBS_BM * MBS_KTB, i);
+            else fb[i] = frag(st + MBS_BM * MBS_KTB, brow + i * 32);
+        }
         const HKQ_LDS float* sas = reinterpret_cast<const HKQ_LDS float*>(st + MBS_SA);
         const HKQ_LDS float* sbs = reinterpret_cast<const HKQ_LDS float*>(st + MBS_SB);
         float sa[TM];
@@ -302,7 +350,7 @@ __global__ __launch_bounds__(64 * MBS_NW, 2) void moe_blockscale_kernel(const Mo
 // reads zero). Every listed block is computed once per word, as the
 // reference's grid does.
 // ---------------------------------------------------------------------------
-template <int SBM>
+template <int SBM, bool BT = false>
 __global__ __launch_bounds__(64 * BS_NW, 1) void moe_blockscale8_kernel(const MoeBsParams p) {
     constexpr int TM = BS_TM, TN = BS_TN, NW = BS_NW;
     using KT = KTile<BS_KT>;
@@ -345,10 +393,11 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void moe_blockscale8_kernel(const Mo
         asm volatile("" : "+v"(a_off[i]));  // kept as the 32-bit offset, not re-derived in the loop
     }
 #pragma unroll
-    for (int i = 0; i < BS_LB; ++i) b_off[i] = dense_row_off<NW, BS_KT>(i, wave, lane, p.swn);
-    const uint8_t* wb = p.W + (int64_t)e * p.swe + (int64_t)n0 * p.swn;
+    for (int i = 0; i < BS_LB; ++i) b_off[i] = moe_bs_b_off<BT, NW, BS_KT>(p, i, wave, lane);
+    const MoeBsB bsrc = moe_bs_b<BT, BS_KT>(p, e, n0, rows_b);
+    const uint8_t* wb = bsrc.base;
     const int64_t a_bytes = min((int64_t)p.T * p.sxm, (int64_t)0x7FFFFFFF);
-    const int64_t b_bytes = min((int64_t)rows_b * p.swn, (int64_t)0x7FFFFFFF);
+    const int64_t b_bytes = bsrc.bytes;
     // scales: row (wave & 3) * 64 + lane, column n0 + (wave & 3) * 64 + lane
     // (waves 4-7 repeat the loads of 0-3, so that every wave issues the same
     // loads); the group moves the base
@@ -374,10 +423,11 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void moe_blockscale8_kernel(const Mo
         const int st = kt & 1;
         if (q < BS_LA + BS_LB) {
             HKQ_LDS uint8_t* dst = reinterpret_cast<HKQ_LDS uint8_t*>((uintptr_t)(lds_base + bs_load_dst(st, q, wave)));
+            const int64_t kbb = BT ? (int64_t)kt * bsrc.kstep : kb;
             if (q < BS_LA)
                 lds_load16(p.X + kb, live && a_bytes > kb ? (uint32_t)(a_bytes - kb) : 0u, dst, a_off[q]);
             else
-                lds_load16(wb + kb, live && b_bytes > kb ? (uint32_t)(b_bytes - kb) : 0u, dst, b_off[q - BS_LA]);
+                lds_load16(wb + kbb, live && b_bytes > kbb ? (uint32_t)(b_bytes - kbb) : 0u, dst, b_off[q - BS_LA]);
         } else {
             HKQ_LDS uint8_t* slot = smem + BS_SC + st * BS_SLOT;
             const int g = live ? kt >> kpg_log2 : 0;
@@ -397,9 +447,9 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void moe_blockscale8_kernel(const Mo
     // lone block) only load: one computing wave per SIMD instead of two
     v16f acc[TN][TM];
     if (wm * TM * 32 < rows)
-        bs8_kloop<SBM, BS_TN, true>(smem, lane, wm, wn * BS_TN * 32, KTN, issue, acc);
+        bs8_kloop<SBM, BS_TN, true, BT>(smem, lane, wm, wn * BS_TN * 32, KTN, issue, acc);
     else
-        bs8_kloop<SBM, BS_TN, false>(smem, lane, wm, wn * BS_TN * 32, KTN, issue, acc);
+        bs8_kloop<SBM, BS_TN, false, BT>(smem, lane, wm, wn * BS_TN * 32, KTN, issue, acc);
 
     const int s0 = start + row0;
     const int nw = n0 + wn * TN * 32;
@@ -444,15 +494,15 @@ extern "C" int hkq_moe_pack_kmajor(const void* src, void* dst, int64_t E, int64_
     return hkq_launch_status();
 }
 
-extern "C" int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, const float* x_scale,
-                                       int64_t xs_stride_m, int64_t xs_stride_k, const float* w_scale,
-                                       int64_t ws_stride_e, int64_t ws_stride_k, int64_t ws_stride_n,
-                                       int64_t group_k, int64_t group_n, const float* bias, int64_t bias_stride_e,
-                                       const int32_t* gather, const int32_t* hist, const int32_t* offs,
-                                       const int32_t* expt_data, int64_t T, int64_t E, int64_t N, int64_t K,
-                                       int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we,
-                                       int64_t stride_wn, int64_t stride_ym, int64_t y_rows, int64_t gather_len,
-                                       hkq_stream_t stream) {
+// wt == 0: W[e] is [N, K] with row stride stride_w (K contiguous); wt == 1:
+// W[e] is [K, N] with row stride stride_w (N contiguous, the reference's layout).
+static int moe_blockscale_impl(const void* X, const void* W, void* Y, const float* x_scale, int64_t xs_stride_m,
+                               int64_t xs_stride_k, const float* w_scale, int64_t ws_stride_e, int64_t ws_stride_k,
+                               int64_t ws_stride_n, int64_t group_k, int64_t group_n, const float* bias,
+                               int64_t bias_stride_e, const int32_t* gather, const int32_t* hist, const int32_t* offs,
+                               const int32_t* expt_data, int64_t T, int64_t E, int64_t N, int64_t K, int64_t grid_m,
+                               int64_t topk, int64_t stride_xm, int64_t stride_we, int64_t stride_w, int wt,
+                               int64_t stride_ym, int64_t y_rows, int64_t gather_len, hkq_stream_t stream) {
     HKQ_CHECK_ARG(T >= 0 && E > 0 && E <= 0xFFFF && N >= 0 && K > 0 && grid_m >= 0 && topk > 0 && topk <= 0xFFFF,
                   "T, grid_m >= 0; 0 < E <= 65535; K > 0; 0 < topk <= 65535");
     HKQ_CHECK_ARG(T < (1 << 30) && N < (1 << 30) && K < (1 << 30) && grid_m < (1 << 30), "dimensions must be < 2^30");
@@ -465,9 +515,14 @@ extern "C" int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, co
                   "scale strides must be >= 0");
     HKQ_CHECK_ARG(stride_xm >= K && stride_xm % 16 == 0, "stride_xm must be >= K and a multiple of 16");
     HKQ_CHECK_ARG(T * stride_xm < (1ll << 31), "X must span less than 2^31 bytes (T * stride_xm)");
-    HKQ_CHECK_ARG(stride_wn >= K && stride_wn % 16 == 0, "stride_wn must be >= K and a multiple of 16 (W[e] is [N, K])");
+    if (wt) {
+        HKQ_CHECK_ARG(stride_w >= N && stride_w % 16 == 0, "stride_wk must be >= N and a multiple of 16 (W[e] is [K, N])");
+        HKQ_CHECK_ARG(K * stride_w < (1ll << 31), "one expert's weights must span less than 2^31 bytes (K * stride_wk)");
+    } else {
+        HKQ_CHECK_ARG(stride_w >= K && stride_w % 16 == 0, "stride_wn must be >= K and a multiple of 16 (W[e] is [N, K])");
+        HKQ_CHECK_ARG(256 * stride_w < (1ll << 31), "256 weight rows must span less than 2^31 bytes");
+    }
     HKQ_CHECK_ARG(stride_we >= 0 && stride_we % 16 == 0, "stride_we must be a non-negative multiple of 16");
-    HKQ_CHECK_ARG(256 * stride_wn < (1ll << 31), "256 weight rows must span less than 2^31 bytes");
     HKQ_CHECK_ARG(stride_ym >= N && stride_ym % 4 == 0, "stride_ym must be >= N and a multiple of 4");
     HKQ_CHECK_ARG(y_rows >= 0 && gather_len >= 0, "y_rows and gather_len must be >= 0");
     HKQ_CHECK_ARG(hist && offs && expt_data, "routing metadata pointers must not be null");
@@ -497,7 +552,10 @@ extern "C" int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, co
     p.y_rows = (int)y_rows;
     p.g_len = gather ? (int)gather_len : (int)y_rows;
     p.gk = (int)group_k; p.gn = (int)group_n;
-    p.sxm = stride_xm; p.swe = stride_we; p.swn = stride_wn; p.sym = stride_ym;
+    p.sxm = stride_xm; p.swe = stride_we; p.sym = stride_ym;
+    p.wt = wt;
+    p.swn = wt ? 1 : stride_w;
+    p.swk = wt ? stride_w : 1;
     p.xsm = xs_stride_m; p.xsk = xs_stride_k; p.wse = ws_stride_e; p.wsk = ws_stride_k; p.wsn = ws_stride_n;
     p.bias_e = bias_stride_e;
     p.xs_elems = xs_elems; p.ws_elems = ws_elems;
@@ -515,15 +573,17 @@ extern "C" int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, co
         const int64_t nblk = grid_m * p.tiles_n;
         if (nblk == 0) return 0;
         const bool ntile = group_n % 32 == 0;
-        auto kern = ntile ? moe_blockscale8_kernel<BS_SB_NTILE> : moe_blockscale8_kernel<BS_SB_COL>;
-        static bool attr8_set[2] = {false, false};
-        if (!attr8_set[ntile]) {
+        auto kern = ntile ? (wt ? moe_blockscale8_kernel<BS_SB_NTILE, true> : moe_blockscale8_kernel<BS_SB_NTILE>)
+                          : (wt ? moe_blockscale8_kernel<BS_SB_COL, true> : moe_blockscale8_kernel<BS_SB_COL>);
+        const int v8 = (ntile ? 1 : 0) + (wt ? 2 : 0);
+        static bool attr8_set[4] = {false, false, false, false};
+        if (!attr8_set[v8]) {
             hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, BS_LDS);
             if (err != hipSuccess) {
                 set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", BS_LDS, hipGetErrorString(err));
                 return (int)err;
             }
-            attr8_set[ntile] = true;
+            attr8_set[v8] = true;
         }
         kern<<<dim3((unsigned)nblk), 64 * BS_NW, BS_LDS, stream>>>(p);
         return hkq_launch_status();
@@ -532,16 +592,48 @@ extern "C" int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, co
     const int64_t nblk = grid_m * p.tiles_n;
     if (nblk == 0) return 0;
     const bool gnw = group_n % 32 == 0;
-    auto kern = gnw ? moe_blockscale_kernel<true> : moe_blockscale_kernel<false>;
-    static bool attr_set[2] = {false, false};
-    if (!attr_set[gnw]) {
+    auto kern = gnw ? (wt ? moe_blockscale_kernel<true, true> : moe_blockscale_kernel<true>)
+                    : (wt ? moe_blockscale_kernel<false, true> : moe_blockscale_kernel<false>);
+    const int v = (gnw ? 1 : 0) + (wt ? 2 : 0);
+    static bool attr_set[4] = {false, false, false, false};
+    if (!attr_set[v]) {
         hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, MBS_LDS);
         if (err != hipSuccess) {
             set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", MBS_LDS, hipGetErrorString(err));
             return (int)err;
         }
-        attr_set[gnw] = true;
+        attr_set[v] = true;
     }
     kern<<<dim3((unsigned)nblk), 64 * MBS_NW, MBS_LDS, stream>>>(p);
     return hkq_launch_status();
+}
+
+extern "C" int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, const float* x_scale,
+                                       int64_t xs_stride_m, int64_t xs_stride_k, const float* w_scale,
+                                       int64_t ws_stride_e, int64_t ws_stride_k, int64_t ws_stride_n,
+                                       int64_t group_k, int64_t group_n, const float* bias, int64_t bias_stride_e,
+                                       const int32_t* gather, const int32_t* hist, const int32_t* offs,
+                                       const int32_t* expt_data, int64_t T, int64_t E, int64_t N, int64_t K,
+                                       int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we,
+                                       int64_t stride_wn, int64_t stride_ym, int64_t y_rows, int64_t gather_len,
+                                       hkq_stream_t stream) {
+    return moe_blockscale_impl(X, W, Y, x_scale, xs_stride_m, xs_stride_k, w_scale, ws_stride_e, ws_stride_k,
+                               ws_stride_n, group_k, group_n, bias, bias_stride_e, gather, hist, offs, expt_data, T, E,
+                               N, K, grid_m, topk, stride_xm, stride_we, stride_wn, 0, stride_ym, y_rows, gather_len,
+                               stream);
+}
+
+extern "C" int hkq_moe_a8w8_blockscale_kn(const void* X, const void* W, void* Y, const float* x_scale,
+                                          int64_t xs_stride_m, int64_t xs_stride_k, const float* w_scale,
+                                          int64_t ws_stride_e, int64_t ws_stride_k, int64_t ws_stride_n,
+                                          int64_t group_k, int64_t group_n, const float* bias, int64_t bias_stride_e,
+                                          const int32_t* gather, const int32_t* hist, const int32_t* offs,
+                                          const int32_t* expt_data, int64_t T, int64_t E, int64_t N, int64_t K,
+                                          int64_t grid_m, int64_t topk, int64_t stride_xm, int64_t stride_we,
+                                          int64_t stride_wk, int64_t stride_ym, int64_t y_rows, int64_t gather_len,
+                                          hkq_stream_t stream) {
+    return moe_blockscale_impl(X, W, Y, x_scale, xs_stride_m, xs_stride_k, w_scale, ws_stride_e, ws_stride_k,
+                               ws_stride_n, group_k, group_n, bias, bias_stride_e, gather, hist, offs, expt_data, T, E,
+                               N, K, grid_m, topk, stride_xm, stride_we, stride_wk, 1, stride_ym, y_rows, gather_len,
+                               stream);
 }

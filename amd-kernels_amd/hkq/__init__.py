@@ -46,6 +46,8 @@ SIGNATURES = {
                         + [_I64] * 12 + [_P]),
     "hkq_moe_a8w8_blockscale": (_I, [_P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64,
                                      _P, _P, _P, _P] + [_I64] * 12 + [_P]),
+    "hkq_moe_a8w8_blockscale_kn": (_I, [_P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64,
+                                     _P, _P, _P, _P] + [_I64] * 12 + [_P]),
     "hkq_moe_pack_kmajor": (_I, [_P, _P] + [_I64] * 7 + [_P]),
     "hkq_rmsnorm_quant": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _P]),
     "hkq_swiglu_quant": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _I, _P]),
@@ -364,19 +366,21 @@ def moe_a8w8(X, W, hist, offs, expt_data, topk, gather=None, x_scale=None, w_sca
 
 
 def moe_a8w8_blockscale(X, W, hist, offs, expt_data, topk, x_scale, w_scale, group_k: int, group_n: int,
-                        gather=None, bias=None, Y=None, y_rows=None, stream=None):
+                        gather=None, bias=None, Y=None, y_rows=None, stream=None, w_kn=False):
     """OGS-routed A8W8 MoE GEMM with per-K-group scales. X [T, K] E4M3FN;
-    W [E, N, K] E4M3FN (K contiguous); x_scale fp32 [T, ceil(K/group_k)];
+    W [E, N, K] E4M3FN (K contiguous), or with w_kn the reference's [E, K, N]
+    (N contiguous, read in place); x_scale fp32 [T, ceil(K/group_k)];
     w_scale fp32 [E, ceil(K/group_k), ceil(N/group_n)] (any strides); bias None
     or fp32 [E, N]. Returns Y bf16 [y_rows (default T*topk), N]."""
     import torch
 
     T, K = X.shape
-    E, N = W.shape[0], W.shape[1]
+    E, N = (W.shape[0], W.shape[2]) if w_kn else (W.shape[0], W.shape[1])
     rows = T * topk if y_rows is None else y_rows
     if Y is None:
         Y = torch.zeros((rows, N), dtype=torch.bfloat16, device=X.device)
-    call("hkq_moe_a8w8_blockscale", _ptr(X), _ptr(W), _ptr(Y), _ptr(x_scale), x_scale.stride(0), x_scale.stride(1),
+    call("hkq_moe_a8w8_blockscale_kn" if w_kn else "hkq_moe_a8w8_blockscale", _ptr(X), _ptr(W), _ptr(Y),
+         _ptr(x_scale), x_scale.stride(0), x_scale.stride(1),
          _ptr(w_scale), w_scale.stride(0), w_scale.stride(1), w_scale.stride(2), group_k, group_n, _opt_ptr(bias), N,
          _opt_ptr(gather), _ptr(hist), _ptr(offs), _ptr(expt_data), T, E, N, K, expt_data.numel(), topk,
          X.stride(0), W.stride(0), W.stride(1), Y.stride(0), rows, gather.numel() if gather is not None else 0,

@@ -280,6 +280,23 @@ int hkq_moe_a8w8_blockscale(const void* X, const void* W, void* Y, const float* 
                             int64_t topk, int64_t stride_xm, int64_t stride_we, int64_t stride_wn, int64_t stride_ym,
                             int64_t y_rows, int64_t gather_len, hkq_stream_t stream);
 
+/* hkq_moe_a8w8_blockscale on the reference's N-contiguous weights: W[e, k, n]
+ * at W + e * stride_we + k * stride_wk + n (stride_wk >= N, a multiple of 16;
+ * K * stride_wk < 2^31), read in place by the kernels (K-tiles staged as rows
+ * of K, the MFMA operand built with transposed LDS reads); every output
+ * element is the one hkq_moe_a8w8_blockscale gives for the same weights in
+ * [E, N, K], bit for bit. Replaces moe_op_gemm_a8w8_blockscale_tk.moe_a8w8_blockscale
+ * with stride_wn == 1, the reference's own call (kernels/moe-gemm/
+ * moe_op_gemm_a8w8_blockscale/kernel.cpp:108, the weight read
+ * W[e*stride_we + k*stride_wk + n*stride_wn]; tests/test_moe.py:771-815). */
+int hkq_moe_a8w8_blockscale_kn(const void* X, const void* W, void* Y, const float* x_scale, int64_t xs_stride_m,
+                               int64_t xs_stride_k, const float* w_scale, int64_t ws_stride_e, int64_t ws_stride_k,
+                               int64_t ws_stride_n, int64_t group_k, int64_t group_n, const float* bias,
+                               int64_t bias_stride_e, const int32_t* gather, const int32_t* hist, const int32_t* offs,
+                               const int32_t* expt_data, int64_t T, int64_t E, int64_t N, int64_t K, int64_t grid_m,
+                               int64_t topk, int64_t stride_xm, int64_t stride_we, int64_t stride_wk,
+                               int64_t stride_ym, int64_t y_rows, int64_t gather_len, hkq_stream_t stream);
+
 /* Byte-plane transpose dst[e][n][r] = src[e][r][n] (src row r at
  * src + e*src_stride_e + r*src_stride_r, N contiguous bytes; dst row n at
  * dst + e*dst_stride_e + n*dst_stride_n, R contiguous bytes). Turns the

@@ -422,6 +422,33 @@ def test_moe_blockscale(orc, T, E, topk, K, N, gk, gn):
     check_rows(orc, Y, ref)
 
 
+# N-contiguous [E, K, N] weights through both block-scale kernels (the 8-wave
+# one for group_k = 128 * 2^j, the 64-wide one otherwise), read in place: the
+# same bits as the K-contiguous weights, ragged N and padded rows of K
+# included.
+@pytest.mark.parametrize("T,E,topk,K,N,gk,gn,pad", [(700, 5, 2, 1024, 512, 128, 128, 0),
+                                                     (600, 3, 2, 512, 1000, 256, 7, 24),
+                                                     (300, 4, 2, 320, 264, 64, 64, 8),
+                                                     (64, 8, 2, 256, 256, 64, 64, 0)])
+def test_moe_blockscale_kn_matches_kmajor(orc, T, E, topk, K, N, gk, gn, pad):
+    require_gpu()
+    _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, T, E, topk, K, N, 61)
+    rng = np.random.default_rng(62)
+    G, C = -(-K // gk), -(-N // gn)
+    xs = (rng.random((T, G)) * 0.02 + 0.001).astype(np.float32)
+    ws = (rng.random((E, G, C)) * 0.02 + 0.001).astype(np.float32)
+    Wkn = np.zeros((E, K, N + pad), np.uint8)
+    Wkn[:, :, :N] = W.transpose(0, 2, 1)
+    Xd, hd, od, edd, gd = dev_u8(X), dev_i32(hist), dev_i32(offs), dev_i32(ed), dev_i32(gather)
+    xsd, wsd = dev_f32(xs), dev_f32(ws)
+    Y = hkq.moe_a8w8_blockscale(Xd, dev_u8(W), hd, od, edd, topk, xsd, wsd, gk, gn, gather=gd)
+    Ykn = hkq.moe_a8w8_blockscale(Xd, dev_u8(Wkn)[:, :, :N], hd, od, edd, topk, xsd, wsd, gk, gn, gather=gd, w_kn=True)
+    torch.cuda.synchronize()
+    assert torch.equal(Y, Ykn), "N-contiguous weights give other bits than K-contiguous ones"
+    ref = orc.moe_blockscale_ref(X, W, xs, ws, None, gather, hist, offs, ed, topk, gk, gn)
+    check_rows(orc, host_bf16_f32(Ykn), ref)
+
+
 def test_moe_blockscale_padding_and_malformed_entries(orc):
     """-1 padding, an expert past E and words with bit 31 set are skipped; a
     token past T reads zero."""
