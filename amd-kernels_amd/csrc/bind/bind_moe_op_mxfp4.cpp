@@ -8,9 +8,11 @@
 // Strides are in elements of each tensor (bytes for the uint8 ones). B and
 // B_mx_scale may be K-contiguous (stride_bk == stride_bmxk == 1: B[e] is
 // [N, K/2]) or the reference test's N-contiguous [E, K/2, N] / [E, K/32, N]
-// (stride_bn == stride_bmxn == 1), which are copied K-major on the stream
-// before the GEMM (hkq_moe_pack_kmajor). Every index the call can reach is
-// checked against the tensors' sizes before the launch.
+// (stride_bn == stride_bmxn == 1), which the kernels read in place
+// (hkq_moe_mxfp4_kn) when K % 256 == 0 and the strides are multiples of 16,
+// and which are otherwise copied K-major on the stream before the GEMM
+// (hkq_moe_pack_kmajor). Every index the call can reach is checked against the
+// tensors' sizes before the launch.
 #include "bind_common.h"
 
 using namespace hkqbind;
@@ -58,10 +60,13 @@ void moe_mxfp4(py::object A, py::object B, py::object C, py::object A_mx_scale, 
     expect(bs.numel() >= extent({{E, stride_bmxe}, {N, stride_bmxn}, {K / 32, stride_bmxk}}),
            "B_mx_scale is smaller than its strides say");
     // N-contiguous weights and scales (tests/test_moe.py:909-925 of the
-    // reference): K-major copies [E, N, K/2] and [E, N, K/32] for this call
+    // reference): read in place where the kernels can, else K-major copies
+    // [E, N, K/2] and [E, N, K/32] for this call
+    const bool in_place = !kmajor && K % 256 == 0 && stride_bk % 16 == 0 && stride_bmxk % 16 == 0 &&
+                          stride_be % 16 == 0 && stride_bmxe % 16 == 0 && bs.ptr % 16 == 0 && b.ptr % 16 == 0;
     Workspace bp, bsp;
     uint64_t b_ptr = b.ptr, bs_ptr = bs.ptr;
-    if (!kmajor) {
+    if (!kmajor && !in_place) {
         bp = pack_kmajor(B, b.ptr, E, K / 2, N, stride_be, stride_bk, "moe_mxfp4 weight prepack");
         bsp = pack_kmajor(B, bs.ptr, E, K / 32, N, stride_bmxe, stride_bmxk, "moe_mxfp4 scale prepack");
         b_ptr = (uint64_t)bp.ptr;
@@ -93,10 +98,11 @@ void moe_mxfp4(py::object A, py::object B, py::object C, py::object A_mx_scale, 
         expect(v.numel() >= num_valid_tokens && v.contiguous(), "topk_weights must hold num_valid_tokens values");
         tw = (const float*)v.ptr;
     }
-    check(hkq_moe_mxfp4((const void*)a.ptr, (const void*)b_ptr, (void*)c.ptr, (const void*)as.ptr,
-                        (const void*)bs_ptr, sa, sb, tw, (const int32_t*)ids.ptr, (const int32_t*)eids.ptr, N, K,
-                        num_valid_tokens, top_k, mul_routed_weight ? 1 : 0, stride_am, stride_be, stride_bn,
-                        stride_cm, stride_amxm, stride_bmxe, stride_bmxn, tokens, E, grid_m, current_stream()),
+    auto fn = in_place ? hkq_moe_mxfp4_kn : hkq_moe_mxfp4;
+    check(fn((const void*)a.ptr, (const void*)b_ptr, (void*)c.ptr, (const void*)as.ptr, (const void*)bs_ptr, sa, sb, tw,
+             (const int32_t*)ids.ptr, (const int32_t*)eids.ptr, N, K, num_valid_tokens, top_k,
+             mul_routed_weight ? 1 : 0, stride_am, stride_be, in_place ? stride_bk : stride_bn, stride_cm, stride_amxm,
+             stride_bmxe, in_place ? stride_bmxk : stride_bmxn, tokens, E, grid_m, current_stream()),
           "moe_mxfp4");
 }
 

@@ -186,8 +186,8 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     static_assert(NS >= 2 && (NS - 1) * NLD + 3 <= 63, "ring depth and vmcnt budget");
     static_assert(!Cfg::SBLK || NS == 2, "the scale-block schedule assumes a 2-stage ring");
     static_assert(Cfg::SB_KT <= 4 && LSA <= 4, "gathered scale rows: at most 4 load slots per lane");
-    static_assert(!BT || (KTB == 128 && Cfg::BN == KTileT::ROW && MODE == MODE_A8W8),
-                  "N-contiguous B: FP8, 128-byte K-tiles of 256 columns");
+    static_assert(!BT || (KTB == 128 && Cfg::BN == KTileT::ROW && (MODE == MODE_A8W8 || MODE == MODE_MXFP4)),
+                  "N-contiguous B: FP8 or FP4, 128-byte K-tiles of 256 columns");
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int KTN = src.KT;
 
@@ -197,6 +197,10 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     // the block moves the offset by 32 bytes. Units of blocks past the last
     // one (the look-ahead past the end) land in a slot no remaining K-tile
     // reads.
+    // BT (N-contiguous B scales, one row of N bytes per 32 values of K): the
+    // block's B part holds its 32 rows of the tile's 256 columns in the KTileT
+    // order (8 KB at BM * 32 in the slot); B group g - BM / 32 carries rows
+    // 4 (g - BM / 32) + lane / 16, and a block moves them by 32 rows.
     HKQ_LDS uint8_t* sblk = smem + NS * STAGE;
     constexpr int SBK = Cfg::SBLK ? Cfg::SB_KT : 1;
     int su_g[SBK];
@@ -214,6 +218,10 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
         const uint32_t a_row = src.sa_gathered ? src.sa_row[k & 3] : (uint32_t)(r * src.lsa);
         const uint32_t b_row = (uint32_t)((r - BM) * src.lsb);
         su_off[k] = (su_a[k] ? a_row : b_row) + half * 16u;
+        if (BT && !su_a[k]) {
+            const int rt = 4 * (g - BM / 32) + lane / 16;
+            su_off[k] = (uint32_t)(rt * src.lsb) + (uint32_t)(KTileT::phys(rt, lane % 16) << 4);
+        }
         asm volatile("" : "+v"(su_off[k]));
     }
     const v4i desc_as = buffer_desc(src.as, (uint32_t)(src.as_bytes < 0x7FFFFFFF ? (src.as_bytes > 0 ? src.as_bytes : 0) : 0x7FFFFFFF));
@@ -221,8 +229,8 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     auto load_scale_unit = [&](int u, auto kslot) {
         constexpr int k = decltype(kslot)::value;
         const int blk = u / Cfg::SB_KT;
-        lds_load16_d(su_a[k] ? desc_as : desc_bs, sblk + (blk & 1) * Cfg::SB_SLOT + su_g[k] * 1024,
-                     su_off[k] + (uint32_t)(blk * 32));
+        const uint32_t adv = BT && !su_a[k] ? (uint32_t)(blk * 32) * (uint32_t)src.lsb : (uint32_t)(blk * 32);
+        lds_load16_d(su_a[k] ? desc_as : desc_bs, sblk + (blk & 1) * Cfg::SB_SLOT + su_g[k] * 1024, su_off[k] + adv);
     };
 
     // Operand buffers: the whole tile's rows, K positions in the lane offsets.
@@ -332,6 +340,14 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     // lane%32, so the swapped-half XOR below is a per-lane constant.
     const int sc_lo = (lane & 31) * 32 + khalf * 4, sc_x = (((lane & 31) >> 3) & 1) << 4;
     const int sk_lo = (lane & 31) * 4 + khalf * 2;
+    // BT scales: per n-tile the lane's row (j >> 1) and byte 8 (j & 1) of
+    // logical chunk (wave's first column)/16 + 2t + g of the block's B part; a
+    // transposed read returns the column's 8 scale bytes of a K-tile (rows
+    // 8 (kt % 4) + 0..7), of which lane half h takes bytes 4h .. 4h+3
+    const TBase<TN> bts = BT && FP4 ? tr_bases<TN>((uint32_t)(uintptr_t)sblk + (uint32_t)(BM * 32) -
+                                                        (uint32_t)(64 * khalf * KTileT::ROW),
+                                                    wn * TN * 32, lane)
+                                    : TBase<TN>{};
     auto read_scale = [&](int stage, int kt, Scales& s, int idx) {
         if constexpr (FP4) {
             const bool isa = idx < TM;
@@ -342,9 +358,16 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
                 // rows with bit 3 set are swapped, so the 32 lanes of a read (32
                 // consecutive rows, 32-byte pitch) hit 16 distinct bank pairs
                 const HKQ_LDS uint8_t* slot = sblk + ((kt / Cfg::SB_KT) & 1) * Cfg::SB_SLOT;
-                const int wave_row = isa ? wm * TM * 32 : BM + wn * TN * 32;
-                const int o = ((kt % Cfg::SB_KT) * 8) ^ sc_x;
-                w = *reinterpret_cast<const HKQ_LDS int*>(slot + wave_row * 32 + sc_lo + o + t * 1024);
+                if (BT && !isa) {
+                    const uint32_t b = bts.v[t] + (uint32_t)(((kt / Cfg::SB_KT) & 1) * Cfg::SB_SLOT) +
+                                       (uint32_t)((kt % Cfg::SB_KT) * 8 * KTileT::ROW);
+                    const v2i v = lds_read_tr8(reinterpret_cast<const HKQ_LDS uint8_t*>((uintptr_t)b));
+                    w = khalf ? v[1] : v[0];
+                } else {
+                    const int wave_row = isa ? wm * TM * 32 : BM + wn * TN * 32;
+                    const int o = ((kt % Cfg::SB_KT) * 8) ^ sc_x;
+                    w = *reinterpret_cast<const HKQ_LDS int*>(slot + wave_row * 32 + sc_lo + o + t * 1024);
+                }
             } else {
                 const HKQ_LDS uint8_t* sca = smem + Cfg::s_stage(NS, stage) + (isa ? 0 : SCA);
                 const int wave_row = isa ? wm * TM * 32 : wn * TN * 32;

@@ -825,8 +825,10 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
 struct MoeFp4Params {
     const uint8_t* A;       // [tokens, sam] bytes, K/2 used
     const uint8_t* As;      // [tokens, sas] e8m0, K/32 used
-    const uint8_t* B;       // expert e at B + e*sbe, row n at + n*sbn (K/2 bytes)
-    const uint8_t* Bs;      // expert e at Bs + e*sbse, row n at + n*sbsn (K/32 bytes)
+    const uint8_t* B;       // expert e at B + e*sbe, row n at + n*sbn (K/2 bytes); wt: row kk of
+                            // K/2 at + kk*sbn (N bytes)
+    const uint8_t* Bs;      // expert e at Bs + e*sbse, row n at + n*sbsn (K/32 bytes); wt: row of 32
+                            // values of K at + (k/32)*sbsn (N bytes)
     uint16_t* C;            // row id at C + id*scm
     const float* a_scale;   // nullptr: 1
     const float* b_scale;   // nullptr: 1
@@ -838,13 +840,14 @@ struct MoeFp4Params {
     int split;     // tiles of the last round cut into their two blocks (pair_unit)
     int xcd_cols;  // pair_walk's column order
     int64_t sam, sas, sbe, sbn, sbse, sbsn, scm;
+    int wt;  // B and Bs N-contiguous ([K/2, N] and [K/32, N] per expert)
 };
 
 constexpr uint32_t FP4_OOB = 0x7FFF0000u;  // a row offset past every operand's bounds
 
 // Rows [pm*128, pm*128 + TM*64) of the sorted routing (one block, or two
 // consecutive blocks of expert e) times columns [n0, n0 + 256), expert e >= 0.
-template <int TM, int KTB, int NS>
+template <int TM, int KTB, int NS, bool BT = false>
 __device__ __forceinline__ void moe_fp4_block(const MoeFp4Params& p, int pm, int e, int n0, HKQ_LDS uint8_t* smem) {
     constexpr int TN = MOE_TN;
     using Cfg = DenseCfg<MODE_MXFP4, MOE_WM, MOE_WN, TM, TN, KTB>;
@@ -870,12 +873,23 @@ __device__ __forceinline__ void moe_fp4_block(const MoeFp4Params& p, int pm, int
     LoopSrc src;
     src.a = p.A;
     src.a_bytes = min((int64_t)p.tokens * p.sam, (int64_t)FP4_OOB);
-    src.b = p.B + (int64_t)e * p.sbe + (int64_t)n0 * p.sbn;
-    src.b_bytes = min((int64_t)rows_b * p.sbn, (int64_t)FP4_OOB);
     src.as = p.As;
     src.as_bytes = min((int64_t)p.tokens * p.sas, (int64_t)FP4_OOB);
-    src.bs = p.Bs + (int64_t)e * p.sbse + (int64_t)n0 * p.sbsn;
-    src.bs_bytes = min((int64_t)rows_b * p.sbsn, (int64_t)FP4_OOB);
+    if constexpr (BT) {
+        // N-contiguous weights and scales: the tile's columns of every row
+        // (columns past N read the next row's bytes, which only reach output
+        // columns that are never stored)
+        src.b = p.B + (int64_t)e * p.sbe + n0;
+        src.b_bytes = min((int64_t)(p.K / 2 - 1) * p.sbn + rows_b, (int64_t)FP4_OOB);
+        src.b_kstep = (int64_t)KTB * p.sbn;
+        src.bs = p.Bs + (int64_t)e * p.sbse + n0;
+        src.bs_bytes = min((int64_t)(p.K / 32 - 1) * p.sbsn + rows_b, (int64_t)FP4_OOB);
+    } else {
+        src.b = p.B + (int64_t)e * p.sbe + (int64_t)n0 * p.sbn;
+        src.b_bytes = min((int64_t)rows_b * p.sbn, (int64_t)FP4_OOB);
+        src.bs = p.Bs + (int64_t)e * p.sbse + (int64_t)n0 * p.sbsn;
+        src.bs_bytes = min((int64_t)rows_b * p.sbsn, (int64_t)FP4_OOB);
+    }
     src.lsa = p.sas;
     src.lsb = p.sbsn;
     src.KT = (p.K / 2) / KTB;
@@ -902,7 +916,9 @@ __device__ __forceinline__ void moe_fp4_block(const MoeFp4Params& p, int pm, int
         const int t = arow_of(r);
         a_off.v[i] = t < 0 ? FP4_OOB : (uint32_t)(t * p.sam) + (uint32_t)(Cfg::KT::load_chunk(lane, r) << 4);
     }
-    const auto b_off = dense_offs<NW, KTB, LB>(wave, lane, p.sbn);
+    TableOff<LB> b_off;
+    if constexpr (BT) b_off = dense_offs_t<NW, LB>(wave, lane, p.sbn);
+    else b_off = dense_offs<NW, KTB, LB>(wave, lane, p.sbn);
 
     // the epilogue's row scales (routed weights), fetched before the K loop
     const float gs = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
@@ -914,7 +930,7 @@ __device__ __forceinline__ void moe_fp4_block(const MoeFp4Params& p, int pm, int
     }
 
     v16f acc[TN][TM];
-    gemm_mainloop<MODE_MXFP4, MOE_WM, MOE_WN, TM, TN, KTB, NS>(src, a_off, b_off, smem, lane, wave, acc);
+    gemm_mainloop<MODE_MXFP4, MOE_WM, MOE_WN, TM, TN, KTB, NS, BT>(src, a_off, b_off, smem, lane, wave, acc);
 
     store_tile_bf16_rows<TM, TN>(
         acc, smem, wave, lane, p.C, p.scm, p.N, nw, p.c16 != 0,
@@ -940,7 +956,7 @@ __device__ __forceinline__ void moe_fp4_zero_block(const MoeFp4Params& p, int pm
 // expert form one 256-row tile, otherwise each block is its own 128-row tile
 // (64 rows when its upper half is padding; with expert -1, zeros). Tile
 // order: pair_walk, one pair at a time.
-template <int KTB, int NS>
+template <int KTB, int NS, bool BT = false>
 __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_mxfp4_kernel(const MoeFp4Params p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem_raw[];
     HKQ_LDS uint8_t* smem = (HKQ_LDS uint8_t*)smem_raw;
@@ -950,7 +966,7 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_mxfp4_kernel(cons
     const int pm0 = 2 * q, pm1 = 2 * q + 1;
     const int e0 = p.expert[pm0], e1 = pm1 < p.grid_m ? p.expert[pm1] : -2;
     if (half < 0 && e0 >= 0 && e0 < p.E && e1 == e0) {
-        moe_fp4_block<4, KTB, NS>(p, pm0, e0, n0, smem);
+        moe_fp4_block<4, KTB, NS, BT>(p, pm0, e0, n0, smem);
         return;
     }
     // the pair's blocks one at a time (both, or the one this unit was given);
@@ -969,9 +985,9 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_mxfp4_kernel(cons
             // tile (every wave reads the same 64 entries: a uniform choice)
             const int id = p.sorted[(int64_t)pm * MOE_BM + MOE_BM / 2 + (threadIdx.x & 63)];
             if (__ballot(id >= 0 && id < p.num_valid) == 0)
-                moe_fp4_block<1, KTB, NS>(p, pm, e, n0, smem);
+                moe_fp4_block<1, KTB, NS, BT>(p, pm, e, n0, smem);
             else
-                moe_fp4_block<2, KTB, NS>(p, pm, e, n0, smem);
+                moe_fp4_block<2, KTB, NS, BT>(p, pm, e, n0, smem);
         }
     }
 }
@@ -1108,15 +1124,18 @@ static int launch_moe_fp4(MoeFp4Params& p, hipStream_t stream) {
     using Half = DenseCfg<MODE_MXFP4, MOE_WM, MOE_WN, 2, MOE_TN, KTB>;
     constexpr int LDS = Whole::lds_bytes(NS) > Half::lds_bytes(NS) ? Whole::lds_bytes(NS) : Half::lds_bytes(NS);
     static_assert(LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
+    // N-contiguous weights (wt) need 128-byte K-tiles (the entry point checks)
     auto kern = moe_mxfp4_kernel<KTB, NS>;
-    static bool attr_set = false;
-    if (!attr_set) {
+    if constexpr (KTB == 128)
+        if (p.wt) kern = moe_mxfp4_kernel<KTB, NS, true>;
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[p.wt]) {
         hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
         if (err != hipSuccess) {
             set_error("hipFuncSetAttribute(MaxDynamicSharedMemorySize=%d) failed: %s", LDS, hipGetErrorString(err));
             return (int)err;
         }
-        attr_set = true;
+        attr_set[p.wt] = true;
     }
     p.tiles_n = (p.N + MOE_BN - 1) / MOE_BN;
     if (p.group_m <= 0) p.group_m = 1;
@@ -1227,13 +1246,16 @@ extern "C" int hkq_moe_a8w8_kn(const void* X, const void* W, void* Y, const floa
                          stride_wk, 1, stride_ym, y_rows, gather_len, stream);
 }
 
-extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* A_mx_scale, const void* B_mx_scale,
-                             const float* A_scale, const float* B_scale, const float* topk_weights,
-                             const int32_t* sorted_token_ids, const int32_t* expert_ids, int64_t N, int64_t K,
-                             int64_t num_valid_tokens, int64_t top_k, int mul_routed_weight, int64_t stride_am,
-                             int64_t stride_be, int64_t stride_bn, int64_t stride_cm, int64_t stride_amxm,
-                             int64_t stride_bmxe, int64_t stride_bmxn, int64_t num_tokens, int64_t num_experts,
-                             int64_t grid_m, hipStream_t stream) {
+// wt == 0: B[e] [N, K/2] (row stride stride_b) and B_mx_scale[e] [N, K/32]
+// (row stride stride_bmx), K contiguous; wt == 1: B[e] [K/2, N] and
+// B_mx_scale[e] [K/32, N], N contiguous (the reference's layout).
+static int moe_mxfp4_impl(const void* A, const void* B, void* C, const void* A_mx_scale, const void* B_mx_scale,
+                          const float* A_scale, const float* B_scale, const float* topk_weights,
+                          const int32_t* sorted_token_ids, const int32_t* expert_ids, int64_t N, int64_t K,
+                          int64_t num_valid_tokens, int64_t top_k, int mul_routed_weight, int64_t stride_am,
+                          int64_t stride_be, int64_t stride_bn, int64_t stride_cm, int64_t stride_amxm,
+                          int64_t stride_bmxe, int64_t stride_bmxn, int64_t num_tokens, int64_t num_experts,
+                          int64_t grid_m, int wt, hipStream_t stream) {
     HKQ_CHECK_ARG(N >= 0 && K > 0 && num_valid_tokens >= 0 && top_k > 0 && top_k <= 0xFFFF && num_tokens >= 0 &&
                       num_experts > 0 && grid_m >= 0,
                   "N, num_valid_tokens, num_tokens, grid_m >= 0; K, num_experts > 0; 0 < top_k <= 65535");
@@ -1243,10 +1265,22 @@ extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* 
     HKQ_CHECK_ARG(K % 128 == 0, "K must be a multiple of 128 (64 bytes of E2M1 pairs)");
     HKQ_CHECK_ARG(N % 4 == 0, "N must be a multiple of 4");
     HKQ_CHECK_ARG(stride_am >= K / 2 && stride_am % 16 == 0, "stride_am must be >= K/2 bytes and a multiple of 16");
-    HKQ_CHECK_ARG(stride_bn >= K / 2 && stride_bn % 16 == 0,
-                  "stride_bn must be >= K/2 bytes and a multiple of 16 (B[e] is [N, K/2], K contiguous)");
+    if (wt) {
+        HKQ_CHECK_ARG(K % 256 == 0, "N-contiguous weights need K to be a multiple of 256");
+        HKQ_CHECK_ARG(stride_bn >= N && stride_bn % 16 == 0,
+                      "stride_bk must be >= N and a multiple of 16 (B[e] is [K/2, N], N contiguous)");
+        HKQ_CHECK_ARG(stride_bmxn >= N && stride_bmxn % 16 == 0,
+                      "stride_bmxk must be >= N and a multiple of 16 (B_mx_scale[e] is [K/32, N])");
+        HKQ_CHECK_ARG((K / 2) * stride_bn < (int64_t)FP4_OOB && (K / 32) * stride_bmxn < (int64_t)FP4_OOB,
+                      "one expert's weights and scales must span less than 2^31 - 2^16 bytes");
+        HKQ_CHECK_ARG(stride_bmxe % 16 == 0 && reinterpret_cast<uintptr_t>(B_mx_scale) % 16 == 0,
+                      "N-contiguous weight scales: B_mx_scale 16-byte aligned, stride_bmxe a multiple of 16");
+    } else {
+        HKQ_CHECK_ARG(stride_bn >= K / 2 && stride_bn % 16 == 0,
+                      "stride_bn must be >= K/2 bytes and a multiple of 16 (B[e] is [N, K/2], K contiguous)");
+    }
     HKQ_CHECK_ARG(stride_be >= 0 && stride_be % 16 == 0, "stride_be must be a non-negative multiple of 16");
-    HKQ_CHECK_ARG(stride_amxm >= K / 32 && stride_bmxn >= K / 32 && stride_bmxe >= 0,
+    HKQ_CHECK_ARG(stride_amxm >= K / 32 && (wt || stride_bmxn >= K / 32) && stride_bmxe >= 0,
                   "scale strides must cover K/32 bytes per row (scales [rows, K/32], K contiguous)");
     HKQ_CHECK_ARG((K / 2) % 128 == 0 || (stride_amxm % 4 == 0 && stride_bmxn % 4 == 0),
                   "with K % 256 != 0 the scale row strides must be multiples of 4");
@@ -1276,6 +1310,7 @@ extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* 
     p.num_valid = (int)num_valid_tokens; p.grid_m = (int)grid_m;
     p.sam = stride_am; p.sas = stride_amxm; p.sbe = stride_be; p.sbn = stride_bn; p.sbse = stride_bmxe;
     p.sbsn = stride_bmxn; p.scm = stride_cm;
+    p.wt = wt;
     p.c16 = (stride_cm % 8 == 0) && (reinterpret_cast<uintptr_t>(C) % 16 == 0);
     // The streaming path when the tiled grid would give fewer than a quarter
     // of the CUs work and there are at most 32 valid gate ids (measured: one
@@ -1284,10 +1319,35 @@ extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* 
     // weight rows must span less than 2 GiB.
     const int64_t ncu = cu_count() > 0 ? cu_count() : 256;
     const bool few_tiles = ((grid_m + 1) / 2) * ((N + MOE_BN - 1) / MOE_BN) * 4 < ncu;
-    if (few_tiles && num_valid_tokens <= MOE_FP4_NARROW_MAX_VALID && stride_amxm % 4 == 0 && stride_bmxn % 4 == 0 &&
+    if (!wt && few_tiles && num_valid_tokens <= MOE_FP4_NARROW_MAX_VALID && stride_amxm % 4 == 0 && stride_bmxn % 4 == 0 &&
         stride_bmxe % 4 == 0 && reinterpret_cast<uintptr_t>(A_mx_scale) % 4 == 0 &&
         reinterpret_cast<uintptr_t>(B_mx_scale) % 4 == 0 && 64 * stride_bn < (1ll << 31) && 64 * stride_bmxn < (1ll << 31))
         return launch_moe_fp4_narrow(p, stream);
     // 128-byte K-tiles when rows have whole ones (K % 256 == 0), else 64-byte ones
     return (K / 2) % 128 == 0 ? launch_moe_fp4<128, 2>(p, stream) : launch_moe_fp4<64, 4>(p, stream);
+}
+
+extern "C" int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* A_mx_scale, const void* B_mx_scale,
+                             const float* A_scale, const float* B_scale, const float* topk_weights,
+                             const int32_t* sorted_token_ids, const int32_t* expert_ids, int64_t N, int64_t K,
+                             int64_t num_valid_tokens, int64_t top_k, int mul_routed_weight, int64_t stride_am,
+                             int64_t stride_be, int64_t stride_bn, int64_t stride_cm, int64_t stride_amxm,
+                             int64_t stride_bmxe, int64_t stride_bmxn, int64_t num_tokens, int64_t num_experts,
+                             int64_t grid_m, hipStream_t stream) {
+    return moe_mxfp4_impl(A, B, C, A_mx_scale, B_mx_scale, A_scale, B_scale, topk_weights, sorted_token_ids,
+                          expert_ids, N, K, num_valid_tokens, top_k, mul_routed_weight, stride_am, stride_be, stride_bn,
+                          stride_cm, stride_amxm, stride_bmxe, stride_bmxn, num_tokens, num_experts, grid_m, 0, stream);
+}
+
+extern "C" int hkq_moe_mxfp4_kn(const void* A, const void* B, void* C, const void* A_mx_scale,
+                                const void* B_mx_scale, const float* A_scale, const float* B_scale,
+                                const float* topk_weights, const int32_t* sorted_token_ids,
+                                const int32_t* expert_ids, int64_t N, int64_t K, int64_t num_valid_tokens,
+                                int64_t top_k, int mul_routed_weight, int64_t stride_am, int64_t stride_be,
+                                int64_t stride_bk, int64_t stride_cm, int64_t stride_amxm, int64_t stride_bmxe,
+                                int64_t stride_bmxk, int64_t num_tokens, int64_t num_experts, int64_t grid_m,
+                                hipStream_t stream) {
+    return moe_mxfp4_impl(A, B, C, A_mx_scale, B_mx_scale, A_scale, B_scale, topk_weights, sorted_token_ids,
+                          expert_ids, N, K, num_valid_tokens, top_k, mul_routed_weight, stride_am, stride_be, stride_bk,
+                          stride_cm, stride_amxm, stride_bmxe, stride_bmxk, num_tokens, num_experts, grid_m, 1, stream);
 }

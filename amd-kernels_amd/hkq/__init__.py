@@ -52,6 +52,7 @@ SIGNATURES = {
     "hkq_rmsnorm_quant": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _P]),
     "hkq_swiglu_quant": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, ctypes.c_float, _I, _I, _P]),
     "hkq_moe_mxfp4": (_I, [_P] * 10 + [_I64, _I64, _I64, _I64, _I] + [_I64] * 10 + [_P]),
+    "hkq_moe_mxfp4_kn": (_I, [_P] * 10 + [_I64, _I64, _I64, _I64, _I] + [_I64] * 10 + [_P]),
     "hkq_moe_topk": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I, _I, _P]),
     "hkq_sum_bitmatrix_rows": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "hkq_sum_bitmatrix_rows_fused": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P]),
@@ -403,22 +404,24 @@ def moe_pack_kmajor(W, out=None, stream=None):
 
 
 def moe_mxfp4(A, As, B, Bs, sorted_ids, expert_ids, num_valid: int, topk: int, a_scale=None, b_scale=None,
-              topk_weights=None, C=None, c_rows=None, stream=None):
+              topk_weights=None, C=None, c_rows=None, stream=None, b_kn=False):
     """MXFP4 MoE over block-sorted routing (align_block_size output, 128-row
     blocks). A uint8 [T, K/2], As uint8 [T, K/32], B uint8 [E, N, K/2], Bs uint8
-    [E, N, K/32] (K contiguous); topk_weights (fp32, indexed by gate id) turns on
-    the routed-weight multiply. Returns C bf16 [c_rows (default num_valid), N]
-    with row = gate id."""
+    [E, N, K/32] (K contiguous), or with b_kn the reference's B [E, K/2, N] and
+    Bs [E, K/32, N] (N contiguous, read in place); topk_weights (fp32, indexed by
+    gate id) turns on the routed-weight multiply. Returns C bf16
+    [c_rows (default num_valid), N] with row = gate id."""
     import torch
 
     T, Kh = A.shape
-    E, N = B.shape[0], B.shape[1]
+    E, N = (B.shape[0], B.shape[2]) if b_kn else (B.shape[0], B.shape[1])
     K = 2 * Kh
     rows = num_valid if c_rows is None else c_rows
     if C is None:
         C = torch.zeros((rows, N), dtype=torch.bfloat16, device=A.device)
     grid_m = sorted_ids.numel() // 128
-    call("hkq_moe_mxfp4", _ptr(A), _ptr(B), _ptr(C), _ptr(As), _ptr(Bs), _opt_ptr(a_scale), _opt_ptr(b_scale),
+    call("hkq_moe_mxfp4_kn" if b_kn else "hkq_moe_mxfp4", _ptr(A), _ptr(B), _ptr(C), _ptr(As), _ptr(Bs),
+         _opt_ptr(a_scale), _opt_ptr(b_scale),
          _opt_ptr(topk_weights), _ptr(sorted_ids), _ptr(expert_ids), N, K, num_valid, topk,
          int(topk_weights is not None), A.stride(0), B.stride(0), B.stride(1), C.stride(0), As.stride(0),
          Bs.stride(0), Bs.stride(1), T, E, grid_m, _stream(stream))

@@ -362,7 +362,20 @@ def main():
             ms_4 = time_launches(launch, steps, warmup)
             moe_res.append({"proj": f"mxfp4 {name}", "N": nn, "K": kk, "ms": round(ms_4, 5),
                             "tflops": round(2.0 * T * topk * nn * kk / (ms_4 * 1e-3) / 1e12, 2)})
-            del wq4, ws4, C4
+            # the reference's N-contiguous B [E, K/2, N] and scales [E, K/32, N], read in place
+            wq4_kn = wq4.transpose(1, 2).contiguous()
+            ws4_kn = ws4.transpose(1, 2).contiguous()
+            del wq4, ws4
+            launch = hkq.bind("hkq_moe_mxfp4_kn", xa4.data_ptr(), wq4_kn.data_ptr(), C4.data_ptr(), xs4.data_ptr(),
+                              ws4_kn.data_ptr(), None, None, None,
+                              sids.data_ptr(), eids.data_ptr(), nn, kk, T * topk, topk, 0, xa4.stride(0),
+                              wq4_kn.stride(0), wq4_kn.stride(1), C4.stride(0), xs4.stride(0), ws4_kn.stride(0),
+                              ws4_kn.stride(1), T, E, total // 128, torch.cuda.current_stream().cuda_stream)
+            log(f"moe mxfp4 {name} [E,K/2,N] N={nn} K={kk}")
+            ms_4 = time_launches(launch, steps, warmup)
+            moe_res.append({"proj": f"mxfp4 {name} [E,K/2,N]", "N": nn, "K": kk, "ms": round(ms_4, 5),
+                            "tflops": round(2.0 * T * topk * nn * kk / (ms_4 * 1e-3) / 1e12, 2)})
+            del wq4_kn, ws4_kn, C4
         res["moe"] = layer_ms
         for (Tr, Er, Kr) in ROUTING_EXTRA:
             lg = seeded_bf16((Tr, Er), 1.0, 30)

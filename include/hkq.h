@@ -321,15 +321,34 @@ int hkq_moe_pack_kmajor(const void* src, void* dst, int64_t E, int64_t R, int64_
  * stride_amxm] and B_mx_scale[e] [N, stride_bmxn] hold e8m0 bytes per 32 K
  * values; expert e at B + e*stride_be, B_mx_scale + e*stride_bmxe; C bf16 rows
  * of stride_cm. K % 128 == 0, N % 4 == 0. Replaces moe_op_mxfp4_tk.moe_mxfp4
- * (kernels/moe-gemm/moe_op_mxfp4/kernel.cpp:263-330), whose weights are
- * [E, K/2, N] (N contiguous): hkq_moe_pack_kmajor transposes them (and their
- * [E, K/32, N] scales). */
+ * (kernels/moe-gemm/moe_op_mxfp4/kernel.cpp:263-330) with K-contiguous
+ * weights; the reference's own [E, K/2, N] weights and [E, K/32, N] scales go
+ * to hkq_moe_mxfp4_kn. */
 int hkq_moe_mxfp4(const void* A, const void* B, void* C, const void* A_mx_scale, const void* B_mx_scale,
                   const float* A_scale, const float* B_scale, const float* topk_weights,
                   const int32_t* sorted_token_ids, const int32_t* expert_ids, int64_t N, int64_t K,
                   int64_t num_valid_tokens, int64_t top_k, int mul_routed_weight, int64_t stride_am,
                   int64_t stride_be, int64_t stride_bn, int64_t stride_cm, int64_t stride_amxm, int64_t stride_bmxe,
                   int64_t stride_bmxn, int64_t num_tokens, int64_t num_experts, int64_t grid_m, hkq_stream_t stream);
+
+/* hkq_moe_mxfp4 on the reference's N-contiguous weights: B[e] [K/2, N] (E2M1
+ * pairs of K for each column, row stride stride_bk) and B_mx_scale[e] [K/32, N]
+ * (row stride stride_bmxk), read in place by the kernels (K-tiles staged as
+ * rows of K, operands and e8m0 scale operands built with transposed LDS
+ * reads); every output element is the one hkq_moe_mxfp4 gives for the same
+ * values in [E, N, K/2] / [E, N, K/32], bit for bit. K % 256 == 0; stride_bk,
+ * stride_bmxk >= N; stride_bk, stride_bmxk, stride_be, stride_bmxe multiples
+ * of 16 and B_mx_scale 16-byte aligned. Decode-sized launches run the tiled
+ * kernel. Replaces moe_op_mxfp4_tk.moe_mxfp4 with stride_bn == stride_bmxn == 1,
+ * the reference's own call (kernels/moe-gemm/moe_op_mxfp4/kernel.cpp:155, the
+ * weight read through stride_bk / stride_bn; tests/test_moe.py:909-925). */
+int hkq_moe_mxfp4_kn(const void* A, const void* B, void* C, const void* A_mx_scale, const void* B_mx_scale,
+                     const float* A_scale, const float* B_scale, const float* topk_weights,
+                     const int32_t* sorted_token_ids, const int32_t* expert_ids, int64_t N, int64_t K,
+                     int64_t num_valid_tokens, int64_t top_k, int mul_routed_weight, int64_t stride_am,
+                     int64_t stride_be, int64_t stride_bk, int64_t stride_cm, int64_t stride_amxm,
+                     int64_t stride_bmxe, int64_t stride_bmxk, int64_t num_tokens, int64_t num_experts,
+                     int64_t grid_m, hkq_stream_t stream);
 
 /* ---- MoE routing metadata producers --------------------------------------- */
 /* All index outputs are deterministic: gates of one expert keep their input

@@ -159,6 +159,39 @@ def test_moe_mxfp4_module_reference_call(orc):
     assert torch.equal(C, C2)
 
 
+# The reference's N-contiguous B [E, K/2, N] and B_mx_scale [E, K/32, N] read
+# in place (hkq_moe_mxfp4_kn: K-tiles of E2M1 pairs staged as rows of K, the
+# operands and the e8m0 scale operands built with transposed LDS reads): the
+# same bits as the K-contiguous layout. Whole 256-row tiles, lone and 64-row
+# blocks, the last round split in blocks, decode-sized routing (the tiled
+# kernel), N not a multiple of 256 or 16, rows of K padded past N.
+@pytest.mark.parametrize("T,E,topk,K,N,pad", [(600, 4, 2, 512, 512, 0), (300, 3, 2, 1024, 1000, 24),
+                                              (4, 8, 2, 512, 256, 0), (2000, 8, 2, 256, 4104, 8)])
+def test_moe_mxfp4_kn_matches_kmajor(orc, T, E, topk, K, N, pad):
+    require_gpu()
+    ids, s, eids = routed(orc, T, E, topk, 71)
+    rng = np.random.default_rng(72)
+    Aq = rng.integers(0, 256, (T, K // 2), dtype=np.uint8)
+    As = rng.integers(120, 134, (T, K // 32), dtype=np.uint8)
+    Bq = rng.integers(0, 256, (E, N, K // 2), dtype=np.uint8)
+    Bs = rng.integers(120, 134, (E, N, K // 32), dtype=np.uint8)
+    Bkn = np.zeros((E, K // 2, N + pad), np.uint8)
+    Bkn[:, :, :N] = Bq.transpose(0, 2, 1)
+    Bskn = np.zeros((E, K // 32, N + pad), np.uint8)
+    Bskn[:, :, :N] = Bs.transpose(0, 2, 1)
+    w = rng.random(len(s)).astype(np.float32)
+    args = (dev_i32(s), dev_i32(eids), T * topk, topk)
+    C = hkq.moe_mxfp4(dev_u8(Aq), dev_u8(As), dev_u8(Bq), dev_u8(Bs), *args, topk_weights=dev_f32(w))
+    Ckn = hkq.moe_mxfp4(dev_u8(Aq), dev_u8(As), dev_u8(Bkn)[:, :, :N], dev_u8(Bskn)[:, :, :N], *args,
+                        topk_weights=dev_f32(w), b_kn=True)
+    torch.cuda.synchronize()
+    assert torch.equal(C, Ckn), "N-contiguous weights give other bits than K-contiguous ones"
+    ref = orc.moe_mxfp4_ref(Aq, As, Bq, Bs, None, None, w, s, eids, N, T * topk, topk, True, T * topk)
+    got = Ckn.float().cpu().numpy()
+    rows = ~np.isnan(ref).any(axis=1)
+    assert_gemm_close(got[rows], ref[rows], "moe mxfp4 [E, K/2, N]")
+
+
 def test_moe_pack_kmajor(orc):
     """The prepack entry point on ragged shapes and padded strides: an exact
     byte transpose of every expert plane, bytes outside the destination rows
@@ -206,3 +239,40 @@ def test_moe_mxfp4_mixtral_full(orc, K, N):
     ref = orc.moe_mxfp4_ref_f32(Aq, As, Bq, Bs, None, None, w, s, eids, N, T * topk, topk, True, T * topk)
     assert not np.isnan(ref).any()
     assert_gemm_close(C.float().cpu().numpy(), ref, f"moe mxfp4 mixtral K={K} N={N}")
+
+
+@pytest.mark.parametrize("K,N", [(4096, 28672), (14336, 4096)])
+def test_moe_mxfp4_mixtral_reference_layout_module(orc, K, N):
+    """Mixtral sizes through moe_op_mxfp4_tk with the reference's own layouts,
+    B [E, K/2, N] and B_mx_scale [E, K/32, N] (stride_bn = stride_bmxn = 1,
+    tests/test_moe.py:909-925), read in place by the kernels; every output row
+    against the fp32 oracle."""
+    require_gpu()
+    import hipkittens as hk
+
+    T, E, topk = 4096, 8, 2
+    gl = torch.Generator(device="cpu").manual_seed(K + 5)
+    logits = torch.randn(T, E, generator=gl)
+    ids = torch.topk(torch.softmax(logits, -1), topk, dim=-1).indices.numpy().astype(np.int32).ravel()
+    s, eids, _, _ = orc.align_block_size(ids, E, 128)
+    Aq, As = orc.mx_quant_fp4(orc.randn_bf16((T, K), seed=K + 6))
+    g = torch.Generator(device="cuda").manual_seed(K + 7)
+    wb = (torch.randn(E * N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    Bq_d, Bs_d = hkq.mx_quant(wb, True)
+    del wb
+    Bkn = Bq_d.view(E, N, K // 2).transpose(1, 2).contiguous()
+    Bskn = Bs_d.view(E, N, K // 32).transpose(1, 2).contiguous()
+    torch.cuda.synchronize()
+    Bq = Bq_d.cpu().numpy().reshape(E, N, K // 2)
+    Bs = Bs_d.cpu().numpy().reshape(E, N, K // 32)
+    del Bq_d, Bs_d
+    C = torch.zeros(len(s), N, dtype=torch.bfloat16, device="cuda")
+    hk.moe.mxfp4.moe_mxfp4(dev_u8(Aq), Bkn, C, dev_u8(As), Bskn, None, None, None, dev_i32(s), dev_i32(eids), N, K,
+                           T * topk, topk, False, K // 2, 1, (K // 2) * N, N, 1, N, 1, K // 32, 1, (K // 32) * N, N, 1,
+                           len(s) // 128, (N + 127) // 128)
+    torch.cuda.synchronize()
+    ref = orc.moe_mxfp4_ref_f32(Aq, As, Bq, Bs, None, None, None, s, eids, N, T * topk, topk, False, len(s))
+    got = C.float().cpu().numpy()
+    rows = ~np.isnan(ref).any(axis=1)
+    assert rows.sum() == T * topk
+    assert_gemm_close(got[rows], ref[rows], f"moe mxfp4 mixtral [E, K/2, N] module K={K} N={N}")
