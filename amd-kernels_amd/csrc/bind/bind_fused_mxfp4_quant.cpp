@@ -2,7 +2,9 @@
 // fused_rmsnorm_mxfp4_quant_fwd(input, weight, output, scales, eps). input bf16
 // [M, D]; weight bf16 [D]; output uint8 [M, D/2] (two E2M1 codes per byte,
 // even column in the low nibble); scales uint8 e8m0 [M, D/32]. D any multiple
-// of 32 up to 8192 (the reference: 4096 or 8192).
+// of 32 up to 8192 (the reference: 4096 or 8192). Elements take the
+// reference's threshold ladder (kernel.cpp:128-150: the largest E2M1 magnitude
+// at or below |y| * 2^-e), so codes and scales equal the reference module's.
 #include "bind_common.h"
 
 using namespace hkqbind;
@@ -22,7 +24,7 @@ void fused_rmsnorm_mxfp4_quant_fwd(py::object input, py::object weight, py::obje
     expect(s.shape.size() == 2 && s.dim(0) == M && s.dim(1) == D / 32, "scales must be [M, D/32]");
     const int64_t lds = row_stride(s, "scales");
     check(hkq_rmsnorm_quant((const void*)x.ptr, (const void*)w.ptr, (void*)q.ptr, (void*)s.ptr, M, D, ldx, ldq, lds,
-                            eps, 1, current_stream()),
+                            eps, 2, current_stream()),
           "fused_rmsnorm_mxfp4_quant_fwd");
 }
 

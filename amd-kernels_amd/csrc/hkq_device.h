@@ -79,6 +79,22 @@ __device__ __forceinline__ uint32_t e2m1_encode8(const float* v) {
     return w;
 }
 
+// E2M1 codes of 8 values (value j in nibble j) by the threshold ladder of the
+// reference's fused MXFP4 quantizer (quantization/fused_mxfp4_quant/
+// kernel.cpp:128-150): the largest grid magnitude at or below |v| (6 from 6 up,
+// 0 below 0.5; NaN fails every comparison: 0), the sign bit of v kept.
+__device__ __forceinline__ uint32_t e2m1_floor8(const float* v) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float a = __builtin_fabsf(v[j]);
+        const uint32_t m = (uint32_t)(a >= 0.5f) + (uint32_t)(a >= 1.0f) + (uint32_t)(a >= 1.5f) +
+                           (uint32_t)(a >= 2.0f) + (uint32_t)(a >= 3.0f) + (uint32_t)(a >= 4.0f) + (uint32_t)(a >= 6.0f);
+        w |= (m | ((__float_as_uint(v[j]) >> 28) & 8u)) << (4 * j);
+    }
+    return w;
+}
+
 // Unbiased shared exponent of the MXFP4 scale rule: P = (bits(amax) + 0x200000)
 // & 0xFF800000 (amax rounded up at the E2M1 mantissa), e = exponent(P) - 2,
 // clamped to [-127, 127]; amax = 0 gives -127 (code 0), amax -> inf gives 127.

@@ -18,7 +18,9 @@
 
 namespace hkq {
 
-enum { NQ_FP8_G128 = 0, NQ_MXFP4 = 1 };
+// MXFP4 elements rounded to nearest even (NQ_MXFP4) or floored by the
+// reference module's ladder (NQ_MXFP4_FLOOR); the shared exponent is the same
+enum { NQ_FP8_G128 = 0, NQ_MXFP4 = 1, NQ_MXFP4_FLOOR = 2 };
 
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
             float t[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) t[j] = y[j] * mul;
-            const uint32_t packed = e2m1_encode8(t);
+            const uint32_t packed = MODE == NQ_MXFP4_FLOOR ? e2m1_floor8(t) : e2m1_encode8(t);
             if (c < nch) {
                 *reinterpret_cast<uint32_t*>(q + (int64_t)row * ldq + (int64_t)c * 4) = packed;
                 if ((lane & 3) == 0) reinterpret_cast<uint8_t*>(s)[(int64_t)row * lds + (c >> 2)] = (uint8_t)(e + 127);
@@ -250,7 +252,7 @@ int swiglu_nc(const uint16_t* y, uint8_t* q, float* s, int M, int F, int64_t ldy
 
 extern "C" int hkq_rmsnorm_quant(const void* x, const void* w, void* q, void* s, int64_t M, int64_t D, int64_t ldx,
                                  int64_t ldq, int64_t lds, float eps, int kind, hkq_stream_t stream) {
-    HKQ_CHECK_ARG(kind == 0 || kind == 1, "kind must be 0 (FP8 1x128) or 1 (MXFP4)");
+    HKQ_CHECK_ARG(kind >= 0 && kind <= 2, "kind must be 0 (FP8 1x128), 1 (MXFP4, nearest) or 2 (MXFP4, floor)");
     HKQ_CHECK_ARG(M >= 0 && M <= INT32_MAX, "M must be in [0, 2^31)");
     HKQ_CHECK_ARG(D >= 128 && D <= 8192 && D % (kind == 0 ? 128 : 32) == 0,
                   "D must be a multiple of 128 (FP8) or 32 (MXFP4) in [128, 8192]");
@@ -269,6 +271,9 @@ extern "C" int hkq_rmsnorm_quant(const void* x, const void* w, void* q, void* s,
     if (kind == 0)
         return rmsnorm_nc<NQ_FP8_G128>((const uint16_t*)x, (const uint16_t*)w, (uint8_t*)q, s, (int)M, (int)D, ldx,
                                       ldq, lds, eps, st);
+    if (kind == 2)
+        return rmsnorm_nc<NQ_MXFP4_FLOOR>((const uint16_t*)x, (const uint16_t*)w, (uint8_t*)q, s, (int)M, (int)D, ldx,
+                                          ldq, lds, eps, st);
     return rmsnorm_nc<NQ_MXFP4>((const uint16_t*)x, (const uint16_t*)w, (uint8_t*)q, s, (int)M, (int)D, ldx, ldq,
                                 lds, eps, st);
 }

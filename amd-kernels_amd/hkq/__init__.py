@@ -189,7 +189,9 @@ def mx_dequant(q, s, K: int, is_fp4: bool = True, stream=None):
 def rmsnorm_quant(x, w, eps: float = 1e-6, kind: int = 0, q=None, s=None, stream=None):
     """RMSNorm + quantization of bf16 [M, D] with weight bf16 [D]. kind 0: 1x128
     FP8 -> (q float8_e4m3fn [M, D], s fp32 [M, D/128]); kind 1: MXFP4 ->
-    (q uint8 [M, D/2], s uint8 e8m0 [M, D/32])."""
+    (q uint8 [M, D/2], s uint8 e8m0 [M, D/32]), elements rounded to nearest
+    even; kind 2: MXFP4 with elements floored by the threshold ladder of
+    kernels/quantization/fused_mxfp4_quant/kernel.cpp:128-150."""
     import torch
 
     M, D = x.shape

@@ -85,7 +85,11 @@ int hkq_mx_dequant(const void* q, const void* s, void* out, int64_t M, int64_t K
  * kind 0: 1x128 FP8, s[m, g] = max(amax/448, 1e-10) fp32 [M, lds],
  *         q = E4M3FN(clamp(y / s)) [M, ldq] (D % 128 == 0);
  * kind 1: MXFP4, s = e8m0 of the MX shared exponent [M, lds] bytes, q = two
- *         E2M1 codes per byte [M, ldq] (D % 32 == 0).
+ *         E2M1 codes per byte [M, ldq] (D % 32 == 0), elements rounded to
+ *         nearest even (the OCP MX rule, as hkq_mx_quant);
+ * kind 2: as kind 1 with elements floored by the threshold ladder of
+ *         fused_mxfp4_quant/kernel.cpp:128-150 (largest E2M1 magnitude at or
+ *         below |y| * 2^-e, sign kept), the reference module's codes.
  * Replaces fused_rmsnorm_fp8_quant_fwd (kernels/quantization/fused_fp8_quant/
  * kernel.cpp:251-268) and fused_rmsnorm_mxfp4_quant_fwd (fused_mxfp4_quant/
  * kernel.cpp:291-308), which accept only D in {4096, 8192} and write an affine

@@ -85,6 +85,26 @@ uint8_t orc_e2m1_encode(float q) {
     return (uint8_t)(sign | m);
 }
 
+/* E2M1 encode by the threshold ladder of the reference's fused MXFP4
+ * quantizer (quantization/fused_mxfp4_quant/kernel.cpp:128-150): the largest
+ * grid magnitude at or below |q| (6 from 6 up, 0 below 0.5), sign bit of q
+ * added (so -0 and a NaN with the sign bit set give 0x8); NaN fails every
+ * comparison: magnitude code 0. */
+uint8_t orc_e2m1_floor(float q) {
+    const uint8_t sign = (uint8_t)((f2bits(q) >> 31) << 3);
+    const float a = fabsf(q);
+    uint8_t m;
+    if (a >= 6.0f) m = 0x7;
+    else if (a >= 4.0f) m = 0x6;
+    else if (a >= 3.0f) m = 0x5;
+    else if (a >= 2.0f) m = 0x4;
+    else if (a >= 1.5f) m = 0x3;
+    else if (a >= 1.0f) m = 0x2;
+    else if (a >= 0.5f) m = 0x1;
+    else m = 0x0;
+    return (uint8_t)(sign | m);
+}
+
 /* E2M1 value table (moe-gemm/moe_op_mxfp4/kernel.cpp:32-35). */
 float orc_e2m1_decode(uint8_t nib) {
     static const float lut[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
@@ -256,6 +276,10 @@ void orc_e2m1_encode_array(const float* x, int64_t n, uint8_t* out) {
     for (int64_t i = 0; i < n; ++i) out[i] = orc_e2m1_encode(x[i]);
 }
 
+void orc_e2m1_floor_array(const float* x, int64_t n, uint8_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_e2m1_floor(x[i]);
+}
+
 void orc_mx_scale_exp_array(const float* amax, int64_t n, int32_t* out) {
     for (int64_t i = 0; i < n; ++i) out[i] = orc_mx_scale_exp(amax[i]);
 }
@@ -264,7 +288,9 @@ void orc_mx_scale_exp_array(const float* amax, int64_t n, int32_t* out) {
 
 /* RMSNorm + quantization (quantization/fused_fp8_quant/kernel.cpp:37-204,
  * fused_mxfp4_quant/kernel.cpp:40-243): y = x * rsqrt(mean(x^2) + eps) * w,
- * then the 1x128 FP8 rule (kind 0) or the MXFP4 rule (kind 1). The reference
+ * then the 1x128 FP8 rule (kind 0) or the MXFP4 rule with elements rounded to
+ * nearest even (kind 1) or floored by the reference's ladder (kind 2,
+ * fused_mxfp4_quant/kernel.cpp:128-150; orc_e2m1_floor). The reference
  * leaves the summation order and the rsqrt rounding open (a 256-thread tree,
  * an approximate rsqrtf); this restatement fixes both as the product does so
  * the codes can be compared bit for bit: 64 partial sums, partial l an fmaf
@@ -313,7 +339,8 @@ void orc_rmsnorm_quant(const uint16_t* x, const uint16_t* w, int64_t M, int64_t 
                 const float mul = ldexpf(1.0f, -e);
                 ((uint8_t*)s)[m * (D / 32) + g0 / 32] = (uint8_t)(e + 127);
                 for (int64_t k = g0; k < g0 + 32; k += 2) {
-                    const uint8_t lo = orc_e2m1_encode(y[k] * mul), hi = orc_e2m1_encode(y[k + 1] * mul);
+                    const uint8_t lo = kind == 2 ? orc_e2m1_floor(y[k] * mul) : orc_e2m1_encode(y[k] * mul);
+                    const uint8_t hi = kind == 2 ? orc_e2m1_floor(y[k + 1] * mul) : orc_e2m1_encode(y[k + 1] * mul);
                     q[m * (D / 2) + k / 2] = (uint8_t)(lo | (hi << 4));
                 }
             }

@@ -17,6 +17,11 @@ e4m3_encode/decode     torch.float8_e4m3fn (the reference test's own encoder,
                        fp32; all 256 codes decoded.
 e2m1_encode/decode     value table (moe-gemm/moe_op_mxfp4/kernel.cpp:32-35) and
                        brute-force nearest-even search over the grid.
+e2m1_floor             the reference quantizer's ladder (fused_mxfp4_quant/
+                       kernel.cpp:128-150) against a brute-force search for the
+                       largest grid magnitude <= |x| over every bf16 value of
+                       magnitude <= 8, every grid point +-1 ulp, NaN / +-inf /
+                       +-0, and known answers (1.4 -> 1.0, 5.99 -> 4, 0.49 -> 0).
 mx_scale_exp           the reference's float formula (fused_mxfp4_quant/
                        kernel.cpp:99-105) evaluated with numpy log2/floor over
                        every positive bf16 value.
@@ -51,7 +56,8 @@ moe_blockscale_ref     per-expert dense gemm_blockscale_ref on the gathered rows
                        the fp64 references within 2^-16 of the sum of |terms|
                        (tests/test_oracle_gemm_ext.py, tests/test_oracle_moe.py).
 rmsnorm_quant          fp64 numpy RMSNorm (the test_parity.py formula of
-                       fused_fp8_quant) then the pinned group / MX quantizers:
+                       fused_fp8_quant) then the pinned group / MX quantizers
+                       (kind 2: the MX scale then e2m1_floor):
                        codes equal except where y sits within an ulp of a
                        rounding boundary; known answers for constant rows
                        (rms = |c| exactly); the fixed-order sum against math.fsum.
@@ -128,6 +134,8 @@ def lib():
             getattr(L, name).restype = None
             getattr(L, name).argtypes = [P, I64, P]
         I = ctypes.c_int
+        L.orc_e2m1_floor_array.restype = None
+        L.orc_e2m1_floor_array.argtypes = [P, I64, P]
         L.orc_rmsnorm_quant.restype = None
         L.orc_rmsnorm_quant.argtypes = [P, P, I64, I64, ctypes.c_float, I, P, P]
         L.orc_swiglu_quant.restype = None
@@ -585,10 +593,21 @@ def moe_mxfp4_ref_f32(Aq, As, Bq, Bs, a_scale, b_scale, topk_w, sorted_ids, expe
 # Quantizers fused with their producer
 # ----------------------------------------------------------------------------
 
+def e2m1_floor(x: np.ndarray) -> np.ndarray:
+    """E2M1 codes of fp32 values by the reference fused quantizer's threshold
+    ladder (quantization/fused_mxfp4_quant/kernel.cpp:128-150): largest grid
+    magnitude at or below |x|, the sign bit of x kept, NaN -> magnitude 0."""
+    a = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.zeros(a.size, np.uint8)
+    lib().orc_e2m1_floor_array(_p(a), a.size, _p(out))
+    return out.reshape(np.shape(x))
+
+
 def rmsnorm_quant(xb: np.ndarray, wb: np.ndarray, eps: float, kind: int):
     """RMSNorm + quantization of bf16 bits [M, D] (weight bits [D]); kind 0:
-    (E4M3FN codes [M, D], fp32 scales [M, D/128]); kind 1: (packed E2M1 [M, D/2],
-    e8m0 [M, D/32])."""
+    (E4M3FN codes [M, D], fp32 scales [M, D/128]); kind 1 (E2M1 elements
+    rounded to nearest even) and kind 2 (floored, the reference module's
+    rule): (packed E2M1 [M, D/2], e8m0 [M, D/32])."""
     x = np.ascontiguousarray(xb, dtype=np.uint16)
     w = np.ascontiguousarray(wb, dtype=np.uint16)
     M, D = x.shape

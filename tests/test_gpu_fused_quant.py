@@ -1,8 +1,9 @@
 """GPU parity of the fused quantizers against the CPU oracle, through the C ABI
 and the reference-named modules.
 
-RMSNorm + 1x128 FP8 / MXFP4: codes and scales bit-exact (the reduction order,
-sqrt and division are fixed, so nothing is left to rounding luck).
+RMSNorm + 1x128 FP8 / MXFP4 (nearest and the reference module's floor ladder):
+codes and scales bit-exact (the reduction order, sqrt and division are fixed,
+so nothing is left to rounding luck).
 SwiGLU + FP8: the activation uses the device exp2 and reciprocal, so codes may
 differ from the oracle's by one E4M3 step where the activation sits at a
 rounding boundary; scales within 4 fp32 ulp; at least 99.9% of codes equal.
@@ -26,12 +27,12 @@ def rms_inputs(orc, M, D, seed):
     return xb, wb
 
 
-# FP8 1x128 (kind 0) needs D % 128 == 0, MXFP4 (kind 1) D % 32 == 0: only
+# FP8 1x128 (kind 0) needs D % 128 == 0, MXFP4 (kinds 1, 2) D % 32 == 0: only
 # valid combinations are generated
 RMS_SHAPES = [(1, 128), (7, 1024), (256, 4096), (33, 5120), (64, 7168), (130, 8192), (5, 2080)]
 
 
-@pytest.mark.parametrize("kind,M,D", [(k, M, D) for k in (0, 1) for (M, D) in RMS_SHAPES
+@pytest.mark.parametrize("kind,M,D", [(k, M, D) for k in (0, 1, 2) for (M, D) in RMS_SHAPES
                                       if D % (128 if k == 0 else 32) == 0])
 def test_rmsnorm_quant_bitexact(orc, kind, M, D):
     require_gpu()
@@ -45,6 +46,23 @@ def test_rmsnorm_quant_bitexact(orc, kind, M, D):
         assert np.array_equal(s.cpu().numpy().view(np.uint32), os_.view(np.uint32))
     else:
         assert np.array_equal(host_u8(s), os_)
+
+
+def test_rmsnorm_mxfp4_floor_differs_from_nearest(orc):
+    """The two MXFP4 element rules share scales and differ on codes: the floor
+    ladder never rounds a magnitude up, so |floor code| <= |nearest code|."""
+    require_gpu()
+    M, D = 64, 4096
+    xb, wb = rms_inputs(orc, M, D, 11)
+    x, w = dev_bf16(xb), dev_bf16(wb)
+    qn, sn = hkq.rmsnorm_quant(x, w, 1e-6, 1)
+    qf, sf = hkq.rmsnorm_quant(x, w, 1e-6, 2)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u8(sn), host_u8(sf))
+    a, b = host_u8(qn), host_u8(qf)
+    na = np.stack([a & 0xF, a >> 4]) & 7
+    nb = np.stack([b & 0xF, b >> 4]) & 7
+    assert np.all(nb <= na) and np.any(nb < na)
 
 
 def test_rmsnorm_quant_strided_rows(orc):
@@ -86,7 +104,8 @@ def test_fused_rmsnorm_modules_reference_call(orc, kind):
         scales = torch.zeros(M, N // 32, dtype=torch.uint8, device="cuda")
         hk.fused_rmsnorm_mxfp4_quant_fwd(x.cuda(), weight.cuda(), out, scales, eps)
     torch.cuda.synchronize()
-    oq, os_ = orc.rmsnorm_quant(xb, wb, eps, kind)
+    # the module keeps the reference's floor ladder for MXFP4 elements (kind 2)
+    oq, os_ = orc.rmsnorm_quant(xb, wb, eps, 2 if kind else 0)
     assert (out != 0).sum().item() > 0  # the reference test's own check
     assert np.array_equal(host_u8(out), oq)
     assert np.array_equal(scales.cpu().numpy().view(np.uint8 if kind else np.uint32), os_.view(np.uint8 if kind else np.uint32))

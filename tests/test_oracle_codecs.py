@@ -103,6 +103,36 @@ def test_e2m1_encode_brute_force(orc):
     assert orc.e2m1_encode(np.array([np.nan], np.float32))[0] == 0x7
 
 
+def brute_e2m1_floor(a: float) -> int:
+    """Largest grid magnitude at or below a, by exhaustive search (a >= 0)."""
+    below = np.flatnonzero(E2M1_GRID <= a)
+    return int(below[-1]) if len(below) else 0
+
+
+def test_e2m1_floor_brute_force(orc):
+    """The reference fused quantizer's ladder (fused_mxfp4_quant/kernel.cpp:
+    128-150): every bf16 value of magnitude <= 8, every grid point and its
+    neighbours one ulp away, saturation, signed zeros, infinities and NaN."""
+    vals = [v for v in all_bf16_values() if abs(v) <= 8.0]
+    extra = []
+    for g in E2M1_GRID[1:]:
+        u = np.float32(g).view(np.int32)
+        extra += [np.float32(g), (u - 1).view(np.float32), (u + 1).view(np.float32)]
+    x = np.array(vals + extra + [-t for t in extra] + [6.5, 100.0, -7.0, np.inf, -np.inf, 0.0, -0.0],
+                 dtype=np.float32)
+    ours = orc.e2m1_floor(x)
+    ref = np.array([brute_e2m1_floor(abs(float(v))) | (8 if np.signbit(v) else 0) for v in x], dtype=np.uint8)
+    assert np.array_equal(ours, ref)
+    # known answers of the ladder, and NaN (every comparison false): magnitude 0, sign kept
+    known = np.array([1.4, 1.5, 5.99, 6.0, 0.49, 0.5, -2.9, -3.0], np.float32)
+    assert orc.e2m1_floor(known).tolist() == [0x2, 0x3, 0x6, 0x7, 0x0, 0x1, 0xC, 0xD]
+    nan = np.array([np.float32(np.nan), -np.float32(np.nan)], np.float32)
+    assert orc.e2m1_floor(nan).tolist() == [0x0, 0x8]
+    # the floor and round-to-nearest-even rules meet exactly on the grid
+    g = np.array(list(E2M1_GRID) + [-v for v in E2M1_GRID[1:]], np.float32)
+    assert np.array_equal(orc.e2m1_floor(g), orc.e2m1_encode(g))
+
+
 def test_mx_scale_rule_matches_float_formula(orc):
     # the reference's float formula: P = (bits + 0x200000) & 0xFF800000;
     # e = clamp(floor(log2(P)) - 2, -127, 127) (fused_mxfp4_quant/kernel.cpp:99-105)

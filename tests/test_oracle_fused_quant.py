@@ -76,6 +76,28 @@ def test_rmsnorm_mxfp4_against_fp64(orc, M, D):
     assert np.all((m < 8.0) & ((m >= 3.5) | (np.abs(y).max(-1) == 0)))
 
 
+@pytest.mark.parametrize("M,D", [(8, 4096), (5, 8192), (3, 160)])
+def test_rmsnorm_mxfp4_floor_against_fp64(orc, M, D):
+    """kind 2 (the reference module's element rule): the scales of kind 1, and
+    each code the largest grid magnitude at or below |y * 2^-e| of the fp64
+    RMSNorm (values within 1e-5 of a grid point may fall either side)."""
+    xb = orc.randn_bf16((M, D), seed=5 * D)
+    wb = orc.randn_bf16((D,), seed=5 * D + 1)
+    eps = 1e-5
+    q, s = orc.rmsnorm_quant(xb, wb, eps, 2)
+    _, s1 = orc.rmsnorm_quant(xb, wb, eps, 1)
+    assert np.array_equal(s, s1)
+    y = rms_ref(xb, wb, eps).reshape(M, D // 32, 32)
+    t = y * 2.0 ** (-(s.astype(np.int64) - 127)[:, :, None].astype(np.float64))
+    codes = np.stack([q & 0xF, q >> 4], axis=-1).reshape(M, D // 32, 32)
+    got = E2M1[codes & 7]
+    idx = np.searchsorted(E2M1, np.abs(t), side="right") - 1
+    want = E2M1[np.clip(idx, 0, 7)]
+    near = np.abs(np.abs(t)[..., None] - E2M1[None, None, None, :]).min(-1) <= 1e-5 * np.maximum(np.abs(t), 1e-30)
+    assert np.all((got == want) | near)
+    assert np.all(((codes & 8) != 0) == np.signbit(t))
+
+
 @pytest.mark.parametrize("kind", [0, 1])
 def test_rmsnorm_constant_rows_known_answer(orc, kind):
     """x = c (a power of two) in every column, eps = 0: sum(x^2) = D c^2 exactly,
