@@ -42,6 +42,7 @@ struct DenseParams {
     int splits;           // K splits of the split/skinny path (1: none)
     int kt_split;         // K-tiles per split
     float* ws;            // split partials (splits > 1)
+    uint64_t* split_cnt;  // splits > 1: per tile, the arrival counter of its splits
     // batched A8W8 GEMMs: grid.y walks the batch; the operands of batch z start
     // z * bs_* further (bytes for A/B, elements for the others); bias bf16 [N]
     // per batch (nullptr: none), added after the scales
@@ -443,34 +444,97 @@ __global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_s
 // ---------------------------------------------------------------------------
 // Smaller tiles and split K. A grid of 256 x 256 tiles that would fill at most
 // half of the CUs runs on 128 x 128 tiles (4 waves of 64 x 64; FP8 with
-// M <= 128 and K <= 8192: 128 x 64 tiles, 4 waves of 32 x 64), and M <= 64
+// M <= 128 and K <= 16384: 128 x 64 tiles, 4 waves of 32 x 64), and M <= 64
 // on one row of (32 or 64) x 256 tiles (4 waves side by side); if that still
 // fills at most half of the CUs, K is split as well: workgroup u computes tile
 // u % tiles over K-tiles [s * kt_split, (s+1) * kt_split), s = u / tiles, and
 // writes its fp32 sums to the workspace in register order (per wave, float4 q
-// of lane l at (q * 64 + l) * 16 bytes: every store is a contiguous 1 KB);
-// dense_reduce_kernel adds the splits element-wise and writes C. Without a
-// split the workgroup runs the epilogue itself, reading the scales from memory.
+// of lane l at (q * 64 + l) * 16 bytes: every store is a contiguous 1 KB).
+// Then it counts itself in at the tile's arrival counter; the split that
+// arrives last (ticket splits - 1) adds the partials of all splits in split
+// order (s = 0, 1, ...: the same fp32 sums whichever split arrives last), runs
+// the epilogue and puts the counter back to SPLIT_IDLE. Without a split the
+// workgroup runs the epilogue itself.
+
+// The scales of a wave's (TM*32) x (TN*32) block (A8W8: rows past M and
+// columns past N read 1; other modes: 1), loaded into registers before the K
+// loop so that the epilogue waits on none of them.
+template <int MODE, int TM, int TN>
+struct EpiScales {
+    float r[TM];
+    float4 c[TN][4];
+    __device__ __forceinline__ void load(const DenseParams& p, int lane, int mw, int nw) {
+        const int khalf = lane >> 5;
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+            const int m = mw + j * 32 + (lane & 31);
+            r[j] = (MODE == MODE_A8W8 && m < p.M) ? static_cast<const float*>(p.sa)[m] : 1.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int n = nw + i * 32 + 8 * g + 4 * khalf;
+                c[i][g] = (MODE == MODE_A8W8 && n < p.N)
+                              ? *reinterpret_cast<const float4*>(static_cast<const float*>(p.sb) + n)
+                              : make_float4(1.f, 1.f, 1.f, 1.f);
+            }
+    }
+};
+
 template <int MODE, int WM, int WN, int TM, int TN>
-__device__ __forceinline__ void dense_epilogue_global(const DenseParams& p, v16f (&acc)[TN][TM], HKQ_LDS uint8_t* smem,
+__device__ __forceinline__ void dense_epilogue_global(const DenseParams& p, v16f (&acc)[TN][TM],
+                                                      const EpiScales<MODE, TM, TN>& sc, HKQ_LDS uint8_t* smem,
                                                       int wave, int lane, int mw, int nw) {
-    const float* sa = static_cast<const float*>(p.sa);
-    const float* sb = static_cast<const float*>(p.sb);
     const int khalf = lane >> 5;
-    auto row_scale = [&](int j) {
-        const int m = mw + j * 32 + (lane & 31);
-        return (MODE == MODE_A8W8 && m < p.M) ? sa[m] : 1.0f;
-    };
-    auto col_scale4 = [&](int i, int g) {
-        const int n = nw + i * 32 + 8 * g + 4 * khalf;
-        return (MODE == MODE_A8W8 && n < p.N) ? *reinterpret_cast<const float4*>(sb + n) : make_float4(1.f, 1.f, 1.f, 1.f);
-    };
+    auto row_scale = [&](int j) { return sc.r[j]; };
+    auto col_scale4 = [&](int i, int g) { return sc.c[i][g]; };
     if (p.bias)
         store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, row_scale, col_scale4,
                                 [&](int i, int g) { return bias4(p, nw + i * 32 + 8 * g + 4 * khalf); });
     else
         store_tile_bf16<TM, TN>(acc, smem, wave, lane, p.C, p.ldc, p.M, p.N, mw, nw, p.c16 != 0, row_scale, col_scale4,
                                 NoBias{});
+}
+
+// Split partials cross XCDs, whose L2s are not coherent with each other: they
+// are written and read with device-scope cache policy (sc1: the store writes
+// through to the coherent level, the load does not hit a line another XCD may
+// have changed), so no whole-L2 write-back or invalidate is needed; a wave's
+// stores are complete (vmcnt 0) before its workgroup counts in.
+constexpr int CPOL_SC1 = 16;
+
+// Arrival counters of split tiles: bits 63..16 hold the SPLIT_MAGIC mark,
+// 15..0 the number of splits counted in. An idle counter is SPLIT_MAGIC << 16
+// (count 0), and the last split of a call leaves it so; one arrival then costs
+// a single fetch-and-add. A counter without the mark (a workspace never used
+// for a split plan, or memory another tensor held) is claimed by compare-and-
+// swap: the arrival whose swap installs a count of 1 is counted by it, every
+// other arrival that found the counter unmarked counts itself in again once it
+// sees the mark. Exactly `splits` arrivals are counted, so exactly one draws
+// the last ticket.
+constexpr uint64_t SPLIT_MAGIC = 0x686B71535054ull;  // 48 bits
+constexpr uint64_t SPLIT_IDLE = SPLIT_MAGIC << 16;
+// Counters sit at the start of the split workspace, one per tile, for at most
+// SPLIT_MAX_TILES tiles (every plan uses the same ones, so partial sums of
+// another plan never overwrite them); the partial sums follow.
+constexpr int SPLIT_MAX_TILES = 512;
+constexpr size_t SPLIT_CNT_BYTES = SPLIT_MAX_TILES * 8;
+
+__device__ __forceinline__ int split_ticket(uint64_t* cnt, int splits) {
+    auto fresh = [&](uint64_t v) { return (v >> 16) == SPLIT_MAGIC && (int)(v & 0xFFFF) < splits; };
+    const uint64_t old = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (fresh(old)) return (int)(old & 0xFFFF);
+    uint64_t cur = old + 1;
+    for (;;) {  // ends: a swap fails only when another arrival changed the counter
+        if (__hip_atomic_compare_exchange_strong(cnt, &cur, SPLIT_IDLE | 1ull, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT))
+            return 0;
+        if (fresh(cur)) {  // claimed by another arrival: this one's increment was dropped with the old value
+            const uint64_t o = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return (int)(o & 0xFFFF);
+        }
+    }
 }
 
 template <int MODE, int WM, int WN, int TM, int TN, int KTB, int MINB, int NS>
@@ -490,58 +554,91 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void dense_tile_kernel(const De
     const int m0 = tm * BM, n0 = tn * BN;
     const int KT = p.kbytes / KTB;
     const int kt0 = split * p.kt_split, kt1 = min(KT, kt0 + p.kt_split);
+    const int wm = wave / WN, wn = wave % WN;
+    const int mw = m0 + wm * TM * 32, nw = n0 + wn * TN * 32;
+
+    // older than the K-tile loads: the loop's vmcnt waits cover them
+    EpiScales<MODE, TM, TN> sc;
+    sc.load(p, lane, mw, nw);
 
     v16f acc[TN][TM];
     dense_kloop<MODE, WM, WN, TM, TN, KTB, NS>(p, m0, n0, kt0, kt1, smem, acc);
 
-    if (p.splits > 1) {
-        v4f* slot = reinterpret_cast<v4f*>(p.ws) + ((int64_t)(split * tiles + tile) * NW + wave) * NQ * 64;
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-#pragma unroll
-            for (int j = 0; j < TM; ++j)
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    __builtin_nontemporal_store(v4f{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                                    acc[i][j][4 * g + 3]},
-                                                slot + ((i * TM + j) * 4 + g) * 64 + lane);
+    if (p.splits == 1) {
+        dense_epilogue_global<MODE, WM, WN, TM, TN>(p, acc, sc, smem, wave, lane, mw, nw);
         return;
     }
-    const int wm = wave / WN, wn = wave % WN;
-    dense_epilogue_global<MODE, WM, WN, TM, TN>(p, acc, smem, wave, lane, m0 + wm * TM * 32, n0 + wn * TN * 32);
-}
-
-// One thread per float4 of the partial sums: adds the splits, scales and
-// writes the four bf16 values of C it covers (D[n][m] layout of the MFMA: the
-// float4 g of m-tile j, n-tile i holds n = i*32 + 8g + 4*(lane/32) + 0..3 of
-// m = j*32 + lane % 32, relative to the wave's sub-tile).
-template <int MODE, int WM, int WN, int TM, int TN>
-__global__ __launch_bounds__(256) void dense_reduce_kernel(const DenseParams p, int64_t total) {
-    constexpr int NW = WM * WN, NQ = TN * TM * 4, BM = WM * TM * 32, BN = WN * TN * 32;
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (gid >= total) return;
-    const int lane = (int)(gid & 63);
-    const int q = (int)((gid >> 6) % NQ);
-    const int64_t wt = (gid >> 6) / NQ;
-    const int wave = (int)(wt % NW), tile = (int)(wt / NW);
-    int tm, tn;
-    tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-    const int i = q / (4 * TM), j = (q / 4) % TM, g = q % 4;
-    const int m = tm * BM + (wave / WN) * TM * 32 + j * 32 + (lane & 31);
-    const int n = tn * BN + (wave % WN) * TN * 32 + i * 32 + 8 * g + 4 * (lane >> 5);
-    if (m >= p.M || n >= p.N) return;
-    const v4f* src = reinterpret_cast<const v4f*>(p.ws) + gid;
-    v4f v = __builtin_nontemporal_load(src);
-    for (int s = 1; s < p.splits; ++s) v += __builtin_nontemporal_load(src + (int64_t)s * total);
-    float a = 1.f;
-    v4f b = v4f{1.f, 1.f, 1.f, 1.f};
-    if constexpr (MODE == MODE_A8W8) {
-        a = static_cast<const float*>(p.sa)[m];
-        b = *reinterpret_cast<const v4f*>(static_cast<const float*>(p.sb) + n);  // N % 4 == 0: n..n+3 < N
+    // this split's partial: float4 q of lane l of wave w at
+    // ((s * tiles + tile) * NW + w) * NQ * 64 + q * 64 + l
+    const uint32_t wave_slot = (uint32_t)(((int64_t)tile * NW + wave) * NQ * 64 + lane) * 16u;
+    const uint32_t split_stride = (uint32_t)tiles * NW * NQ * 64 * 16u;
+    const __amdgpu_buffer_rsrc_t ws =
+        __builtin_amdgcn_make_buffer_rsrc(p.ws, 0, (int)(split_stride * (uint32_t)p.splits), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const v4f v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, v), ws,
+                                                       (uint32_t)split * split_stride + wave_slot +
+                                                           (uint32_t)(((i * TM + j) * 4 + g) * 64 * 16),
+                                                       0, CPOL_SC1);
+            }
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    // count this split in (one thread per workgroup); the flag lies past the
+    // epilogue's staging, in the (idle) K-tile ring
+    static_assert(Cfg::EP_BYTES + 16 <= Cfg::lds_bytes(NS), "room for the split flag");
+    HKQ_LDS int& last_split = *reinterpret_cast<HKQ_LDS int*>(smem + Cfg::lds_bytes(NS) - 16);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const bool last = split_ticket(p.split_cnt + tile, p.splits) == p.splits - 1;
+        if (last) __hip_atomic_store(p.split_cnt + tile, SPLIT_IDLE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_split = last;
     }
-    const uint32_t lo = pk_bf16(v[0] * a * b[0], v[1] * a * b[1]);
-    const uint32_t hi = pk_bf16(v[2] * a * b[2], v[3] * a * b[3]);
-    *reinterpret_cast<v2i*>(p.C + (int64_t)m * p.ldc + n) = v2i{(int)lo, (int)hi};
+    __syncthreads();
+    if (!last_split) return;
+    // sum in split order; the other splits' float4 come in chunks of RCH
+    // splits, all loads of a chunk in flight together (three splits' worth of
+    // registers where the budget allows: 8 float4 per lane, or one workgroup
+    // per CU)
+    constexpr int RCH = (NQ <= 8 || MINB == 1) ? 3 : 1;
+    v16f sum[TN][TM];
+    for (int s0 = 0; s0 < p.splits; s0 += RCH) {
+        v4f part[RCH][NQ] = {};
+#pragma unroll
+        for (int c = 0; c < RCH; ++c) {
+            const int s = s0 + c;
+            if (s < p.splits && s != split) {
+#pragma unroll
+                for (int q = 0; q < NQ; ++q)
+                    part[c][q] = __builtin_bit_cast(
+                        v4f, __builtin_amdgcn_raw_buffer_load_b128(ws, (uint32_t)s * split_stride + wave_slot +
+                                                                           (uint32_t)(q * 64 * 16),
+                                                                   0, CPOL_SC1));
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < RCH; ++c) {
+            const int s = s0 + c;
+            if (s >= p.splits) break;
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int q = (i * TM + j) * 4 + g;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float x = s == split ? acc[i][j][4 * g + e] : part[c][q][e];
+                            sum[i][j][4 * g + e] = s == 0 ? x : sum[i][j][4 * g + e] + x;
+                        }
+                    }
+        }
+    }
+    dense_epilogue_global<MODE, WM, WN, TM, TN>(p, sum, sc, smem, wave, lane, mw, nw);
 }
 
 // ---------------------------------------------------------------------------
@@ -731,10 +828,11 @@ static DensePlan dense_plan(int mode, int64_t M, int64_t N, int64_t kbytes, bool
     } else if (ktb == 128 && 2 * ntiles(DENSE_BM, DENSE_BN) <= ncu) {
         pl.geo = GEO_128;
         bm = bn = 128;
-        // FP8 with M <= 128 and K <= 8192: 128 x 64 tiles (4 waves of 32 x 64),
-        // twice the workgroups for the same K split (measured faster on the
-        // BASELINE sweep's M = 96 / 128 shapes; not for FP4 or longer K)
-        if (mode == MODE_A8W8 && M <= 128 && KT <= 64) {
+        // FP8 with M <= 128 and K <= 16384: 128 x 64 tiles (4 waves of 32 x 64),
+        // twice the workgroups for the same K split and a quarter of the
+        // partial sums the last split reads (measured on MI355X: 128x4096x4096
+        // 10.0 us, 128x4096x14336 18.0 us against 24.1 on 128 x 128 tiles)
+        if (mode == MODE_A8W8 && M <= 128 && KT <= 128) {
             pl.geo = GEO_128x64;
             bn = 64;
         }
@@ -744,7 +842,8 @@ static DensePlan dense_plan(int mode, int64_t M, int64_t N, int64_t kbytes, bool
     pl.kt_split = (int)KT;
     // split K when the tiles fill at most half of the CUs, keeping at least 4
     // K-tiles per split
-    if (allow_split && pl.geo != GEO_256 && pl.tiles > 0 && 2 * pl.tiles <= ncu && KT >= 8) {
+    if (allow_split && pl.geo != GEO_256 && pl.tiles > 0 && 2 * pl.tiles <= ncu && pl.tiles <= SPLIT_MAX_TILES &&
+        KT >= 8) {
         int64_t s = (ncu + pl.tiles - 1) / pl.tiles;
         s = std::min<int64_t>(s, KT / 4);
         if (s > 1) {
@@ -753,7 +852,8 @@ static DensePlan dense_plan(int mode, int64_t M, int64_t N, int64_t kbytes, bool
             pl.kt_split = (int)per;
         }
     }
-    if (pl.splits > 1) pl.ws_bytes = (size_t)pl.splits * (size_t)pl.tiles * (size_t)(bm * bn) * 4;
+    // the arrival counters, then the partial sums
+    if (pl.splits > 1) pl.ws_bytes = SPLIT_CNT_BYTES + (size_t)pl.splits * (size_t)pl.tiles * (size_t)(bm * bn) * 4;
     return pl;
 }
 
@@ -772,12 +872,11 @@ static int launch_dense_tiles(DenseParams& p, const DensePlan& pl, hipStream_t s
     p.kt_split = pl.kt_split;
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     if (tiles == 0) return 0;
+    if (p.splits > 1) {  // dense_plan's workspace: the arrival counters, then the partial sums
+        p.split_cnt = reinterpret_cast<uint64_t*>(p.ws);
+        p.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(p.ws) + SPLIT_CNT_BYTES);
+    }
     kern<<<dim3((unsigned)(tiles * p.splits), (unsigned)std::max(1, p.batch)), 64 * WM * WN, LDS, stream>>>(p);
-    if (int e = hkq_launch_status()) return e;
-    if (p.splits == 1) return 0;
-    const int64_t total = tiles * Cfg::NW * (TN * TM * 4) * 64;  // float4 per split
-    auto red = dense_reduce_kernel<MODE, WM, WN, TM, TN>;
-    red<<<dim3((unsigned)((total + 255) / 256)), 256, 0, stream>>>(p, total);
     return hkq_launch_status();
 }
 
@@ -904,15 +1003,24 @@ static int launch_dense_ktb(DenseParams& p, void* ws, size_t ws_bytes, hipStream
         // 11.3, 128x6144x4096 13.3 -> 11.4; at 1.5 rounds, 1024x6144x4096,
         // two per CU win: 29.6 vs 36.5). MXFP4's scale blocks assume 2 stages.
         const int ncu = cu_count() > 0 ? cu_count() : 256;
-        const bool one_round = MODE != MODE_MXFP4 && pl.tiles * pl.splits * std::max(1, p.batch) <= ncu;
+        const bool one_round = pl.tiles * pl.splits * std::max(1, p.batch) <= ncu;
         if (pl.geo == GEO_128) {
-            if constexpr (MODE != MODE_MXFP4)
-                if (one_round) return launch_dense_tiles<MODE, 2, 2, 2, 2, KTB, 1, 3>(p, pl, stream);
+            if (one_round) {
+                if constexpr (MODE == MODE_MXFP4) {  // the scale blocks keep 2 stages
+                    return launch_dense_tiles<MODE, 2, 2, 2, 2, KTB, 1, 2>(p, pl, stream);
+                } else {
+                    if (pl.kt_split >= 4) return launch_dense_tiles<MODE, 2, 2, 2, 2, KTB, 1, 4>(p, pl, stream);
+                    return launch_dense_tiles<MODE, 2, 2, 2, 2, KTB, 1, 3>(p, pl, stream);
+                }
+            }
             return launch_dense_tiles<MODE, 2, 2, 2, 2, KTB, 2>(p, pl, stream);
         }
         if constexpr (MODE == MODE_A8W8)
             if (pl.geo == GEO_128x64) {
-                if (one_round) return launch_dense_tiles<MODE, 4, 1, 1, 2, KTB, 1, 3>(p, pl, stream);
+                if (one_round) {
+                    if (pl.kt_split >= 6) return launch_dense_tiles<MODE, 4, 1, 1, 2, KTB, 1, 6>(p, pl, stream);
+                    return launch_dense_tiles<MODE, 4, 1, 1, 2, KTB, 1, 3>(p, pl, stream);
+                }
                 return launch_dense_tiles<MODE, 4, 1, 1, 2, KTB, 2>(p, pl, stream);
             }
     }
@@ -974,10 +1082,11 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
 
 }  // extern "C"
 
-// Split-K partial sums of hkq_gemm_a8w8_noalloc: a library-owned workspace
-// that each GPU holds from the library's load to the end of the process, so
-// that the entry point allocates nothing. Its size bounds every split plan on
-// 256 CUs (at most 1.5 * 256 tile splits of 128 x 128 fp32 sums: 25.2 MB).
+// Split-K counters and partial sums of hkq_gemm_a8w8_noalloc: a library-owned
+// workspace that each GPU holds from the library's load to the end of the
+// process, so that the entry point allocates nothing. Its size bounds every
+// split plan on 256 CUs (at most 1.5 * 256 tile splits of 128 x 128 fp32
+// sums: 25.2 MB, after 4 KB of counters).
 constexpr size_t HKQ_SCRATCH_BYTES = size_t(32) << 20;
 static __device__ __align__(256) uint8_t scratch[HKQ_SCRATCH_BYTES];
 

@@ -236,7 +236,9 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
     // Operand buffers: the whole tile's rows, K positions in the lane offsets.
     // Rows that read zero have offsets at or past 2^31 (OOB), past every
     // extent; the loads of K-tiles kt >= KTN (the ring's look-ahead past the
-    // end) read rows' later bytes or zero, into stages the loop never reads.
+    // end, into stages the loop never reads) take such an offset too, so they
+    // count for vmcnt without fetching anything (a split's K range would
+    // otherwise pull NS K-tiles of the next split's bytes).
     const v4i desc_a = buffer_desc(src.a, (uint32_t)(src.a_bytes < 0x7FFFFFFF ? (src.a_bytes > 0 ? src.a_bytes : 0) : 0x7FFFFFFF));
     const v4i desc_b = buffer_desc(src.b, (uint32_t)(src.b_bytes < 0x7FFFFFFF ? (src.b_bytes > 0 ? src.b_bytes : 0) : 0x7FFFFFFF));
 
@@ -259,11 +261,13 @@ __device__ __forceinline__ void gemm_mainloop(const LoopSrc& src, const AOff& a_
             }
         }
         if (idx < LA) {
-            lds_load16_d(desc_a, smem + Cfg::a_stage(NS, stage) + (idx * NW + wave) * 1024, a_off.v[idx] + (uint32_t)kb);
+            lds_load16_d(desc_a, smem + Cfg::a_stage(NS, stage) + (idx * NW + wave) * 1024,
+                         live ? a_off.v[idx] + (uint32_t)kb : 0x80000000u);
         } else if (idx < LA + LB) {
             const int i = idx - LA;
             const uint32_t kbb = BT ? (uint32_t)(kt * src.b_kstep) : (uint32_t)kb;
-            lds_load16_d(desc_b, smem + Cfg::b_stage(NS, stage) + (i * NW + wave) * 1024, b_off.v[i] + kbb);
+            lds_load16_d(desc_b, smem + Cfg::b_stage(NS, stage) + (i * NW + wave) * 1024,
+                         live ? b_off.v[i] + kbb : 0x80000000u);
         } else if (idx < LA + LB + LSA) {
             const int g = ((idx - LA - LB) * NW + wave) % GA;
             const int kb4 = kt * 4;

@@ -122,12 +122,18 @@ int hkq_gemm_a8w8(const void* A, const void* B, const float* sa, const float* sb
 
 /* hkq_gemm_a8w8 with a caller-provided device workspace (16-byte aligned).
  * Shapes whose tiles would fill at most half of the CUs (256 x 256 tiles
- * become 128 x 128, or (32 or 64) x 256 for M <= 64, first) split K over
- * several workgroups and add the fp32 partials in a second kernel; that needs
- * hkq_gemm_a8w8_workspace(M, N, K) bytes (0: no split for this shape; M <= 16
- * runs a single-launch streaming kernel that needs none). With a smaller
- * workspace (or NULL) the call runs unsplit. Same results either way up to fp32 summation order. The
- * workspace is in use until the work queued on `stream` completes. No
+ * become 128 x 128 or 128 x 64, or (32 or 64) x 256 for M <= 64, first) split
+ * K over several workgroups in one launch: each writes its fp32 partial sums
+ * to the workspace, and the last split of a tile to finish adds all of them in
+ * split order and writes C (bit-identical whichever split finishes last).
+ * That needs hkq_gemm_a8w8_workspace(M, N, K) bytes (0: no split for this
+ * shape; M <= 16 runs a single-launch streaming kernel that needs none). With
+ * a smaller workspace (or NULL) the call runs unsplit. Same results either way
+ * up to fp32 summation order. The workspace needs no clearing: its first 4 KB
+ * hold per-tile arrival counters that each call leaves marked idle (a
+ * workspace that held other data is claimed on first use, at the cost of one
+ * compare-and-swap per counter). It is in use until the work queued on
+ * `stream` completes; calls that may overlap need separate workspaces. No
  * counterpart in the reference, whose kernels have no split path; the drop-in
  * modules (gemm_a8w8_tk, gemm_a8w8_per_token_scale_tk) call it with a
  * workspace from torch's allocator. */
@@ -137,7 +143,7 @@ int hkq_gemm_a8w8_ws(const void* A, const void* B, const float* sa, const float*
                      hkq_stream_t stream);
 
 /* hkq_gemm_a8w8_ws without a caller workspace and without allocating: the
- * split-K partials go to a library-owned device array of
+ * split-K counters and partials go to a library-owned device array of
  * hkq_gemm_a8w8_noalloc_max_workspace() bytes (32 MiB) that each GPU the
  * library runs on holds until the process ends. Shapes whose plan needs more
  * are rejected with hipErrorInvalidValue (none on a 256-CU MI355X). Every call

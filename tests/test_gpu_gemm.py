@@ -110,7 +110,7 @@ def test_gemm_a8w8_baseline_sizes_full(orc, M, N, K):
 # Smaller-tile and split-K plans: M <= 64 uses (32 or 64) x 256 tiles, few
 # 256 x 256 tiles become 128 x 128 tiles (128 x 64 for FP8 with M <= 128 and
 # K <= 8192), and if those are still few (with a long enough K) K is split
-# into fp32 partials added by a second kernel.
+# into fp32 partials that the last split of each tile to finish adds up.
 SPLIT_SHAPES = [(1, 4096, 14336), (16, 2048, 4096), (48, 1024, 2048), (128, 4096, 4096), (96, 28672, 4096), (24, 28672, 4096),
                 (1024, 4096, 14336), (640, 1000, 8192), (256, 1024, 8192), (300, 2052, 2048), (100, 1000, 2048),
                 (128, 6144, 4096)]
@@ -129,6 +129,75 @@ def test_gemm_a8w8_split_and_skinny(orc, M, N, K):
     ref = orc.gemm_a8w8_ref_f32(A, B, sa, sb)
     assert_gemm_close(host_bf16_f32(C1), ref, f"a8w8 split {M}x{N}x{K}")
     assert_gemm_close(host_bf16_f32(C0), ref, f"a8w8 unsplit {M}x{N}x{K}")
+
+
+def _a8w8_ws_launcher(Ad, Bd, sad, sbd, C, ws):
+    M, K = Ad.shape
+    N = Bd.shape[0]
+    return lambda: hkq.call("hkq_gemm_a8w8_ws", Ad.data_ptr(), Bd.data_ptr(), sad.data_ptr(), sbd.data_ptr(),
+                            C.data_ptr(), M, N, K, K, K, N, ws.data_ptr(), ws.numel(),
+                            torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 4096, 4096), (64, 4096, 14336), (1024, 1024, 8192)])
+def test_gemm_a8w8_split_workspace_states(orc, M, N, K):
+    """The split plan's per-tile arrival counters live in the workspace and
+    need no clearing: a workspace full of 0xFF bytes, one left by a call of
+    another shape, and the same call repeated all give the same bytes, which
+    match the oracle (the partials are added in split order, whichever split
+    finishes last)."""
+    require_gpu()
+    A, B, sa, sb = a8w8_inputs(orc, M, N, K, seed=M + N + K + 5)
+    Ad, Bd, sad, sbd = dev_u8(A), dev_u8(B), dev_f32(sa), dev_f32(sb)
+    need = hkq.lib().hkq_gemm_a8w8_workspace(M, N, K)
+    assert need > 0
+    ws = torch.full((need + (1 << 20),), 0xFF, dtype=torch.uint8, device="cuda")
+    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    run = _a8w8_ws_launcher(Ad, Bd, sad, sbd, C, ws)
+    run()
+    torch.cuda.synchronize()
+    first = C.clone()
+    assert_gemm_close(host_bf16_f32(first), orc.gemm_a8w8_ref_f32(A, B, sa, sb), f"a8w8 split {M}x{N}x{K}")
+    # another shape's split plan on the same workspace, then this one again, twice
+    A2, B2, sa2, sb2 = a8w8_inputs(orc, 96, 2048, 4096, seed=9)
+    C2 = torch.empty((96, 2048), dtype=torch.bfloat16, device="cuda")
+    _a8w8_ws_launcher(dev_u8(A2), dev_u8(B2), dev_f32(sa2), dev_f32(sb2), C2, ws)()
+    for _ in range(2):
+        C.fill_(0)
+        run()
+        torch.cuda.synchronize()
+        assert torch.equal(C.view(torch.int16), first.view(torch.int16))
+
+
+def test_gemm_a8w8_split_graph_replay(orc):
+    """A split GEMM captured in a HIP graph replays with one tag: every replay
+    (with eager work and synchronization between them) equals the eager call."""
+    require_gpu()
+    M, N, K = 128, 4096, 4096
+    A, B, sa, sb = a8w8_inputs(orc, M, N, K, seed=77)
+    Ad, Bd, sad, sbd = dev_u8(A), dev_u8(B), dev_f32(sa), dev_f32(sb)
+    ws = torch.empty((hkq.lib().hkq_gemm_a8w8_workspace(M, N, K),), dtype=torch.uint8, device="cuda")
+    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    run = _a8w8_ws_launcher(Ad, Bd, sad, sbd, C, ws)
+    run()
+    torch.cuda.synchronize()
+    eager = C.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            run()
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(4):
+        C.fill_(0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(C.view(torch.int16), eager.view(torch.int16)), f"replay {i}"
+        run()  # an eager call (a new tag) between replays
+        torch.cuda.synchronize()
+        assert torch.equal(C.view(torch.int16), eager.view(torch.int16))
 
 
 def test_gemm_workspace_plans():
