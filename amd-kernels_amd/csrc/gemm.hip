@@ -901,6 +901,9 @@ static int launch_dense_whole(DenseParams& p, hipStream_t stream) {
     const int64_t split = (!batched && last > 0 && 2 * last <= ncu && p.M > DENSE_BM / 2) ? last : 0;
     p.n_whole = (int)(tiles - split);
     p.n_split = (int)split;
+    // MXFP4 stays on the one-tile kernel: its stream (the K loop below with
+    // compile-time scale slots, C stored from registers since the ring and the
+    // scale blocks fill the LDS) spills and measured 1.8x slower on MI355X.
     if constexpr (KTB == 128 && MODE != MODE_MXFP4) {
         // the persistent streaming kernel: one workgroup per CU, whole tiles as
         // a K-tile stream (needs K-tiles per tile % 8 == 0; one 2-D GEMM without

@@ -76,29 +76,45 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const B
         asm volatile("" : "+s"(d));
         return reinterpret_cast<HKQ_LDS uint8_t*>(d + c);
     };
-    // scale unit u of the tile `ls` (see gemm_mainloop)
-    auto load_scale_unit = [&](int u) {
-        const int blk = u / Cfg::SB_KT;
-        const int g = ((u % Cfg::SB_KT) * NW + wave) % Cfg::SB_GROUPS;
-        const bool live = ls_live && blk * Cfg::SB_KT < KTN;
+    // MXFP4 scale units (see gemm_mainloop): unit u of a block is loaded by
+    // every wave into group ((u % SB_KT) * NW + wave) % SB_GROUPS, so per unit
+    // slot k = u % SB_KT a wave's group and its lanes' row offsets are fixed:
+    // computed once here (the 32-bit row offsets relative to the tile's first
+    // scale row), the slot is a template argument at every use.
+    constexpr int SBK = Cfg::SBLK ? Cfg::SB_KT : 1;
+    int su_g[SBK];
+    bool su_a[SBK];
+    uint32_t su_off[SBK];
+#pragma unroll
+    for (int k = 0; k < SBK; ++k) {
+        const int g = (k * NW + wave) % (Cfg::SBLK ? Cfg::SB_GROUPS : 1);
         const int r = g * 32 + (lane >> 1);
-        const bool isa = g * 32 < BM;
-        const uint8_t* base = (isa ? ls.as : ls.bs) + blk * 32;
-        const uint32_t ext = isa ? ls.as_bytes : ls.bs_bytes, kb = (uint32_t)blk * 32u;
+        su_g[k] = g;
+        su_a[k] = g * 32 < BM;
+        // row slot s = lane / 2 of the group; its two 16-byte halves are stored
+        // swapped when bit 3 of s is set (see read_scale)
         const uint32_t half = (uint32_t)((lane & 1) ^ ((lane >> 4) & 1));
-        const uint32_t a_row = (uint32_t)r * seq.lsa;
-        const uint32_t b_row = (uint32_t)(r - BM) * seq.lsb;
-        const uint32_t off = (isa ? a_row : b_row) + half * 16u;
-        lds_load16_u(base, live && ext > kb ? ext - kb : 0u, sblk + (blk & 1) * Cfg::SB_SLOT + g * 1024, off);
+        su_off[k] = (su_a[k] ? (uint32_t)r * seq.lsa : (uint32_t)(r - BM) * seq.lsb) + half * 16u;
+        asm volatile("" : "+v"(su_off[k]));
+    }
+    // scale unit u (slot K = u % SB_KT) of the tile `ls`
+    auto load_scale_unit = [&](int u, auto kslot) {
+        constexpr int K = decltype(kslot)::value;
+        const int blk = u / Cfg::SB_KT;
+        const bool live = ls_live && blk * Cfg::SB_KT < KTN;
+        const uint8_t* base = (su_a[K] ? ls.as : ls.bs) + blk * 32;
+        const uint32_t ext = su_a[K] ? ls.as_bytes : ls.bs_bytes, kb = (uint32_t)blk * 32u;
+        lds_load16_u(base, live && ext > kb ? ext - kb : 0u, sblk + (blk & 1) * Cfg::SB_SLOT + su_g[K] * 1024,
+                     su_off[K]);
     };
 
     // load instruction idx of K-tile kl of `ld` into `stage`; MXFP4: scale
-    // unit kl + SB_KT - 1 of `ls`, counted in `ls`'s own K-tiles (kl + SB_KT - 1
-    // - KTN once `ls` has switched ahead of `ld`)
-    auto load_piece = [&](int kl, int ul, int stage, int idx) {
+    // unit kl + SB_KT - 1 of `ls` (slot KS), counted in `ls`'s own K-tiles
+    // (kl + SB_KT - 1 - KTN once `ls` has switched ahead of `ld`)
+    auto load_piece = [&](int kl, int ul, int stage, int idx, auto kslot) {
         if constexpr (Cfg::SBLK) {
             if (idx == LA + LB) {
-                load_scale_unit(ul);
+                load_scale_unit(ul, kslot);
                 return;
             }
         }
@@ -162,13 +178,15 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const B
         int a[TM], b[TN];
     };
     const int sc_lo = (lane & 31) * 32 + khalf * 4, sc_x = (((lane & 31) >> 3) & 1) << 4;
-    auto read_scale = [&](int kt, Scales& s, int idx) {
+    // the scale words of K-tile kt (slot Q = kt % SB_KT of its block)
+    auto read_scale = [&](int kt, Scales& s, int idx, auto qslot) {
         if constexpr (FP4) {
+            constexpr int Q = decltype(qslot)::value;
             const bool isa = idx < TM;
             const int t = isa ? idx : idx - TM;
             const HKQ_LDS uint8_t* slot = sblk + ((kt / Cfg::SB_KT) & 1) * Cfg::SB_SLOT;
             const int wave_row = isa ? wm * TM * 32 : BM + wn * TN * 32;
-            const int o = ((kt % Cfg::SB_KT) * 8) ^ sc_x;
+            const int o = (Q * 8) ^ sc_x;
             const int w = *reinterpret_cast<const HKQ_LDS int*>(slot + wave_row * 32 + sc_lo + o + t * 1024);
             if (isa) s.a[t] = w;
             else s.b[t] = w;
@@ -203,22 +221,29 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const B
         }
     };
 
+    using Q0 = std::integral_constant<int, 0>;
+    using Q1 = std::integral_constant<int, 1>;
+    using Q2 = std::integral_constant<int, 2>;
+    using Q3 = std::integral_constant<int, 3>;
     Frags F[2];
     Scales S[2];
     epi.begin(0);
+    // units 0 .. SB_KT-2 of block 0, then K-tiles 0 and 1, whose loads carry
+    // units SB_KT-1 and SB_KT (slots 3 and 0)
     if constexpr (Cfg::SBLK) {
-#pragma unroll
-        for (int u = 0; u + 1 < Cfg::SB_KT; ++u) load_scale_unit(u);
+        load_scale_unit(0, Q0{});
+        load_scale_unit(1, Q1{});
+        load_scale_unit(2, Q2{});
     }
 #pragma unroll
-    for (int t = 0; t < NS; ++t)
+    for (int i = 0; i < NLD; ++i) load_piece(0, Cfg::SB_KT - 1, 0, i, Q3{});
 #pragma unroll
-        for (int i = 0; i < NLD; ++i) load_piece(t, t + Cfg::SB_KT - 1, t, i);
+    for (int i = 0; i < NLD; ++i) load_piece(1, Cfg::SB_KT, 1, i, Q0{});
     tile_barrier<(NS - 1) * NLD>();
 #pragma unroll
     for (int i = 0; i < NRD; ++i) read_piece(0, 0, F[0], i);
 #pragma unroll
-    for (int i = 0; i < NSC; ++i) read_scale(0, S[0], i);
+    for (int i = 0; i < NSC; ++i) read_scale(0, S[0], i, Q0{});
 
     int cur = 0;  // the tile being computed
     // One K-tile (see gemm_mainloop); FIRST: the tile's first K-tile, whose
@@ -228,12 +253,17 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const B
     // VM: vector-memory operations younger than K-tile kt+1's loads when the
     // body waits for them (the C stores and scale loads of an epilogue that ran
     // after those loads were issued may stay in flight)
-    auto ktile_vm = [&](int kt, int stage, auto parity, auto first, auto last, auto vm) {
-        constexpr int P = decltype(parity)::value;
+    // Q: kt % SB_KT (MXFP4's scale slots; K-tiles per tile are a multiple of
+    // 8, so it also fixes the stage and the fragment parity)
+    auto ktile_vm = [&](int kt, auto qslot, auto first, auto last, auto vm) {
+        constexpr int Q = decltype(qslot)::value;
+        constexpr int P = Q & 1;
         constexpr bool FIRST = decltype(first)::value;
         constexpr bool LAST = decltype(last)::value;
         constexpr int VM = decltype(vm)::value;
-        const int next_stage = stage ^ 1;
+        using KS = std::integral_constant<int, (Q + 1) % 4>;  // kt + NS + SB_KT - 1 = kt + 5
+        using QN = std::integral_constant<int, (Q + 1) % 4>;  // K-tile kt + 1
+        const int stage = P, next_stage = P ^ 1;
         const int kl = kt + NS < KTN ? kt + NS : kt + NS - KTN;
         const int ul = kt + NS + Cfg::SB_KT - 1 < KTN ? kt + NS + Cfg::SB_KT - 1 : kt + NS + Cfg::SB_KT - 1 - KTN;
         // K-step 1's fragment reads go out over the first half of K-step 0's
@@ -253,55 +283,62 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const B
         for (int c = 0; c < NMF; ++c) {
             mfma_one(F[1], 1, S[P], c, std::false_type{});
 #pragma unroll
-            for (int i = c * NLD / NMF; i < (c + 1) * NLD / NMF; ++i) load_piece(kl, ul, stage, i);
+            for (int i = c * NLD / NMF; i < (c + 1) * NLD / NMF; ++i) load_piece(kl, ul, stage, i, KS{});
             if constexpr (!LAST) {
 #pragma unroll
                 for (int i = c * NRD / NMF; i < (c + 1) * NRD / NMF; ++i) read_piece(next_stage, 0, F[0], i);
 #pragma unroll
-                for (int i = c * NSC / NMF; i < (c + 1) * NSC / NMF; ++i) read_scale(kt + 1, S[P ^ 1], i);
+                for (int i = c * NSC / NMF; i < (c + 1) * NSC / NMF; ++i) read_scale(kt + 1, S[P ^ 1], i, QN{});
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto ktile = [&](int kt, int stage, auto parity, auto first, auto last) {
-        ktile_vm(kt, stage, parity, first, last, std::integral_constant<int, (NS - 2) * NLD>{});
+    auto ktile = [&](int kt, auto qslot, auto first, auto last) {
+        ktile_vm(kt, qslot, first, last, std::integral_constant<int, (NS - 2) * NLD>{});
     };
 
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
+    using F0 = std::false_type;
     for (int t = 0; t < seq.tiles; ++t) {
         cur = t;
         if (t > 0) {
             epi.begin(t);
             // K-tile 1's loads went out before the previous tile's epilogue:
             // its C stores (and this tile's scale loads) need not be waited for
-            ktile_vm(0, 0, P0{}, std::true_type{}, std::false_type{},
-                     std::integral_constant<int, (NS - 2) * NLD + Epi::VM_ISSUED>{});
+            constexpr int VM_EPI = (NS - 2) * NLD + Epi::VM_ISSUED;
+            ktile_vm(0, Q0{}, std::true_type{}, F0{}, std::integral_constant<int, VM_EPI < 63 ? VM_EPI : 63>{});
         } else {
-            ktile(0, 0, P0{}, std::true_type{}, std::false_type{});
+            ktile(0, Q0{}, std::true_type{}, F0{});
         }
-        ktile(1, 1, P1{}, std::false_type{}, std::false_type{});
+        ktile(1, Q1{}, F0{}, F0{});
         // The sources switch between K-tile bodies (a branch inside one would
         // split its MFMA/load interleave): the scale units of the next tile
         // start with K-tile KTN - 5 (MXFP4), its data with K-tile KTN - 2.
-        constexpr int PEEL = Cfg::SBLK ? 6 : 2;
-        for (int kt = 2; kt + PEEL < KTN; kt += 2) {
-            ktile(kt, 0, P0{}, std::false_type{}, std::false_type{});
-            ktile(kt + 1, 1, P1{}, std::false_type{}, std::false_type{});
-        }
+        // MXFP4 runs four K-tiles per iteration, so that every scale slot is a
+        // constant (KTN % 8 == 0: the loop ends at KTN - 6).
         if constexpr (Cfg::SBLK) {
-            ktile(KTN - 6, 0, P0{}, std::false_type{}, std::false_type{});
+            for (int kt = 2; kt + 6 < KTN; kt += 4) {
+                ktile(kt, Q2{}, F0{}, F0{});
+                ktile(kt + 1, Q3{}, F0{}, F0{});
+                ktile(kt + 2, Q0{}, F0{}, F0{});
+                ktile(kt + 3, Q1{}, F0{}, F0{});
+            }
+            ktile(KTN - 6, Q2{}, F0{}, F0{});
             ls_live = t + 1 < seq.tiles;
             ls = seq.src(min(t + 1, seq.tiles - 1));
-            ktile(KTN - 5, 1, P1{}, std::false_type{}, std::false_type{});
-            ktile(KTN - 4, 0, P0{}, std::false_type{}, std::false_type{});
-            ktile(KTN - 3, 1, P1{}, std::false_type{}, std::false_type{});
+            ktile(KTN - 5, Q3{}, F0{}, F0{});
+            ktile(KTN - 4, Q0{}, F0{}, F0{});
+            ktile(KTN - 3, Q1{}, F0{}, F0{});
+        } else {
+            for (int kt = 2; kt + 2 < KTN; kt += 2) {
+                ktile(kt, Q0{}, F0{}, F0{});
+                ktile(kt + 1, Q1{}, F0{}, F0{});
+            }
         }
         ld_live = t + 1 < seq.tiles;
         ld = seq.src(min(t + 1, seq.tiles - 1));
         if constexpr (Seq::GATHER) seq.a_rows(min(t + 1, seq.tiles - 1), a_off);
-        ktile(KTN - 2, 0, P0{}, std::false_type{}, std::false_type{});
-        ktile(KTN - 1, 1, P1{}, std::false_type{}, std::true_type{});
+        ktile(KTN - 2, Q2{}, F0{}, F0{});
+        ktile(KTN - 1, Q3{}, F0{}, std::true_type{});
         mfma_drain();
         // Pin the finished accumulators here: without it the compiler sinks
         // the last K-tile's MFMAs past their scheduling barriers into the
@@ -319,7 +356,7 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const B
 #pragma unroll
         for (int i = 0; i < NRD; ++i) read_piece(0, 0, F[0], i);
 #pragma unroll
-        for (int i = 0; i < NSC; ++i) read_scale(0, S[0], i);
+        for (int i = 0; i < NSC; ++i) read_scale(0, S[0], i, Q0{});
     }
     tile_barrier<0>();  // no load in flight, every wave past its reads
 }
