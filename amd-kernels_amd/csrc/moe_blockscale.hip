@@ -116,7 +116,37 @@ struct MoeBsParams {
     int64_t xs_elems, ws_elems;  // reads of the scale tensors stay below these extents
     int64_t swk;
     int wt;
+    int ncu;  // CUs of the device (0: no tail split)
 };
+
+// Word index from which ExptData entries compute their own 128-row block
+// instead of pairing with the next: when the grid's 256-row tiles (one per
+// block pair or lone block, per column tile) come to fewer than 4 rounds and
+// leave a last round that fills at most half of the CUs, that round's tiles
+// are cut in two (measured on MI355X, Mixtral down, 592 tiles: 0.701 ->
+// 0.671 ms; with 16 rounds, gate/up, the cut made it slower). Counted per
+// workgroup from the expert histogram (the valid entries are the first
+// sum(ceil(hist / 128)), in expert order); it moves work between workgroups,
+// never changes which rows are computed.
+__device__ __forceinline__ int bs_tail_from(const MoeBsParams& p) {
+    if (p.ncu <= 0) return p.grid_m;
+    const int lane = threadIdx.x & 63;
+    int nb = 0, un = 0;
+    for (int x = lane; x < p.E; x += 64) {
+        const int h = p.hist[x];
+        const int b = h > 0 ? (h + 127) / 128 : 0;
+        nb += b;
+        un += (b + 1) / 2;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        nb += __shfl_xor(nb, o);
+        un += __shfl_xor(un, o);
+    }
+    const int last = (un * p.tiles_n) % p.ncu;
+    if (un * p.tiles_n >= 4 * p.ncu || last == 0 || 2 * last > p.ncu) return p.grid_m;
+    return max(0, min(nb, p.grid_m) - 2 * ((last + p.tiles_n - 1) / p.tiles_n));
+}
 
 // The expert's weight source of a tile at column n0: base, extent (bytes from
 // the base; N-contiguous columns past N read the next row's bytes, which only
@@ -365,8 +395,10 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void moe_blockscale8_kernel(const Mo
     const int ed = p.expt_data[pm];
     const int e = ed & 0xFFFF, b = ed >> 16;
     if (ed < 0 || e >= p.E) return;  // uniform: -1 or a malformed entry
-    if ((b & 1) && pm > 0 && p.expt_data[pm - 1] == ed - 0x10000) return;  // the pair's first word computes it
-    const bool pair = !(b & 1) && pm + 1 < p.grid_m && p.expt_data[pm + 1] == ed + 0x10000;
+    const int tail_from = __builtin_amdgcn_readfirstlane(bs_tail_from(p));
+    // the pair's first word computes it (unless this word is in the tail)
+    if ((b & 1) && pm > 0 && pm < tail_from && p.expt_data[pm - 1] == ed - 0x10000) return;
+    const bool pair = !(b & 1) && pm + 1 < tail_from && pm + 1 < p.grid_m && p.expt_data[pm + 1] == ed + 0x10000;
     const int m_e = p.hist[e], start = p.offs[e];
     const int row0 = b * 128;
     const int rows = min(m_e - row0, pair ? BS_BM : 128);
@@ -570,6 +602,7 @@ static int moe_blockscale_impl(const void* X, const void* W, void* Y, const floa
     const int64_t kpg = group_k / BS_KT;  // K-tiles per scale group
     if (bs8_on && K % BS_KT == 0 && group_k % BS_KT == 0 && (kpg & (kpg - 1)) == 0) {
         p.tiles_n = (int)((N + BS_BN - 1) / BS_BN);
+        p.ncu = cu_count();
         const int64_t nblk = grid_m * p.tiles_n;
         if (nblk == 0) return 0;
         const bool ntile = group_n % 32 == 0;

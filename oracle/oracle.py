@@ -498,7 +498,8 @@ def _tiles_rows(gather, hist, offs, expt_data, topk, E, block_m=128):
         if n <= 0:
             continue
         sidx = int(offs[e]) + b * block_m + np.arange(n)
-        out.append((e, sidx, np.asarray(gather)[sidx] // topk))
+        # no gather: sorted row s reads row s of X (the down projection's input)
+        out.append((e, sidx, sidx if gather is None else np.asarray(gather)[sidx] // topk))
     return out
 
 

@@ -521,21 +521,28 @@ def test_moe_blockscale_padded_rows(orc):
     check_rows(orc, host_bf16_f32(Yp[:, :N].contiguous()), ref)
 
 
-def test_moe_blockscale_mixtral_group128(orc):
-    """Mixtral-8x7B gate/up (T=4096, E=8, top-2, K=4096, N=28672) with 1x128
+@pytest.mark.parametrize("proj", ["gate_up", "down"])
+def test_moe_blockscale_mixtral_group128(orc, proj):
+    """Mixtral-8x7B gate/up (T=4096, E=8, top-2, K=4096, N=28672) and down
+    (the 8192 expert-sorted rows, K=14336, N=4096: few enough tiles that the
+    last round's block pairs are computed as single blocks) with 1x128
     activation groups and 128x128 weight blocks, every routed row against the
     fp32 oracle with the same group scales."""
     require_gpu()
-    T, E, topk, K, N = 4096, 8, 2, 4096, 28672
+    T, E, topk = 4096, 8, 2
     hist, offs, gather, ed = mixtral_routing(orc, T, E, topk, 77)
-    X, xs = orc.quant_rowwise(orc.randn_bf16((T, K), seed=78), 128, "fp8")   # xs [T, K/128]
+    if proj == "gate_up":
+        K, N, rows, tk, gat = 4096, 28672, T, topk, gather
+    else:
+        K, N, rows, tk, gat = 14336, 4096, T * topk, 1, None
+    X, xs = orc.quant_rowwise(orc.randn_bf16((rows, K), seed=78), 128, "fp8")   # xs [rows, K/128]
     W, _ = device_weights_fp8(E, N, K, seed=79)
     rng = np.random.default_rng(80)
     ws = (rng.random((E, K // 128, N // 128)) * 2e-4 + 1e-4).astype(np.float32)
-    Y = run_moe_bs(X, W, hist, offs, gather, ed, topk, xs, ws, 128, 128)
-    ref = orc.moe_ref_f32(X, W, xs, ws, gather, hist, offs, ed, topk, group_k=128, group_n=128)
+    Y = run_moe_bs(X, W, hist, offs, gat, ed, tk, xs, ws, 128, 128)
+    ref = orc.moe_ref_f32(X, W, xs, ws, gat, hist, offs, ed, tk, group_k=128, group_n=128)
     assert not np.isnan(ref).any()
-    assert_gemm_close(Y, ref, "moe blockscale mixtral g128")
+    assert_gemm_close(Y, ref, f"moe blockscale mixtral g128 {proj}")
 
 
 def test_moe_hipkittens_modules(orc):

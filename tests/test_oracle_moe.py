@@ -101,3 +101,26 @@ def test_moe_fp32_references_match_fp64(orc):
     ref = orc.moe_mxfp4_ref(Aq, As, Bq, Bs, 0.5, bsc, w, s, eids, N, T * topk, topk, True, T * topk)
     got = orc.moe_mxfp4_ref_f32(Aq, As, Bq, Bs, 0.5, bsc, w, s, eids, N, T * topk, topk, True, T * topk)
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_moe_refs_without_gather(orc):
+    """Without a gather list (the down projection: X holds the expert-sorted
+    rows) sorted row s reads row s of X: the same outputs as a gather list
+    that names row s for every s (gather[s] = s * topk), for the fp32 and
+    fp64 references."""
+    T, E, topk, K, N = 150, 4, 2, 256, 96
+    hist, offs, gather, ed = _routing(orc, T, E, topk, 13)
+    rows = T * topk
+    X, xs = orc.quant_rowwise(orc.randn_bf16((rows, K), seed=14), 128, "fp8")
+    W, _ = orc.quant_rowwise(orc.randn_bf16((E * N, K), seed=15, std=0.05), None, "fp8")
+    W = W.reshape(E, N, K)
+    rng = np.random.default_rng(16)
+    ws = (rng.random((E, K // 128, (N + 127) // 128)) + 0.5).astype(np.float32)
+    ident = (np.arange(rows, dtype=np.int32) * topk).astype(np.int32)
+    a = orc.moe_ref_f32(X, W, xs, ws, None, hist, offs, ed, 1, group_k=128, group_n=128)
+    b = orc.moe_ref_f32(X, W, xs, ws, ident, hist, offs, ed, topk, group_k=128, group_n=128)
+    assert not np.isnan(a).any()
+    np.testing.assert_array_equal(a, b[:rows])  # b has X.shape[0] * topk rows, the ones past `rows` unlisted
+    c = orc.moe_blockscale_ref(X, W, xs, ws, None, None, hist, offs, ed, 1, 128, 128)
+    d = orc.moe_blockscale_ref(X, W, xs, ws, None, ident, hist, offs, ed, topk, 128, 128)
+    np.testing.assert_array_equal(c, d[:rows])
