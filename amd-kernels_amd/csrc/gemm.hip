@@ -233,10 +233,8 @@ __global__ __launch_bounds__(64 * DENSE_WAVES_M * DENSE_WAVES_N, 1) void dense_g
 // and its K loop is bound by that traffic; the deeper ring gives the loads
 // two K-tiles of lead (measured on MI355X, with the staged epilogue below:
 // 4096 x 14336 x 4096 308.8K -> 293.7K cycles per workgroup, 179.4 -> 173.8 us).
-constexpr int STREAM_SCL = 2 * DENSE_BM * 4;       // one scale slot: 256 row + 256 column scales
-constexpr int STREAM_STG_PITCH = 144;              // staged row: 64 bf16 columns + 16 bytes
-constexpr int STREAM_STG = 32 * STREAM_STG_PITCH;  // one wave's staging area: 32 rows
-constexpr int HALF_NS = 3;                         // ring stages of a half tile
+constexpr int STREAM_SCL = 2 * DENSE_BM * 4;  // one scale slot: 256 row + 256 column scales
+constexpr int HALF_NS = 3;                    // ring stages of a half tile
 
 template <int MODE>
 constexpr int stream_ring_lds() {
@@ -309,21 +307,8 @@ struct DirectEpi {
             lds_load4(static_cast<const float*>(p->sb) + n0, (uint32_t)rows_b * 4u, slot + DENSE_BM * 4 + wave * 256, off);
         }
     }
-    // Stores: per (n-tile pair ip, m-tile j) the wave's 32 rows x 64 columns
-    // (2 n-tiles: one 128-byte line per row) are scaled, converted and written
-    // to the wave's staging area (row pitch STREAM_STG_PITCH; each lane writes
-    // its 4 consecutive columns of a register group as 8 bytes), then read
-    // back so that lane l holds 16 bytes of row l / 8 at column 8 * (l % 8),
-    // and written with four 16-byte buffer stores, each covering 8 whole
-    // 128-byte lines of C (32 per wave and tile). Stores of 32-byte pieces
-    // straight from the accumulator layout (32 partial lines per instruction)
-    // held the epilogue up for longer: all CUs store their tiles at about the
-    // same time and those partial lines cost the memory path more requests.
-    // Lanes whose row or columns lie outside C get an offset past the buffer,
-    // so every wave issues the same stores whatever the tile's edge. N % 4 == 0
-    // leaves one partial case: 8 columns of which the last 4 lie past N (the
-    // store would run into the next row); in a wave whose columns end there,
-    // such lanes write their first 4 columns with an extra 8-byte store.
+    // Stores through the wave's staging area (stream_store_tile), with the
+    // tile's row and column scales from its LDS slot.
     __device__ void end(int k, v16f (&acc)[TN][TM]) {
         int m0, n0;
         seq->coords(k, m0, n0);
@@ -331,71 +316,17 @@ struct DirectEpi {
         const int khalf = lane >> 5, r = lane & 31;
         const HKQ_LDS float* sl = reinterpret_cast<const HKQ_LDS float*>(scl + (k & 1) * STREAM_SCL);
         const int mw0 = m0 + wm * TM * 32, nw0 = n0 + wn * TN * 32;
-        uint16_t* base = p->C + (int64_t)mw0 * p->ldc + nw0;
-        const auto rc = make_rsrc(base, 0x7FFFFFFFu);
-        const int rows = p->M - mw0, cols = p->N - nw0;  // of the wave's sub-tile inside C
-        const bool ragged = cols < TN * 32 && (cols & 7) != 0;
         float rs[TM];
 #pragma unroll
         for (int j = 0; j < TM; ++j) rs[j] = MODE == MODE_A8W8 ? sl[wm * TM * 32 + j * 32 + r] : 1.0f;
-        // The lane's offsets come from an opaque copy of the lane each tile:
-        // left visible, the compiler hoists them out of the tile loop as
-        // invariants and spills them.
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        const int sr = ln >> 3, sc = (ln & 7) * 8;  // the store lane's row in an 8-row group, first column
-        const uint32_t so = (uint32_t)((sr * p->ldc + sc) * 2);
-        const uint32_t wr_lo = (uint32_t)(r * STREAM_STG_PITCH + 8 * khalf);
-        const uint32_t rd_lo = (uint32_t)(sr * STREAM_STG_PITCH + (ln & 7) * 16);
-        static_assert(TN % 2 == 0, "n-tiles in pairs");
-#pragma unroll
-        for (int ip = 0; ip < TN; ip += 2) {
-            v4f cs[2][4];
-#pragma unroll
-            for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    cs[ii][g] = MODE == MODE_A8W8
-                                    ? *reinterpret_cast<const HKQ_LDS v4f*>(sl + DENSE_BM + wn * TN * 32 + (ip + ii) * 32 +
-                                                                            8 * g + 4 * khalf)
-                                    : v4f{1.f, 1.f, 1.f, 1.f};
-#pragma unroll
-            for (int j = 0; j < TM; ++j) {
-#pragma unroll
-                for (int ii = 0; ii < 2; ++ii) {
-                    // Explicit reads out of the accumulator registers, in store
-                    // order: the compiler's own copies tend to be hoisted to the
-                    // start of the epilogue, all 256 of them live at once.
-                    float v[16];
-#pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[ip + ii][j][e]));
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const float a = rs[j];
-                        const uint32_t lo = pk_bf16(v[4 * g + 0] * a * cs[ii][g][0], v[4 * g + 1] * a * cs[ii][g][1]);
-                        const uint32_t hi = pk_bf16(v[4 * g + 2] * a * cs[ii][g][2], v[4 * g + 3] * a * cs[ii][g][3]);
-                        *reinterpret_cast<HKQ_LDS v2i*>(stg + wr_lo + (ii * 32 + 8 * g) * 2) = v2i{(int)lo, (int)hi};
-                    }
-                }
-                // LDS operations of a wave complete in order: the reads see the
-                // writes above, and the next group's writes follow these reads
-                v4i dv[4];
-#pragma unroll
-                for (int pp = 0; pp < 4; ++pp)
-                    dv[pp] = *reinterpret_cast<const HKQ_LDS v4i*>(stg + rd_lo + pp * 8 * STREAM_STG_PITCH);
-#pragma unroll
-                for (int pp = 0; pp < 4; ++pp) {
-                    const int m = j * 32 + pp * 8 + sr, c = ip * 32 + sc;
-                    const uint32_t at = so + (uint32_t)(((j * 32 + pp * 8) * p->ldc + ip * 32) * 2);
-                    __builtin_amdgcn_raw_buffer_store_b128(dv[pp], rc, m < rows && c + 8 <= cols ? at : OOB, 0, 0);
-                    if (ragged)
-                        __builtin_amdgcn_raw_buffer_store_b64(v2i{dv[pp][0], dv[pp][1]}, rc,
-                                                              m < rows && c + 4 == cols ? at : OOB, 0, 0);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
+        stream_store_tile<TM, TN>(
+            acc, stg, p->C + (int64_t)mw0 * p->ldc + nw0, p->ldc, p->M - mw0, p->N - nw0, rs,
+            [&](int i, int g) {
+                return MODE == MODE_A8W8 ? *reinterpret_cast<const HKQ_LDS v4f*>(sl + DENSE_BM + wn * TN * 32 + i * 32 +
+                                                                                 8 * g + 4 * khalf)
+                                         : v4f{1.f, 1.f, 1.f, 1.f};
+            },
+            lane);
     }
 };
 

@@ -361,4 +361,94 @@ __device__ __forceinline__ void gemm_stream(const Seq& seq, AOff& a_off, const B
     tile_barrier<0>();  // no load in flight, every wave past its reads
 }
 
+// Epilogue stores of a stream tile, shared by the stream kernels: per (n-tile
+// pair ip, m-tile j) the wave's 32 rows x 64 columns (2 n-tiles: one 128-byte
+// line per row) are scaled, converted and written to the wave's staging area
+// (row pitch STREAM_STG_PITCH; each lane writes its 4 consecutive columns of a
+// register group as 8 bytes), then read back so that lane l holds 16 bytes of
+// row l / 8 at column 8 * (l % 8), and written with four 16-byte buffer
+// stores, each covering 8 whole 128-byte lines of C (32 per wave and tile).
+// Stores of 32-byte pieces straight from the accumulator layout (32 partial
+// lines per instruction) held the epilogue up for longer: all CUs store their
+// tiles at about the same time and those partial lines cost the memory path
+// more requests. The stores are non-temporal: C is not read again by the
+// kernel, and kept out of the caches it leaves them to the operands (measured
+// on MI355X, A8W8 4096x28672x4096: 362.6 -> 332.0 us; 8192x28672x4096: 708 ->
+// 662 us; 4096x14336x4096 within noise); whole lines keep them merged (the
+// same policy on 32-byte pieces was 24% slower).
+// Lanes whose row or columns lie outside C get an offset past the buffer, so
+// every wave issues the same stores whatever the tile's edge. N % 4 == 0
+// leaves one partial case: 8 columns of which the last 4 lie past N (the
+// store would run into the next row); in a wave whose columns end there, such
+// lanes write their first 4 columns with an extra 8-byte store.
+//   base: C at the wave's first row and column, ldc its row pitch (elements);
+//   rows / cols: of the wave's sub-tile inside C; rs[j]: the row scale of the
+//   lane's row (lane % 32) of m-tile j; col_scale(i, g): the 4 column scales of
+//   n-tile i, columns 8g + 4 (lane / 32) + 0..3.
+constexpr int STREAM_STG_PITCH = 144;              // staged row: 64 bf16 columns + 16 bytes
+constexpr int STREAM_STG = 32 * STREAM_STG_PITCH;  // one wave's staging area: 32 rows
+constexpr int CPOL_NT = 2;                         // buffer-store cache policy: non-temporal
+
+template <int TM, int TN, typename ColScale>
+__device__ __forceinline__ void stream_store_tile(v16f (&acc)[TN][TM], HKQ_LDS uint8_t* stg, uint16_t* base, int64_t ldc,
+                                                  int rows, int cols, const float (&rs)[TM], ColScale col_scale,
+                                                  int lane) {
+    static_assert(TN % 2 == 0, "n-tiles in pairs");
+    const int khalf = lane >> 5, r = lane & 31;
+    const auto rc = make_rsrc(base, 0x7FFFFFFFu);
+    const bool ragged = cols < TN * 32 && (cols & 7) != 0;
+    // The lane's offsets come from an opaque copy of the lane each tile: left
+    // visible, the compiler hoists them out of the tile loop as invariants and
+    // spills them.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int sr = ln >> 3, sc = (ln & 7) * 8;  // the store lane's row in an 8-row group, first column
+    const uint32_t so = (uint32_t)((sr * ldc + sc) * 2);
+    const uint32_t wr_lo = (uint32_t)(r * STREAM_STG_PITCH + 8 * khalf);
+    const uint32_t rd_lo = (uint32_t)(sr * STREAM_STG_PITCH + (ln & 7) * 16);
+#pragma unroll
+    for (int ip = 0; ip < TN; ip += 2) {
+        v4f cs[2][4];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) cs[ii][g] = col_scale(ip + ii, g);
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+                // Explicit reads out of the accumulator registers, in store
+                // order: the compiler's own copies tend to be hoisted to the
+                // start of the epilogue, all 256 of them live at once.
+                float v[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[ip + ii][j][e]));
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float a = rs[j];
+                    const uint32_t lo = pk_bf16(v[4 * g + 0] * a * cs[ii][g][0], v[4 * g + 1] * a * cs[ii][g][1]);
+                    const uint32_t hi = pk_bf16(v[4 * g + 2] * a * cs[ii][g][2], v[4 * g + 3] * a * cs[ii][g][3]);
+                    *reinterpret_cast<HKQ_LDS v2i*>(stg + wr_lo + (ii * 32 + 8 * g) * 2) = v2i{(int)lo, (int)hi};
+                }
+            }
+            // LDS operations of a wave complete in order: the reads see the
+            // writes above, and the next group's writes follow these reads
+            v4i dv[4];
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp)
+                dv[pp] = *reinterpret_cast<const HKQ_LDS v4i*>(stg + rd_lo + pp * 8 * STREAM_STG_PITCH);
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+                const int m = j * 32 + pp * 8 + sr, c = ip * 32 + sc;
+                const uint32_t at = so + (uint32_t)(((j * 32 + pp * 8) * ldc + ip * 32) * 2);
+                __builtin_amdgcn_raw_buffer_store_b128(dv[pp], rc, m < rows && c + 8 <= cols ? at : OOB, 0, CPOL_NT);
+                if (ragged)
+                    __builtin_amdgcn_raw_buffer_store_b64(v2i{dv[pp][0], dv[pp][1]}, rc,
+                                                          m < rows && c + 4 == cols ? at : OOB, 0, CPOL_NT);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
 }  // namespace hkq

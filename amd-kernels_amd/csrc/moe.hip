@@ -437,8 +437,8 @@ static int launch_moe_narrow(const MoeParams& p, int64_t routed_rows, hipStream_
 // are consecutive blocks of one expert (256-row tiles) form one stream: the
 // next tile's first K-tiles load during the current tile's last ones, its
 // gather entries reach LDS while the current tile computes (the tiled kernel
-// waits for them in each tile's prologue), and the epilogue stores C from
-// registers. The lone blocks run before or after the stream with the tiled
+// waits for them in each tile's prologue), and the epilogue stages C through
+// LDS areas that take the place of the unit-building lists. The lone blocks run before or after the stream with the tiled
 // kernel's block code (64-row blocks on a 3-stage ring: a 64 x 256 tile has
 // little MFMA work to hide its loads behind).
 // LEAN scale layouts only (no bias; column scales absent, per expert or per
@@ -454,7 +454,11 @@ constexpr int MS_CNT = MS_RL + MS_MAXU * 16;  // unit counts
 constexpr int MS_MAXE = 1024;                 // routing entries (the host checks)
 constexpr int MS_WP = MS_CNT + 64;            // whole pairs: e, row0, start, rows (4 ints each)
 constexpr int MS_RP = MS_WP + MS_MAXE / 2 * 16;  // lone blocks: the entry (1 int each)
-constexpr int MS_LDS = MS_RP + MS_MAXE * 4;
+// the epilogue's staging areas (one per wave) take the place of the whole-pair
+// and lone-block lists, which are read only while the unit lists are built
+constexpr int MS_STG = MS_WP;
+constexpr int MS_LDS = MS_RP + MS_MAXE * 4 > MS_STG + MOE_WM * MOE_WN * STREAM_STG ? MS_RP + MS_MAXE * 4
+                                                                                     : MS_STG + MOE_WM * MOE_WN * STREAM_STG;
 static_assert(MS_LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
 static_assert(DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 2, MOE_TN, 128>::lds_bytes(2) <= MS_WL &&
                   DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 1, MOE_TN, 128>::lds_bytes(3) <= MS_WL,
@@ -529,10 +533,10 @@ struct MoeStreamSeq {
     }
 };
 
-// Epilogue of a stream tile: the A8W8 stream's register epilogue (one 16-byte
-// store per lane and (n-tile, m-tile, 16 columns), lanes outside C sent past
-// the buffer) into the tile's sorted rows, with the row scales (gathered per
-// token) and the column scales fetched into LDS when the tile begins.
+// Epilogue of a stream tile: the dense stream's staged stores
+// (stream_store_tile) into the tile's sorted rows, with the row scales
+// (gathered per token) and the column scales fetched into LDS when the tile
+// begins.
 struct MoeStreamEpi {
     static constexpr int TM = 4, TN = MOE_TN;
     // per wave: the epilogue's C stores, then begin()'s row-scale, column-scale
@@ -541,6 +545,7 @@ struct MoeStreamEpi {
     const MoeStreamSeq* seq;
     const MoeParams* p;
     HKQ_LDS uint8_t* scl;
+    HKQ_LDS uint8_t* stg;  // this wave's STREAM_STG bytes of staging
     int lane, wave;
     __device__ void begin(int k) {
         const MoeStreamSeq::Unit u = seq->unit(k);
@@ -562,65 +567,17 @@ struct MoeStreamEpi {
         const HKQ_LDS float* sl = reinterpret_cast<const HKQ_LDS float*>(scl + (k & 1) * MS_SLOT);
         const int s0 = u.start + u.row0;
         const int mw0 = wm * TM * 32, nw0 = u.n0 + wn * TN * 32;
-        uint16_t* base = p->Y + (int64_t)(s0 + mw0) * p->sym + nw0;
-        const auto rc = make_rsrc(base, 0x7FFFFFFFu);
-        const int rows = min(u.rows, p->y_rows - s0) - mw0, cols = p->N - nw0;
-        const bool ragged = cols < TN * 32 && (cols & 7) != 0;
-        uint32_t roff[TM];
         float rs[TM];
-        const int kc = 8 * khalf;
 #pragma unroll
-        for (int j = 0; j < TM; ++j) {
-            const int m = j * 32 + r;
-            roff[j] = m < rows ? (uint32_t)((m * p->sym + kc) * 2) : OOB;
-            asm volatile("" : "+v"(roff[j]));
-            rs[j] = p->xs ? sl[mw0 + m] : 1.0f;
-        }
-        static_assert(TN % 2 == 0, "n-tiles in pairs");
-#pragma unroll
-        for (int ip = 0; ip < TN; ip += 2) {
-            v4f cs[2][4];
-#pragma unroll
-            for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    cs[ii][g] = p->ws ? *reinterpret_cast<const HKQ_LDS v4f*>(sl + 256 + wn * TN * 32 + (ip + ii) * 32 +
-                                                                             8 * g + 4 * khalf)
-                                      : v4f{1.f, 1.f, 1.f, 1.f};
-#pragma unroll
-            for (int j = 0; j < TM; ++j) {
-#pragma unroll
-                for (int ii = 0; ii < 2; ++ii) {
-                    const int i = ip + ii;
-                    float v[16];
-#pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[i][j][e]));
-                    uint32_t w[4][2];
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const float a = rs[j];
-                        w[g][0] = pk_bf16(v[4 * g + 0] * a * cs[ii][g][0], v[4 * g + 1] * a * cs[ii][g][1]);
-                        w[g][1] = pk_bf16(v[4 * g + 2] * a * cs[ii][g][2], v[4 * g + 3] * a * cs[ii][g][3]);
-                    }
-#pragma unroll
-                    for (int q = 0; q < 2; ++q) {
-                        const auto s0v = __builtin_amdgcn_permlane32_swap(w[2 * q][0], w[2 * q + 1][0], false, false);
-                        const auto s1v = __builtin_amdgcn_permlane32_swap(w[2 * q][1], w[2 * q + 1][1], false, false);
-                        const int c = i * 32 + 16 * q;
-                        const int left = cols - c;
-                        const uint32_t off = kc + 8 <= left ? roff[j] + (uint32_t)(c * 2) : OOB;
-                        __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)s0v[0], (int)s1v[0], (int)s0v[1], (int)s1v[1]},
-                                                               rc, off, 0, 0);
-                        if (ragged) {
-                            const uint32_t off4 = kc + 4 == left ? roff[j] + (uint32_t)(c * 2) : OOB;
-                            __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)s0v[0], (int)s1v[0]}, rc, off4, 0, 0);
-                        }
-                    }
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
+        for (int j = 0; j < TM; ++j) rs[j] = p->xs ? sl[mw0 + j * 32 + r] : 1.0f;
+        stream_store_tile<TM, TN>(
+            acc, stg, p->Y + (int64_t)(s0 + mw0) * p->sym + nw0, p->sym, min(u.rows, p->y_rows - s0) - mw0,
+            p->N - nw0, rs,
+            [&](int i, int g) {
+                return p->ws ? *reinterpret_cast<const HKQ_LDS v4f*>(sl + 256 + wn * TN * 32 + i * 32 + 8 * g + 4 * khalf)
+                             : v4f{1.f, 1.f, 1.f, 1.f};
+            },
+            lane);
     }
 };
 
@@ -740,7 +697,7 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
         TableOff<MoeWhole::LB> b_off;
         if constexpr (BT) b_off = dense_offs_t<MoeWhole::NW, MoeWhole::LB>(wave, lane, p.swk);
         else b_off = dense_offs<MoeWhole::NW, 128, MoeWhole::LB>(wave, lane, p.swn);
-        MoeStreamEpi epi{&seq, &p, smem + MS_SCL, lane, wave};
+        MoeStreamEpi epi{&seq, &p, smem + MS_SCL, smem + MS_STG + wave * STREAM_STG, lane, wave};
         v16f acc[MOE_TN][4];
         gemm_stream<MODE_A8W8, MOE_WM, MOE_WN, 4, MOE_TN, BT>(seq, a_off, b_off, smem, lane, wave, acc, epi);
     }
