@@ -602,14 +602,17 @@ struct NarrowFrag {
     uint32_t sb[NT], sa[MT];  // FP4: e8m0 scales of the step's 4 blocks (byte q is the lane's)
 };
 
-template <int MT, int NT>
-constexpr int narrow_depth() { return NT >= 4 ? 4 : NT == 2 ? 6 : 8; }
+// K-steps of loads in flight per wave (measured on MI355X: FP8 with two
+// column tiles per workgroup 8 rather than 6, 1x6144x4096 8.33 -> 7.94 us;
+// deeper rings for one or four column tiles, and for FP4, were slower)
+template <int MODE, int MT, int NT>
+constexpr int narrow_depth() { return NT >= 4 ? 4 : NT == 2 ? (MODE == MODE_MXFP4 ? 6 : 8) : 8; }
 
 template <int MODE, int MT, int NT>
 __global__ __launch_bounds__(64 * NARROW_WAVES) void narrow_gemm_kernel(const DenseParams pb) {
     constexpr bool FP4 = MODE == MODE_MXFP4;
     constexpr int SB = FP4 ? 64 : 128;  // bytes of a row per 128-value K-step
-    constexpr int DEPTH = narrow_depth<MT, NT>();
+    constexpr int DEPTH = narrow_depth<MODE, MT, NT>();
     __shared__ v4f red[NARROW_WAVES][NT][MT][64];
     const DenseParams p = batch_slice(pb);
     const int lane = threadIdx.x & 63;
