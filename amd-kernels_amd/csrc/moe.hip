@@ -59,12 +59,11 @@ constexpr int MOE_BM = 128;  // rows per OGS routing block
 constexpr int MOE_WM = 2, MOE_WN = 2, MOE_TN = 4, MOE_BN = MOE_WN * MOE_TN * 32;
 
 // Rows [row0, row0 + TM*64) of expert e (sorted rows start + row0 + r) times
-// columns [n0, n0 + 256). LEAN: no bias, and the column scales absent, one
+// columns [n0, n0 + TN*64). LEAN: no bias, and the column scales absent, one
 // per expert or one per channel readable as float4 (ws_vec); the epilogue
 // then carries no code for the other layouts.
-template <int TM, int KTB, int NS, bool LEAN, bool BT = false>
+template <int TM, int KTB, int NS, bool LEAN, bool BT = false, int TN = MOE_TN>
 __device__ __forceinline__ void moe_block(const MoeParams& p, int e, int row0, int n0, HKQ_LDS uint8_t* smem) {
-    constexpr int TN = MOE_TN;
     using Cfg = DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, TM, TN, KTB>;
     constexpr int NW = Cfg::NW, BM = Cfg::BM, BN = Cfg::BN, LA = Cfg::LA, LB = Cfg::LB;
     const int lane = threadIdx.x & 63;
@@ -460,8 +459,17 @@ constexpr int MS_STG = MS_WP;
 constexpr int MS_LDS = MS_RP + MS_MAXE * 4 > MS_STG + MOE_WM * MOE_WN * STREAM_STG ? MS_RP + MS_MAXE * 4
                                                                                      : MS_STG + MOE_WM * MOE_WN * STREAM_STG;
 static_assert(MS_LDS <= 160 * 1024, "LDS budget of a CDNA4 CU");
+// Lone blocks run as 128-column pieces (256 with N-contiguous weights, whose
+// K-tiles are 256 columns wide): twice as many pieces as 256-column tiles, so
+// that they spread over more workgroups (measured on MI355X, Mixtral down: the
+// workgroups with a lone tile after their two stream tiles ended ~85 us after
+// the others).
+constexpr int MS_LONE_BN = 128, MS_LONE_TN = MS_LONE_BN / (MOE_WN * 32);
+constexpr int MS_LONE_NS1 = 5, MS_LONE_NS2 = 4;  // ring stages of 64- and 128-row pieces
 static_assert(DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 2, MOE_TN, 128>::lds_bytes(2) <= MS_WL &&
-                  DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 1, MOE_TN, 128>::lds_bytes(3) <= MS_WL,
+                  DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 1, MOE_TN, 128>::lds_bytes(3) <= MS_WL &&
+                  DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 2, MS_LONE_TN, 128>::lds_bytes(MS_LONE_NS2) <= MS_WL &&
+                  DenseCfg<MODE_A8W8, MOE_WM, MOE_WN, 1, MS_LONE_TN, 128>::lds_bytes(MS_LONE_NS1) <= MS_WL,
               "the tiled blocks after the stream leave the unit lists alone");
 
 struct MoeStreamSeq {
@@ -641,7 +649,8 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
         }
         const int k = lane;
         const int w = b + k * G, r = (G - 1 - b) + k * G;
-        const bool wl_live = w < nwp * p.tiles_n, rl_live = r < nrp * p.tiles_n;
+        const int tiles_l = BT ? p.tiles_n : (p.N + MS_LONE_BN - 1) / MS_LONE_BN;
+        const bool wl_live = w < nwp * p.tiles_n, rl_live = r < nrp * tiles_l;
         if (wl_live) {
             int qi, tn;
             pair_walk(w, nwp, p.tiles_n, p.group_m, p.xcd_cols, qi, tn);
@@ -655,10 +664,10 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
         }
         if (rl_live) {
             int qi, tn;
-            pair_walk(r, nrp, p.tiles_n, p.group_m, p.xcd_cols, qi, tn);
+            pair_walk(r, nrp, tiles_l, p.group_m, BT ? p.xcd_cols : (tiles_l >= 32 ? 1 : 0), qi, tn);
             HKQ_LDS int* d = rl + 4 * k;
             d[0] = rp[qi];
-            d[1] = tn * MOE_BN;
+            d[1] = tn * (BT ? MOE_BN : MS_LONE_BN);
         }
         const uint64_t cw = __ballot(wl_live), cr = __ballot(rl_live);
         if (lane == 0) {
@@ -674,10 +683,17 @@ __global__ __launch_bounds__(64 * MOE_WM * MOE_WN, 1) void moe_stream_kernel(con
             const int ed = __builtin_amdgcn_readfirstlane(rl[4 * i]), n0 = __builtin_amdgcn_readfirstlane(rl[4 * i + 1]);
             const int e = ed & 0xFFFF, bk = ed >> 16;
             __syncthreads();  // every wave is done with the LDS of what ran before
-            if (p.hist[e] - bk * MOE_BM <= MOE_BM / 2)
-                moe_block<1, 128, 3, true, BT>(p, e, bk * MOE_BM, n0, smem);
-            else
-                moe_block<2, 128, 2, true, BT>(p, e, bk * MOE_BM, n0, smem);
+            if constexpr (BT) {
+                if (p.hist[e] - bk * MOE_BM <= MOE_BM / 2)
+                    moe_block<1, 128, 3, true, BT>(p, e, bk * MOE_BM, n0, smem);
+                else
+                    moe_block<2, 128, 2, true, BT>(p, e, bk * MOE_BM, n0, smem);
+            } else {
+                if (p.hist[e] - bk * MOE_BM <= MOE_BM / 2)
+                    moe_block<1, 128, MS_LONE_NS1, true, false, MS_LONE_TN>(p, e, bk * MOE_BM, n0, smem);
+                else
+                    moe_block<2, 128, MS_LONE_NS2, true, false, MS_LONE_TN>(p, e, bk * MOE_BM, n0, smem);
+            }
         }
     };
     // Odd workgroups run their lone units before the stream, even ones after
@@ -740,7 +756,8 @@ static int launch_moe(MoeParams& p, hipStream_t stream) {
         const char* se = std::getenv("HKQ_MOE_STREAM");
         const int64_t ncu = cu_count();
         if (!(se && se[0] == '0') && lean && ncu > 0 && (p.K / 128) % 8 == 0 && nblk >= 2 * ncu &&
-            ((int64_t)p.grid_m * p.tiles_n + ncu - 1) / ncu <= MS_MAXU && p.grid_m <= MS_MAXE && p.sym % 8 == 0 &&
+            ((int64_t)p.grid_m * (p.wt ? p.tiles_n : (p.N + MS_LONE_BN - 1) / MS_LONE_BN) + ncu - 1) / ncu <= MS_MAXU &&
+            p.grid_m <= MS_MAXE && p.sym % 8 == 0 &&
             reinterpret_cast<uintptr_t>(p.Y) % 16 == 0 &&
             (int64_t)p.T * p.xs_tok * 4 < (1ll << 31) && 256 * p.sym * 2 < (1ll << 31)) {
             auto skern = p.wt ? moe_stream_kernel<true> : moe_stream_kernel<false>;
