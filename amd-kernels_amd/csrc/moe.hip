@@ -906,9 +906,16 @@ __device__ __forceinline__ void moe_fp4_block(const MoeFp4Params& p, int pm, int
     v16f acc[TN][TM];
     gemm_mainloop<MODE_MXFP4, MOE_WM, MOE_WN, TM, TN, KTB, NS, BT>(src, a_off, b_off, smem, lane, wave, acc);
 
+    // The output rows (gate ids) of the wave's TM*32 rows, loaded before the
+    // staging so that the store loop takes them from registers: a global load
+    // per pass of rows there held every pass up (measured on MI355X, Mixtral
+    // gate/up: 9.7 us per 256-row tile's epilogue).
+    int rid[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) rid[h] = h * 64 < TM * 32 ? gate_of(wm * TM * 32 + h * 64 + lane) : -1;
     store_tile_bf16_rows<TM, TN>(
         acc, smem, wave, lane, p.C, p.scm, p.N, nw, p.c16 != 0,
-        [&](int r) { return (int64_t)gate_of(wm * TM * 32 + r); }, [&](int j) { return rs[j]; },
+        [&](int r) { return (int64_t)__shfl(r < 64 ? rid[0] : rid[1], r & 63); }, [&](int j) { return rs[j]; },
         [&](int, int) { return make_float4(1.f, 1.f, 1.f, 1.f); }, NoBias{});
 }
 
