@@ -151,27 +151,47 @@ __device__ __forceinline__ int bs_tail_from(const MoeBsParams& p) {
 // Word index of the li-th word that computes a tile, in word order (-1 past
 // the last): a valid word (e < E) that is not the second word of a pair, the
 // second word (e | (b+1) << 16, b even) following its pair's first one before
-// tail_from. Every wave of the workgroup finds the same word, 64 words per
-// ballot.
+// tail_from. Every wave of the workgroup finds the same word, 512 words per
+// step (8 consecutive words per lane, their loads issued together).
 __device__ __forceinline__ int bs_leader(const MoeBsParams& p, int li, int tail_from) {
+    constexpr int W = 8;
     const int lane = threadIdx.x & 63;
     int base = 0, carry = -1;  // expt_data[m0 - 1]
-    for (int m0 = 0; m0 < p.grid_m; m0 += 64) {
-        const int m = m0 + lane;
-        const int ed = m < p.grid_m ? p.expt_data[m] : -1;
-        const int up = __shfl(ed, (lane + 63) & 63);
-        const int prev = lane == 0 ? carry : up;
-        const bool valid = ed >= 0 && (ed & 0xFFFF) < p.E;
-        const bool second = valid && ((ed >> 16) & 1) && m > 0 && m < tail_from && prev == ed - 0x10000;
-        const uint64_t bl = __ballot(valid && !second);
-        const int cnt = __popcll(bl);
-        if (li < base + cnt) {  // uniform
-            const int rank = __popcll(bl & ((1ull << lane) - 1ull));
-            const uint64_t hit = __ballot(valid && !second && rank == li - base);
-            return m0 + __builtin_ctzll(hit);
+    for (int m0 = 0; m0 < p.grid_m; m0 += 64 * W) {
+        const int mw = m0 + lane * W;
+        int ed[W];
+#pragma unroll
+        for (int k = 0; k < W; ++k) ed[k] = mw + k < p.grid_m ? p.expt_data[mw + k] : -1;
+        const int up = __shfl(ed[W - 1], (lane + 63) & 63);
+        uint32_t lead = 0;
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+            const int prev = k > 0 ? ed[k - 1] : (lane == 0 ? carry : up);
+            const bool valid = ed[k] >= 0 && (ed[k] & 0xFFFF) < p.E;
+            const bool second = valid && ((ed[k] >> 16) & 1) && mw + k > 0 && mw + k < tail_from && prev == ed[k] - 0x10000;
+            lead |= (valid && !second) ? 1u << k : 0u;
         }
-        base += cnt;
-        carry = __shfl(ed, 63);
+        const int c = __popc(lead);
+        int incl = c;  // inclusive prefix of the lanes' counts
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o);
+            if (lane >= o) incl += v;
+        }
+        const int total = __shfl(incl, 63);
+        if (li < base + total) {  // uniform
+            const int excl = base + incl - c;
+            const bool here = li >= excl && li < excl + c;
+            int pos = -1;
+            if (here) {
+                uint32_t mk = lead;
+                for (int q = 0; q < li - excl; ++q) mk &= mk - 1;
+                pos = mw + __builtin_ctz(mk);
+            }
+            return __shfl(pos, __builtin_ctzll(__ballot(here)));
+        }
+        base += total;
+        carry = __shfl(ed[W - 1], 63);
     }
     return -1;
 }

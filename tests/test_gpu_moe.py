@@ -477,6 +477,26 @@ def test_moe_blockscale_padding_and_malformed_entries(orc):
     check_rows(orc, Y, ref)
 
 
+@pytest.mark.parametrize("shift", [0, 1])
+def test_moe_blockscale_many_words(orc, shift):
+    """More than 512 ExptData words (64 experts x top-8 over 8192 tokens): the
+    8-wave kernel's workgroups find their computing word 512 words at a time,
+    so pairs sit across lane groups and across the 512-word steps; shift 1
+    puts a -1 word first, moving every pair by one position."""
+    require_gpu()
+    T, E, topk, K, N = 8192, 64, 8, 256, 256
+    _, hist, offs, gather, ed, X, _, W, _ = make_problem(orc, T, E, topk, K, N, 71)
+    assert len(ed) > 512
+    words = np.concatenate([np.full(shift, -1, np.int32), ed]).astype(np.int32)
+    rng = np.random.default_rng(72)
+    xs = (rng.random((T, K // 128)) * 0.02 + 0.005).astype(np.float32)
+    ws = (rng.random((E, K // 128, N // 128)) * 0.002 + 0.0005).astype(np.float32)
+    Y = run_moe_bs(X, W, hist, offs, gather, words, topk, xs, ws, 128, 128)
+    ref = orc.moe_blockscale_ref(X, W, xs, ws, None, gather, hist, offs, words, topk, 128, 128)
+    assert (~np.isnan(ref).any(axis=1)).all()  # every (token, choice) routed
+    check_rows(orc, Y, ref)
+
+
 @pytest.mark.parametrize("gk,gn", [(128, 128), (256, 1)])
 def test_moe_blockscale_block_pairs(orc, gk, gn):
     """The 8-wave kernel computes two routing blocks of an expert per workgroup
