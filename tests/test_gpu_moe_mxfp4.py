@@ -52,17 +52,19 @@ def test_moe_mxfp4(orc, T, E, topk, K, N):
     assert_gemm_close(C.float().cpu().numpy(), ref, "moe mxfp4")
 
 
-def test_moe_mxfp4_whole_and_split_tiles(orc):
+@pytest.mark.parametrize("N", [9216, 11264])
+def test_moe_mxfp4_whole_and_split_tiles(orc, N):
     """Enough 256-column tiles that most run as whole pairs of blocks while the
-    sparse last round (on 256 CUs: 8 pairs x 36 = 288 tiles = 256 + 32) runs block by block."""
+    sparse last round runs block by block: on 256 CUs, 8 pairs x 36 = 288
+    tiles = 256 + 32 and 8 pairs x 44 = 352 = 256 + 96."""
     require_gpu()
-    T, E, topk, K, N = 1000, 4, 2, 256, 9216
+    T, E, topk, K = 1000, 4, 2, 256
     Aq, As, Bq, Bs = problem(orc, T, E, K, N, 31)
     ids, s, eids = routed(orc, T, E, topk, 31)
     C = hkq.moe_mxfp4(dev_u8(Aq), dev_u8(As), dev_u8(Bq), dev_u8(Bs), dev_i32(s), dev_i32(eids), T * topk, topk)
     torch.cuda.synchronize()
     ref = orc.moe_mxfp4_ref(Aq, As, Bq, Bs, None, None, None, s, eids, N, T * topk, topk, False, T * topk)
-    assert_gemm_close(C.float().cpu().numpy(), ref, "moe mxfp4 whole + split")
+    assert_gemm_close(C.float().cpu().numpy(), ref, f"moe mxfp4 whole + split N={N}")
 
 
 def test_moe_mxfp4_gpu_routing_and_special_blocks(orc):
