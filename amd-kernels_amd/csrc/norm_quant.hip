@@ -91,9 +91,9 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
             m = max_num(m, __builtin_fabsf(y[j]));
         }
         if (MODE == NQ_FP8_G128) {
-            m = group_max<16>(m);
-            const float sc = max_num(m / 448.0f, 1e-10f);
-            const float rc = 1.0f / sc;
+            m = group_max_abs<16>(m);
+            const float sc = fp8_group_scale(m);
+            const float rc = recip_scale(sc);
             float v[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] = max_num(min_num(y[j] * rc, 448.0f), -448.0f);
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
                 if ((lane & 15) == 0) reinterpret_cast<float*>(s)[(int64_t)row * lds + (c >> 4)] = sc;
             }
         } else {
-            m = group_max<4>(m);
+            m = group_max_abs<4>(m);
             const int e = mx_scale_exp(m);
             const float mul = exp2i(-e);
             float t[8];
@@ -174,12 +174,12 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
     }
     float sc_tok = 0.0f, rc_tok = 0.0f;
     if (GROUP == 0) {
-        m = group_max<64>(m);
+        m = group_max_abs<64>(m);
         if (lane == 0) wmax[wave] = m;
         __syncthreads();
         m = max_num(max_num(wmax[0], wmax[1]), max_num(wmax[2], wmax[3]));
-        sc_tok = max_num(m / 448.0f, 1e-10f);
-        rc_tok = 1.0f / sc_tok;
+        sc_tok = fp8_group_scale(m);
+        rc_tok = recip_scale(sc_tok);
         if (t == 0) s[row] = sc_tok;
     }
 #pragma unroll
@@ -191,9 +191,9 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
             float mg = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) mg = max_num(mg, __builtin_fabsf(act[i][j]));
-            mg = group_max<16>(mg);
-            sc = max_num(mg / 448.0f, 1e-10f);
-            rc = 1.0f / sc;
+            mg = group_max_abs<16>(mg);
+            sc = fp8_group_scale(mg);
+            rc = recip_scale(sc);
         }
         float v[8];
 #pragma unroll

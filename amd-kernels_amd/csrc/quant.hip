@@ -82,14 +82,14 @@ __global__ __launch_bounds__(256) void per_token_kernel(const uint16_t* __restri
         v[c] = ch < nch ? ld_stream16(xr + ch) : make_uint4(0, 0, 0, 0);
         m = max_num(m, amax8(v[c]));
     }
-    m = group_max<64>(m);
+    m = group_max_abs<64>(m);
     __shared__ float red[4];
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
     m = max_num(max_num(red[0], red[1]), max_num(red[2], red[3]));
     const float qmax = KIND == KIND_FP8 ? 448.0f : 127.0f;
-    const float sc = max_num(m / qmax, 1e-10f);
-    const float r = 1.0f / sc;
+    const float sc = KIND == KIND_FP8 ? fp8_group_scale(m) : max_num(m / qmax, 1e-10f);
+    const float r = KIND == KIND_FP8 ? recip_scale(sc) : 1.0f / sc;
     if (tid == 0) s[row] = sc;
     uint2* qr = reinterpret_cast<uint2*>(q + row * ldq);
 #pragma unroll
@@ -117,9 +117,9 @@ __global__ __launch_bounds__(256) void group_kernel(const uint16_t* __restrict__
         const int64_t row = ok ? ch / cpr : 0, col = ok ? ch - row * cpr : 0;
         uint4 v = ok ? ld_stream16(reinterpret_cast<const uint4*>(x + row * ldx) + col)
                      : make_uint4(0, 0, 0, 0);
-        float m = group_max<GL>(amax8(v));
-        const float sc = max_num(m / qmax, 1e-10f);
-        const float r = 1.0f / sc;
+        float m = group_max_abs<GL>(amax8(v));
+        const float sc = KIND == KIND_FP8 ? fp8_group_scale(m) : max_num(m / qmax, 1e-10f);
+        const float r = KIND == KIND_FP8 ? recip_scale(sc) : 1.0f / sc;
         if (ok) {
             reinterpret_cast<uint2*>(q + row * ldq)[col] = encode8<KIND>(v, r);
             if ((threadIdx.x & (GL - 1)) == 0) s[row * lds + col / GL] = sc;
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(const uint16_t* __restric
         const int64_t row = ok ? ch / cpr : 0, col = ok ? ch - row * cpr : 0;
         uint4 v = ok ? ld_stream16(reinterpret_cast<const uint4*>(x + row * ldx) + col)
                      : make_uint4(0, 0, 0, 0);
-        const float m = group_max<4>(amax8(v));
+        const float m = group_max_abs<4>(amax8(v));
         uint32_t w[4] = {v.x, v.y, v.z, v.w};
         if (FP4) {
             const int e = mx_scale_exp(m);
