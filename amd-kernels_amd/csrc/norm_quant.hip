@@ -18,6 +18,9 @@
 
 namespace hkq {
 
+// buffer-instruction cache policies (gfx950): non-temporal loads and stores
+constexpr int CPOL_NT_LD = 2, CPOL_NT_ST = 2;
+
 // MXFP4 elements rounded to nearest even (NQ_MXFP4) or floored by the
 // reference module's ladder (NQ_MXFP4_FLOOR); the shared exponent is the same
 enum { NQ_FP8_G128 = 0, NQ_MXFP4 = 1, NQ_MXFP4_FLOOR = 2 };
@@ -48,23 +51,33 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
                                                             void* __restrict__ s, int M, int D, int64_t ldx,
                                                             int64_t ldq, int64_t lds, float eps) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= M) return;  // wave-uniform; no barriers below
+    // wave-uniform (made visibly so: the buffer resources below are then built in SGPRs)
+    const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    if (row >= M) return;  // no barriers below
     const int nch = D >> 3;
-    const uint4* xr = reinterpret_cast<const uint4*>(x + (int64_t)row * ldx);
-    const uint4* wr = reinterpret_cast<const uint4*>(w);
+    // Buffer loads and stores over the row: chunks past D read zero and their
+    // stores are dropped by the buffer bounds, so no lane branches around them
+    // (only whole chunk columns past D are skipped, a wave-uniform test).
+    const auto rx = make_rsrc(x + (int64_t)row * ldx, (uint32_t)D * 2u);
+    const auto rw = make_rsrc(w, (uint32_t)D * 2u);
     // x and the weight are both requested before the reduction, so the
     // weight's (cache-resident) loads overlap the row's HBM loads
     uint4 xv[NC], wv[NC];
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
-        const int c = lane + 64 * i;
-        xv[i] = c < nch ? ld_stream16(xr + c) : make_uint4(0, 0, 0, 0);
+        xv[i] = make_uint4(0, 0, 0, 0);
+        if (64 * i < nch) {
+            const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(lane + 64 * i) * 16u, 0, CPOL_NT_LD);
+            xv[i] = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+        }
     }
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
-        const int c = lane + 64 * i;
-        wv[i] = c < nch ? wr[c] : make_uint4(0, 0, 0, 0);
+        wv[i] = make_uint4(0, 0, 0, 0);
+        if (64 * i < nch) {
+            const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)(lane + 64 * i) * 16u, 0, 0);
+            wv[i] = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+        }
     }
     float ss = 0.0f;
 #pragma unroll
@@ -76,6 +89,9 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
     }
     ss = group_sum<64>(ss);
     const float r = 1.0f / __builtin_sqrtf(ss / (float)D + eps);
+    const auto rq = make_rsrc(q + (int64_t)row * ldq, (uint32_t)(MODE == NQ_FP8_G128 ? D : D / 2));
+    const auto rs = MODE == NQ_FP8_G128 ? make_rsrc(static_cast<float*>(s) + (int64_t)row * lds, (uint32_t)(D / 128) * 4u)
+                                        : make_rsrc(static_cast<uint8_t*>(s) + (int64_t)row * lds, (uint32_t)(D / 32));
 
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
@@ -99,12 +115,11 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
             for (int j = 0; j < 8; ++j) v[j] = max_num(min_num(y[j] * rc, 448.0f), -448.0f);
             const uint32_t lo = cvt_pk4_e4m3(v[0], v[1], v[2], v[3]);
             const uint32_t hi = cvt_pk4_e4m3(v[4], v[5], v[6], v[7]);
-            if (c < nch) {
-                // non-temporal: measured on MI355X, [4096, 4096] 12.1 -> 10.3 us
-                // (the same policy made the SwiGLU kernel's codes 8% slower)
-                __builtin_nontemporal_store(v2i{(int)lo, (int)hi}, reinterpret_cast<v2i*>(q + (int64_t)row * ldq + (int64_t)c * 8));
-                if ((lane & 15) == 0) reinterpret_cast<float*>(s)[(int64_t)row * lds + (c >> 4)] = sc;
-            }
+            // non-temporal: measured on MI355X, [4096, 4096] 12.1 -> 10.3 us
+            // (the same policy made the SwiGLU kernel's codes 8% slower)
+            __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)lo, (int)hi}, rq, (uint32_t)c * 8u, 0, CPOL_NT_ST);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(sc), rs, (lane & 15) == 0 ? (uint32_t)(c >> 4) * 4u : 0x80000000u,
+                                                  0, 0);
         } else {
             m = group_max_abs<4>(m);
             const int e = mx_scale_exp(m);
@@ -113,10 +128,9 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
 #pragma unroll
             for (int j = 0; j < 8; ++j) t[j] = y[j] * mul;
             const uint32_t packed = MODE == NQ_MXFP4_FLOOR ? e2m1_floor8(t) : e2m1_encode8(t);
-            if (c < nch) {
-                *reinterpret_cast<uint32_t*>(q + (int64_t)row * ldq + (int64_t)c * 4) = packed;
-                if ((lane & 3) == 0) reinterpret_cast<uint8_t*>(s)[(int64_t)row * lds + (c >> 2)] = (uint8_t)(e + 127);
-            }
+            __builtin_amdgcn_raw_buffer_store_b32((int)packed, rq, (uint32_t)c * 4u, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b8((unsigned char)(e + 127), rs, (lane & 3) == 0 ? (uint32_t)(c >> 2) : 0x80000000u,
+                                                 0, 0);
         }
     }
 }
