@@ -102,19 +102,37 @@ __global__ __launch_bounds__(256) void per_token_kernel(const uint16_t* __restri
 // 1 x G groups (G in {32,...,512}, power of two, G/8 lanes per group): every
 // thread owns 8 consecutive elements; the G/8 lanes of a group reduce amax with
 // xor-shuffles. Grid-stride over all 8-element chunks of the [M, K] matrix.
+// Row and column of flat chunk ch (< total + 256) of a matrix with cpr chunks
+// per row. When total + 256 < 2^31 and cpr < 2^16 (a wave-uniform test), the
+// quotient comes from div_recip (3 VALU instructions) instead of a 64-bit
+// integer division (~40).
+struct ChunkIndex {
+    int64_t cpr;
+    double rcpr;
+    bool small;
+    __device__ ChunkIndex(int64_t cpr_, int64_t total)
+        : cpr(cpr_), rcpr(1.0 / (double)cpr_), small(total < 0x7FFFFF00 && cpr_ < 0x10000) {}
+    __device__ __forceinline__ void operator()(int64_t ch, int64_t& row, int64_t& col) const {
+        row = small ? (int64_t)div_recip((int)ch, rcpr) : ch / cpr;
+        col = ch - row * cpr;
+    }
+};
+
 template <int KIND, int GL>
 __global__ __launch_bounds__(256) void group_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
                                                     float* __restrict__ s, int64_t M, int64_t K, int64_t ldx,
                                                     int64_t ldq, int64_t lds) {
     const int64_t cpr = K >> 3;  // chunks per row
     const int64_t total = M * cpr;
+    const ChunkIndex index(cpr, total);
     const float qmax = KIND == KIND_FP8 ? 448.0f : 127.0f;
     for (int64_t base = (int64_t)blockIdx.x * 256; base < total; base += (int64_t)gridDim.x * 256) {
         // total is a multiple of GL (K % G == 0) and base of 256, so a whole
         // group is either in range or out of range together.
         const int64_t ch = base + threadIdx.x;
         const bool ok = ch < total;
-        const int64_t row = ok ? ch / cpr : 0, col = ok ? ch - row * cpr : 0;
+        int64_t row, col;
+        index(ok ? ch : 0, row, col);
         uint4 v = ok ? ld_stream16(reinterpret_cast<const uint4*>(x + row * ldx) + col)
                      : make_uint4(0, 0, 0, 0);
         float m = group_max_abs<GL>(amax8(v));
@@ -160,10 +178,12 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(const uint16_t* __restric
                                                        uint8_t* __restrict__ s, int64_t M, int64_t K, int64_t ldx) {
     const int64_t cpr = K >> 3;
     const int64_t total = M * cpr;
+    const ChunkIndex index(cpr, total);
     for (int64_t base = (int64_t)blockIdx.x * 256; base < total; base += (int64_t)gridDim.x * 256) {
         const int64_t ch = base + threadIdx.x;
         const bool ok = ch < total;
-        const int64_t row = ok ? ch / cpr : 0, col = ok ? ch - row * cpr : 0;
+        int64_t row, col;
+        index(ok ? ch : 0, row, col);
         uint4 v = ok ? ld_stream16(reinterpret_cast<const uint4*>(x + row * ldx) + col)
                      : make_uint4(0, 0, 0, 0);
         const float m = group_max_abs<4>(amax8(v));
@@ -224,8 +244,10 @@ __global__ __launch_bounds__(256) void mx_dequant_kernel(const uint8_t* __restri
                                                          uint16_t* __restrict__ out, int64_t M, int64_t K) {
     const int64_t cpr = K >> 3;
     const int64_t total = M * cpr;
+    const ChunkIndex index(cpr, total);
     for (int64_t ch = (int64_t)blockIdx.x * 256 + threadIdx.x; ch < total; ch += (int64_t)gridDim.x * 256) {
-        const int64_t row = ch / cpr, col = ch - row * cpr;
+        int64_t row, col;
+        index(ch, row, col);
         const uint32_t sc = s[row * (K >> 5) + (col >> 2)];
         const float mul = sc == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(sc << 23);  // 2^-127 is subnormal
         float f[8];
