@@ -84,6 +84,39 @@ def test_rmsnorm_quant_strided_rows(orc):
     assert np.array_equal(sh[:, : D // 128], os_) and np.all(sh[:, D // 128:] == -1.0)
 
 
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_rmsnorm_quant_special_values(orc, kind):
+    """Rows and weights that drive the group scale to its edges, bit-exact
+    against the oracle: a row holding +inf (the norm's r becomes 0, the inf
+    element NaN), a row holding NaN, weights near the bf16 maximum (y
+    overflows to +-inf: amax = inf, FP8 scale inf, reciprocal 0), weights near
+    the bf16 minimum normal (FP8 scale floored at 1e-10) and a weight group
+    whose amax / 448 lies around the 1e-10 floor."""
+    require_gpu()
+    M, D = 12, 2048
+    xb, wb = rms_inputs(orc, M, D, 77)
+    xb[3, 17] = 0x7F80                                          # +inf
+    xb[4, 300] = 0x7FC1                                         # NaN
+    xb[5, 1000] = 0xFF80                                        # -inf
+    wf = orc.bf16_bits_to_f32(wb).copy()
+    wf[0:128] = np.sign(wf[0:128]) * 3.0e38                     # y overflows in the first FP8 group
+    wf[128:256] *= 1e-36                                        # amax / 448 far below 1e-10
+    wf[256:384] = np.sign(wf[256:384]) * np.geomspace(5e-9, 3e-8, 128)  # amax / 448 at 1.0-1.5e-10
+    wf[384:416] = 0.0                                           # a zero MXFP4 block
+    wb = orc.f32_to_bf16_bits(wf.astype(np.float32))
+    eps = 1e-6
+    q, s = hkq.rmsnorm_quant(dev_bf16(xb), dev_bf16(wb), eps, kind)
+    torch.cuda.synchronize()
+    oq, os_ = orc.rmsnorm_quant(xb, wb, eps, kind)
+    assert np.array_equal(host_u8(q), oq)
+    if kind == 0:
+        sh = s.cpu().numpy()
+        assert np.isinf(os_[:, 0]).any() and (os_ == np.float32(1e-10)).any()  # both scale edges are reached
+        assert np.array_equal(sh.view(np.uint32), os_.view(np.uint32))
+    else:
+        assert np.array_equal(host_u8(s), os_)
+
+
 @pytest.mark.parametrize("kind", [0, 1])
 def test_fused_rmsnorm_modules_reference_call(orc, kind):
     """tests/test_misc.py:552-601 of the reference as written: M=256, N=4096,
