@@ -50,35 +50,43 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ w, uint8_t* __restrict__ q,
                                                             void* __restrict__ s, int M, int D, int64_t ldx,
                                                             int64_t ldq, int64_t lds, float eps) {
+    // the weight row, shared by the workgroup's four rows: held in LDS rather
+    // than in every lane's registers, so that more rows fit in flight per SIMD
+    __shared__ uint4 wl[NC * 64];
     const int lane = threadIdx.x & 63;
     // wave-uniform (made visibly so: the buffer resources below are then built in SGPRs)
     const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-    if (row >= M) return;  // no barriers below
     const int nch = D >> 3;
     // Buffer loads and stores over the row: chunks past D read zero and their
     // stores are dropped by the buffer bounds, so no lane branches around them
     // (only whole chunk columns past D are skipped, a wave-uniform test).
     const auto rx = make_rsrc(x + (int64_t)row * ldx, (uint32_t)D * 2u);
     const auto rw = make_rsrc(w, (uint32_t)D * 2u);
-    // x and the weight are both requested before the reduction, so the
-    // weight's (cache-resident) loads overlap the row's HBM loads
-    uint4 xv[NC], wv[NC];
+    // the weight's loads go out first (every wave, also one past M, takes its
+    // share and the barrier), then the row's HBM loads, which stay in flight
+    // while the weight is written to LDS
+    constexpr int WPT = (NC * 64 + 255) / 256;  // weight chunks per thread
+    uint4 wt[WPT];
+#pragma unroll
+    for (int i = 0; i < WPT; ++i) {
+        const int c = (int)threadIdx.x + 256 * i;
+        const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rw, c < NC * 64 ? (uint32_t)c * 16u : 0x80000000u, 0, 0);
+        wt[i] = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+    }
+    uint4 xv[NC];
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
         xv[i] = make_uint4(0, 0, 0, 0);
-        if (64 * i < nch) {
+        if (row < M && 64 * i < nch) {
             const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(lane + 64 * i) * 16u, 0, CPOL_NT_LD);
             xv[i] = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
         }
     }
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
-        wv[i] = make_uint4(0, 0, 0, 0);
-        if (64 * i < nch) {
-            const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)(lane + 64 * i) * 16u, 0, 0);
-            wv[i] = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
-        }
-    }
+    for (int i = 0; i < WPT; ++i)
+        if (threadIdx.x + 256 * i < NC * 64) wl[threadIdx.x + 256 * i] = wt[i];
+    __syncthreads();
+    if (row >= M) return;  // no barriers below
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
@@ -99,7 +107,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __re
         if (64 * i >= nch) break;  // wave-uniform: no lane has a chunk here
         float xf[8], wf[8], y[8];
         unpack8(xv[i], xf);
-        unpack8(wv[i], wf);
+        unpack8(wl[c], wf);
         float m = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
