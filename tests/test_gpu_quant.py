@@ -110,6 +110,24 @@ def test_group_quant_1x128_blockscale_shapes(orc, M, K):
     assert np.array_equal(s.cpu().numpy(), so) and np.array_equal(host_u8(q), qo)
 
 
+@pytest.mark.parametrize("K", [524288 - 128, 524288, 524288 + 1024])
+def test_group_and_mx_quant_wide_rows(orc, K):
+    """Rows of about 2^19 elements: from K / 8 = 2^16 chunks per row the
+    kernels take a chunk's row from a 64-bit division instead of the double
+    reciprocal (which needs fewer than 2^16 chunks per row); both sides of the
+    switch, and rows that end inside a workgroup's chunks."""
+    require_gpu()
+    M = 3
+    xb = orc.randn_bf16((M, K), seed=K % 1000)
+    q, s = hkq.group_quant(dev_bf16(xb), 128, hkq.KIND_FP8)
+    q4, s4 = hkq.mx_quant(dev_bf16(xb), True)
+    torch.cuda.synchronize()
+    qo, so = orc.quant_rowwise(xb, 128, "fp8")
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32)) and np.array_equal(host_u8(q), qo)
+    qo4, so4 = orc.mx_quant_fp4(xb)
+    assert np.array_equal(host_u8(s4), so4) and np.array_equal(host_u8(q4), qo4)
+
+
 def mx_edge(orc, xb):
     xb[0, :32] = 0                                                               # zero block -> code 0
     xb[0, 32:64] = orc.f32_to_bf16_bits(np.full(32, 7.0, np.float32))          # amax rounds up
