@@ -152,16 +152,28 @@ __device__ __forceinline__ int bs_tail_from(const MoeBsParams& p) {
 // the last): a valid word (e < E) that is not the second word of a pair, the
 // second word (e | (b+1) << 16, b even) following its pair's first one before
 // tail_from. Every wave of the workgroup finds the same word, 512 words per
-// step (8 consecutive words per lane, their loads issued together).
-__device__ __forceinline__ int bs_leader(const MoeBsParams& p, int li, int tail_from) {
-    constexpr int W = 8;
+// step (8 consecutive words per lane, their loads issued together); the
+// caller loads the first step's words (bs_words), ahead of the histogram
+// loads that tail_from waits on.
+constexpr int BS_LW = 8;
+__device__ __forceinline__ void bs_words(const MoeBsParams& p, int m0, int (&ed)[BS_LW]) {
+    const int mw = m0 + (int)(threadIdx.x & 63) * BS_LW;
+#pragma unroll
+    for (int k = 0; k < BS_LW; ++k) ed[k] = mw + k < p.grid_m ? p.expt_data[mw + k] : -1;
+}
+__device__ __forceinline__ int bs_leader(const MoeBsParams& p, int li, int tail_from, const int (&ed0)[BS_LW]) {
+    constexpr int W = BS_LW;
     const int lane = threadIdx.x & 63;
     int base = 0, carry = -1;  // expt_data[m0 - 1]
     for (int m0 = 0; m0 < p.grid_m; m0 += 64 * W) {
         const int mw = m0 + lane * W;
         int ed[W];
+        if (m0 == 0) {
 #pragma unroll
-        for (int k = 0; k < W; ++k) ed[k] = mw + k < p.grid_m ? p.expt_data[mw + k] : -1;
+            for (int k = 0; k < W; ++k) ed[k] = ed0[k];
+        } else {
+            bs_words(p, m0, ed);
+        }
         const int up = __shfl(ed[W - 1], (lane + 63) & 63);
         uint32_t lead = 0;
 #pragma unroll
@@ -445,8 +457,10 @@ __global__ __launch_bounds__(64 * BS_NW, 1) void moe_blockscale8_kernel(const Mo
     // workgroup per word, every transition between workgroups on a CU left it
     // idle ~4.5 us; measured on MI355X, Mixtral gate/up: 134 us per CU of gaps).
     const int li = blockIdx.x / p.tiles_n, tn = blockIdx.x % p.tiles_n;
+    int ed0[BS_LW];
+    bs_words(p, 0, ed0);
     const int tail_from = __builtin_amdgcn_readfirstlane(bs_tail_from(p));
-    const int pm = __builtin_amdgcn_readfirstlane(bs_leader(p, li, tail_from));
+    const int pm = __builtin_amdgcn_readfirstlane(bs_leader(p, li, tail_from, ed0));
     if (pm < 0) return;  // uniform: a spare workgroup
     const int ed = p.expt_data[pm];
     const int e = ed & 0xFFFF, b = ed >> 16;
