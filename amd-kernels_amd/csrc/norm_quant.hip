@@ -36,7 +36,8 @@ __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
 
 // --------------------------------------------------------------------------
 // RMSNorm + quantization. One wave per row, four rows per workgroup; lane l
-// holds the 16-byte chunks c = l + 64 i (8 bf16 each) of x in registers.
+// holds the 16-byte chunks c = l + 64 i (8 bf16 each) of x in registers, the
+// workgroup's rows share the weight row in LDS.
 //   sum  = fma-chain of x^2 over the lane's chunks (i, then element order),
 //          then the xor butterfly over lanes;
 //   r    = 1 / sqrt(sum / D + eps)   (correctly rounded sqrt and division);
